@@ -1,0 +1,222 @@
+// C-ABI entry points of libtsattn.so (declared in include/tsattn.h).
+//
+// Validation mirrors the contract checks of the reference's
+// scaled_dot_product_attention (src/tensorsmith/nn/attention.py:36-62) so a
+// caller binding the library directly gets the same refusals; the Python
+// host layer maps TSATTN_ERR_INVALID to ValueError / TypeError.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <atomic>
+
+#include "mfma_common.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+std::atomic<int> g_policy{0};     // 0 auto, 1 generic kernels only
+thread_local int g_last_path = 0; // 0 none, 1 generic, 2 mfma, 3 decode
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char *where) {
+  if (e == hipSuccess) return TSATTN_OK;
+  return fail(TSATTN_ERR_HIP, "%s: %s", where, hipGetErrorString(e));
+}
+
+bool is_float_dtype(int d) {
+  return d == TSATTN_F32 || d == TSATTN_F16 || d == TSATTN_BF16 || d == TSATTN_F64;
+}
+
+int check_view(const tsattn_view *v, const char *name) {
+  if (!v) return fail(TSATTN_ERR_INVALID, "%s view is NULL", name);
+  if (!v->data) return fail(TSATTN_ERR_INVALID, "%s data pointer is NULL", name);
+  if (v->stride[3] != 1) return fail(TSATTN_ERR_INVALID, "%s innermost stride must be 1", name);
+  return TSATTN_OK;
+}
+
+int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
+  if (!p) return fail(TSATTN_ERR_INVALID, "problem is NULL");
+  if (!is_float_dtype(p->dtype))
+    return fail(TSATTN_ERR_INVALID, "attention inputs must have the same floating-point dtype");
+  if (p->batch <= 0 || p->heads_q <= 0 || p->heads_kv <= 0 || p->len_q <= 0 || p->len_kv <= 0 ||
+      p->dim_qk <= 0 || p->dim_v <= 0)
+    return fail(TSATTN_ERR_INVALID, "query/key head dimensions must match and sequences must be nonempty");
+  if (p->heads_q % p->heads_kv)
+    return fail(TSATTN_ERR_INVALID,
+                "grouped-query attention requires enable_gqa and query heads divisible by KV heads");
+  if (!isfinite(p->scale)) return fail(TSATTN_ERR_INVALID, "attention scale must be finite");
+  if (p->causal_offset < 0)
+    return fail(TSATTN_ERR_INVALID, "invalid dropout probability, block size, or causal offset");
+  if (p->mask_kind != TSATTN_MASK_NONE) {
+    if (p->mask_kind != TSATTN_MASK_BOOL && p->mask_kind != TSATTN_MASK_ADDITIVE)
+      return fail(TSATTN_ERR_INVALID, "unknown mask kind %d", p->mask_kind);
+    if (!p->mask.data) return fail(TSATTN_ERR_INVALID, "mask data pointer is NULL");
+    if (p->mask_kind == TSATTN_MASK_BOOL && p->mask_dtype != TSATTN_BOOL)
+      return fail(TSATTN_ERR_INVALID, "boolean masks must have dtype TSATTN_BOOL");
+    if (p->mask_kind == TSATTN_MASK_ADDITIVE && !is_float_dtype(p->mask_dtype))
+      return fail(TSATTN_ERR_INVALID, "attention masks must be boolean or floating point");
+  }
+  if (p->dim_qk > 512 || p->dim_v > 512)
+    return fail(TSATTN_ERR_UNSUPPORTED, "head dims above 512 are not supported (got %d/%d)",
+                p->dim_qk, p->dim_v);
+  tsattn::Problem q{};
+  q.B = p->batch;
+  q.Hq = p->heads_q;
+  q.Hkv = p->heads_kv;
+  q.Sq = p->len_q;
+  q.Sk = p->len_kv;
+  q.Dqk = p->dim_qk;
+  q.Dv = p->dim_v;
+  q.rep = p->heads_q / p->heads_kv;
+  q.scale = p->scale;
+  q.causal = p->is_causal ? 1 : 0;
+  q.offset = p->causal_offset;
+  q.kv_len = p->kv_len;
+  q.kv_prefix = p->kv_prefix;
+  q.mask.kind = p->mask_kind;
+  q.mask.dtype = p->mask_dtype;
+  q.mask.data = p->mask.data;
+  q.mask.s0 = p->mask.stride[0];
+  q.mask.s1 = p->mask.stride[1];
+  q.mask.s2 = p->mask.stride[2];
+  q.mask.s3 = p->mask.stride[3];
+  *out = q;
+  return TSATTN_OK;
+}
+
+size_t acc_size(int dtype) { return dtype == TSATTN_F64 ? sizeof(double) : sizeof(float); }
+
+}  // namespace
+
+extern "C" {
+
+int tsattn_abi_version(void) { return TSATTN_ABI_VERSION; }
+
+const char *tsattn_last_error(void) { return g_error; }
+
+int tsattn_set_kernel_policy(int policy) {
+  if (policy < 0 || policy > 1) return fail(TSATTN_ERR_INVALID, "unknown kernel policy %d", policy);
+  g_policy.store(policy);
+  return TSATTN_OK;
+}
+
+int tsattn_last_kernel_path(void) { return g_last_path; }
+
+int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                        const tsattn_view *v, const tsattn_view *out, void *lse, void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
+      (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
+    return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v),
+               vo = tsattn::make_view(out);
+  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && tsattn::aligned16(vq) &&
+      tsattn::aligned16(vk) && tsattn::aligned16(vv) && tsattn::aligned16(vo)) {
+    g_last_path = 2;
+    return hip_status(tsattn::launch_mfma_forward(pr, p->dtype, vq, vk, vv, vo,
+                                                  static_cast<float *>(lse), st),
+                      "mfma forward launch");
+  }
+  g_last_path = 1;
+  return hip_status(tsattn::launch_generic_forward(pr, p->dtype, vq, vk, vv, vo, lse, st),
+                    "generic forward launch");
+}
+
+size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p) {
+  if (!p || p->batch <= 0 || p->heads_q <= 0 || p->len_q <= 0) return 0;
+  return static_cast<size_t>(p->batch) * p->heads_q * p->len_q * acc_size(p->dtype);
+}
+
+int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                         const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,
+                         const void *lse, const tsattn_view *dq, const tsattn_view *dk,
+                         const tsattn_view *dv, void *workspace, size_t workspace_bytes,
+                         void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
+      (rc = check_view(v, "value")) || (rc = check_view(out, "output")) ||
+      (rc = check_view(dout, "upstream gradient")) || (rc = check_view(dq, "dq")) ||
+      (rc = check_view(dk, "dk")) || (rc = check_view(dv, "dv")))
+    return rc;
+  if (!lse) return fail(TSATTN_ERR_INVALID, "backward needs the saved LSE");
+  const size_t need = tsattn_sdpa_backward_workspace(p);
+  if (!workspace || workspace_bytes < need)
+    return fail(TSATTN_ERR_INVALID, "backward workspace too small: %zu < %zu bytes",
+                workspace_bytes, need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v),
+               vo = tsattn::make_view(out), vg = tsattn::make_view(dout),
+               vdq = tsattn::make_view(dq), vdk = tsattn::make_view(dk),
+               vdv = tsattn::make_view(dv);
+  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && tsattn::aligned16(vq) &&
+      tsattn::aligned16(vk) && tsattn::aligned16(vv) && tsattn::aligned16(vo) &&
+      tsattn::aligned16(vg) && tsattn::aligned16(vdq) && tsattn::aligned16(vdk) &&
+      tsattn::aligned16(vdv)) {
+    g_last_path = 2;
+    return hip_status(tsattn::launch_mfma_backward(pr, p->dtype, vq, vk, vv, vo, vg,
+                                                   static_cast<const float *>(lse), vdq, vdk,
+                                                   vdv, static_cast<float *>(workspace), st),
+                      "mfma backward launch");
+  }
+  g_last_path = 1;
+  return hip_status(tsattn::launch_generic_backward(pr, p->dtype, vq, vk, vv, vo, vg, lse, vdq,
+                                                    vdk, vdv, workspace, st),
+                    "generic backward launch");
+}
+
+size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len) {
+  tsattn::Problem pr;
+  if (check_problem(p, &pr)) return 0;
+  return tsattn::decode_workspace_bytes(pr, split_len);
+}
+
+int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                          const tsattn_view *v, const tsattn_view *out, int32_t split_len,
+                          void *workspace, size_t workspace_bytes, void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
+      (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
+    return rc;
+  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
+  if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(tsattn::make_view(q)) ||
+      !tsattn::aligned16(tsattn::make_view(k)) || !tsattn::aligned16(tsattn::make_view(v)))
+    return fail(TSATTN_ERR_UNSUPPORTED,
+                "decode kernel needs <= 8 query rows per KV head, f16/bf16, equal head dims in "
+                "{64,128,256} and 16-byte aligned rows");
+  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(TSATTN_ERR_INVALID, "decode workspace too small: %zu < %zu bytes",
+                workspace_bytes, need);
+  g_last_path = 3;
+  return hip_status(tsattn::launch_decode(pr, p->dtype, tsattn::make_view(q), tsattn::make_view(k),
+                                          tsattn::make_view(v), tsattn::make_view(out), split_len,
+                                          workspace, static_cast<hipStream_t>(stream)),
+                    "decode launch");
+}
+
+int tsattn_key_mask_lengths(const uint8_t *mask, int64_t stride_b, int64_t stride_k,
+                            int32_t batch, int32_t len_kv, int32_t *kv_len, int32_t *kv_prefix,
+                            void *stream) {
+  if (!mask || !kv_len) return fail(TSATTN_ERR_INVALID, "mask and kv_len must be non-NULL");
+  if (batch <= 0 || len_kv <= 0) return fail(TSATTN_ERR_INVALID, "batch and len_kv must be positive");
+  return hip_status(tsattn::launch_key_mask_lengths(mask, stride_b, stride_k, batch, len_kv, kv_len,
+                                                    kv_prefix, static_cast<hipStream_t>(stream)),
+                    "key mask lengths launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,308 @@
+// KV-cache decode attention for gfx950: a few query rows per KV head against
+// a long cached prefix; bound by HBM bandwidth, not by math.
+//
+// Math: the reference's online softmax (src/tensorsmith/nn/attention.py:
+// 185-193) applied twice.  Each workgroup reduces one split of the cache to a
+// partial state (running max m, denominator l, accumulator acc) -- inside it
+// every lane keeps its own state over the keys it streams, so no cross-lane
+// traffic happens per key -- and decode_merge_kernel combines the splits with
+// the same rescale-by-exp(m - M) rule.  Fully masked rows give 0.
+//
+// Memory layout: each key row is read by D/8 neighbouring lanes as 16-byte
+// loads (one wave instruction covers 64*16 B of consecutive keys), U such
+// instructions for K and U for V are issued before any is consumed, so every
+// wave keeps 2*U KiB in flight.
+#include "mfma_common.h"
+
+namespace tsattn {
+namespace {
+
+constexpr int NT = 256;
+constexpr int U = 4;  // key instructions in flight per batch (per operand)
+constexpr int kMaxRows = 8;
+
+struct DecArgs {
+  Problem p;
+  View q, k, v, o;
+  float *ws;
+  int split_len, max_splits, rows;  // rows = rep * Sq query rows per KV head
+  float sl;                         // scale * log2(e)
+};
+
+// Keys any row may attend to: [0, eff_end).
+__device__ __forceinline__ int eff_end(const Problem &p, int b) {
+  int e = kv_end_for(p, b);
+  if (p.causal) {
+    const int64_t lim = static_cast<int64_t>(p.Sq) - 1 + p.offset + 1;
+    if (lim < e) e = static_cast<int>(lim < 0 ? 0 : lim);
+  }
+  return e;
+}
+
+__device__ __forceinline__ void merge_state(float &m, float &l, float *acc, float m2, float l2,
+                                            const float *acc2) {
+  const float mx = fmaxf(m, m2);
+  const float base = mx == -INFINITY ? 0.f : mx;
+  const float c1 = fast_exp2(m - base), c2 = fast_exp2(m2 - base);
+  l = l * c1 + l2 * c2;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = acc[e] * c1 + acc2[e] * c2;
+  m = mx;
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack8(u32x4 x, float *out) {
+  const T *e = reinterpret_cast<const T *>(&x);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
+}
+
+template <typename T, int D, int R>
+__global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
+  constexpr int LPK = D / 8;      // lanes per key row
+  constexpr int KPI = 64 / LPK;   // keys per wave instruction
+  constexpr int BATCH = KPI * U;  // keys per wave per batch
+  __shared__ float red[4][R][10 * LPK];
+
+  const Problem &p = a.p;
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int dc = lane % LPK, kg = lane / LPK;
+  const int end = eff_end(p, b);
+  const int k_begin = split * a.split_len;
+  if (k_begin >= end) return;  // this split holds no keys for row b
+  const int k_stop = min(k_begin + a.split_len, end);
+
+  // Query rows r = rr * Sq + i (query head hk*rep + rr, position i), pre-scaled
+  // so that s = q.k is already in log2 units.
+  float qv[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r < a.rows) {
+      const int hq = hk * p.rep + r / p.Sq, i = r % p.Sq;
+      const T *qp = static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1 +
+                    static_cast<int64_t>(i) * a.q.s2 + dc * 8;
+      unpack8<T>(ld16(qp), qv[r]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[r][e] *= a.sl;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qv[r][e] = 0.f;
+    }
+  }
+  float m[R], l[R], acc[R][8];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    m[r] = -INFINITY;
+    l[r] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
+  }
+
+  const T *kbase = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1 + dc * 8;
+  const T *vbase = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1 + dc * 8;
+  const float log2e = kLog2e;
+  for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
+    u32x4 kr[U], vr[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = kb + u * KPI + kg;
+      const bool ok = key < k_stop;
+      kr[u] = ok ? ld16(kbase + static_cast<int64_t>(key) * a.k.s2) : u32x4{0, 0, 0, 0};
+      vr[u] = ok ? ld16(vbase + static_cast<int64_t>(key) * a.v.s2) : u32x4{0, 0, 0, 0};
+    }
+    float s[U][R];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float kf[8];
+      unpack8<T>(kr[u], kf);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) d = fmaf(qv[r][e], kf[e], d);
+#pragma unroll
+        for (int x = LPK / 2; x >= 1; x >>= 1) d += __shfl_xor(d, x, 64);
+        s[u][r] = d;
+      }
+    }
+    // masks: invalid keys, causal, user mask (bool or additive, any broadcast)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int key = kb + u * KPI + kg;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = r % p.Sq;
+        bool ok = key < k_stop && r < a.rows &&
+                  (!p.causal || static_cast<int64_t>(i) + p.offset >= key);
+        if (ok && p.mask.kind != TSATTN_MASK_NONE) {
+          const int hq = hk * p.rep + r / p.Sq;
+          const int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
+                             static_cast<int64_t>(key) * p.mask.s3;
+          if (p.mask.kind == TSATTN_MASK_BOOL)
+            ok = static_cast<const uint8_t *>(p.mask.data)[mi] != 0;
+          else
+            s[u][r] += load_additive<float>(p.mask.data, mi, p.mask.dtype) * log2e;
+        }
+        if (!ok) s[u][r] = -INFINITY;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float mb = m[r];
+#pragma unroll
+      for (int u = 0; u < U; ++u) mb = fmaxf(mb, s[u][r]);
+      const float base = mb == -INFINITY ? 0.f : mb;
+      const float corr = fast_exp2(m[r] - base);
+      l[r] *= corr;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[r][e] *= corr;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const float pv = fast_exp2(s[u][r] - base);
+        l[r] += pv;
+        float vf[8];
+        unpack8<T>(vr[u], vf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pv, vf[e], acc[r][e]);
+      }
+      m[r] = mb;
+    }
+  }
+
+  // Merge the key groups of the wave (lanes dc, dc+LPK, ...), then the waves.
+#pragma unroll
+  for (int x = LPK; x < 64; x <<= 1) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float a2[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) a2[e] = __shfl_xor(acc[r][e], x, 64);
+      const float m2 = __shfl_xor(m[r], x, 64), l2 = __shfl_xor(l[r], x, 64);
+      merge_state(m[r], l[r], acc[r], m2, l2, a2);
+    }
+  }
+  if (kg == 0) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float *slot = &red[w][r][dc * 10];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) slot[e] = acc[r][e];
+      slot[8] = m[r];
+      slot[9] = l[r];
+    }
+  }
+  __syncthreads();
+  if (w != 0 || kg != 0) return;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (r >= a.rows) break;
+#pragma unroll
+    for (int ww = 1; ww < 4; ++ww) {
+      const float *slot = &red[ww][r][dc * 10];
+      merge_state(m[r], l[r], acc[r], slot[8], slot[9], slot);
+    }
+    float *out = a.ws + ((static_cast<int64_t>(b * p.Hkv + hk) * a.max_splits + split) * a.rows + r) *
+                            static_cast<int64_t>(D + 2);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[dc * 8 + e] = acc[r][e];
+    if (dc == 0) {
+      out[D] = m[r];
+      out[D + 1] = l[r];
+    }
+  }
+}
+
+// One wave per output row (b, hq, i): combine the splits' partial states.
+template <typename T, int D>
+__global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
+  const Problem &p = a.p;
+  const int b = blockIdx.y, row = blockIdx.x;  // row = hq * Sq + i
+  const int hq = row / p.Sq, i = row - hq * p.Sq;
+  const int hk = hq / p.rep, r = (hq - hk * p.rep) * p.Sq + i;
+  const int lane = threadIdx.x;
+  const int end = eff_end(p, b);
+  const int n = end > 0 ? (end + a.split_len - 1) / a.split_len : 0;
+  const float *base = a.ws + (static_cast<int64_t>(b * p.Hkv + hk) * a.max_splits * a.rows + r) *
+                                 static_cast<int64_t>(D + 2);
+  const int64_t stride = static_cast<int64_t>(a.rows) * (D + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < n; ++s) M = fmaxf(M, base[s * stride + D]);
+  const float mb = M == -INFINITY ? 0.f : M;
+  constexpr int PER = (D + 63) / 64;
+  float acc[PER] = {};
+  float L = 0.f;
+  for (int s = 0; s < n; ++s) {
+    const float *part = base + s * stride;
+    const float c = fast_exp2(part[D] - mb);
+    L += part[D + 1] * c;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) {
+      const int d = lane + 64 * t;
+      if (d < D) acc[t] += part[d] * c;
+    }
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  T *op = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
+          static_cast<int64_t>(i) * a.o.s2;
+#pragma unroll
+  for (int t = 0; t < PER; ++t) {
+    const int d = lane + 64 * t;
+    if (d < D) op[d] = static_cast<T>(acc[t] * inv);
+  }
+}
+
+template <typename T, int D, int R>
+hipError_t launch_rows(const DecArgs &a, hipStream_t st) {
+  const Problem &p = a.p;
+  decode_split_kernel<T, D, R><<<dim3(a.max_splits, p.Hkv, p.B), dim3(NT), 0, st>>>(a);
+  decode_merge_kernel<T, D><<<dim3(p.Hq * p.Sq, p.B), dim3(64), 0, st>>>(a);
+  return hipGetLastError();
+}
+
+template <typename T, int D>
+hipError_t launch_dim(const DecArgs &a, hipStream_t st) {
+  if (a.rows <= 1) return launch_rows<T, D, 1>(a, st);
+  if (a.rows <= 2) return launch_rows<T, D, 2>(a, st);
+  if (a.rows <= 4) return launch_rows<T, D, 4>(a, st);
+  return launch_rows<T, D, 8>(a, st);
+}
+
+int choose_split(const Problem &p, int split_len) {
+  if (split_len > 0) return split_len;
+  int s = 512;
+  while (s > 64 && static_cast<int64_t>(p.B) * p.Hkv * ((p.Sk + s - 1) / s) < 4096) s >>= 1;
+  return s;
+}
+
+}  // namespace
+
+bool decode_supported(const Problem &p, int dtype) {
+  if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
+  if (p.Dqk != p.Dv || (p.Dqk != 64 && p.Dqk != 128 && p.Dqk != 256)) return false;
+  return p.rep * p.Sq <= kMaxRows;
+}
+
+size_t decode_workspace_bytes(const Problem &p, int split_len) {
+  const int s = choose_split(p, split_len);
+  const int64_t splits = (p.Sk + s - 1) / s;
+  return static_cast<size_t>(p.B) * p.Hkv * splits * p.rep * p.Sq * (p.Dv + 2) * sizeof(float);
+}
+
+hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,
+                         int split_len, void *workspace, hipStream_t st) {
+  DecArgs a{p, q, k, v, o, static_cast<float *>(workspace), 0, 0, p.rep * p.Sq,
+            static_cast<float>(p.scale) * kLog2e};
+  a.split_len = choose_split(p, split_len);
+  a.max_splits = (p.Sk + a.split_len - 1) / a.split_len;
+  if (dtype == TSATTN_BF16) {
+    if (p.Dqk == 64) return launch_dim<bf16, 64>(a, st);
+    if (p.Dqk == 128) return launch_dim<bf16, 128>(a, st);
+    return launch_dim<bf16, 256>(a, st);
+  }
+  if (p.Dqk == 64) return launch_dim<f16, 64>(a, st);
+  if (p.Dqk == 128) return launch_dim<f16, 128>(a, st);
+  return launch_dim<f16, 256>(a, st);
+}
+
+}  // namespace tsattn

@@ -1,0 +1,425 @@
+// Generic attention kernels: one wavefront per query (or key) row, VALU math
+// in the accumulator type (float for f32/f16/bf16, double for f64).
+//
+// These carry every case the reference allows that the MFMA kernels do not
+// specialise: fp32 / fp64 inputs, any head dims (Dv != Dqk included,
+// reference tests/test_transformer.py:44-46), boolean or additive masks of any
+// broadcast shape, any scale sign.  Same recurrence as the reference's
+// streaming backend (src/tensorsmith/nn/attention.py:175-198) and its VJP
+// (:220-244): running max / sum / accumulator per row over 64-key chunks, and
+// P recomputed from the saved LSE in the backward.
+#include "tsattn_internal.h"
+
+namespace tsattn {
+namespace {
+
+constexpr int kWaves = 4;        // rows per workgroup
+constexpr int kChunk = 64;       // keys (or queries) per chunk = one lane each
+constexpr int kMaxDimSlots = 8;  // head dims up to 8 * 64 = 512
+
+template <typename A>
+__device__ __forceinline__ A neg_inf() {
+  return -static_cast<A>(INFINITY);
+}
+
+__device__ __forceinline__ float exp_acc(float x) { return expf(x); }
+__device__ __forceinline__ double exp_acc(double x) { return exp(x); }
+__device__ __forceinline__ float log_acc(float x) { return logf(x); }
+__device__ __forceinline__ double log_acc(double x) { return log(x); }
+
+template <typename A>
+__device__ __forceinline__ A wave_max(A x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    A y = __shfl_xor(x, m, 64);
+    x = x > y ? x : y;
+  }
+  return x;
+}
+
+template <typename A>
+__device__ __forceinline__ A wave_sum(A x) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m, 64);
+  return x;
+}
+
+// Score of (query row held in `qrow`, key j), with the reference's order:
+// scale, then mask (bool -> -inf, additive -> +), then causal (:102-113).
+template <typename T, typename A>
+__device__ __forceinline__ A score(const Problem &p, const A *qrow, const T *krow, int b, int hq,
+                                   int i, int j, int kv_end) {
+  if (j >= kv_end) return neg_inf<A>();
+  if (p.causal && static_cast<int64_t>(i) + p.offset < static_cast<int64_t>(j)) return neg_inf<A>();
+  A acc = 0;
+  for (int d = 0; d < p.Dqk; ++d) acc += qrow[d] * to_acc<A>(krow[d]);
+  A s = acc * static_cast<A>(p.scale);
+  if (p.mask.kind != TSATTN_MASK_NONE) {
+    int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
+                 static_cast<int64_t>(j) * p.mask.s3;
+    if (p.mask.kind == TSATTN_MASK_BOOL) {
+      if (!static_cast<const uint8_t *>(p.mask.data)[mi]) return neg_inf<A>();
+    } else {
+      s += load_additive<A>(p.mask.data, mi, p.mask.dtype);
+    }
+  }
+  return s;
+}
+
+template <typename T>
+__device__ __forceinline__ const T *row_ptr(View v, int b, int h, int s) {
+  return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1 + static_cast<int64_t>(s) * v.s2;
+}
+template <typename T>
+__device__ __forceinline__ T *row_ptr_mut(View v, int b, int h, int s) {
+  return const_cast<T *>(row_ptr<T>(v, b, h, s));
+}
+
+// ---------------------------------------------------------------------------
+// Forward: grid (ceil(Sq/4), Hq, B); wave w owns query row blockIdx.x*4 + w.
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void generic_forward_kernel(Problem p, View q, View k, View v,
+                                                              View o, A *lse) {
+  extern __shared__ unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = blockIdx.z, hq = blockIdx.y, hk = hq / p.rep;
+  const int i = blockIdx.x * kWaves + w;
+  const bool row_ok = i < p.Sq;
+  A *qrow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + kChunk);
+  A *pbuf = qrow + p.Dqk;
+  const int kv_end = kv_end_for(p, b);
+
+  if (row_ok) {
+    const T *qp = row_ptr<T>(q, b, hq, i);
+    for (int d = lane; d < p.Dqk; d += 64) qrow[d] = to_acc<A>(qp[d]);
+  }
+  // Uniform chunk count for the workgroup: the furthest key any of its rows sees.
+  int64_t last_row = static_cast<int64_t>(blockIdx.x) * kWaves + kWaves - 1;
+  if (last_row > p.Sq - 1) last_row = p.Sq - 1;
+  int64_t stop = kv_end;
+  if (p.causal && last_row + p.offset + 1 < stop) stop = last_row + p.offset + 1;
+  if (stop < 0) stop = 0;
+  __syncthreads();
+
+  A m = neg_inf<A>(), l = 0;
+  A acc[kMaxDimSlots];
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) acc[t] = 0;
+
+  for (int j0 = 0; j0 < stop; j0 += kChunk) {
+    const int j = j0 + lane;
+    A s = neg_inf<A>();
+    if (row_ok) s = score<T, A>(p, qrow, row_ptr<T>(k, b, hk, j < p.Sk ? j : 0), b, hq, i, j, kv_end);
+    const A cmax = wave_max(s);
+    const A m_new = m > cmax ? m : cmax;
+    const A base = isfinite(m_new) ? m_new : A(0);
+    const A corr = exp_acc(m - base);
+    const A pj = exp_acc(s - base);
+    l = l * corr + wave_sum(pj);
+    m = m_new;
+#pragma unroll
+    for (int t = 0; t < kMaxDimSlots; ++t) acc[t] *= corr;
+    pbuf[lane] = pj;
+    __syncthreads();
+    const int n = (stop - j0) < kChunk ? static_cast<int>(stop - j0) : kChunk;
+    for (int jj = 0; jj < n; ++jj) {
+      const A pv = pbuf[jj];
+      if (pv == A(0)) continue;  // masked or underflowed key: contributes nothing
+      const T *vrow = row_ptr<T>(v, b, hk, j0 + jj);
+#pragma unroll
+      for (int t = 0; t < kMaxDimSlots; ++t) {
+        const int d = lane + 64 * t;
+        if (d < p.Dv) acc[t] += pv * to_acc<A>(vrow[d]);
+      }
+    }
+    __syncthreads();
+  }
+  if (!row_ok) return;
+  const A inv = l > A(0) ? A(1) / l : A(1);
+  T *op = row_ptr_mut<T>(o, b, hq, i);
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) {
+    const int d = lane + 64 * t;
+    if (d < p.Dv) op[d] = from_acc<T, A>(acc[t] * inv);
+  }
+  if (lse && lane == 0)
+    lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i] = l > A(0) ? m + log_acc(l) : neg_inf<A>();
+}
+
+// ---------------------------------------------------------------------------
+// Backward pass 1: delta_i = sum_d dout_i,d * out_i,d (attention.py:232).
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void generic_delta_kernel(Problem p, View o, View dout, A *delta) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = blockIdx.z, hq = blockIdx.y, i = blockIdx.x * kWaves + w;
+  if (i >= p.Sq) return;
+  const T *op = row_ptr<T>(o, b, hq, i);
+  const T *gp = row_ptr<T>(dout, b, hq, i);
+  A s = 0;
+  for (int d = lane; d < p.Dv; d += 64) s += to_acc<A>(op[d]) * to_acc<A>(gp[d]);
+  s = wave_sum(s);
+  if (lane == 0) delta[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i] = s;
+}
+
+// ---------------------------------------------------------------------------
+// Backward pass 2: dq_i = scale * sum_j p_ij (dp_ij - delta_i) k_j (:237-239).
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View k, View v,
+                                                         View dout, const A *lse, const A *delta,
+                                                         View dq) {
+  extern __shared__ unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = blockIdx.z, hq = blockIdx.y, hk = hq / p.rep;
+  const int i = blockIdx.x * kWaves + w;
+  const bool row_ok = i < p.Sq;
+  A *qrow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + p.Dv + kChunk);
+  A *grow = qrow + p.Dqk;
+  A *dsbuf = grow + p.Dv;
+  const int kv_end = kv_end_for(p, b);
+  A row_lse = 0, row_delta = 0;
+  if (row_ok) {
+    const T *qp = row_ptr<T>(q, b, hq, i);
+    const T *gp = row_ptr<T>(dout, b, hq, i);
+    for (int d = lane; d < p.Dqk; d += 64) qrow[d] = to_acc<A>(qp[d]);
+    for (int d = lane; d < p.Dv; d += 64) grow[d] = to_acc<A>(gp[d]);
+    const int64_t r = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i;
+    row_lse = lse[r];
+    if (!isfinite(row_lse)) row_lse = 0;  // safe_lse (:231)
+    row_delta = delta[r];
+  }
+  int64_t last_row = static_cast<int64_t>(blockIdx.x) * kWaves + kWaves - 1;
+  if (last_row > p.Sq - 1) last_row = p.Sq - 1;
+  int64_t stop = kv_end;
+  if (p.causal && last_row + p.offset + 1 < stop) stop = last_row + p.offset + 1;
+  if (stop < 0) stop = 0;
+  __syncthreads();
+
+  A acc[kMaxDimSlots];
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) acc[t] = 0;
+  const A scale = static_cast<A>(p.scale);
+  for (int j0 = 0; j0 < stop; j0 += kChunk) {
+    const int j = j0 + lane;
+    A ds = 0;
+    if (row_ok && j < kv_end) {
+      const T *krow = row_ptr<T>(k, b, hk, j);
+      const A s = score<T, A>(p, qrow, krow, b, hq, i, j, kv_end);
+      const A pij = exp_acc(s - row_lse);
+      if (pij != A(0)) {
+        const T *vrow = row_ptr<T>(v, b, hk, j);
+        A dp = 0;
+        for (int d = 0; d < p.Dv; ++d) dp += grow[d] * to_acc<A>(vrow[d]);
+        ds = pij * (dp - row_delta) * scale;
+      }
+    }
+    dsbuf[lane] = ds;
+    __syncthreads();
+    const int n = (stop - j0) < kChunk ? static_cast<int>(stop - j0) : kChunk;
+    for (int jj = 0; jj < n; ++jj) {
+      const A c = dsbuf[jj];
+      if (c == A(0)) continue;
+      const T *krow = row_ptr<T>(k, b, hk, j0 + jj);
+#pragma unroll
+      for (int t = 0; t < kMaxDimSlots; ++t) {
+        const int d = lane + 64 * t;
+        if (d < p.Dqk) acc[t] += c * to_acc<A>(krow[d]);
+      }
+    }
+    __syncthreads();
+  }
+  if (!row_ok) return;
+  T *out = row_ptr_mut<T>(dq, b, hq, i);
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) {
+    const int d = lane + 64 * t;
+    if (d < p.Dqk) out[d] = from_acc<T, A>(acc[t]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward pass 3: per key row j of KV head hk, summed over the query heads
+// of its group (:240-247): dv_j = sum_i p_ij dout_i, dk_j = sum_i ds_ij q_i.
+// grid (ceil(Sk/4), Hkv, B).
+// ---------------------------------------------------------------------------
+template <typename T, typename A>
+__global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, View k, View v,
+                                                           View dout, const A *lse, const A *delta,
+                                                           View dk, View dv) {
+  extern __shared__ unsigned char smem_raw[];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int b = blockIdx.z, hk = blockIdx.y;
+  const int j = blockIdx.x * kWaves + w;
+  const int kv_end = kv_end_for(p, b);
+  const bool key_ok = j < p.Sk;
+  A *krow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + p.Dv + 2 * kChunk);
+  A *vrow = krow + p.Dqk;
+  A *pbuf = vrow + p.Dv;
+  A *dsbuf = pbuf + kChunk;
+  if (key_ok) {
+    const T *kp = row_ptr<T>(k, b, hk, j);
+    const T *vp = row_ptr<T>(v, b, hk, j);
+    for (int d = lane; d < p.Dqk; d += 64) krow[d] = to_acc<A>(kp[d]);
+    for (int d = lane; d < p.Dv; d += 64) vrow[d] = to_acc<A>(vp[d]);
+  }
+  // First query row that can see any key of this workgroup (causal).
+  int64_t first_key = static_cast<int64_t>(blockIdx.x) * kWaves;
+  int64_t start = 0;
+  if (p.causal) {
+    start = first_key - p.offset;
+    if (start < 0) start = 0;
+    start = (start / kChunk) * kChunk;
+  }
+  __syncthreads();
+
+  A acc_k[kMaxDimSlots], acc_v[kMaxDimSlots];
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) acc_k[t] = acc_v[t] = 0;
+  const A scale = static_cast<A>(p.scale);
+  for (int r = 0; r < p.rep; ++r) {
+    const int hq = hk * p.rep + r;
+    for (int64_t i0 = start; i0 < p.Sq; i0 += kChunk) {
+      const int i = static_cast<int>(i0) + lane;
+      A pij = 0, ds = 0;
+      if (key_ok && j < kv_end && i < p.Sq) {
+        // q row i is read straight from memory (lane-private row)
+        const T *qp = row_ptr<T>(q, b, hq, i);
+        A acc = 0;
+        for (int d = 0; d < p.Dqk; ++d) acc += to_acc<A>(qp[d]) * krow[d];
+        A s = acc * scale;
+        bool ok = !(p.causal && static_cast<int64_t>(i) + p.offset < static_cast<int64_t>(j));
+        if (ok && p.mask.kind != TSATTN_MASK_NONE) {
+          int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
+                       static_cast<int64_t>(j) * p.mask.s3;
+          if (p.mask.kind == TSATTN_MASK_BOOL) {
+            ok = static_cast<const uint8_t *>(p.mask.data)[mi] != 0;
+          } else {
+            s += load_additive<A>(p.mask.data, mi, p.mask.dtype);
+          }
+        }
+        if (ok) {
+          const int64_t rr = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i;
+          A l = lse[rr];
+          if (!isfinite(l)) l = 0;
+          pij = exp_acc(s - l);
+          if (pij != A(0)) {
+            const T *gp = row_ptr<T>(dout, b, hq, i);
+            A dp = 0;
+            for (int d = 0; d < p.Dv; ++d) dp += to_acc<A>(gp[d]) * vrow[d];
+            ds = pij * (dp - delta[rr]) * scale;
+          }
+        }
+      }
+      pbuf[lane] = pij;
+      dsbuf[lane] = ds;
+      __syncthreads();
+      const int n = (p.Sq - i0) < kChunk ? static_cast<int>(p.Sq - i0) : kChunk;
+      for (int ii = 0; ii < n; ++ii) {
+        const A pv = pbuf[ii], dsv = dsbuf[ii];
+        if (pv == A(0) && dsv == A(0)) continue;
+        const T *gp = row_ptr<T>(dout, b, hq, static_cast<int>(i0) + ii);
+        const T *qp = row_ptr<T>(q, b, hq, static_cast<int>(i0) + ii);
+#pragma unroll
+        for (int t = 0; t < kMaxDimSlots; ++t) {
+          const int d = lane + 64 * t;
+          if (d < p.Dv) acc_v[t] += pv * to_acc<A>(gp[d]);
+          if (d < p.Dqk) acc_k[t] += dsv * to_acc<A>(qp[d]);
+        }
+      }
+      __syncthreads();
+    }
+  }
+  if (!key_ok) return;
+  T *kout = row_ptr_mut<T>(dk, b, hk, j);
+  T *vout = row_ptr_mut<T>(dv, b, hk, j);
+#pragma unroll
+  for (int t = 0; t < kMaxDimSlots; ++t) {
+    const int d = lane + 64 * t;
+    if (d < p.Dqk) kout[d] = from_acc<T, A>(acc_k[t]);
+    if (d < p.Dv) vout[d] = from_acc<T, A>(acc_v[t]);
+  }
+}
+
+template <typename T, typename A>
+hipError_t forward_impl(const Problem &p, View q, View k, View v, View o, void *lse,
+                        hipStream_t st) {
+  dim3 grid((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
+  size_t smem = static_cast<size_t>(kWaves) * (p.Dqk + kChunk) * sizeof(A);
+  generic_forward_kernel<T, A><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+  return hipGetLastError();
+}
+
+template <typename T, typename A>
+hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View dout,
+                         const void *lse, View dq, View dk, View dv, void *delta,
+                         hipStream_t st) {
+  A *dl = static_cast<A *>(delta);
+  const A *ls = static_cast<const A *>(lse);
+  dim3 grid_q((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
+  generic_delta_kernel<T, A><<<grid_q, dim3(256), 0, st>>>(p, o, dout, dl);
+  size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
+  generic_dq_kernel<T, A><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq);
+  dim3 grid_k((p.Sk + kWaves - 1) / kWaves, p.Hkv, p.B);
+  size_t smem_k = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A);
+  generic_dkdv_kernel<T, A><<<grid_k, dim3(256), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_generic_forward(const Problem &p, int dtype, View q, View k, View v, View o,
+                                  void *lse, hipStream_t st) {
+  switch (dtype) {
+    case TSATTN_F32: return forward_impl<float, float>(p, q, k, v, o, lse, st);
+    case TSATTN_F64: return forward_impl<double, double>(p, q, k, v, o, lse, st);
+    case TSATTN_F16: return forward_impl<f16, float>(p, q, k, v, o, lse, st);
+    case TSATTN_BF16: return forward_impl<bf16, float>(p, q, k, v, o, lse, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, View v, View o,
+                                   View dout, const void *lse, View dq, View dk, View dv,
+                                   void *delta, hipStream_t st) {
+  switch (dtype) {
+    case TSATTN_F32: return backward_impl<float, float>(p, q, k, v, o, dout, lse, dq, dk, dv, delta, st);
+    case TSATTN_F64: return backward_impl<double, double>(p, q, k, v, o, dout, lse, dq, dk, dv, delta, st);
+    case TSATTN_F16: return backward_impl<f16, float>(p, q, k, v, o, dout, lse, dq, dk, dv, delta, st);
+    case TSATTN_BF16: return backward_impl<bf16, float>(p, q, k, v, o, dout, lse, dq, dk, dv, delta, st);
+  }
+  return hipErrorInvalidValue;
+}
+
+// Key-padding mask -> (kv_len, kv_prefix): one wave per batch row.
+__global__ __launch_bounds__(64) void key_mask_lengths_kernel(const uint8_t *mask, int64_t sb,
+                                                              int64_t sk, int K, int32_t *kv_len,
+                                                              int32_t *kv_prefix) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  int last = -1, count = 0;
+  for (int j = lane; j < K; j += 64) {
+    if (mask[b * sb + static_cast<int64_t>(j) * sk]) {
+      last = j;
+      ++count;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    int o = __shfl_xor(last, m, 64);
+    last = last > o ? last : o;
+    count += __shfl_xor(count, m, 64);
+  }
+  if (lane == 0) {
+    kv_len[b] = last + 1;
+    if (kv_prefix) kv_prefix[b] = (count == last + 1) ? 1 : 0;
+  }
+}
+
+hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
+                                   int32_t *kv_len, int32_t *kv_prefix, hipStream_t st) {
+  key_mask_lengths_kernel<<<dim3(B), dim3(64), 0, st>>>(mask, sb, sk, K, kv_len, kv_prefix);
+  return hipGetLastError();
+}
+
+}  // namespace tsattn

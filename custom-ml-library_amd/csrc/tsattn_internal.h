@@ -1,0 +1,117 @@
+// Internal declarations shared by the libtsattn.so translation units.
+// Everything here is gfx950-only HIP; nothing is exported except through
+// include/tsattn.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "tsattn.h"
+
+namespace tsattn {
+
+// ---------------------------------------------------------------------------
+// Element types and conversions (storage T <-> accumulator A).
+// ---------------------------------------------------------------------------
+using bf16 = __bf16;
+using f16 = _Float16;
+
+template <typename A, typename T>
+__device__ __forceinline__ A to_acc(T x) {
+  return static_cast<A>(static_cast<float>(x));
+}
+template <>
+__device__ __forceinline__ double to_acc<double, double>(double x) {
+  return x;
+}
+template <>
+__device__ __forceinline__ float to_acc<float, float>(float x) {
+  return x;
+}
+
+template <typename T, typename A>
+__device__ __forceinline__ T from_acc(A x) {
+  return static_cast<T>(x);  // RNE on gfx950 (v_cvt_pk_bf16_f32 / v_cvt_f16_f32)
+}
+
+// Reads one element of a mask of runtime dtype as the accumulator type.
+template <typename A>
+__device__ __forceinline__ A load_additive(const void *base, int64_t idx, int dtype) {
+  switch (dtype) {
+    case TSATTN_F64: return static_cast<A>(static_cast<const double *>(base)[idx]);
+    case TSATTN_F16: return static_cast<A>(static_cast<float>(static_cast<const f16 *>(base)[idx]));
+    case TSATTN_BF16:
+      return static_cast<A>(static_cast<float>(static_cast<const bf16 *>(base)[idx]));
+    default: return static_cast<A>(static_cast<const float *>(base)[idx]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launch descriptors (plain structs passed by value to kernels).
+// ---------------------------------------------------------------------------
+struct View {
+  const void *data;
+  int64_t s0, s1, s2;  // batch, head, sequence strides (elements); dim stride is 1
+};
+
+inline View make_view(const tsattn_view *v) {
+  return View{v->data, v->stride[0], v->stride[1], v->stride[2]};
+}
+
+struct MaskDesc {
+  int kind;   // tsattn_mask_kind
+  int dtype;  // TSATTN_BOOL or a float type
+  const void *data;
+  int64_t s0, s1, s2, s3;
+};
+
+struct Problem {
+  int B, Hq, Hkv, Sq, Sk, Dqk, Dv, rep;
+  double scale;
+  int causal;
+  int64_t offset;
+  const int32_t *kv_len;
+  const int32_t *kv_prefix;
+  MaskDesc mask;
+};
+
+// Valid keys for batch row b: [0, kv_end).
+__device__ __forceinline__ int kv_end_for(const Problem &p, int b) {
+  int e = p.Sk;
+  if (p.kv_len) {
+    int l = p.kv_len[b];
+    e = l < e ? l : e;
+    e = e < 0 ? 0 : e;
+  }
+  return e;
+}
+
+// ---------------------------------------------------------------------------
+// Launchers (each returns hipSuccess or the launch error).
+// ---------------------------------------------------------------------------
+hipError_t launch_generic_forward(const Problem &p, int dtype, View q, View k, View v, View o,
+                                  void *lse, hipStream_t st);
+hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, View v, View o,
+                                   View dout, const void *lse, View dq, View dk, View dv,
+                                   void *delta, hipStream_t st);
+
+// MFMA kernels: f16 / bf16, dim_qk == dim_v in {64, 128}, scale > 0,
+// no mask other than a key mask [B,1,1,K] (+ kv_len / kv_prefix).
+bool mfma_supported(const Problem &p, int dtype);
+hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,
+                               float *lse, hipStream_t st);
+hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
+                                View dout, const float *lse, View dq, View dk, View dv,
+                                float *delta, hipStream_t st);
+
+// Split-K decode.
+bool decode_supported(const Problem &p, int dtype);
+size_t decode_workspace_bytes(const Problem &p, int split_len);
+hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,
+                         int split_len, void *workspace, hipStream_t st);
+
+hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
+                                   int32_t *kv_len, int32_t *kv_prefix, hipStream_t st);
+
+}  // namespace tsattn

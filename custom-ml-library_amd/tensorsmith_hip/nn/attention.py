@@ -1,0 +1,272 @@
+"""``scaled_dot_product_attention`` on hip devices, through ``libtsattn.so``.
+
+Same signature, argument meaning and refusals as the reference
+(``src/tensorsmith/nn/attention.py:16-86``), with ``"hip"`` added to the
+backend allowlist and chosen by ``auto`` on a hip device (as ``native`` is on
+Metal, ``:78-80``).  ``dense`` and ``streaming`` name the same exact math;
+on hip both run the HIP kernels (online softmax, saved LSE, recomputing VJP).
+Dropout is refused like the reference's streaming backend (``:83-84``).
+
+Kernel routing (all on the GPU, none on the CPU):
+
+* training / prefill: ``tsattn_sdpa_forward`` + ``tsattn_sdpa_backward``
+  (MFMA kernels for f16/bf16 and head dim 64/128, generic kernels otherwise);
+* inference with a handful of query rows per KV head (cached decode):
+  ``tsattn_decode_forward``, split across the cache.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+
+from .. import _lib
+from ..device import current_stream
+from ..tensor import Tensor, is_grad_enabled
+
+BACKENDS = {"auto", "dense", "streaming", "native", "hip"}
+DECODE_MIN_KEYS = 128  # below this the prefill kernel is as fast
+
+
+def _dtype_code(dtype) -> int:
+    name = str(dtype).split(".")[-1]
+    codes = {"float32": _lib.F32, "float16": _lib.F16, "bfloat16": _lib.BF16, "float64": _lib.F64}
+    if name not in codes:
+        raise TypeError("attention inputs must have the same floating-point dtype")
+    return codes[name]
+
+
+def _operand(t):
+    """Raw torch tensor with a unit innermost stride (copies only if needed)."""
+    return t if t.stride(-1) == 1 or t.shape[-1] == 1 else t.contiguous()
+
+
+def _view(t) -> _lib.View:
+    v = _lib.View()
+    v.data = t.data_ptr()
+    st = list(t.stride())
+    if t.shape[-1] == 1:
+        st[-1] = 1
+    for i, s in enumerate(st):
+        v.stride[i] = s
+    return v
+
+
+def _aligned16(t) -> bool:
+    return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3])
+
+
+def _problem(b, hq, hkv, sq, sk, dqk, dv, dtype_code, scale, is_causal, offset):
+    p = _lib.Problem()
+    p.dtype = dtype_code
+    p.batch, p.heads_q, p.heads_kv = b, hq, hkv
+    p.len_q, p.len_kv, p.dim_qk, p.dim_v = sq, sk, dqk, dv
+    p.scale = scale
+    p.is_causal = 1 if is_causal else 0
+    p.causal_offset = offset
+    p.mask_kind = _lib.MASK_NONE
+    return p
+
+
+def scaled_dot_product_attention(
+    query: Tensor,
+    key: Tensor,
+    value: Tensor,
+    attn_mask: Tensor | None = None,
+    dropout_p: float = 0.0,
+    is_causal: bool = False,
+    *,
+    scale: float | None = None,
+    causal_offset: int = 0,
+    backend: str = "auto",
+    block_size: int = 64,
+    enable_gqa: bool = False,
+) -> Tensor:
+    """Attention for [batch, heads, sequence, channels] tensors.
+
+    Boolean masks use True=allowed; floating masks are added to scores. Fully
+    masked rows return zero with zero gradients. ``causal_offset`` is the
+    absolute position of the first query in a cached key sequence.
+    ``block_size`` is accepted for signature compatibility; the kernels use
+    their own tiles.
+    """
+    # --- the reference's validation, same order and messages (:36-62) ---
+    if any(t.ndim != 4 for t in (query, key, value)):
+        raise ValueError("attention expects [batch, heads, sequence, channels]")
+    if query.device != key.device or query.device != value.device:
+        raise ValueError("attention tensors must be on the same device")
+    if query.dtype != key.dtype or query.dtype != value.dtype or "float" not in str(query.dtype):
+        raise TypeError("attention inputs must have the same floating-point dtype")
+    if query.shape[0] != key.shape[0] or key.shape[:3] != value.shape[:3]:
+        raise ValueError("attention batch/head dimensions and key/value lengths must agree")
+    repetitions = query.shape[1] // key.shape[1] if key.shape[1] else 0
+    if query.shape[1] != key.shape[1] and (
+        not enable_gqa or not repetitions or query.shape[1] % key.shape[1]
+    ):
+        raise ValueError(
+            "grouped-query attention requires enable_gqa and query heads divisible by KV heads"
+        )
+    if query.shape[-1] != key.shape[-1] or min(*query.shape, *key.shape, *value.shape) <= 0:
+        raise ValueError("query/key head dimensions must match and sequences must be nonempty")
+    if not 0 <= dropout_p < 1 or block_size <= 0 or causal_offset < 0:
+        raise ValueError("invalid dropout probability, block size, or causal offset")
+    if backend not in BACKENDS:
+        raise ValueError("attention backend must be auto, dense, streaming, native, or hip")
+    b, hq, qlen, dim = query.shape
+    hkv, klen, dim_v = key.shape[1], key.shape[2], value.shape[-1]
+    multiplier = 1 / math.sqrt(dim) if scale is None else scale
+    if not math.isfinite(multiplier):
+        raise ValueError("attention scale must be finite")
+    if query.device.type != "hip":
+        raise RuntimeError(
+            "tensorsmith_hip runs attention on hip devices only; move the tensors to 'hip'"
+        )
+    if backend == "native":
+        raise ValueError("native attention requires Metal and equal query/value head dimensions")
+    if dropout_p:
+        raise ValueError("attention dropout currently requires the dense backend")
+
+    code = _dtype_code(query.dtype)
+    q, k, v = (_operand(t._data) for t in (query, key, value))
+    import torch
+
+    tdev = q.device
+    prob = _problem(b, hq, hkv, qlen, klen, dim, dim_v, code, multiplier, is_causal, causal_offset)
+    keep = []  # device buffers the launch reads, alive until the call returns
+
+    if attn_mask is not None:
+        if not any(name in str(attn_mask.dtype) for name in ("bool", "float")):
+            raise TypeError("attention masks must be boolean or floating point")
+        if attn_mask.requires_grad or attn_mask.device != query.device:
+            raise ValueError("attention masks must be non-differentiable and on the input device")
+        try:
+            mask = torch.broadcast_to(attn_mask._data, (b, hq, qlen, klen))
+        except (ValueError, RuntimeError) as error:
+            raise ValueError("attention mask is not broadcastable to [B,H,Q,K]") from error
+        boolean = "bool" in str(attn_mask.dtype)
+        prob.mask_kind = _lib.MASK_BOOL if boolean else _lib.MASK_ADDITIVE
+        prob.mask_dtype = _lib.BOOL if boolean else _dtype_code(attn_mask.dtype)
+        prob.mask = _view(mask)
+        prob.mask.stride[3] = mask.stride(3)
+        keep.append(mask)
+        if boolean and mask.stride(1) == 0 and mask.stride(2) == 0:
+            # key-padding mask [B,1,1,K]: derive per-row key lengths on device
+            lens = torch.empty(2, b, dtype=torch.int32, device=tdev)
+            _lib.check(
+                _lib.load().tsattn_key_mask_lengths(
+                    ctypes.c_void_p(mask.data_ptr()), mask.stride(0), mask.stride(3), b, klen,
+                    ctypes.c_void_p(lens[0].data_ptr()), ctypes.c_void_p(lens[1].data_ptr()),
+                    ctypes.c_void_p(current_stream(query.device)),
+                ),
+                "key mask lengths",
+            )
+            prob.kv_len = lens[0].data_ptr()
+            prob.kv_prefix = lens[1].data_ptr()
+            keep.append(lens)
+
+    lib = _lib.load()
+    stream = ctypes.c_void_p(current_stream(query.device))
+    recording = is_grad_enabled() and any(t.requires_grad for t in (query, key, value))
+    out = torch.empty((b, hq, qlen, dim_v), dtype=q.dtype, device=tdev)
+    vq, vk, vv, vo = _view(q), _view(k), _view(v), _view(out)
+
+    use_decode = (
+        not recording
+        and code in (_lib.F16, _lib.BF16)
+        and dim == dim_v
+        and dim in (64, 128, 256)
+        and repetitions * qlen <= 8
+        and klen >= DECODE_MIN_KEYS
+        and all(_aligned16(t) for t in (q, k, v))
+    )
+    if use_decode:
+        nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
+        _lib.check(
+            lib.tsattn_decode_forward(
+                ctypes.byref(prob), vq, vk, vv, vo, 0, ctypes.c_void_p(ws.data_ptr()), nbytes,
+                stream,
+            ),
+            "decode forward",
+        )
+        return Tensor._from_op(out, (query, key, value), None, "sdpa_hip")
+
+    lse = None
+    if recording:
+        lse_dtype = torch.float64 if code == _lib.F64 else torch.float32
+        lse = torch.empty((b, hq, qlen), dtype=lse_dtype, device=tdev)
+    _lib.check(
+        lib.tsattn_sdpa_forward(
+            ctypes.byref(prob), vq, vk, vv, vo,
+            ctypes.c_void_p(None if lse is None else lse.data_ptr()), stream,
+        ),
+        "attention forward",
+    )
+    if not recording:
+        return Tensor._from_op(out, (query, key, value), None, "sdpa_hip")
+
+    def backward(upstream, _keep=keep):  # _keep: mask / length buffers the kernels read
+        g = _operand(upstream)
+        if g.dtype != out.dtype:
+            g = g.to(out.dtype)
+        dq = torch.empty(q.shape, dtype=q.dtype, device=tdev)
+        dk = torch.empty(k.shape, dtype=k.dtype, device=tdev)
+        dv = torch.empty(v.shape, dtype=v.dtype, device=tdev)
+        nbytes = lib.tsattn_sdpa_backward_workspace(ctypes.byref(prob))
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
+        _lib.check(
+            lib.tsattn_sdpa_backward(
+                ctypes.byref(prob), vq, vk, vv, vo, _view(g), ctypes.c_void_p(lse.data_ptr()),
+                _view(dq), _view(dk), _view(dv), ctypes.c_void_p(ws.data_ptr()), nbytes,
+                ctypes.c_void_p(current_stream(query.device)),
+            ),
+            "attention backward",
+        )
+        return dq, dk, dv
+
+    return Tensor._from_op(out, (query, key, value), backward, "sdpa_hip")
+
+
+def rotary_embedding(input: Tensor, offset: int = 0, base: float = 10000.0,
+                     rotary_dim: int | None = None) -> Tensor:
+    """Interleaved-pair RoPE for [..., sequence, channels] with inverse-rotation VJP.
+
+    Same contract as the reference (``src/tensorsmith/nn/attention.py:255-296``):
+    pairs (2i, 2i+1) rotate by angle ``pos * base**(-2i/dim)``, positions start
+    at ``offset``, channels past ``rotary_dim`` pass through.
+    """
+    if input.ndim < 2:
+        raise ValueError("RoPE requires at least sequence and channel dimensions")
+    dim = input.shape[-1] if rotary_dim is None else rotary_dim
+    if dim <= 0 or dim % 2 or dim > input.shape[-1] or offset < 0 or base <= 0 or not math.isfinite(base):
+        raise ValueError("RoPE requires a positive even rotary dimension and valid positions/base")
+    x = input._data
+    seq = input.shape[-2]
+    freqs = base ** (-(np.arange(0, dim, 2, dtype=np.float32)) / np.float32(dim))
+    angles = np.arange(offset, offset + seq, dtype=np.float32)[:, None] * freqs[None, :]
+    cos = np.repeat(np.cos(angles), 2, axis=-1)
+    sin = np.repeat(np.sin(angles), 2, axis=-1)
+    import torch
+
+    cos_t = torch.from_numpy(cos).to(device=x.device, dtype=x.dtype)
+    sin_t = torch.from_numpy(sin).to(device=x.device, dtype=x.dtype)
+
+    def rotate(raw):
+        pairs = raw.reshape(*raw.shape[:-1], dim // 2, 2)
+        return torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).reshape(raw.shape)
+
+    part = x[..., :dim]
+    result = part * cos_t + rotate(part) * sin_t
+    if dim < input.shape[-1]:
+        result = torch.cat((result, x[..., dim:]), dim=-1)
+
+    def backward(g):
+        front = g[..., :dim]
+        dx = front * cos_t - rotate(front) * sin_t
+        if dim < input.shape[-1]:
+            dx = torch.cat((dx, g[..., dim:]), dim=-1)
+        return (dx,)
+
+    return Tensor._from_op(result, (input,), backward, "rope")

@@ -1,0 +1,157 @@
+/*
+ * tsattn.h -- C ABI of libtsattn.so, the MI355X (gfx950) attention kernels
+ * behind tensorsmith's `scaled_dot_product_attention(..., backend="hip")`.
+ *
+ * The reference (KavinP21/custom-ml-library, package `tensorsmith`) computes
+ * this path in Python/NumPy and has no FFI for it; each entry point below
+ * names the reference code it replaces.  Its user-kernel FFI precedent is
+ * `cuda.RawKernel` (src/tensorsmith/cuda.py:129-185): contiguous device
+ * buffers plus explicitly typed scalars, launched on the caller's stream.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer owned by the caller; the library keeps
+ *    no allocation.  Calls are asynchronous on `stream` (a hipStream_t, or
+ *    NULL for the default stream).
+ *  - Tensors are strided 4-D views [B, H, S, D] with strides in elements; the
+ *    innermost (D) stride must be 1.  Broadcast masks use zero strides.
+ *  - Every entry returns a tsattn_status; on failure tsattn_last_error()
+ *    describes it (thread-local string, valid until the next call on the
+ *    same thread).
+ *  - Row log-sum-exp (LSE) buffers are contiguous [B, Hq, Sq], natural log,
+ *    float (double for TSATTN_F64); fully masked rows hold -inf.
+ */
+#ifndef TSATTN_H
+#define TSATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSATTN_ABI_VERSION 1
+
+typedef enum {
+  TSATTN_OK = 0,
+  TSATTN_ERR_INVALID = 1,     /* contract violation (ValueError / TypeError) */
+  TSATTN_ERR_UNSUPPORTED = 2, /* valid request these kernels do not implement */
+  TSATTN_ERR_HIP = 3          /* HIP runtime error (RuntimeError) */
+} tsattn_status;
+
+typedef enum {
+  TSATTN_F32 = 0,
+  TSATTN_F16 = 1,
+  TSATTN_BF16 = 2,
+  TSATTN_F64 = 3,
+  TSATTN_BOOL = 4, /* masks only: one byte per element, nonzero = allowed */
+  TSATTN_I8 = 5    /* quantised KV cache storage */
+} tsattn_dtype;
+
+typedef enum {
+  TSATTN_MASK_NONE = 0,
+  TSATTN_MASK_BOOL = 1,    /* True = allowed (attention.py:105-107) */
+  TSATTN_MASK_ADDITIVE = 2 /* added to the scaled scores */
+} tsattn_mask_kind;
+
+/* A strided 4-D view [B, H, S, D]; stride[3] must be 1 for operands. */
+typedef struct tsattn_view {
+  void *data;
+  int64_t stride[4];
+} tsattn_view;
+
+/*
+ * One attention problem: the arguments of scaled_dot_product_attention
+ * (src/tensorsmith/nn/attention.py:16-29) after its validation (:36-62).
+ * `kv_len` (device, [batch] int32, nullable) limits the keys of row b to
+ * [0, kv_len[b]); `kv_prefix` (device, [batch] int32, nullable) marks rows
+ * whose boolean key mask is exactly that prefix, letting kernels skip the
+ * per-element mask test (both written by tsattn_key_mask_lengths).
+ */
+typedef struct tsattn_problem {
+  int32_t dtype; /* tsattn_dtype of q, k, v, outputs and gradients */
+  int32_t batch, heads_q, heads_kv, len_q, len_kv, dim_qk, dim_v;
+  double scale;
+  int32_t is_causal;
+  int64_t causal_offset; /* key j allowed for query i iff i + offset >= j */
+  const int32_t *kv_len;
+  const int32_t *kv_prefix;
+  int32_t mask_kind;  /* tsattn_mask_kind */
+  int32_t mask_dtype; /* TSATTN_BOOL, or the additive mask's float type */
+  tsattn_view mask;   /* broadcast to [B, Hq, Sq, Sk] */
+} tsattn_problem;
+
+/* ABI version of the loaded library (== TSATTN_ABI_VERSION). */
+int tsattn_abi_version(void);
+
+/* Human-readable description of the last failure on this thread. */
+const char *tsattn_last_error(void);
+
+/*
+ * Kernel-family policy for sdpa forward/backward: 0 = automatic (MFMA kernels
+ * where they apply, generic kernels otherwise), 1 = generic kernels only.
+ * A diagnostic knob with no counterpart in the reference (it has one
+ * algorithm per backend name); tests use it to run both families on the
+ * same inputs.
+ */
+int tsattn_set_kernel_policy(int policy);
+
+/* Kernel family of this thread's last launch: 1 generic, 2 MFMA, 3 decode. */
+int tsattn_last_kernel_path(void);
+
+/*
+ * Forward: out = softmax(scale * q k^T + mask) v, with the online-softmax
+ * recurrence of the reference's streaming backend and its saved row LSE.
+ * Replaces src/tensorsmith/nn/attention.py:175-198 (streaming forward) and,
+ * for the same math, :132-145 (dense forward without dropout).
+ * `lse` may be NULL (inference, like the `native` early return at :172-173).
+ */
+int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                        const tsattn_view *v, const tsattn_view *out, void *lse, void *stream);
+
+/* Bytes of scratch tsattn_sdpa_backward needs (row deltas). */
+size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
+
+/*
+ * Backward: dq, dk, dv from the saved LSE, recomputing P = exp(S - LSE)
+ * blockwise, with delta = rowsum(dout * out).  Replaces
+ * src/tensorsmith/nn/attention.py:200-248 (incl. the GQA group sums at
+ * :245-247).  Deterministic: no atomics, every element is written once.
+ */
+int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                         const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,
+                         const void *lse, const tsattn_view *dq, const tsattn_view *dk,
+                         const tsattn_view *dv, void *workspace, size_t workspace_bytes,
+                         void *stream);
+
+/* Bytes of scratch tsattn_decode_forward needs for `split_len` keys per split. */
+size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);
+
+/*
+ * KV-cache decode: few query rows (len_q * heads_q / heads_kv <= 8 per KV
+ * head) against a long cached prefix, split across the cache in chunks of
+ * `split_len` keys (0 = choose), partial (max, sum, acc) merged as in the
+ * reference's online softmax (attention.py:185-193).  Replaces the dense
+ * path the reference takes for cached decode (MultiHeadAttention.forward,
+ * src/tensorsmith/nn/transformer.py:142-154 -> attention.py:132-145).
+ * k/v are the cache views [B, Hkv, capacity, D] with len_kv active keys.
+ */
+int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                          const tsattn_view *v, const tsattn_view *out, int32_t split_len,
+                          void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Boolean key mask [B, K] (strides in bytes-as-elements) -> kv_len[b] = 1 +
+ * last allowed key (0 if none) and kv_prefix[b] = 1 iff the allowed keys are
+ * exactly [0, kv_len[b]).  Serves the reference's key-padding masks
+ * (docs/transformers.md:55, shape [B,1,1,K]).
+ */
+int tsattn_key_mask_lengths(const uint8_t *mask, int64_t stride_b, int64_t stride_k,
+                            int32_t batch, int32_t len_kv, int32_t *kv_len, int32_t *kv_prefix,
+                            void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSATTN_H */

@@ -1,0 +1,126 @@
+"""Direct C-ABI drivers for the GPU tests (torch tensors in, torch tensors out).
+
+These call ``libtsattn.so`` exactly as a foreign binding would: raw device
+pointers, element strides, a ``tsattn_problem`` and the current stream.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+import torch
+
+from tensorsmith_hip import _lib
+
+TORCH_DTYPES = {"float32": torch.float32, "float64": torch.float64,
+                "float16": torch.float16, "bfloat16": torch.bfloat16}
+CODES = {torch.float32: _lib.F32, torch.float64: _lib.F64, torch.float16: _lib.F16,
+         torch.bfloat16: _lib.BF16}
+
+
+def dev_tensor(x: np.ndarray, dtype: str) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(x)).to("cuda").to(TORCH_DTYPES[dtype])
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach()
+    if t.dtype in (torch.bfloat16, torch.float16):
+        t = t.float()
+    return t.cpu().numpy()
+
+
+def view(t: torch.Tensor) -> _lib.View:
+    v = _lib.View()
+    v.data = t.data_ptr()
+    for i, s in enumerate(t.stride()):
+        v.stride[i] = s
+    return v
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def problem(q, k, v, *, causal=False, offset=0, scale=None, mask=None, kv_len=None,
+            kv_prefix=None):
+    b, hq, sq, d = q.shape
+    p = _lib.Problem()
+    p.dtype = CODES[q.dtype]
+    p.batch, p.heads_q, p.heads_kv, p.len_q = b, hq, k.shape[1], sq
+    p.len_kv, p.dim_qk, p.dim_v = k.shape[2], d, v.shape[3]
+    p.scale = 1 / math.sqrt(d) if scale is None else scale
+    p.is_causal = int(causal)
+    p.causal_offset = offset
+    p.kv_len = None if kv_len is None else kv_len.data_ptr()
+    p.kv_prefix = None if kv_prefix is None else kv_prefix.data_ptr()
+    p.mask_kind = _lib.MASK_NONE
+    if mask is not None:
+        m = torch.broadcast_to(mask, (b, hq, sq, k.shape[2]))
+        if m.dtype == torch.bool:
+            p.mask_kind, p.mask_dtype = _lib.MASK_BOOL, _lib.BOOL
+        else:
+            p.mask_kind, p.mask_dtype = _lib.MASK_ADDITIVE, CODES[m.dtype]
+        p.mask = view(m)
+        p._mask_keep = m
+    return p
+
+
+def forward(q, k, v, **kw):
+    """(out, lse) through tsattn_sdpa_forward; returns the kernel path used."""
+    p = problem(q, k, v, **kw)
+    out = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device)
+    lse = torch.empty(q.shape[:3], dtype=torch.float64 if q.dtype == torch.float64 else torch.float32,
+                      device=q.device)
+    lib = _lib.load()
+    _lib.check(lib.tsattn_sdpa_forward(ctypes.byref(p), view(q), view(k), view(v), view(out),
+                                       ctypes.c_void_p(lse.data_ptr()), stream()), "forward")
+    return out, lse, lib.tsattn_last_kernel_path()
+
+
+def backward(q, k, v, out, g, lse, **kw):
+    p = problem(q, k, v, **kw)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    lib = _lib.load()
+    nbytes = lib.tsattn_sdpa_backward_workspace(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    _lib.check(lib.tsattn_sdpa_backward(
+        ctypes.byref(p), view(q), view(k), view(v), view(out), view(g),
+        ctypes.c_void_p(lse.data_ptr()), view(dq), view(dk), view(dv),
+        ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "backward")
+    return dq, dk, dv, lib.tsattn_last_kernel_path()
+
+
+def decode(q, k, v, split_len=0, **kw):
+    p = problem(q, k, v, **kw)
+    out = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    nbytes = lib.tsattn_decode_workspace(ctypes.byref(p), split_len)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.tsattn_decode_forward(ctypes.byref(p), view(q), view(k), view(v), view(out),
+                                         split_len, ctypes.c_void_p(ws.data_ptr()), nbytes,
+                                         stream()), "decode")
+    return out
+
+
+def key_lengths(mask: torch.Tensor):
+    """kv_len / kv_prefix of a bool key mask [B, K] via tsattn_key_mask_lengths."""
+    b, kl = mask.shape
+    out = torch.empty(2, b, dtype=torch.int32, device=mask.device)
+    _lib.check(_lib.load().tsattn_key_mask_lengths(
+        ctypes.c_void_p(mask.data_ptr()), mask.stride(0), mask.stride(1), b, kl,
+        ctypes.c_void_p(out[0].data_ptr()), ctypes.c_void_p(out[1].data_ptr()), stream()),
+        "key lengths")
+    return out[0], out[1]
+
+
+class generic_only:
+    """Context: force the generic kernel family (tsattn_set_kernel_policy(1))."""
+
+    def __enter__(self):
+        _lib.set_kernel_policy(1)
+
+    def __exit__(self, *exc):
+        _lib.set_kernel_policy(0)
+        return False

@@ -1,0 +1,269 @@
+"""HIP kernels vs the oracle, through the C ABI (needs an MI355X).
+
+Tolerances (stated here, enforced below):
+
+* fp32 / fp64 (generic kernels): the reference's cross-backend bound
+  ``rtol=1e-4, atol=3e-5`` for fp32 (``tests/test_transformer.py:92``);
+  ``1e-10`` relative for fp64.
+* bf16: relative-L2 <= 1e-2 (O) / 2e-2 (dQ, dK, dV); max-abs <= 2e-2 * max|ref|;
+  LSE max-abs <= 1e-3.
+* fp16: relative-L2 <= 2e-3 (O) / 5e-3 (grads); max-abs <= 5e-3 * max|ref|;
+  LSE max-abs <= 1e-3.
+
+The reference values are the oracle's fp32 math on the same rounded inputs
+(what the reference does for half inputs, ``attention.py:63,90-92``).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover - CPU containers
+    pytest.skip("no GPU", allow_module_level=True)
+
+import abi  # noqa: E402
+from conftest import golden_kwargs, rel_l2  # noqa: E402
+from oracle import attention as A  # noqa: E402
+from oracle.halfprec import round_to  # noqa: E402
+from oracle.inputs import attention_inputs  # noqa: E402
+from tensorsmith_hip import _lib  # noqa: E402
+
+TOL = {
+    "bfloat16": dict(o=1e-2, g=2e-2, mx=2e-2),
+    "float16": dict(o=2e-3, g=5e-3, mx=5e-3),
+}
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def check_half(got, ref, dtype, kind, name):
+    t = TOL[dtype]
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = rel_l2(got, ref)
+    scale = np.abs(ref).max() or 1.0
+    mx = np.abs(got - ref).max() / scale
+    floor = rel_l2(round_to(ref.astype(np.float32), dtype), ref)
+    say(f"  {name}: rel_l2={err:.2e} (rounding floor {floor:.1e}) max_abs/max|ref|={mx:.2e}")
+    assert np.isfinite(got).all(), name
+    assert err <= t[kind], f"{name}: rel_l2 {err:.3e} > {t[kind]}"
+    assert mx <= t["mx"], f"{name}: max-abs {mx:.3e} > {t['mx']}"
+
+
+def check_lse(got, ref_lse, name):
+    ref = ref_lse[..., 0] if ref_lse.ndim == 4 else ref_lse
+    np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref), err_msg=name)
+    live = np.isfinite(ref)
+    if live.any():
+        err = np.abs(got[live] - ref[live]).max()
+        say(f"  {name}: lse max-abs={err:.2e}")
+        assert err <= 1e-3, name
+
+
+# ---------------------------------------------------------------------------
+# Generic kernels (fp64 / fp32) against the torch-written golden fixtures
+# ---------------------------------------------------------------------------
+
+
+@pytest.mark.parametrize("dtype", ["float64", "float32"])
+def test_golden_fixtures_generic(golden, dtype):
+    for name, case in golden.items():
+        kw, mask = golden_kwargs(case)
+        say(f"golden {name} {dtype}")
+        q, k, v, g = (abi.dev_tensor(case[x], dtype) for x in ("q", "k", "v", "g"))
+        m = None
+        if mask is not None:
+            m = torch.from_numpy(mask).cuda()
+            if m.dtype != torch.bool:
+                m = m.to(abi.TORCH_DTYPES[dtype])
+        args = dict(causal=kw["is_causal"], offset=kw["causal_offset"], scale=kw.get("scale"),
+                    mask=m)
+        out, lse, path = abi.forward(q, k, v, **args)
+        assert path == _lib.PATH_GENERIC
+        dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, **args)
+        torch.cuda.synchronize()
+        tol = dict(rtol=1e-10, atol=1e-12) if dtype == "float64" else dict(rtol=1e-4, atol=3e-5)
+        np.testing.assert_allclose(abi.host(out), case["out"], **tol, err_msg=f"{name} out")
+        lse_h = abi.host(lse)
+        np.testing.assert_array_equal(np.isneginf(lse_h), np.isneginf(case["lse"]))
+        live = np.isfinite(case["lse"])
+        np.testing.assert_allclose(lse_h[live], case["lse"][live], **tol)
+        for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+            np.testing.assert_allclose(abi.host(got), case[key], **tol, err_msg=f"{name} {key}")
+
+
+# ---------------------------------------------------------------------------
+# MFMA kernels (bf16 / fp16, D = 64 / 128) against the oracle
+# ---------------------------------------------------------------------------
+
+MFMA_CASES = [
+    # (B, Hq, Hkv, Sq, Sk, D, causal, offset)
+    (2, 2, 2, 128, 128, 128, True, 0),
+    (1, 3, 3, 300, 300, 128, True, 0),
+    (2, 2, 2, 200, 333, 64, True, 133),
+    (1, 2, 2, 77, 190, 128, False, 0),
+    (1, 4, 2, 160, 160, 64, True, 0),     # GQA
+    (2, 2, 1, 65, 257, 128, True, 192),  # GQA + offset + ragged
+    (1, 1, 1, 1, 300, 128, True, 299),    # one query row (decode shape through prefill)
+]
+
+
+def _oracle(inp, dtype, causal, offset, mask=None, gqa=False):
+    return A.sdpa(inp.q, inp.k, inp.v, mask, causal, dtype=dtype, causal_offset=offset,
+                  backend="streaming", enable_gqa=gqa)
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+@pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_mfma_forward_backward(dtype, case):
+    b, hq, hkv, sq, sk, d, causal, off = case
+    say(f"mfma {dtype} {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=11)
+    ref = _oracle(inp, dtype, causal, off, gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    out, lse, path = abi.forward(q, k, v, causal=causal, offset=off)
+    assert path == _lib.PATH_MFMA
+    dq, dk, dv, bpath = abi.backward(q, k, v, out, g, lse, causal=causal, offset=off)
+    assert bpath == _lib.PATH_MFMA
+    torch.cuda.synchronize()
+    check_half(abi.host(out), ref.out, dtype, "o", "O")
+    check_lse(abi.host(lse), ref.lse, "LSE")
+    # the oracle's VJP uses its own fp32 O; the kernels use the returned (rounded) O
+    rdq, rdk, rdv = ref.backward_compute(inp.do)
+    check_half(abi.host(dq), rdq, dtype, "g", "dQ")
+    check_half(abi.host(dk), rdk, dtype, "g", "dK")
+    check_half(abi.host(dv), rdv, dtype, "g", "dV")
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_mfma_agrees_with_generic_on_same_inputs(dtype):
+    inp = attention_inputs(2, 2, 190, 128, dtype, value_scale=0.5, seed=5)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    say(f"mfma vs generic {dtype}")
+    out_m, lse_m, _ = abi.forward(q, k, v, causal=True)
+    dq_m, dk_m, dv_m, _ = abi.backward(q, k, v, out_m, g, lse_m, causal=True)
+    with abi.generic_only():
+        out_g, lse_g, path = abi.forward(q, k, v, causal=True)
+        assert path == _lib.PATH_GENERIC
+        dq_g, dk_g, dv_g, _ = abi.backward(q, k, v, out_m, g, lse_m, causal=True)
+    torch.cuda.synchronize()
+    check_half(abi.host(out_m), abi.host(out_g), dtype, "o", "O mfma/generic")
+    check_lse(abi.host(lse_m), abi.host(lse_g), "LSE mfma/generic")
+    for a_, b_, n in ((dq_m, dq_g, "dQ"), (dk_m, dk_g, "dK"), (dv_m, dv_g, "dV")):
+        check_half(abi.host(a_), abi.host(b_), dtype, "g", n + " mfma/generic")
+
+
+@pytest.mark.parametrize("prefix", [True, False])
+def test_mfma_key_padding_mask(prefix):
+    dtype = "bfloat16"
+    b, h, s, d = 3, 2, 200, 128
+    inp = attention_inputs(b, h, s, d, dtype, value_scale=0.5, seed=9)
+    lengths = np.array([200, 131, 64])
+    keymask = np.arange(s)[None, :] < lengths[:, None]
+    if not prefix:
+        keymask[1, 17] = False  # a hole inside the valid prefix
+        keymask[2, 150] = True  # an allowed key past the padding
+    mask4 = keymask[:, None, None, :]
+    say(f"key mask prefix={prefix}")
+    ref = A.sdpa(inp.q, inp.k, inp.v, mask4, True, dtype=dtype, backend="streaming")
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    km = torch.from_numpy(keymask).cuda()
+    kv_len, kv_prefix = abi.key_lengths(km)
+    torch.cuda.synchronize()
+    last = np.array([np.nonzero(r)[0].max() + 1 for r in keymask])
+    np.testing.assert_array_equal(kv_len.cpu().numpy(), last)
+    np.testing.assert_array_equal(kv_prefix.cpu().numpy(),
+                                  [int(r[:l].all()) for r, l in zip(keymask, last)])
+    m4 = km[:, None, None, :]
+    out, lse, path = abi.forward(q, k, v, causal=True, mask=m4, kv_len=kv_len, kv_prefix=kv_prefix)
+    assert path == _lib.PATH_MFMA
+    dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, causal=True, mask=m4, kv_len=kv_len,
+                                 kv_prefix=kv_prefix)
+    torch.cuda.synchronize()
+    check_half(abi.host(out), ref.out, dtype, "o", "O")
+    check_lse(abi.host(lse), ref.lse, "LSE")
+    for got, want, n in zip((dq, dk, dv), ref.backward_compute(inp.do), ("dQ", "dK", "dV")):
+        check_half(abi.host(got), want, dtype, "g", n)
+
+
+# ---------------------------------------------------------------------------
+# Decode kernel
+# ---------------------------------------------------------------------------
+
+DECODE_CASES = [
+    # (B, Hq, Hkv, Sq, cap, D, lengths)
+    (4, 4, 4, 1, 1000, 128, [1000, 517, 3, 880]),
+    (2, 8, 2, 1, 700, 64, [700, 129]),      # GQA 4 rows per kv head
+    (2, 4, 4, 2, 600, 128, [600, 400]),     # two new tokens (causal)
+    (1, 2, 2, 1, 2048, 256, [2048]),
+]
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: f"b{c[0]}h{c[1]}kv{c[2]}q{c[3]}d{c[5]}")
+def test_decode_matches_oracle(dtype, case):
+    b, hq, hkv, sq, cap, d, lengths = case
+    say(f"decode {dtype} {case[:6]}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=cap, with_grad=False, seed=3)
+    lengths = np.array(lengths)
+    # query rows sit at the end of each sequence: causal offset = len - sq
+    q, k, v = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v))
+    kv_len = torch.tensor(lengths, dtype=torch.int32, device="cuda")
+    offset = int(lengths.max()) - sq
+    for split in (0, 64, 256):
+        out = abi.decode(q, k, v, split_len=split, causal=True, offset=offset, kv_len=kv_len)
+        torch.cuda.synchronize()
+        got = abi.host(out)
+        for bi in range(b):
+            ref = A.sdpa(inp.q[bi:bi + 1], inp.k[bi:bi + 1, :, :lengths[bi]],
+                         inp.v[bi:bi + 1, :, :lengths[bi]], None, True, dtype=dtype,
+                         causal_offset=offset, backend="dense", enable_gqa=hkv != hq)
+            check_half(got[bi:bi + 1], ref.out, dtype, "o", f"b{bi} split{split}")
+
+
+def test_decode_with_bool_mask_and_float_mask():
+    dtype = "float16"
+    inp = attention_inputs(2, 2, 1, 128, dtype, seq_k=300, with_grad=False, seed=4)
+    q, k, v = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v))
+    rng = np.random.default_rng(0)
+    bmask = rng.random((2, 1, 1, 300)) > 0.3
+    fmask = (rng.standard_normal((1, 2, 1, 300)) * 0.5).astype(np.float32)
+    for mask in (bmask, fmask):
+        say(f"decode mask {mask.dtype}")
+        out = abi.decode(q, k, v, mask=torch.from_numpy(mask).cuda())
+        torch.cuda.synchronize()
+        ref = A.sdpa(inp.q, inp.k, inp.v, mask, False, dtype=dtype, backend="dense")
+        check_half(abi.host(out), ref.out, dtype, "o", f"mask {mask.dtype}")
+
+
+# ---------------------------------------------------------------------------
+# Error paths forced from the host (no kernel ever faults)
+# ---------------------------------------------------------------------------
+
+
+def test_abi_rejects_bad_arguments_before_launch():
+    q = torch.zeros(1, 2, 4, 8, device="cuda")
+    p = abi.problem(q, q, q)
+    p.heads_kv = 3  # 2 % 3 != 0
+    out = torch.empty_like(q)
+    lib = _lib.load()
+    rc = lib.tsattn_sdpa_forward(abi.ctypes.byref(p), abi.view(q), abi.view(q), abi.view(q),
+                                 abi.view(out), None, abi.stream())
+    assert rc == _lib.ERR_INVALID and "divisible" in _lib.last_error()
+    p = abi.problem(q, q, q)
+    p.scale = float("inf")
+    rc = lib.tsattn_sdpa_forward(abi.ctypes.byref(p), abi.view(q), abi.view(q), abi.view(q),
+                                 abi.view(out), None, abi.stream())
+    assert rc == _lib.ERR_INVALID and "finite" in _lib.last_error()
+    bad = abi.view(q)
+    bad.stride[3] = 2
+    p = abi.problem(q, q, q)
+    rc = lib.tsattn_sdpa_forward(abi.ctypes.byref(p), bad, abi.view(q), abi.view(q),
+                                 abi.view(out), None, abi.stream())
+    assert rc == _lib.ERR_INVALID
