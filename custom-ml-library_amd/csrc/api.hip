@@ -135,7 +135,8 @@ int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsa
 
 size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p) {
   if (!p || p->batch <= 0 || p->heads_q <= 0 || p->len_q <= 0) return 0;
-  return static_cast<size_t>(p->batch) * p->heads_q * p->len_q * acc_size(p->dtype);
+  // row deltas, then (MFMA path) the row LSE in log2 units
+  return 2 * static_cast<size_t>(p->batch) * p->heads_q * p->len_q * acc_size(p->dtype);
 }
 
 int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,

@@ -72,6 +72,9 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
   const int k_begin = split * a.split_len;
   if (k_begin >= end) return;  // this split holds no keys for row b
   const int k_stop = min(k_begin + a.split_len, end);
+  // A key mask that is exactly the prefix [0, kv_len[b]) is already applied by k_stop.
+  const bool masked = p.mask.kind != TSATTN_MASK_NONE &&
+                      !(p.kv_prefix && p.kv_prefix[b] && p.mask.s1 == 0 && p.mask.s2 == 0);
 
   // Query rows r = rr * Sq + i (query head hk*rep + rr, position i), pre-scaled
   // so that s = q.k is already in log2 units.
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
         const int i = r % p.Sq;
         bool ok = key < k_stop && r < a.rows &&
                   (!p.causal || static_cast<int64_t>(i) + p.offset >= key);
-        if (ok && p.mask.kind != TSATTN_MASK_NONE) {
+        if (ok && masked) {
           const int hq = hk * p.rep + r / p.Sq;
           const int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
                              static_cast<int64_t>(key) * p.mask.s3;
@@ -255,8 +258,8 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
 template <typename T, int D, int R>
 hipError_t launch_rows(const DecArgs &a, hipStream_t st) {
   const Problem &p = a.p;
-  decode_split_kernel<T, D, R><<<dim3(a.max_splits, p.Hkv, p.B), dim3(NT), 0, st>>>(a);
-  decode_merge_kernel<T, D><<<dim3(p.Hq * p.Sq, p.B), dim3(64), 0, st>>>(a);
+  { Probe pr_("decode_split", st); decode_split_kernel<T, D, R><<<dim3(a.max_splits, p.Hkv, p.B), dim3(NT), 0, st>>>(a); }
+  { Probe pr_("decode_merge", st); decode_merge_kernel<T, D><<<dim3(p.Hq * p.Sq, p.B), dim3(64), 0, st>>>(a); }
   return hipGetLastError();
 }
 

@@ -347,7 +347,7 @@ hipError_t forward_impl(const Problem &p, View q, View k, View v, View o, void *
                         hipStream_t st) {
   dim3 grid((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
   size_t smem = static_cast<size_t>(kWaves) * (p.Dqk + kChunk) * sizeof(A);
-  generic_forward_kernel<T, A><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+  { Probe pr_("generic_fwd", st); generic_forward_kernel<T, A><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse)); }
   return hipGetLastError();
 }
 
@@ -358,12 +358,12 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
   A *dl = static_cast<A *>(delta);
   const A *ls = static_cast<const A *>(lse);
   dim3 grid_q((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
-  generic_delta_kernel<T, A><<<grid_q, dim3(256), 0, st>>>(p, o, dout, dl);
+  { Probe pr_("generic_bwd_delta", st); generic_delta_kernel<T, A><<<grid_q, dim3(256), 0, st>>>(p, o, dout, dl); }
   size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
-  generic_dq_kernel<T, A><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq);
+  { Probe pr_("generic_bwd_dq", st); generic_dq_kernel<T, A><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq); }
   dim3 grid_k((p.Sk + kWaves - 1) / kWaves, p.Hkv, p.B);
   size_t smem_k = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A);
-  generic_dkdv_kernel<T, A><<<grid_k, dim3(256), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
+  { Probe pr_("generic_bwd_dkdv", st); generic_dkdv_kernel<T, A><<<grid_k, dim3(256), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv); }
   return hipGetLastError();
 }
 
@@ -418,7 +418,7 @@ __global__ __launch_bounds__(64) void key_mask_lengths_kernel(const uint8_t *mas
 
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st) {
-  key_mask_lengths_kernel<<<dim3(B), dim3(64), 0, st>>>(mask, sb, sk, K, kv_len, kv_prefix);
+  { Probe pr_("key_mask_lengths", st); key_mask_lengths_kernel<<<dim3(B), dim3(64), 0, st>>>(mask, sb, sk, K, kv_len, kv_prefix); }
   return hipGetLastError();
 }
 

@@ -1,7 +1,7 @@
 // Attention backward for gfx950 with MFMA 32x32x16 (f16/bf16 in, fp32
 // accumulate).  Follows the reference's streaming VJP (src/tensorsmith/nn/
 // attention.py:220-247):
-//   delta_i = sum_d dO_id O_id                     (row_delta_kernel)
+//   delta_i = sum_d dO_id O_id                     (row_prep_kernel)
 //   P_ij = exp(S_ij - LSE_i), dS_ij = P_ij (dP_ij - delta_i), dP = dO V^T
 //   dV = P^T dO, dK = scale dS^T Q                 (dkdv_kernel)
 //   dQ = scale dS K                                (dq_kernel)
@@ -9,32 +9,41 @@
 // so every gradient element is written exactly once: no atomics, bitwise
 // deterministic results (checkpoint recompute reproduces them exactly).
 // The dK/dV kernel sums the query heads of a GQA group itself (:245-247).
+//
+// Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
+// transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
 #include "mfma_common.h"
 
 namespace tsattn {
 namespace {
 
 constexpr int NT = 256;
+constexpr int NW = NT / 64;
 
 struct BwdArgs {
   Problem p;
   View q, k, v, o, dout, dq, dk, dv;
   const float *lse;
-  float *delta;
-  float sl;     // scale * log2(e)
-  float scale;  // final gradient scale
+  float *delta;  // [rows] delta, then [rows] lse2 = safe(lse) * log2(e)
+  float sl;      // scale * log2(e)
+  float scale;   // final gradient scale
 };
 
 template <typename T>
 __device__ __forceinline__ T *mut(View v) {
   return static_cast<T *>(const_cast<void *>(v.data));
 }
+template <typename T>
+__device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
+  return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
+}
 
 // ---------------------------------------------------------------------------
-// delta = rowsum(dO * O) in fp32; D/8 threads per row.
+// Row pre-pass: delta = rowsum(dO * O) and lse2 = (isfinite(lse) ? lse : 0) *
+// log2(e) -- the reference's safe_lse (attention.py:231) in exp2 units.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-__global__ __launch_bounds__(NT) void row_delta_kernel(BwdArgs a) {
+__global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
   constexpr int TPR = D / 8;
   constexpr int RPB = NT / TPR;
   const Problem &p = a.p;
@@ -58,38 +67,29 @@ __global__ __launch_bounds__(NT) void row_delta_kernel(BwdArgs a) {
   }
 #pragma unroll
   for (int m = TPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-  if (row < rows && part == 0) a.delta[row] = s;
+  if (row < rows && part == 0) {
+    a.delta[row] = s;
+    const float l = a.lse[row];
+    a.delta[rows + row] = isfinite(l) ? l * kLog2e : 0.f;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // dK / dV: one workgroup = 128 keys of one (b, kv head); wave w owns keys
-// kw..kw+31.  Query tiles of 64 rows (all query heads of the group) stream
-// through LDS twice: row-major (A operand of S = Q K^T and dP = dO V^T) and
-// transposed (A operand of dV^T = dO^T P and dK^T = Q^T dS).
+// kw..kw+31 (K, V rows as B operands in registers).  Query tiles of 64 rows
+// (all query heads of the group) stream through LDS as row-major Q and dO:
+// 16-byte row reads feed S = Q K^T and dP = dO V^T, transpose reads feed
+// dV^T = dO^T P and dK^T = Q^T dS.
 // ---------------------------------------------------------------------------
 constexpr int KB = 128;  // keys per workgroup
 constexpr int QT = 64;   // query rows per tile
 
 template <typename T, int D>
-struct KVLayout {
-  static constexpr int RSTR = D + 8;   // row-major stride (elements)
-  static constexpr int TSTR = QT + 4;  // transposed stride (elements)
-  static constexpr int R_BYTES = QT * RSTR * 2;
-  static constexpr int T_BYTES = D * TSTR * 2;
-  // stage: Q | dO | Q^T | dO^T | lse2[QT] | delta[QT]
-  static constexpr int OFF_G = R_BYTES;
-  static constexpr int OFF_QT = 2 * R_BYTES;
-  static constexpr int OFF_GT = 2 * R_BYTES + T_BYTES;
-  static constexpr int OFF_L = 2 * R_BYTES + 2 * T_BYTES;
-  static constexpr int OFF_D = OFF_L + QT * 4;
-  static constexpr int STAGE = OFF_D + QT * 4;
-  static constexpr int BYTES = 2 * STAGE;
-};
-
-template <typename T, int D>
 __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
-  using L = KVLayout<T, D>;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int TILE = QT * D;
+  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][Q | dO]
+  __shared__ __attribute__((aligned(16))) float rowv[2][2 * QT];    // [stage][lse2 | delta]
+
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
   const int n_kb = (p.Sk + KB - 1) / KB;
@@ -104,18 +104,18 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
   const bool key_live = key < kv_end &&
                         (!keymask || static_cast<const uint8_t *>(p.mask.data)
                                          [b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
 
   // K and V rows of this lane's key as B operands (K^T / V^T with N = key).
   u32x4 kf[D / 16], vf[D / 16];
   {
-    const T *kp = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1 +
-                  static_cast<int64_t>(key) * a.k.s2;
-    const T *vp = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1 +
-                  static_cast<int64_t>(key) * a.v.s2;
+    const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
+    const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+    const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      kf[ks] = key < kv_end ? ld16(kp + ks * 16 + h * 8) : u32x4{0, 0, 0, 0};
-      vf[ks] = key < kv_end ? ld16(vp + ks * 16 + h * 8) : u32x4{0, 0, 0, 0};
+      kf[ks] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (ks * 16 + h * 8) * 2);
+      vf[ks] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (ks * 16 + h * 8) * 2);
     }
   }
 
@@ -128,64 +128,49 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
   }
   const int n_qt = k0 < kv_end ? (p.Sq - q_start + QT - 1) / QT : 0;
   const int n_iter = n_qt * p.rep;
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
 
-  TileRegs<T, D, QT> qreg, greg;
-  float lreg = 0.f;  // thread < QT: lse2 of row; QT <= thread < 2*QT: delta
-  auto load_iter = [&](int itn) {
+  auto issue = [&](int itn, int stage) {
     const int r = itn / n_qt, q0 = q_start + (itn - r * n_qt) * QT;
     const int hq = hk * p.rep + r;
-    qreg.load(static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1, a.q.s2, q0, p.Sq, tid);
-    greg.load(static_cast<const T *>(a.dout.data) + b * a.dout.s0 + hq * a.dout.s1, a.dout.s2, q0,
-              p.Sq, tid);
-    if (tid < 2 * QT) {
-      const int row = q0 + (tid & (QT - 1));
-      const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + row;
-      if (row >= p.Sq) {
-        lreg = 0.f;
-      } else if (tid < QT) {
-        const float v = a.lse[idx];
-        lreg = isfinite(v) ? v * kLog2e : 0.f;  // safe_lse (attention.py:231)
-      } else {
-        lreg = a.delta[idx];
-      }
+    T *qt = lds + stage * 2 * TILE;
+    const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+    tile_to_lds<D, QT, NW>(qrs, qs_b, q0, qt, w, lane);
+    tile_to_lds<D, QT, NW>(grs, gs_b, q0, qt + TILE, w, lane);
+    if (w < 2) {
+      const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
+      const rsrc_t rrs = make_rsrc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
+      buf_load4_lds(rrs, &rowv[stage][w == 0 ? 0 : QT], static_cast<uint32_t>(q0 + lane) * 4);
     }
-  };
-  auto store_iter = [&](int stage) {
-    unsigned char *s = smem + stage * L::STAGE;
-    qreg.store_rows(reinterpret_cast<T *>(s), L::RSTR, tid);
-    greg.store_rows(reinterpret_cast<T *>(s + L::OFF_G), L::RSTR, tid);
-    qreg.store_cols(reinterpret_cast<T *>(s + L::OFF_QT), L::TSTR, tid);
-    greg.store_cols(reinterpret_cast<T *>(s + L::OFF_GT), L::TSTR, tid);
-    if (tid < 2 * QT) reinterpret_cast<float *>(s + L::OFF_L)[tid] = lreg;
   };
 
   f32x16 dk_acc[D / 32], dv_acc[D / 32];
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
   const float sl = a.sl;
+  const bool causal = p.causal != 0;
 
-  if (n_iter > 0) {
-    load_iter(0);
-    store_iter(0);
-  }
+  zero_lds<NT>(lds, sizeof(lds), tid);
+  zero_lds<NT>(rowv, sizeof(rowv), tid);
+  __syncthreads();
+  if (n_iter > 0) issue(0, 0);
+  wait_vmem();
   __syncthreads();
 
   for (int itn = 0; itn < n_iter; ++itn) {
     const int stage = itn & 1;
     const int q0 = q_start + (itn % n_qt) * QT;
-    if (itn + 1 < n_iter) load_iter(itn + 1);
+    if (itn + 1 < n_iter) issue(itn + 1, stage ^ 1);
 
     // Does any (query row of this tile, key of this wave) pair survive?
-    const bool wave_live = kw < kv_end && (!p.causal || static_cast<int64_t>(q0) + QT - 1 + p.offset >= kw);
+    const bool wave_live = kw < kv_end && (!causal || static_cast<int64_t>(q0) + QT - 1 + p.offset >= kw);
     if (wave_live) {
-      const unsigned char *s = smem + stage * L::STAGE;
-      const T *ql = reinterpret_cast<const T *>(s);
-      const T *gl = reinterpret_cast<const T *>(s + L::OFF_G);
-      const T *qtl = reinterpret_cast<const T *>(s + L::OFF_QT);
-      const T *gtl = reinterpret_cast<const T *>(s + L::OFF_GT);
-      const float *ll = reinterpret_cast<const float *>(s + L::OFF_L);
-      const float *dl = reinterpret_cast<const float *>(s + L::OFF_D);
-      const bool edge = (p.causal && static_cast<int64_t>(q0) + p.offset < kw + 31) ||
+      const T *qt = lds + stage * 2 * TILE;
+      const T *gt = qt + TILE;
+      const float *ll = rowv[stage];
+      const float *dl = rowv[stage] + QT;
+      const bool edge = (causal && static_cast<int64_t>(q0) + p.offset < kw + 31) ||
                         kw + 32 > kv_end || q0 + QT > p.Sq || keymask;
 
       unsigned pp[4][4], pd[4][4];
@@ -194,9 +179,8 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
         f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < D / 16; ++ks) {
-          const int off = (sub * 32 + c) * L::RSTR + ks * 16 + h * 8;
-          sacc = mfma32<T>(ld16(ql + off), kf[ks], sacc);
-          dpacc = mfma32<T>(ld16(gl + off), vf[ks], dpacc);
+          sacc = mfma32<T>(row_frag<T, D>(qt, sub * 32, ks * 16, lane), kf[ks], sacc);
+          dpacc = mfma32<T>(row_frag<T, D>(gt, sub * 32, ks * 16, lane), vf[ks], dpacc);
         }
         // sacc[i] = S[q0 + 32 sub + crow(i, h)][key]
 #pragma unroll
@@ -210,16 +194,13 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int i = g * 4 + e;
-            bool ok = true;
-            if (edge) {
-              const int qrow = q0 + rq + e;
-              ok = key_live && qrow < p.Sq &&
-                   (!p.causal || static_cast<int64_t>(qrow) + p.offset >= key);
-            }
-            pv[e] = ok ? fast_exp2(fmaf(sacc[i], sl, -lv[e])) : 0.f;
+            const int qrow = q0 + rq + e;
+            const bool ok = !edge | (key_live & (qrow < p.Sq) &
+                                     (!causal | (static_cast<int64_t>(qrow) + p.offset >= key)));
+            const float ex = fast_exp2(fmaf(sacc[i], sl, -lv[e]));
+            pv[e] = ok ? ex : 0.f;
             dsv[e] = pv[e] * (dpacc[i] - dv4[e]);
           }
-          // element pair (i, i+1) -> kstep 2*sub + (i >> 3), dword (i & 7) >> 1
           const int ks = 2 * sub + (g >> 1), dw = (g & 1) * 2;
           pp[ks][dw] = pack2<T>(pv[0], pv[1]);
           pp[ks][dw + 1] = pack2<T>(pv[2], pv[3]);
@@ -234,16 +215,13 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
         const u32x4 bd = {pd[ks][0], pd[ks][1], pd[ks][2], pd[ks][3]};
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          const int off = (dt * 32 + c) * L::TSTR + ks * 16 + h * 4;
-          const u32x2 glo = ld8(gtl + off), ghi = ld8(gtl + off + 8);
-          const u32x2 qlo = ld8(qtl + off), qhi = ld8(qtl + off + 8);
-          dv_acc[dt] = mfma32<T>(u32x4{glo[0], glo[1], ghi[0], ghi[1]}, bp, dv_acc[dt]);
-          dk_acc[dt] = mfma32<T>(u32x4{qlo[0], qlo[1], qhi[0], qhi[1]}, bd, dk_acc[dt]);
+          dv_acc[dt] = mfma32<T>(tr_frag<T, D>(gt, ks * 16, dt * 32, lane), bp, dv_acc[dt]);
+          dk_acc[dt] = mfma32<T>(tr_frag<T, D>(qt, ks * 16, dt * 32, lane), bd, dk_acc[dt]);
         }
       }
     }
 
-    if (itn + 1 < n_iter) store_iter(stage ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -268,28 +246,19 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: one workgroup = 128 query rows of one (b, q head); wave w owns 32 rows.
-// Key tiles of 64 stream through LDS as K, V (A operands of S^T = K Q^T and
-// dP^T = V dO^T) and K^T (A operand of dQ^T = K^T dS^T).
+// dQ: one workgroup = 128 query rows of one (b, q head); wave w owns 32 rows
+// (Q, dO rows as B operands in registers).  Key tiles of 64 stream through
+// LDS as row-major K and V: row reads feed S^T = K Q^T and dP^T = V dO^T,
+// transpose reads of K feed dQ^T = K^T dS^T.
 // ---------------------------------------------------------------------------
 constexpr int QB = 128;  // query rows per workgroup
 constexpr int KT = 64;   // keys per tile
 
 template <typename T, int D>
-struct QLayout {
-  static constexpr int RSTR = D + 8;
-  static constexpr int TSTR = KT + 4;
-  static constexpr int R_ELEMS = KT * RSTR;
-  static constexpr int T_ELEMS = D * TSTR;
-  static constexpr int STAGE = 2 * R_ELEMS + T_ELEMS;  // K | V | K^T
-  static constexpr int BYTES = 2 * STAGE * 2;
-};
+__global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
+  constexpr int TILE = KT * D;
+  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][K | V]
 
-template <typename T, int D>
-__global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
-  using L = QLayout<T, D>;
-  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  T *lds = reinterpret_cast<T *>(smem);
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
   const int n_qb = (p.Sq + QB - 1) / QB;
@@ -301,9 +270,10 @@ __global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
   const int q0 = qb * QB, qw = q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  const bool causal = p.causal != 0;
 
   int64_t lim = kv_end, wlim = kv_end;
-  if (p.causal) {
+  if (causal) {
     lim = min(lim, static_cast<int64_t>(min(q0 + QB, p.Sq) - 1) + p.offset + 1);
     wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
   }
@@ -314,36 +284,29 @@ __global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
   u32x4 qf[D / 16], gf[D / 16];
   float lse2 = 0.f, delta = 0.f;
   {
-    const T *qp = static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1 +
-                  static_cast<int64_t>(qrow) * a.q.s2;
-    const T *gp = static_cast<const T *>(a.dout.data) + b * a.dout.s0 + hq * a.dout.s1 +
-                  static_cast<int64_t>(qrow) * a.dout.s2;
-    const bool ok = qrow < p.Sq;
+    const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
+    const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      qf[ks] = ok ? ld16(qp + ks * 16 + h * 8) : u32x4{0, 0, 0, 0};
-      gf[ks] = ok ? ld16(gp + ks * 16 + h * 8) : u32x4{0, 0, 0, 0};
+      qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+      gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
     }
-    if (ok) {
-      const int64_t idx = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
-      const float lv = a.lse[idx];
-      lse2 = isfinite(lv) ? lv * kLog2e : 0.f;
-      delta = a.delta[idx];
-    }
+    const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+    const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq;
+    const rsrc_t drs = make_rsrc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
+    const rsrc_t lrs = make_rsrc(a.delta + rows + base, static_cast<uint32_t>(p.Sq) * 4);
+    delta = buf_load_f32(drs, static_cast<uint32_t>(qrow) * 4);
+    lse2 = buf_load_f32(lrs, static_cast<uint32_t>(qrow) * 4);
   }
 
-  const T *kbase = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1;
-  const T *vbase = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1;
-  TileRegs<T, D, KT> kreg, vreg;
-  auto load_tile = [&](int kv0) {
-    kreg.load(kbase, a.k.s2, kv0, kv_end, tid);
-    vreg.load(vbase, a.v.s2, kv0, kv_end, tid);
-  };
-  auto store_tile = [&](int stage) {
-    T *s = lds + stage * L::STAGE;
-    kreg.store_rows(s, L::RSTR, tid);
-    vreg.store_rows(s + L::R_ELEMS, L::RSTR, tid);
-    kreg.store_cols(s + 2 * L::R_ELEMS, L::TSTR, tid);
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
+  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  auto issue = [&](int kv0, int stage) {
+    T *kt = lds + stage * 2 * TILE;
+    tile_to_lds<D, KT, NW>(krs, ks_b, kv0, kt, w, lane);
+    tile_to_lds<D, KT, NW>(vrs, vs_b, kv0, kt + TILE, w, lane);
   };
 
   f32x16 acc[D / 32];
@@ -352,33 +315,31 @@ __global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
   const float sl = a.sl;
   const uint8_t *kmask = static_cast<const uint8_t *>(p.mask.data);
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  zero_lds<NT>(lds, sizeof(lds), tid);
+  __syncthreads();
+  if (n_tiles > 0) issue(0, 0);
+  wait_vmem();
   __syncthreads();
 
   for (int it = 0; it < n_tiles; ++it) {
     const int stage = it & 1;
     const int kv0 = it * KT;
-    if (it + 1 < n_tiles) load_tile(kv0 + KT);
+    if (it + 1 < n_tiles) issue(kv0 + KT, stage ^ 1);
 
     if (it < w_tiles) {
-      const T *kl = lds + stage * L::STAGE;
-      const T *vl = kl + L::R_ELEMS;
-      const T *ktl = kl + 2 * L::R_ELEMS;
+      const T *kt = lds + stage * 2 * TILE;
+      const T *vt = kt + TILE;
       f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const int off = (t * 32 + c) * L::RSTR + ks * 16 + h * 8;
-          s[t] = mfma32<T>(ld16(kl + off), qf[ks], s[t]);
-          dp[t] = mfma32<T>(ld16(vl + off), gf[ks], dp[t]);
+          s[t] = mfma32<T>(row_frag<T, D>(kt, t * 32, ks * 16, lane), qf[ks], s[t]);
+          dp[t] = mfma32<T>(row_frag<T, D>(vt, t * 32, ks * 16, lane), gf[ks], dp[t]);
         }
       }
       const bool edge = (kv0 + KT > kv_end) || keymask ||
-                        (p.causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
+                        (causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
       unsigned long long kbits = ~0ull;
       if (edge && keymask) {
         const int key = kv0 + lane;
@@ -393,13 +354,12 @@ __global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
           float ds[2];
 #pragma unroll
           for (int e = 0; e < 2; ++e) {
-            bool ok = true;
-            if (edge) {
-              const int kk = t * 32 + crow(i + e, h);
-              const int key = kv0 + kk;
-              ok = key < kv_end && (!p.causal || qpos >= key) && ((kbits >> kk) & 1ull);
-            }
-            const float pv = ok ? fast_exp2(fmaf(s[t][i + e], sl, -lse2)) : 0.f;
+            const int kk = t * 32 + crow(i + e, h);
+            const int key = kv0 + kk;
+            const bool ok = !edge | ((key < kv_end) & (!causal | (qpos >= key)) &
+                                     (((kbits >> kk) & 1ull) != 0));
+            const float ex = fast_exp2(fmaf(s[t][i + e], sl, -lse2));
+            const float pv = ok ? ex : 0.f;
             ds[e] = pv * (dp[t][i + e] - delta);
           }
           pd[t * 2 + (i >> 3)][(i & 7) >> 1] = pack2<T>(ds[0], ds[1]);
@@ -409,15 +369,12 @@ __global__ __launch_bounds__(NT, 1) void dq_kernel(BwdArgs a) {
       for (int ks = 0; ks < 4; ++ks) {
         const u32x4 bd = {pd[ks][0], pd[ks][1], pd[ks][2], pd[ks][3]};
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const T *kr = ktl + (dt * 32 + c) * L::TSTR + ks * 16 + h * 4;
-          const u32x2 lo = ld8(kr), hi = ld8(kr + 8);
-          acc[dt] = mfma32<T>(u32x4{lo[0], lo[1], hi[0], hi[1]}, bd, acc[dt]);
-        }
+        for (int dt = 0; dt < D / 32; ++dt)
+          acc[dt] = mfma32<T>(tr_frag<T, D>(kt, ks * 16, dt * 32, lane), bd, acc[dt]);
       }
     }
 
-    if (it + 1 < n_tiles) store_tile(stage ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -441,20 +398,11 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
   constexpr int RPB = NT / (D / 8);
-  row_delta_kernel<T, D><<<dim3((rows + RPB - 1) / RPB), dim3(NT), 0, st>>>(a);
-
-  static bool attr_set = false;  // raise the dynamic-LDS limit once per instantiation
-  if (!attr_set) {
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&dkdv_kernel<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, KVLayout<T, D>::BYTES);
-    hipFuncSetAttribute(reinterpret_cast<const void *>(&dq_kernel<T, D>),
-                        hipFuncAttributeMaxDynamicSharedMemorySize, QLayout<T, D>::BYTES);
-    attr_set = true;
-  }
+  { Probe pr_("bwd_row_prep", st); row_prep_kernel<T, D><<<dim3((rows + RPB - 1) / RPB), dim3(NT), 0, st>>>(a); }
   const int n_kb = (p.Sk + KB - 1) / KB;
-  dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), KVLayout<T, D>::BYTES, st>>>(a);
+  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
   const int n_qb = (p.Sq + QB - 1) / QB;
-  dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), QLayout<T, D>::BYTES, st>>>(a);
+  { Probe pr_("bwd_dq_mfma", st); dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a); }
   return hipGetLastError();
 }
 

@@ -124,6 +124,110 @@ struct TileRegs {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Buffer resources: loads whose byte offset falls past `bytes` return zeros,
+// so ragged tiles need no branches.  Offsets are 32-bit: the host only routes
+// views whose per-head extent fits (mfma_extent_ok).
+// ---------------------------------------------------------------------------
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, static_cast<int>(bytes),
+                                           kRsrcFlags);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), 0, 0);
+}
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, static_cast<int>(off), 0, 0));
+}
+// Lane l's 16 bytes land at lds_wave + 16*l (lds_wave is wave-uniform).
+__device__ __forceinline__ void buf_load16_lds(rsrc_t r, void *lds_wave, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)(lds_wave), 16,
+      static_cast<int>(off), 0, 0, 0);
+}
+__device__ __forceinline__ void buf_load4_lds(rsrc_t r, void *lds_wave, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void *)(lds_wave), 4,
+      static_cast<int>(off), 0, 0, 0);
+}
+// Wait for this wave's outstanding vector-memory loads (incl. LDS-direct ones):
+// s_waitcnt vmcnt(0) with expcnt / lgkmcnt left at their maxima (gfx9 encoding).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// ---------------------------------------------------------------------------
+// Swizzled LDS tiles: [rows][D] 16-bit elements, row-major, no padding; the
+// 16-byte chunk c of row r sits at chunk position c ^ swz(r).  Eight lanes
+// reading one chunk column of 8 consecutive rows hit 8 distinct bank groups
+// (16-byte row reads), and 16 lanes reading 32 bytes of 4 consecutive rows
+// hit 4 distinct 32-byte bank groups (transpose reads).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ constexpr int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+
+template <int D>
+__device__ __forceinline__ constexpr int toff(int r, int col) {
+  return r * D + ((((col >> 3) ^ swz(r))) << 3) + (col & 7);
+}
+
+// Direct global -> LDS copy of ROWS rows (from row0) of one head into a
+// swizzled tile, split over NW waves; rows at or past the resource bound
+// arrive as zeros.  `stride_b` is the row stride in bytes.
+template <int D, int ROWS, int NW>
+__device__ __forceinline__ void tile_to_lds(rsrc_t r, uint32_t stride_b, int row0, void *tile,
+                                            int wave, int lane) {
+  constexpr int LOADS = ROWS * D * 2 / 1024;
+#pragma unroll
+  for (int n = wave; n < LOADS; n += NW) {
+    const int off = n * 1024 + lane * 16;
+    const int row = off / (D * 2);
+    const int chunk = ((off % (D * 2)) >> 4) ^ swz(row);
+    buf_load16_lds(r, static_cast<unsigned char *>(tile) + n * 1024,
+                   static_cast<uint32_t>(row0 + row) * stride_b + chunk * 16);
+  }
+}
+
+// Zero `bytes` of LDS (multiple of 16) with all NT threads.  Run once before
+// the first tile load: whatever a range-checked load leaves in padded rows is
+// then either zero or a finite value from an earlier tile, so masked rows
+// (probability 0) never multiply a stale NaN.
+template <int NT>
+__device__ __forceinline__ void zero_lds(void *p, int bytes, int tid) {
+  u32x4 *q = static_cast<u32x4 *>(p);
+  for (int i = tid; i < bytes / 16; i += NT) q[i] = u32x4{0, 0, 0, 0};
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ u32x2 ds_read_tr(const T *p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4 *)(const_cast<T *>(p)));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A operand (M = 32 columns from mbase, K = 16 rows from kbase) of a swizzled
+// row-major tile, i.e. the transpose of the stored rows.  Element j of lane
+// (c, h) is tile[kbase + 8(j>>2) + 4h + (j&3)][mbase + c]: the K order that a
+// C tile hands over as a B operand (see crow()).
+template <typename T, int D>
+__device__ __forceinline__ u32x4 tr_frag(const T *tile, int kbase, int mbase, int lane) {
+  const int i = lane & 15, g = lane >> 4, h = lane >> 5;
+  const int col = mbase + 16 * (g & 1) + 4 * (i & 3);
+  const int r0 = kbase + 4 * h + (i >> 2);
+  const u32x2 a = ds_read_tr(tile + toff<D>(r0, col));
+  const u32x2 b = ds_read_tr(tile + toff<D>(r0 + 8, col));
+  return u32x4{a[0], a[1], b[0], b[1]};
+}
+
+// A operand (M = 32 rows from rbase, K = 16 columns from kbase) of a
+// swizzled tile: lane (c, h) reads row rbase + c, columns kbase + 8h .. +7.
+template <typename T, int D>
+__device__ __forceinline__ u32x4 row_frag(const T *tile, int rbase, int kbase, int lane) {
+  return ld16(tile + toff<D>(rbase + (lane & 31), kbase + 8 * (lane >> 5)));
+}
+
 inline bool aligned16(View v) {
   return (reinterpret_cast<uintptr_t>(v.data) % 16 == 0) && v.s0 % 8 == 0 && v.s1 % 8 == 0 &&
          v.s2 % 8 == 0;

@@ -7,14 +7,13 @@
 // log l; fully masked rows give O = 0, LSE = -inf.
 //
 // Work split: one workgroup = 4 wavefronts = 128 query rows of one (b, h);
-// each wave owns 32 rows.  Key/value tiles of 64 rows stream through LDS,
-// double buffered (global -> registers during the MFMAs of the previous
-// tile, registers -> LDS after it).  The wave computes S^T = K Q^T so that
-// each lane owns one query column: the softmax statistics and the rescale of
-// the accumulator O^T = V^T P^T stay lane-local, and P^T leaves the
-// accumulator registers as the next contraction's B operand without any
-// data movement.  V is written to LDS transposed (V^T) because the PV
-// contraction runs along keys.
+// each wave owns 32 rows.  Key and value tiles of 64 rows are copied global
+// -> LDS by direct buffer loads (no staging registers), double buffered, into
+// swizzled row-major tiles.  The wave computes S^T = K Q^T so that each lane
+// owns one query column: the softmax statistics and the rescale of the
+// accumulator O^T = V^T P^T stay lane-local, and P^T leaves the accumulator
+// registers as the next contraction's B operand without data movement.  The
+// V^T operand is read from the row-major V tile with LDS transpose reads.
 #include "mfma_common.h"
 
 namespace tsattn {
@@ -23,6 +22,7 @@ namespace {
 constexpr int BM = 128;  // query rows per workgroup
 constexpr int BN = 64;   // keys per tile
 constexpr int NT = 256;  // threads
+constexpr int NW = NT / 64;
 
 struct FwdArgs {
   Problem p;
@@ -33,19 +33,15 @@ struct FwdArgs {
   int total;
 };
 
-template <typename T, int D>
-struct FwdTile {
-  static constexpr int KSTR = D + 8;   // K row stride (elements): 16 B pad -> conflict-free b128 reads
-  static constexpr int VSTR = BN + 4;  // V^T row stride (elements): 8 B pad
-  static constexpr int K_ELEMS = BN * KSTR;
-  static constexpr int V_ELEMS = D * VSTR;
-  static constexpr int STAGE = K_ELEMS + V_ELEMS;
-};
+template <typename T>
+__device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
+  return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
+}
 
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
-  using L = FwdTile<T, D>;
-  __shared__ __attribute__((aligned(16))) T lds[2 * L::STAGE];
+  constexpr int TILE = BN * D;  // elements per K (or V) tile
+  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][K | V]
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
@@ -70,27 +66,23 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const int n_tiles = lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0;
   const int w_tiles = wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0;
 
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2;
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2;
+  const uint32_t vs_b = static_cast<uint32_t>(a.v.s2) * 2;
+  const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+
   // Q fragments (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8h .. +7].
   u32x4 qf[D / 16];
-  {
-    const T *qp = static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1 +
-                  static_cast<int64_t>(qrow) * a.q.s2;
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks)
-      qf[ks] = qrow < p.Sq ? ld16(qp + ks * 16 + h * 8) : u32x4{0, 0, 0, 0};
-  }
+  for (int ks = 0; ks < D / 16; ++ks)
+    qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
 
-  const T *kbase = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1;
-  const T *vbase = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1;
-  TileRegs<T, D, BN> kreg, vreg;
-  auto load_tile = [&](int kv0) {
-    kreg.load(kbase, a.k.s2, kv0, kv_end, tid);
-    vreg.load(vbase, a.v.s2, kv0, kv_end, tid);
-  };
-  auto store_tile = [&](int stage) {
-    T *kl = lds + stage * L::STAGE;
-    kreg.store_rows(kl, L::KSTR, tid);
-    vreg.store_cols(kl + L::K_ELEMS, L::VSTR, tid);
+  auto issue = [&](int kv0, int stage) {
+    T *kt = lds + stage * 2 * TILE;
+    tile_to_lds<D, BN, NW>(krs, ks_b, kv0, kt, w, lane);
+    tile_to_lds<D, BN, NW>(vrs, vs_b, kv0, kt + TILE, w, lane);
   };
 
   f32x16 oacc[D / 32];
@@ -100,28 +92,26 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const float sl = a.sl;
   const uint8_t *kmask = static_cast<const uint8_t *>(p.mask.data);
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
+  zero_lds<NT>(lds, sizeof(lds), tid);
+  __syncthreads();
+  if (n_tiles > 0) issue(0, 0);
+  wait_vmem();
   __syncthreads();
 
   for (int it = 0; it < n_tiles; ++it) {
     const int stage = it & 1;
     const int kv0 = it * BN;
-    if (it + 1 < n_tiles) load_tile(kv0 + BN);
+    if (it + 1 < n_tiles) issue(kv0 + BN, stage ^ 1);
 
     if (it < w_tiles) {
-      const T *kl = lds + stage * L::STAGE;
-      const T *vl = kl + L::K_ELEMS;
+      const T *kt = lds + stage * 2 * TILE;
+      const T *vt = kt + TILE;
       f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
       for (int ks = 0; ks < D / 16; ++ks) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          const u32x4 kf = ld16(kl + (t * 32 + c) * L::KSTR + ks * 16 + h * 8);
-          s[t] = mfma32<T>(kf, qf[ks], s[t]);
-        }
+        for (int t = 0; t < 2; ++t)
+          s[t] = mfma32<T>(row_frag<T, D>(kt, t * 32, ks * 16, lane), qf[ks], s[t]);
       }
 
       const bool edge = (kv0 + BN > kv_end) || keymask ||
@@ -134,14 +124,15 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
           kbits = __ballot(ok);
         }
         const int64_t qpos = static_cast<int64_t>(qrow) + p.offset;
+        const bool causal = p.causal != 0;
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
             const int kk = t * 32 + crow(i, h);
             const int key = kv0 + kk;
-            const bool ok = key < kv_end && (!p.causal || qpos >= key) && ((kbits >> kk) & 1ull);
-            if (!ok) s[t][i] = -INFINITY;
+            const bool ok = (key < kv_end) & (!causal | (qpos >= key)) & (((kbits >> kk) & 1ull) != 0);
+            s[t][i] = ok ? s[t][i] : -INFINITY;
           }
         }
       }
@@ -176,16 +167,12 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       for (int ks = 0; ks < 4; ++ks) {
         const u32x4 bf = {pb[ks][0], pb[ks][1], pb[ks][2], pb[ks][3]};
 #pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          const T *vr = vl + (dt * 32 + c) * L::VSTR + ks * 16 + h * 4;
-          const u32x2 lo = ld8(vr), hi = ld8(vr + 8);
-          const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
-          oacc[dt] = mfma32<T>(vf, bf, oacc[dt]);
-        }
+        for (int dt = 0; dt < D / 32; ++dt)
+          oacc[dt] = mfma32<T>(tr_frag<T, D>(vt, ks * 16, dt * 32, lane), bf, oacc[dt]);
       }
     }
 
-    if (it + 1 < n_tiles) store_tile(stage ^ 1);
+    wait_vmem();
     __syncthreads();
   }
 
@@ -211,7 +198,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 
 template <typename T, int D>
 hipError_t launch(const FwdArgs &a, hipStream_t st) {
-  fwd_kernel<T, D><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  { Probe pr_("fwd_mfma", st); fwd_kernel<T, D><<<dim3(a.total), dim3(NT), 0, st>>>(a); }
   return hipGetLastError();
 }
 

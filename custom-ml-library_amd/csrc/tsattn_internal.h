@@ -88,6 +88,27 @@ __device__ __forceinline__ int kv_end_for(const Problem &p, int b) {
 }
 
 // ---------------------------------------------------------------------------
+// Kernel timing probes: when enabled (tsattn_profile_enable), every kernel
+// launch is bracketed by hipEvents recorded on its own stream; durations are
+// aggregated per kernel name by tsattn_profile_read.  Disabled: one relaxed
+// atomic load per launch.
+// ---------------------------------------------------------------------------
+bool probes_on();
+void probe_begin(const char *name, hipStream_t st);
+void probe_end(hipStream_t st);
+
+struct Probe {
+  bool on;
+  hipStream_t st;
+  Probe(const char *name, hipStream_t s) : on(probes_on()), st(s) {
+    if (on) probe_begin(name, st);
+  }
+  ~Probe() {
+    if (on) probe_end(st);
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Launchers (each returns hipSuccess or the launch error).
 // ---------------------------------------------------------------------------
 hipError_t launch_generic_forward(const Problem &p, int dtype, View q, View k, View v, View o,

@@ -77,6 +77,12 @@ SIGNATURES = {
         c_int,
         [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p],
     ),
+    "tsattn_profile_enable": (c_int, [c_int]),
+    "tsattn_profile_reset": (c_int, []),
+    "tsattn_profile_read": (
+        c_int,
+        [c_int, ctypes.c_char_p, c_size_t, POINTER(ctypes.c_longlong), POINTER(c_double)],
+    ),
 }
 
 _lock = threading.Lock()
@@ -134,3 +140,25 @@ def set_kernel_policy(policy: int) -> None:
 
 def last_kernel_path() -> int:
     return load().tsattn_last_kernel_path()
+
+
+def profile_enable(on: bool) -> None:
+    """Bracket every kernel launch with hipEvents on its stream (diagnostic)."""
+    load().tsattn_profile_enable(1 if on else 0)
+
+
+def profile_reset() -> None:
+    load().tsattn_profile_reset()
+
+
+def profile_read() -> dict[str, tuple[int, float]]:
+    """{kernel name: (launches, summed ms)} of the probed launches so far."""
+    lib = load()
+    out = {}
+    buf = ctypes.create_string_buffer(64)
+    n, ms = ctypes.c_longlong(), c_double()
+    i = 0
+    while lib.tsattn_profile_read(i, buf, 64, ctypes.byref(n), ctypes.byref(ms)) == OK:
+        out[buf.value.decode()] = (int(n.value), float(ms.value))
+        i += 1
+    return out

@@ -100,6 +100,20 @@ int tsattn_set_kernel_policy(int policy);
 int tsattn_last_kernel_path(void);
 
 /*
+ * Kernel timing probes (diagnostic, no counterpart in the reference; the
+ * benchmark uses them to time the dominant kernel on its own stream).
+ * While enabled, every kernel launch is bracketed by hipEvents recorded on
+ * the launch stream.  tsattn_profile_read(i, ...) synchronises on the
+ * recorded events and returns the name, launch count and summed duration
+ * (ms) of the i-th distinct kernel (returns -1 past the last one);
+ * tsattn_profile_reset clears the totals.
+ */
+int tsattn_profile_enable(int on);
+int tsattn_profile_reset(void);
+int tsattn_profile_read(int index, char *name, size_t name_len, long long *launches,
+                        double *total_ms);
+
+/*
  * Forward: out = softmax(scale * q k^T + mask) v, with the online-softmax
  * recurrence of the reference's streaming backend and its saved row LSE.
  * Replaces src/tensorsmith/nn/attention.py:175-198 (streaming forward) and,
@@ -109,7 +123,7 @@ int tsattn_last_kernel_path(void);
 int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                         const tsattn_view *v, const tsattn_view *out, void *lse, void *stream);
 
-/* Bytes of scratch tsattn_sdpa_backward needs (row deltas). */
+/* Bytes of scratch tsattn_sdpa_backward needs (row deltas and row LSEs). */
 size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
 
 /*
