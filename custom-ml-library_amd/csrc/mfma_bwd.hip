@@ -75,53 +75,49 @@ __global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: one workgroup = 128 keys of one (b, kv head); wave w owns keys
-// kw..kw+31 (K, V rows as B operands in registers).  Query tiles of 64 rows
-// (all query heads of the group) stream through LDS as row-major Q and dO:
-// 16-byte row reads feed S = Q K^T and dP = dO V^T, transpose reads feed
+// dK / dV: one workgroup = 128 keys of one (b, kv head), 8 wavefronts.  The
+// workgroup's K and V rows stay in LDS for its whole life (B operands of
+// S = Q K^T and dP = dO V^T); query tiles of 64 rows (all query heads of the
+// group) stream through LDS as row-major Q and dO.  Wave w owns key group
+// kg = w & 3 (32 keys) and query half qh = w >> 2 (32 rows of each tile), so
+// a wave's persistent state is just its dK^T / dV^T accumulators and two
+// waves share each SIMD; the two query halves' partial sums are added
+// through LDS once at the end.  Row reads feed S and dP, transpose reads feed
 // dV^T = dO^T P and dK^T = Q^T dS.
 // ---------------------------------------------------------------------------
-constexpr int KB = 128;  // keys per workgroup
-constexpr int QT = 64;   // query rows per tile
+constexpr int KB = 128;   // keys per workgroup
+constexpr int QT = 64;    // query rows per tile
+constexpr int NTK = 512;  // threads of the dK/dV kernel
+constexpr int NWK = NTK / 64;
 
 template <typename T, int D>
-__global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
-  constexpr int TILE = QT * D;
-  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][Q | dO]
-  __shared__ __attribute__((aligned(16))) float rowv[2][2 * QT];    // [stage][lse2 | delta]
+__global__ __launch_bounds__(NTK, 1) void dkdv_kernel(BwdArgs a) {
+  constexpr int KTILE = KB * D, QTILE = QT * D;
+  __shared__ __attribute__((aligned(1024))) T kv_lds[2 * KTILE];       // K | V of the 128 keys
+  __shared__ __attribute__((aligned(1024))) T qg_lds[2 * 2 * QTILE];   // [stage][Q | dO]
+  __shared__ __attribute__((aligned(16))) float rowv[2][2 * QT];       // [stage][lse2 | delta]
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int kg = w & 3, qh = w >> 2;
   const int n_kb = (p.Sk + KB - 1) / KB;
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   const int bh = logical / n_kb;
   const int kb = logical - bh * n_kb;  // early key blocks see the most queries: run them first
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
-  const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
+  const int k0 = kb * KB, kw = k0 + 32 * kg, key = kw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   const bool key_live = key < kv_end &&
                         (!keymask || static_cast<const uint8_t *>(p.mask.data)
                                          [b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-
-  // K and V rows of this lane's key as B operands (K^T / V^T with N = key).
-  u32x4 kf[D / 16], vf[D / 16];
-  {
-    const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
-    const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-    const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
-#pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
-      kf[ks] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (ks * 16 + h * 8) * 2);
-      vf[ks] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (ks * 16 + h * 8) * 2);
-    }
-  }
+  const bool causal = p.causal != 0;
 
   // Query tiles: only rows that can see a key of this block (causal).
   int q_start = 0;
-  if (p.causal) {
+  if (causal) {
     int64_t s = static_cast<int64_t>(k0) - p.offset;
     q_start = s <= 0 ? 0 : static_cast<int>(s < p.Sq ? s : p.Sq);
     q_start = (q_start / QT) * QT;
@@ -133,11 +129,11 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
   auto issue = [&](int itn, int stage) {
     const int r = itn / n_qt, q0 = q_start + (itn - r * n_qt) * QT;
     const int hq = hk * p.rep + r;
-    T *qt = lds + stage * 2 * TILE;
+    T *qt = qg_lds + stage * 2 * QTILE;
     const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
-    tile_to_lds<D, QT, NW>(qrs, qs_b, q0, qt, w, lane);
-    tile_to_lds<D, QT, NW>(grs, gs_b, q0, qt + TILE, w, lane);
+    tile_to_lds<D, QT, NWK>(qrs, qs_b, q0, qt, w, lane);
+    tile_to_lds<D, QT, NWK>(grs, gs_b, q0, qt + QTILE, w, lane);
     if (w < 2) {
       const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
       const rsrc_t rrs = make_rsrc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
@@ -149,74 +145,84 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
 #pragma unroll
   for (int dt = 0; dt < D / 32; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
   const float sl = a.sl;
-  const bool causal = p.causal != 0;
+  const T *kt = kv_lds;
+  const T *vt = kv_lds + KTILE;
 
-  zero_lds<NT>(lds, sizeof(lds), tid);
-  zero_lds<NT>(rowv, sizeof(rowv), tid);
+  zero_lds<NTK>(kv_lds, sizeof(kv_lds), tid);
+  zero_lds<NTK>(qg_lds, sizeof(qg_lds), tid);
+  zero_lds<NTK>(rowv, sizeof(rowv), tid);
   __syncthreads();
-  if (n_iter > 0) issue(0, 0);
+  if (n_iter > 0) {
+    const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
+    const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+    const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+    tile_to_lds<D, KB, NWK>(krs, ks_b, k0, kv_lds, w, lane);
+    tile_to_lds<D, KB, NWK>(vrs, vs_b, k0, kv_lds + KTILE, w, lane);
+    issue(0, 0);
+  }
   wait_vmem();
   __syncthreads();
 
   for (int itn = 0; itn < n_iter; ++itn) {
     const int stage = itn & 1;
     const int q0 = q_start + (itn % n_qt) * QT;
+    const int qs = q0 + 32 * qh;  // first query row of this wave's half
     if (itn + 1 < n_iter) issue(itn + 1, stage ^ 1);
 
-    // Does any (query row of this tile, key of this wave) pair survive?
-    const bool wave_live = kw < kv_end && (!causal || static_cast<int64_t>(q0) + QT - 1 + p.offset >= kw);
+    // Does any (query row of this half tile, key of this wave) pair survive?
+    const bool wave_live = kw < kv_end && qs < p.Sq &&
+                           (!causal || static_cast<int64_t>(qs) + 31 + p.offset >= kw);
     if (wave_live) {
-      const T *qt = lds + stage * 2 * TILE;
-      const T *gt = qt + TILE;
+      const T *qt = qg_lds + stage * 2 * QTILE;
+      const T *gt = qt + QTILE;
       const float *ll = rowv[stage];
       const float *dl = rowv[stage] + QT;
-      const bool edge = (causal && static_cast<int64_t>(q0) + p.offset < kw + 31) ||
-                        kw + 32 > kv_end || q0 + QT > p.Sq || keymask;
+      const bool edge = (causal && static_cast<int64_t>(qs) + p.offset < kw + 31) ||
+                        kw + 32 > kv_end || qs + 32 > p.Sq || keymask;
 
-      unsigned pp[4][4], pd[4][4];
+      f32x16 sacc = f32x16{}, dpacc = f32x16{};
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        f32x16 sacc = f32x16{}, dpacc = f32x16{};
-#pragma unroll
-        for (int ks = 0; ks < D / 16; ++ks) {
-          sacc = mfma32<T>(row_frag<T, D>(qt, sub * 32, ks * 16, lane), kf[ks], sacc);
-          dpacc = mfma32<T>(row_frag<T, D>(gt, sub * 32, ks * 16, lane), vf[ks], dpacc);
-        }
-        // sacc[i] = S[q0 + 32 sub + crow(i, h)][key]
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int rq = sub * 32 + g * 8 + h * 4;
-          const float4 l4 = *reinterpret_cast<const float4 *>(ll + rq);
-          const float4 d4 = *reinterpret_cast<const float4 *>(dl + rq);
-          const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-          const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-          float pv[4], dsv[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int i = g * 4 + e;
-            const int qrow = q0 + rq + e;
-            const bool ok = !edge | (key_live & (qrow < p.Sq) &
-                                     (!causal | (static_cast<int64_t>(qrow) + p.offset >= key)));
-            const float ex = fast_exp2(fmaf(sacc[i], sl, -lv[e]));
-            pv[e] = ok ? ex : 0.f;
-            dsv[e] = pv[e] * (dpacc[i] - dv4[e]);
-          }
-          const int ks = 2 * sub + (g >> 1), dw = (g & 1) * 2;
-          pp[ks][dw] = pack2<T>(pv[0], pv[1]);
-          pp[ks][dw + 1] = pack2<T>(pv[2], pv[3]);
-          pd[ks][dw] = pack2<T>(dsv[0], dsv[1]);
-          pd[ks][dw + 1] = pack2<T>(dsv[2], dsv[3]);
-        }
+      for (int ks = 0; ks < D / 16; ++ks) {
+        sacc = mfma32<T>(row_frag<T, D>(qt, 32 * qh, ks * 16, lane),
+                         row_frag<T, D>(kt, 32 * kg, ks * 16, lane), sacc);
+        dpacc = mfma32<T>(row_frag<T, D>(gt, 32 * qh, ks * 16, lane),
+                          row_frag<T, D>(vt, 32 * kg, ks * 16, lane), dpacc);
       }
-      // dV^T += dO^T P, dK^T += Q^T dS over the 64 query rows (4 ksteps of 16).
+      // sacc[i] = S[qs + crow(i, h)][key]
+      unsigned pp[2][4], pd[2][4];
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
+      for (int g = 0; g < 4; ++g) {
+        const int rq = 32 * qh + g * 8 + h * 4;
+        const float4 l4 = *reinterpret_cast<const float4 *>(ll + rq);
+        const float4 d4 = *reinterpret_cast<const float4 *>(dl + rq);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
+        float pv[4], dsv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = g * 4 + e;
+          const int qrow = q0 + rq + e;
+          const bool ok = !edge | (key_live & (qrow < p.Sq) &
+                                   (!causal | (static_cast<int64_t>(qrow) + p.offset >= key)));
+          const float ex = fast_exp2(fmaf(sacc[i], sl, -lv[e]));
+          pv[e] = ok ? ex : 0.f;
+          dsv[e] = pv[e] * (dpacc[i] - dv4[e]);
+        }
+        const int ks = g >> 1, dw = (g & 1) * 2;
+        pp[ks][dw] = pack2<T>(pv[0], pv[1]);
+        pp[ks][dw + 1] = pack2<T>(pv[2], pv[3]);
+        pd[ks][dw] = pack2<T>(dsv[0], dsv[1]);
+        pd[ks][dw + 1] = pack2<T>(dsv[2], dsv[3]);
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS over this wave's 32 query rows.
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
         const u32x4 bp = {pp[ks][0], pp[ks][1], pp[ks][2], pp[ks][3]};
         const u32x4 bd = {pd[ks][0], pd[ks][1], pd[ks][2], pd[ks][3]};
 #pragma unroll
         for (int dt = 0; dt < D / 32; ++dt) {
-          dv_acc[dt] = mfma32<T>(tr_frag<T, D>(gt, ks * 16, dt * 32, lane), bp, dv_acc[dt]);
-          dk_acc[dt] = mfma32<T>(tr_frag<T, D>(qt, ks * 16, dt * 32, lane), bd, dk_acc[dt]);
+          dv_acc[dt] = mfma32<T>(tr_frag<T, D>(gt, 32 * qh + ks * 16, dt * 32, lane), bp, dv_acc[dt]);
+          dk_acc[dt] = mfma32<T>(tr_frag<T, D>(qt, 32 * qh + ks * 16, dt * 32, lane), bd, dk_acc[dt]);
         }
       }
     }
@@ -225,7 +231,30 @@ __global__ __launch_bounds__(NT, 1) void dkdv_kernel(BwdArgs a) {
     __syncthreads();
   }
 
-  if (key >= p.Sk) return;
+  // Add the two query halves through LDS (the tile buffers are free now):
+  // red[kg][dt][i][lane], one pass for dK, one for dV.
+  float *red = reinterpret_cast<float *>(qg_lds);
+  static_assert(sizeof(qg_lds) >= 4 * (D / 32) * 16 * 64 * sizeof(float), "reduction buffer");
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
+    if (qh == 1) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) red[((kg * (D / 32) + dt) * 16 + i) * 64 + lane] = acc[dt][i];
+    }
+    __syncthreads();
+    if (qh == 0) {
+#pragma unroll
+      for (int dt = 0; dt < D / 32; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[dt][i] += red[((kg * (D / 32) + dt) * 16 + i) * 64 + lane];
+    }
+    __syncthreads();
+  }
+
+  if (qh != 0 || key >= p.Sk) return;
   // lane holds dK^T[d = 32 dt + crow(i, h)][key]
   T *dkp = mut<T>(a.dk) + b * a.dk.s0 + hk * a.dk.s1 + static_cast<int64_t>(key) * a.dk.s2;
   T *dvp = mut<T>(a.dv) + b * a.dv.s0 + hk * a.dv.s1 + static_cast<int64_t>(key) * a.dv.s2;
@@ -400,7 +429,7 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
   constexpr int RPB = NT / (D / 8);
   { Probe pr_("bwd_row_prep", st); row_prep_kernel<T, D><<<dim3((rows + RPB - 1) / RPB), dim3(NT), 0, st>>>(a); }
   const int n_kb = (p.Sk + KB - 1) / KB;
-  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
+  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NTK), 0, st>>>(a); }
   const int n_qb = (p.Sq + QB - 1) / QB;
   { Probe pr_("bwd_dq_mfma", st); dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a); }
   return hipGetLastError();

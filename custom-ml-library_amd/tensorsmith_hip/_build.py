@@ -37,13 +37,8 @@ FLAGS = [
 ]
 
 
-# Per-source extra flags.  The backward dK/dV kernel keeps K, V operands and
-# two fp32 accumulator tiles live across its loop; LLVM's default heuristic
-# then parks values in AGPRs and shuttles them back with v_accvgpr moves on
-# every iteration.  Forcing the VGPR form of MFMA removes ~90% of those moves.
-EXTRA_FLAGS = {
-    "mfma_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-}
+# Per-source extra hipcc flags (none needed at present).
+EXTRA_FLAGS: dict[str, list[str]] = {}
 
 
 def hipcc() -> str:
