@@ -55,6 +55,8 @@ def parse():
     ap.add_argument("--decode-steps", type=int, default=50)
     ap.add_argument("--cpu-heads", type=int, default=16, help="heads in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode"], default="all",
+                    help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
 
 
@@ -270,10 +272,19 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "decode":
+        dec_res, _ = bench_decode(ts, torch, args.decode_steps, args.warmup)
+        print(json.dumps({"decode": dec_res}), flush=True)
+        return
     print(f"[bench] fwd+bwd B{B} H{H} S{S} D{D} bf16: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
     main_res, host = bench_fwd_bwd(ts, torch, args.steps, args.warmup)
     print(f"[bench] fwd+bwd {main_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
+    if args.workload == "fwd_bwd":
+        print(json.dumps({"value": main_res["value"], "ms_per_step": main_res["ms_per_step"],
+                          "roofline": main_res["roofline"], "kernels": main_res["kernels"]}),
+              flush=True)
+        return
     dec_res, dec_host = bench_decode(ts, torch, args.decode_steps, args.warmup)
     print(f"[bench] decode {dec_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
     cpu = None

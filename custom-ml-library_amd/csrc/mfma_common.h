@@ -159,16 +159,27 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 
 // ---------------------------------------------------------------------------
 // Swizzled LDS tiles: [rows][D] 16-bit elements, row-major, no padding; the
-// 16-byte chunk c of row r sits at chunk position c ^ swz(r).  Eight lanes
-// reading one chunk column of 8 consecutive rows hit 8 distinct bank groups
-// (16-byte row reads), and 16 lanes reading 32 bytes of 4 consecutive rows
-// hit 4 distinct 32-byte bank groups (transpose reads).
+// 16-byte chunk c of row r sits at chunk position c ^ swz<D>(r).  gfx950's
+// LDS has 64 four-byte banks and serves 16 lanes of a 16-byte read (or 32
+// lanes of an 8-byte read) per cycle.  The swizzle makes both access shapes
+// conflict-free:
+//  * row reads: 16 lanes read one chunk column of 16 consecutive rows;
+//  * transpose reads: 32 lanes read 4 consecutive chunks of 4 consecutive
+//    rows (4 rows x 64 bytes).
+// D = 128 (a row covers all 64 banks): swz = 4*(r&3) + ((r>>2)&3), a bijection
+// on 16 aligned rows whose high two bits differ across 4 aligned rows.
+// D = 64 (two rows per bank line): swz = 4*((r>>1)&1) + ((r>>2)&3), a
+// bijection on each row parity of 16 aligned rows that moves rows r and r+2
+// to different 4-chunk groups.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ constexpr int swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+template <int D>
+__device__ __forceinline__ constexpr int swz(int r) {
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+}
 
 template <int D>
 __device__ __forceinline__ constexpr int toff(int r, int col) {
-  return r * D + ((((col >> 3) ^ swz(r))) << 3) + (col & 7);
+  return r * D + ((((col >> 3) ^ swz<D>(r))) << 3) + (col & 7);
 }
 
 // Direct global -> LDS copy of ROWS rows (from row0) of one head into a
@@ -182,7 +193,7 @@ __device__ __forceinline__ void tile_to_lds(rsrc_t r, uint32_t stride_b, int row
   for (int n = wave; n < LOADS; n += NW) {
     const int off = n * 1024 + lane * 16;
     const int row = off / (D * 2);
-    const int chunk = ((off % (D * 2)) >> 4) ^ swz(row);
+    const int chunk = ((off % (D * 2)) >> 4) ^ swz<D>(row);
     buf_load16_lds(r, static_cast<unsigned char *>(tile) + n * 1024,
                    static_cast<uint32_t>(row0 + row) * stride_b + chunk * 16);
   }
