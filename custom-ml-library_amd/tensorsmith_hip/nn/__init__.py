@@ -1,5 +1,14 @@
 """Neural-network pieces on the attention path (reference ``tensorsmith.nn``)."""
 
+from . import functional
 from .attention import rotary_embedding, scaled_dot_product_attention
+from .cache import KVCache
+from .layers import GELU, Dropout, Embedding, LayerNorm, Linear
+from .module import Module, Parameter
+from .transformer import MultiHeadAttention
 
-__all__ = ["rotary_embedding", "scaled_dot_product_attention"]
+__all__ = [
+    "Dropout", "Embedding", "GELU", "KVCache", "LayerNorm", "Linear", "Module",
+    "MultiHeadAttention", "Parameter", "functional", "rotary_embedding",
+    "scaled_dot_product_attention",
+]

@@ -1,0 +1,139 @@
+"""Preallocated KV cache on a hip device (reference ``src/tensorsmith/nn/cache.py``).
+
+Same API, validation order and storage layout as the reference: keys and
+values live in ``[B, H_kv, capacity, D]`` device arrays, ``append`` writes the
+slice ``[:, :, length:length+T]`` after checking every shape and the
+capacity, ``get`` returns views of the active prefix, and the optional int8
+mode stores symmetric per-token/head codes with one fp32 scale each
+(``scale = max(max|x| / 127, 1e-8)``, ``q = round(x / scale)``, ``:73-77``),
+dequantised on ``get`` (``:91-98``).  The views ``get`` returns feed the decode
+kernel directly (no copy: the kernel takes the cache's strides).
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from ..device import device as parse_device
+from ..tensor import Tensor, backend_dtype, is_grad_enabled, to_numpy
+
+
+class KVCache:
+    """Preallocated [B,H,capacity,D] keys/values for autoregressive inference."""
+
+    def __init__(self, batch_size: int, num_heads: int, head_dim: int, max_seq_len: int, *,
+                 device=None, dtype="float32", quantized: bool = False, value_dim=None):
+        if min(batch_size, num_heads, head_dim, max_seq_len) <= 0:
+            raise ValueError("cache dimensions and capacity must be positive")
+        self.batch_size, self.num_heads, self.head_dim = batch_size, num_heads, head_dim
+        self.value_dim = head_dim if value_dim is None else value_dim
+        if self.value_dim <= 0:
+            raise ValueError("value_dim must be positive")
+        self.max_seq_len = max_seq_len
+        self.device = parse_device(device)
+        if self.device.type != "hip":
+            raise RuntimeError("tensorsmith_hip keeps KV caches on hip devices")
+        self.dtype = backend_dtype(dtype, self.device)
+        if "float" not in str(self.dtype):
+            raise TypeError("cache compute dtype must be floating point")
+        self.quantized = quantized
+        self.length = 0
+        import torch
+
+        dev = self.device.torch
+        storage = torch.int8 if quantized else self.dtype
+        shape = (batch_size, num_heads, max_seq_len)
+        self._keys = torch.zeros(shape + (head_dim,), dtype=storage, device=dev)
+        self._values = torch.zeros(shape + (self.value_dim,), dtype=storage, device=dev)
+        self._key_scales = torch.ones(shape + (1,), dtype=torch.float32, device=dev) if quantized else None
+        self._value_scales = (torch.ones(shape + (1,), dtype=torch.float32, device=dev)
+                              if quantized else None)
+
+    def append(self, key: Tensor, value: Tensor) -> tuple[Tensor, Tensor]:
+        """Append a chunk after validating all shapes and capacity."""
+        if key.device != self.device or value.device != self.device:
+            raise ValueError("cache and key/value tensors must be on the same device")
+        if is_grad_enabled() and (key.requires_grad or value.requires_grad):
+            raise RuntimeError("KVCache is inference-only; use no_grad() for differentiable inputs")
+        prefix = (self.batch_size, self.num_heads)
+        if key.ndim != 4 or key.shape[:2] != prefix or key.shape[-1] != self.head_dim:
+            raise ValueError("key shape does not match cache configuration")
+        if value.shape != key.shape[:3] + (self.value_dim,):
+            raise ValueError("value shape does not match cache configuration")
+        stop = self.length + key.shape[2]
+        if key.shape[2] == 0 or stop > self.max_seq_len:
+            raise ValueError(f"cache capacity {self.max_seq_len} exceeded or empty append")
+        window = slice(self.length, stop)
+        keys, values = key._data.to(self.dtype), value._data.to(self.dtype)
+        if self.quantized:
+            keys, key_scales = _quantize(keys)
+            values, value_scales = _quantize(values)
+            self._key_scales[:, :, window] = key_scales
+            self._value_scales[:, :, window] = value_scales
+        self._keys[:, :, window] = keys
+        self._values[:, :, window] = values
+        self.length = stop
+        return self.get()
+
+    def get(self) -> tuple[Tensor, Tensor]:
+        keys = self._keys[:, :, : self.length]
+        values = self._values[:, :, : self.length]
+        if self.quantized:
+            keys = (keys.float() * self._key_scales[:, :, : self.length]).to(self.dtype)
+            values = (values.float() * self._value_scales[:, :, : self.length]).to(self.dtype)
+        return Tensor(keys, device=self.device), Tensor(values, device=self.device)
+
+    def reset(self) -> None:
+        """Reuse the allocation; future appends overwrite old entries."""
+        self.length = 0
+
+    def truncate(self, length: int) -> None:
+        if not 0 <= length <= self.length:
+            raise ValueError("truncate length must be between zero and the current length")
+        self.length = length
+
+    def reorder(self, indices) -> None:
+        """Reorder or duplicate batch rows for fixed-width beam search."""
+        host = to_numpy(indices._data if isinstance(indices, Tensor) else indices)
+        host = np.asarray(host)
+        if host.shape != (self.batch_size,) or host.dtype.kind not in "iu":
+            raise ValueError("beam indices must be one integer per cache batch row")
+        if (host < 0).any() or (host >= self.batch_size).any():
+            raise ValueError("beam index out of range")
+        import torch
+
+        order = torch.as_tensor(host.astype(np.int64), device=self._keys.device)
+        self._keys, self._values = self._keys[order], self._values[order]
+        if self.quantized:
+            self._key_scales = self._key_scales[order]
+            self._value_scales = self._value_scales[order]
+
+    @property
+    def storage(self) -> tuple:
+        """Raw persistent arrays."""
+        return self._keys, self._values, self._key_scales, self._value_scales
+
+    @property
+    def memory_bytes(self) -> int:
+        """Allocated persistent payload, excluding temporary dequantised arrays."""
+        arrays = [self._keys, self._values]
+        if self.quantized:
+            arrays += [self._key_scales, self._value_scales]
+        return sum(math.prod(a.shape) * a.element_size() for a in arrays)
+
+    def __len__(self):
+        return self.length
+
+    def __repr__(self):
+        return (f"KVCache(length={self.length}, capacity={self.max_seq_len}, "
+                f"quantized={self.quantized}, device='{self.device}')")
+
+
+def _quantize(raw):
+    import torch
+
+    raw = raw.float()
+    scale = torch.clamp(raw.abs().amax(dim=-1, keepdim=True) / 127, min=1e-8)
+    return torch.round(raw / scale).to(torch.int8), scale

@@ -1,0 +1,202 @@
+"""Host-side checks that need no GPU: the C ABI's symbols and struct layout,
+validation-only ABI calls, the reference's argument checks, and the autograd
+engine (on NumPy-backed host tensors)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import shutil
+import subprocess
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import tensorsmith_hip as ts
+from tensorsmith_hip import _lib
+from tensorsmith_hip.amp import _cast_inputs
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "tsattn.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(tsattn_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert len(declared) >= 12
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert sorted(_lib.SIGNATURES) == declared
+    assert lib.tsattn_abi_version() == _lib.ABI_VERSION
+
+
+@pytest.mark.skipif(shutil.which("gcc") is None, reason="gcc unavailable")
+def test_struct_layout_matches_header(tmp_path):
+    src = tmp_path / "layout.c"
+    src.write_text(
+        '#include <stddef.h>\n#include <stdio.h>\n#include "tsattn.h"\n'
+        "int main(void){\n"
+        'printf("%zu %zu %zu\\n", sizeof(tsattn_view), sizeof(tsattn_problem), offsetof(tsattn_problem, scale));\n'
+        'printf("%zu %zu %zu %zu\\n", offsetof(tsattn_problem, causal_offset), offsetof(tsattn_problem, kv_len),'
+        " offsetof(tsattn_problem, mask_kind), offsetof(tsattn_problem, mask));\n"
+        "return 0;}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", str(ROOT / "include"), str(src), "-o", str(exe)], check=True)
+    out = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    P = _lib.Problem
+    want = [ctypes.sizeof(_lib.View), ctypes.sizeof(P), P.scale.offset, P.causal_offset.offset,
+            P.kv_len.offset, P.mask_kind.offset, P.mask.offset]
+    assert [int(x) for x in out] == want
+
+
+def _problem(**kw):
+    p = _lib.Problem()
+    p.dtype, p.batch, p.heads_q, p.heads_kv = _lib.F32, 1, 2, 2
+    p.len_q, p.len_kv, p.dim_qk, p.dim_v, p.scale = 4, 4, 8, 8, 0.5
+    for k, v in kw.items():
+        setattr(p, k, v)
+    return p
+
+
+@pytest.mark.parametrize("field,value,code,text", [
+    ("heads_kv", 3, _lib.ERR_INVALID, "divisible"),
+    ("scale", float("nan"), _lib.ERR_INVALID, "finite"),
+    ("causal_offset", -1, _lib.ERR_INVALID, "offset"),
+    ("len_q", 0, _lib.ERR_INVALID, "nonempty"),
+    ("dtype", 7, _lib.ERR_INVALID, "floating"),
+    ("dim_qk", 1024, _lib.ERR_UNSUPPORTED, "512"),
+])
+def test_abi_rejects_invalid_problems_without_launching(field, value, code, text):
+    lib = _lib.load()
+    p = _problem(**{field: value})
+    view = _lib.View()
+    view.data = 64  # never dereferenced: validation fails first
+    view.stride[3] = 1
+    rc = lib.tsattn_sdpa_forward(ctypes.byref(p), view, view, view, view, None, None)
+    assert rc == code
+    assert text in _lib.last_error()
+    with pytest.raises(NotImplementedError if code == _lib.ERR_UNSUPPORTED else (ValueError, TypeError)):
+        _lib.check(rc, "forward")
+
+
+def test_abi_rejects_null_views_and_small_workspace():
+    lib = _lib.load()
+    p = _problem()
+    v = _lib.View()
+    v.data = 64
+    v.stride[3] = 1
+    assert lib.tsattn_sdpa_forward(ctypes.byref(p), None, v, v, v, None, None) == _lib.ERR_INVALID
+    bad = _lib.View()
+    bad.data = 64
+    bad.stride[3] = 2
+    assert lib.tsattn_sdpa_forward(ctypes.byref(p), bad, v, v, v, None, None) == _lib.ERR_INVALID
+    need = lib.tsattn_sdpa_backward_workspace(ctypes.byref(p))
+    assert need == 2 * 1 * 2 * 4 * 4
+    rc = lib.tsattn_sdpa_backward(ctypes.byref(p), v, v, v, v, v, ctypes.c_void_p(64), v, v, v,
+                                  ctypes.c_void_p(64), need - 1, None)
+    assert rc == _lib.ERR_INVALID and "workspace" in _lib.last_error()
+    assert lib.tsattn_key_mask_lengths(None, 1, 1, 1, 1, None, None, None) == _lib.ERR_INVALID
+
+
+def test_reference_argument_checks_before_device():
+    """The reference's refusals (attention.py:36-62), same exception types."""
+    q = ts.tensor(np.zeros((1, 2, 3, 4), np.float32))
+    A = ts.nn.scaled_dot_product_attention
+    with pytest.raises(ValueError, match="batch, heads"):
+        A(ts.tensor(np.zeros((2, 3, 4), np.float32)), q, q)
+    with pytest.raises(TypeError):
+        A(q, ts.tensor(np.zeros((1, 2, 3, 4), np.float64)), q)
+    with pytest.raises(ValueError, match="grouped-query"):
+        A(ts.tensor(np.zeros((1, 4, 3, 4), np.float32)), q, q)
+    with pytest.raises(ValueError, match="dropout"):
+        A(q, q, q, dropout_p=1.0)
+    with pytest.raises(ValueError, match="offset"):
+        A(q, q, q, causal_offset=-1)
+    with pytest.raises(ValueError, match="backend"):
+        A(q, q, q, backend="flash")
+    with pytest.raises(ValueError, match="finite"):
+        A(q, q, q, scale=float("inf"))
+    with pytest.raises(RuntimeError, match="hip devices only"):
+        A(q, q, q)
+
+
+def test_kvcache_and_mha_validation_on_host():
+    with pytest.raises(ValueError):
+        ts.nn.KVCache(0, 2, 4, 8, device="cpu")
+    with pytest.raises(RuntimeError, match="hip"):
+        ts.nn.KVCache(1, 2, 4, 8, device="cpu")
+    with pytest.raises(ValueError):
+        ts.nn.MultiHeadAttention(10, 3)
+    with pytest.raises(ValueError):
+        ts.nn.MultiHeadAttention(8, 2, backend="flash")
+    m = ts.nn.MultiHeadAttention(8, 2, backend="hip")
+    assert m.head_dim == 4 and len(list(m.parameters())) == 4
+
+
+def test_device_parsing():
+    assert str(ts.device("hip")) == "hip:0" and str(ts.device("hip:3")) == "hip:3"
+    assert ts.device("cpu").type == "cpu"
+    with pytest.raises(ValueError):
+        ts.device("cuda")
+    with pytest.raises(ValueError):
+        ts.Device("cpu", 1)
+
+
+def _fd_check(fn, arrays, upstream, eps=1e-6):
+    tensors = [ts.tensor(a, dtype="float64", requires_grad=True) for a in arrays]
+    (fn(*tensors) * ts.tensor(upstream, dtype="float64")).sum().backward()
+    for t, raw in zip(tensors, arrays):
+        for flat in range(min(raw.size, 6)):
+            pos = np.unravel_index(flat * (raw.size // 6 or 1) % raw.size, raw.shape)
+            orig = raw[pos]
+            raw[pos] = orig + eps
+            hi = (fn(*[ts.tensor(a, dtype="float64") for a in arrays]).numpy() * upstream).sum()
+            raw[pos] = orig - eps
+            lo = (fn(*[ts.tensor(a, dtype="float64") for a in arrays]).numpy() * upstream).sum()
+            raw[pos] = orig
+            assert abs(t.grad.numpy()[pos] - (hi - lo) / (2 * eps)) < 1e-6
+
+
+def test_autograd_engine_vjps_on_host():
+    rng = np.random.default_rng(0)
+    a, b = rng.standard_normal((2, 3, 4)), rng.standard_normal((4, 5))
+    _fd_check(lambda x, y: (x @ y) * 2.0 - 1.0, [a, b], rng.standard_normal((2, 3, 5)))
+    _fd_check(lambda x: (x**3).sum(axis=1, keepdims=True), [a], rng.standard_normal((2, 1, 4)))
+    _fd_check(lambda x: x.permute(2, 0, 1).reshape(4, 6)[1:3] / 3.0, [a],
+              rng.standard_normal((2, 6)))
+    _fd_check(lambda x: ts.cat([x, x * x], dim=1).mean(axis=0), [a], rng.standard_normal((6, 4)))
+
+
+def test_backward_engine_contract():
+    """Contributions sum over branches; the tape frees unless retain_graph."""
+    x = ts.tensor(np.array([1.0, 2.0]), requires_grad=True)
+    y = x * x + x
+    y.sum().backward(retain_graph=True)
+    np.testing.assert_allclose(x.grad.numpy(), [3.0, 5.0])
+    y.sum().backward()
+    np.testing.assert_allclose(x.grad.numpy(), [6.0, 10.0])
+    with pytest.raises(RuntimeError, match="freed"):
+        y.sum().backward()
+    with ts.no_grad():
+        z = x * 2.0
+    assert not z.requires_grad
+
+
+def test_autocast_policy():
+    w = ts.tensor(np.ones((2, 2), np.float32))
+    x64 = ts.tensor(np.ones((2, 2)), dtype="float64")
+    with ts.autocast("cpu"):
+        a, b = _cast_inputs(w, w)
+        assert str(a.dtype) == "float16" and str(b.dtype) == "float16"
+        c, d = _cast_inputs(w, x64)
+        assert str(c.dtype) == "float32"
+    a, _ = _cast_inputs(w, w)
+    assert str(a.dtype) == "float32"
+    with pytest.raises(ValueError):
+        ts.autocast("cpu", dtype="bfloat16")
