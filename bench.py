@@ -53,9 +53,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--decode-steps", type=int, default=50)
-    ap.add_argument("--cpu-heads", type=int, default=16, help="heads in the CPU baseline sample")
+    ap.add_argument("--cpu-batches", type=int, default=4,
+                    help="batch rows (of 16 heads each) in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode"], default="all",
+    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode", "copy"], default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
 
@@ -203,7 +204,7 @@ def cpu_threads():
     return len(os.sched_getaffinity(0))
 
 
-def cpu_baseline(torch, host, dec_host, heads):
+def cpu_baseline(torch, host, dec_host, batches):
     """The NumPy oracle (reference algorithm) on a sample of the same inputs."""
     import numpy as np
 
@@ -212,24 +213,23 @@ def cpu_baseline(torch, host, dec_host, heads):
     def to_np(t):
         return t.float().cpu().numpy()
 
-    # fwd+bwd: batch 0, first `heads` heads, streaming backend, block 64
-    q, k, v, g = (to_np(host[x][:1, :heads]) for x in ("q", "k", "v", "g"))
+    # fwd+bwd: the first `batches` batch rows (all heads), streaming backend, block 64
+    q, k, v, g = (to_np(host[x][:batches]) for x in ("q", "k", "v", "g"))
 
     def run():
         r = A.sdpa(q, k, v, None, True, dtype="bfloat16", backend="streaming", block_size=64)
         r.backward(g)
 
-    run()  # warmup
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
         run()
         times.append(time.perf_counter() - t0)
     med = float(np.median(times))
-    flops = causal_fwd_flops(1, heads, S, D) * 3.5
-    # decode: the reference's dense path on 16 sequences of the decode workload
+    flops = causal_fwd_flops(batches, H, S, D) * 3.5
+    # decode: the reference's dense path on every sequence of the decode workload
     lens = dec_host["lengths"]
-    nseq = 16
+    nseq = DEC_B
     dq = to_np(dec_host["q"][:nseq])
     dk = [to_np(dec_host["k"][b, :, : lens[b]][None]) for b in range(nseq)]
     dv = [to_np(dec_host["v"][b, :, : lens[b]][None]) for b in range(nseq)]
@@ -241,7 +241,7 @@ def cpu_baseline(torch, host, dec_host, heads):
 
     dec()
     dts = []
-    for _ in range(3):
+    for _ in range(5):
         t0 = time.perf_counter()
         dec()
         dts.append(time.perf_counter() - t0)
@@ -249,12 +249,12 @@ def cpu_baseline(torch, host, dec_host, heads):
     cores = cpu_threads()
     return {
         "value": flops / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-        "sample": f"causal fwd+bwd of batch 0, heads 0..{heads - 1} (S=2048 D=128, bf16 values "
-                  f"in fp32), NumPy streaming block 64, median of 3 after 1 warmup: "
+        "sample": f"causal fwd+bwd of batch rows 0..{batches - 1} x {H} heads (S=2048 D=128, "
+                  f"bf16 values in fp32), NumPy streaming block 64, median of 3: "
                   f"{med:.2f} s per sample",
         "decode": {"value": nseq / dmed, "unit": "tokens/s", "cores": cores, "kind": "port",
-                   "sample": f"dense decode of sequences 0..{nseq - 1} (fp16 values in fp32), "
-                             f"median of 3: {dmed:.3f} s"},
+                   "sample": f"dense decode of all {nseq} sequences (fp16 values in fp32), "
+                             f"median of 5 after 1 warmup: {dmed:.3f} s"},
     }
 
 
@@ -272,6 +272,16 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X (no GPU visible)", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "copy":
+        # Calibration for rocprofv3 FETCH_SIZE / WRITE_SIZE: a device copy of
+        # exactly 1 GiB (reads 1 GiB, writes 1 GiB), launched `steps` times.
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(args.steps):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": src.numel() * 4, "launches": args.steps}), flush=True)
+        return
     if args.workload == "decode":
         dec_res, _ = bench_decode(ts, torch, args.decode_steps, args.warmup)
         print(json.dumps({"decode": dec_res}), flush=True)
@@ -290,7 +300,7 @@ def main():
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (NumPy oracle sample)", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(torch, host, dec_host, args.cpu_heads)
+        cpu = cpu_baseline(torch, host, dec_host, args.cpu_batches)
         dec_res["cpu_baseline"] = cpu.pop("decode")
     line = {
         "metric": "attention fwd+bwd TFLOP/s at B16 H16 S2048 D128 bf16; decode tokens/s",

@@ -84,10 +84,13 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
   q.mask.kind = p->mask_kind;
   q.mask.dtype = p->mask_dtype;
   q.mask.data = p->mask.data;
-  q.mask.s0 = p->mask.stride[0];
-  q.mask.s1 = p->mask.stride[1];
-  q.mask.s2 = p->mask.stride[2];
-  q.mask.s3 = p->mask.stride[3];
+  // A stride along a dimension of extent 1 is never applied; zeroing it lets
+  // the kernels recognise a [B,1,1,K] key-padding mask by its strides alone
+  // (e.g. a decode step's query dimension of length 1).
+  q.mask.s0 = p->batch == 1 ? 0 : p->mask.stride[0];
+  q.mask.s1 = p->heads_q == 1 ? 0 : p->mask.stride[1];
+  q.mask.s2 = p->len_q == 1 ? 0 : p->mask.stride[2];
+  q.mask.s3 = p->len_kv == 1 ? 0 : p->mask.stride[3];
   *out = q;
   return TSATTN_OK;
 }

@@ -151,7 +151,7 @@ def scaled_dot_product_attention(
         prob.mask = _view(mask)
         prob.mask.stride[3] = mask.stride(3)
         keep.append(mask)
-        if boolean and mask.stride(1) == 0 and mask.stride(2) == 0:
+        if boolean and all(mask.stride(d) == 0 or mask.shape[d] == 1 for d in (1, 2)):
             # key-padding mask [B,1,1,K]: derive per-row key lengths on device
             lens = torch.empty(2, b, dtype=torch.int32, device=tdev)
             _lib.check(

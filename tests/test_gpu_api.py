@@ -72,6 +72,37 @@ def test_masks_all_masked_rows_and_streaming_parity():
                 np.testing.assert_allclose(a, b, rtol=1e-4, atol=3e-5)
 
 
+@pytest.mark.parametrize("sq", [1, 2])
+def test_key_padding_decode_never_reads_padded_keys(sq):
+    """A [B,1,1,K] boolean padding mask bounds each row at its length: the cache
+    rows past it are never loaded, so NaN there cannot reach the output.
+    (The mask is built as ``m[:, None, None, :]``, whose size-1 dims carry
+    non-zero strides -- the layout a decode step's mask has.)"""
+    dtype = "float16"
+    b, h, cap, d = 4, 4, 1024, 128
+    inp = attention_inputs(b, h, sq, d, dtype, seq_k=cap, with_grad=False, seed=21)
+    lengths = np.array([1024, 700, 130, 515])
+    keymask = np.arange(cap)[None, :] < lengths[:, None]
+    k_pad, v_pad = inp.k.copy(), inp.v.copy()
+    for bi, n in enumerate(lengths):
+        k_pad[bi, :, n:] = np.nan
+        v_pad[bi, :, n:] = np.nan
+    m = torch.from_numpy(keymask).cuda()[:, None, None, :]
+    assert m.stride(1) != 0 and m.stride(2) != 0
+    say(f"key-padding decode sq={sq}")
+    with ts.no_grad():
+        out = ts.nn.scaled_dot_product_attention(
+            T(inp.q, dtype), T(k_pad, dtype), T(v_pad, dtype), ts.Tensor(m, device=HIP))
+    assert _lib.last_kernel_path() == _lib.PATH_DECODE
+    got = out.numpy()
+    assert np.isfinite(got).all()
+    for bi, n in enumerate(lengths):
+        ref = A.sdpa(inp.q[bi:bi + 1], inp.k[bi:bi + 1, :, :n], inp.v[bi:bi + 1, :, :n], None,
+                     False, dtype=dtype, backend="dense")
+        err = rel_l2(got[bi:bi + 1], ref.out)
+        assert err < 2e-3, (bi, err)
+
+
 def test_vjp_central_differences_float64_on_hip():
     """The reference's check_vjp (tests/test_transformer.py:13-33) through the hip kernels."""
     np.random.seed(19)
