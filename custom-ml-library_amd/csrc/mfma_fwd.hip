@@ -3,26 +3,40 @@
 //
 // Algorithm: the reference's streaming forward (src/tensorsmith/nn/
 // attention.py:175-198) -- running max m, denominator l and accumulator per
-// query row, rescaled by exp(m - m') per key tile; O = acc / l; LSE = m +
-// log l; fully masked rows give O = 0, LSE = -inf.
+// query row, rescaled by exp(m - m') when the max moves; O = acc / l;
+// LSE = m + log l; fully masked rows give O = 0, LSE = -inf.
 //
-// Work split: one workgroup = 4 wavefronts = 128 query rows of one (b, h);
-// each wave owns 32 rows.  Key and value tiles of 64 rows are copied global
-// -> LDS by direct buffer loads (no staging registers), double buffered, into
-// swizzled row-major tiles.  The wave computes S^T = K Q^T so that each lane
-// owns one query column: the softmax statistics and the rescale of the
-// accumulator O^T = V^T P^T stay lane-local, and P^T leaves the accumulator
-// registers as the next contraction's B operand without data movement.  The
-// V^T operand is read from the row-major V tile with LDS transpose reads.
+// Work split: one workgroup = 4 wavefronts = 128 query rows of one (b, h),
+// two workgroups per CU; each wave owns 32 rows and computes S^T = K Q^T, so
+// each lane owns one query column: the softmax statistics stay lane-local,
+// and P^T leaves the accumulator registers as the B operand of
+// O^T += V^T P^T.  K is read from LDS as row fragments, V^T with LDS
+// transpose reads.
+//
+// Schedule: per key tile of 32 rows a wave runs one MFMA block -- PV of the
+// previous tile fused with S of the current one, 16 MFMAs at D = 128, the
+// LDS fragments of each step prefetched two steps ahead -- then the softmax
+// of the current tile on the VALU.  The two waves sharing a SIMD belong to
+// different workgroups, so one's MFMA block overlaps the other's softmax.
+// Key/value tiles stream global -> LDS by direct (DMA) buffer loads into a
+// 4-stage ring, issued two tiles ahead; the per-tile barrier is a bare
+// s_barrier (no memory fence), and each wave waits only for the next tile.
+//
+// Rescaling is lazy: the reference max m is raised (and O, l rescaled) only
+// when a row's max exceeds it by more than kTau (in log2 units), so P <= 2^kTau
+// and most tiles skip the rescale.  O / l and the LSE are exact for any m.
 #include "mfma_common.h"
 
 namespace tsattn {
 namespace {
 
 constexpr int BM = 128;  // query rows per workgroup
-constexpr int BN = 64;   // keys per tile
+constexpr int BN = 32;   // keys per tile
 constexpr int NT = 256;  // threads
 constexpr int NW = NT / 64;
+constexpr int PD = 2;    // tiles issued ahead
+constexpr int NS = PD + 2;  // K/V ring stages: tile j is read in iterations j and j + 1
+constexpr float kTau = 8.f;
 
 struct FwdArgs {
   Problem p;
@@ -38,23 +52,125 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
 }
 
+// gfx9 s_waitcnt immediates: vmcnt(n) (0 <= n <= 7) or lgkmcnt(0), the other
+// counters at their maxima.  n is wave-uniform.
+__device__ __forceinline__ void wait_vm(int n) {
+  switch (n) {
+    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
+    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
+    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
+    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
+    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
+    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+  }
+}
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// Workgroup barrier without a memory fence: outstanding global -> LDS loads
+// of later tiles stay in flight.  The scheduler may not move code across it.
+__device__ __forceinline__ void phase_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Buffer descriptor (raw, 32-bit records) as four SGPRs for inline assembly.
+__device__ __forceinline__ u32x4 make_desc(const void *base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, bytes,
+               static_cast<uint32_t>(kRsrcFlags)};
+}
+
+// 16-byte global -> LDS load: lane l's bytes land at LDS address m0 + 16 l.
+// Issued as assembly so that the compiler does not treat later LDS reads as
+// depending on it (it would wait for every such load before each read); the
+// kernel orders these loads itself with s_waitcnt vmcnt + s_barrier.
+// The byte offset is voff (per lane) + soff (wave-uniform).
+__device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+
+// max(x, x of lane l ^ 32) without an LDS round trip: v_permlane32_swap
+// exchanges the upper half of `a` with the lower half of `b`, so afterwards
+// {a, b} holds {own, partner} in every lane.  (Assembly: the compiler builtin
+// returns the same register for both halves when its operands are equal.)
+__device__ __forceinline__ float half_swap_max(float x) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+  return static_cast<uint32_t>(
+      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
+}
+
+// K / V tile layout in LDS: [BN x D] 16-bit elements cut into blocks of 16
+// rows x 4 sixteen-byte chunks (1 KiB), block (r / 16, k / 4) at
+// 1 KiB * ((r / 16) * D/32 + k / 4).  Inside a block, chunk k of row r sits at
+// slot 4 (r % 16) + ((k % 4) ^ ((r / 4) % 4)).  One DMA instruction fills one
+// block (four lanes per 64-byte row segment); K row fragments and V transpose
+// fragments are conflict-free, and every fragment address is one of four
+// per-lane bases plus a compile-time offset.
+template <typename T, int D>
+struct TileReader {
+  static constexpr int QG = D / 32;
+  uint32_t k_even, k_odd, v_lo, v_hi;  // byte offsets within a tile
+
+  __device__ __forceinline__ explicit TileReader(int lane) {
+    const int c = lane & 31, h = lane >> 5, i16 = lane & 15, g = lane >> 4;
+    const int kb = (c >> 4) * QG * 1024 + (c & 15) * 64;
+    k_even = kb + ((h ^ ((c >> 2) & 3)) << 4);
+    k_odd = kb + (((2 + h) ^ ((c >> 2) & 3)) << 4);
+    const int sel = 2 * (g & 1) + ((i16 & 3) >> 1);
+    v_lo = (((4 * h + (i16 >> 2)) * 4 + (sel ^ h)) << 4) + (i16 & 1) * 8;
+    v_hi = (((8 + 4 * h + (i16 >> 2)) * 4 + (sel ^ (h + 2))) << 4) + (i16 & 1) * 8;
+  }
+  // A operand of S^T = K Q^T: rows 32 t + c, columns 16 i + 8 h .. +7.
+  __device__ __forceinline__ u32x4 k_frag(const char *tile, int t, int i) const {
+    return ld16(tile + ((i & 1) ? k_odd : k_even) + (2 * t * QG + (i >> 1)) * 1024);
+  }
+  // A operand of O^T += V^T P^T: V^T rows 32 dt + c (value dims), k-step ks
+  // over keys in the order a C tile hands over (see crow()).
+  __device__ __forceinline__ u32x4 v_frag(const char *tile, int ks, int dt) const {
+    const char *blk = tile + (ks * QG + dt) * 1024;
+    const u32x2 a = ds_read_tr<T>(reinterpret_cast<const T *>(blk + v_lo));
+    const u32x2 b = ds_read_tr<T>(reinterpret_cast<const T *>(blk + v_hi));
+    return u32x4{a[0], a[1], b[0], b[1]};
+  }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
-  constexpr int TILE = BN * D;  // elements per K (or V) tile
-  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][K | V]
+  constexpr int TILE_B = BN * D * 2;        // bytes per K (or V) tile
+  constexpr int NBLK = TILE_B / 1024;       // 1 KiB blocks per tile
+  constexpr int LPT = 2 * NBLK / NW;        // DMA loads per wave per K+V tile
+  constexpr int SKS = D / 16;               // k-steps of S^T = K Q^T
+  constexpr int PDT = D / 32;               // 32-row blocks of O^T
+  constexpr int QG = D / 32;                // 4-chunk groups per row
+  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
+  static_assert(SKS == 2 * PDT, "one S and one PV MFMA per step");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * 2 * TILE_B];  // [stage][K | V]
 
   const Problem &p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, in an SGPR
   const int logical = xcd_remap(blockIdx.x, a.total);
   const int bh = logical / a.n_qblocks;
   const int qb = a.n_qblocks - 1 - (logical - bh * a.n_qblocks);  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
-  const int q0 = qb * BM, qw = q0 + w * 32, qrow = qw + c;
+  const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
 
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
 
-  // Key range of the workgroup (all its rows) and of this wave.
+  // Key tiles of the workgroup (all its rows) and of this wave.
   int64_t lim = kv_end, wlim = kv_end;
   const int last_q = min(q0 + BM, p.Sq) - 1;
   const int last_qw = min(qw + 32, p.Sq) - 1;
@@ -70,110 +186,176 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2;
   const uint32_t vs_b = static_cast<uint32_t>(a.v.s2) * 2;
   const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
-  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
 
   // Q fragments (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8h .. +7].
-  u32x4 qf[D / 16];
+  u32x4 qf[SKS];
 #pragma unroll
-  for (int ks = 0; ks < D / 16; ++ks)
+  for (int ks = 0; ks < SKS; ++ks)
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+  // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
+  // DMA loads below, so a first use of qf inside the main loop would make it
+  // wait there for tiles still in flight.
+#pragma unroll
+  for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]));
 
-  auto issue = [&](int kv0, int stage) {
-    T *kt = lds + stage * 2 * TILE;
-    tile_to_lds<D, BN, NW>(krs, ks_b, kv0, kt, w, lane);
-    tile_to_lds<D, BN, NW>(vrs, vs_b, kv0, kt + TILE, w, lane);
+  const uint32_t lds0 = lds_addr(lds);
+  // DMA of key tile `tile` into its ring stage.  The K and V blocks of a tile
+  // are numbered e = 0 .. 2 NBLK - 1 (K first); wave w loads e = w, w + 8, ...
+  // Block n = (rg, qg) = (n / QG, n % QG); its lane l fetches row 16 rg + l/4,
+  // chunk 4 qg + ((l % 4) ^ ((l / 16) % 4)).  qg = w % QG for all of the
+  // wave's blocks, so the per-lane part of the offset is loop-invariant and
+  // the row part is wave-uniform.
+  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
+  const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
+  const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
+  auto issue = [&](int tile) {
+    const uint32_t st = lds0 + (tile % NS) * 2 * TILE_B;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = w + NW * u;
+      const int n = e < NBLK ? e : e - NBLK;
+      const uint32_t row0 = static_cast<uint32_t>(tile * BN + 16 * (n / QG));
+      if (e < NBLK) dma16(kdesc, st + n * 1024, koff, row0 * ks_b);
+      else dma16(vdesc, st + TILE_B + n * 1024, voff, row0 * vs_b);
+    }
+  };
+  // Loads this wave may leave in flight once tile jn has landed: those of the
+  // (at most PD - 1) later tiles already issued.
+  auto in_flight_after = [&](int jn) {
+    const int later = min(PD - 1, n_tiles - 1 - jn);
+    return later > 0 ? later * LPT : 0;
   };
 
-  f32x16 oacc[D / 32];
+  const TileReader<T, D> rd(lane);
+  f32x16 oacc[PDT];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) oacc[dt] = f32x16{};
+  for (int dt = 0; dt < PDT; ++dt) oacc[dt] = f32x16{};
+  f32x16 s = f32x16{};
+  u32x4 pb[2];  // P^T of the previous tile, packed: B operands of its 2 PV k-steps
   float m = -INFINITY, l = 0.f;
   const float sl = a.sl;
-  const uint8_t *kmask = static_cast<const uint8_t *>(p.mask.data);
+  // This lane's allowed keys are [0, klim) (cache end and causal window),
+  // further thinned by the key mask row kmask_b when there is one.
+  int klim = kv_end;
+  if (p.causal) {
+    const int64_t cl = static_cast<int64_t>(qrow) + p.offset + 1;
+    if (cl < kv_end) klim = cl < 0 ? 0 : static_cast<int>(cl);
+  }
+  const uint8_t *kmask_b =
+      keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
 
   zero_lds<NT>(lds, sizeof(lds), tid);
   __syncthreads();
-  if (n_tiles > 0) issue(0, 0);
-  wait_vmem();
+  for (int t = 0; t < PD && t < n_tiles; ++t) issue(t);
+  wait_vm(in_flight_after(0));
   __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
-    const int stage = it & 1;
-    const int kv0 = it * BN;
-    if (it + 1 < n_tiles) issue(kv0 + BN, stage ^ 1);
+  // MFMA block of key tile j: O^T += V_{j-1}^T P_{j-1}^T and S_j^T = K_j Q^T.
+  // Step i issues S k-step i and PV MFMA i (value block i % PDT, key k-step
+  // i / PDT), so dependent S MFMAs are two issues apart, while the fragments
+  // of step i+1 load.  One code path for every block keeps the accumulators
+  // in place: the first block runs PV with P = 0 (its V stage is still the
+  // zeroed LDS), and past the wave's last tile S is computed and ignored.
+  auto mfma_block = [&](int j) {
+    const char *kt = lds + (j % NS) * 2 * TILE_B;
+    const char *vt = lds + ((j + NS - 1) % NS) * 2 * TILE_B + TILE_B;
+    constexpr int FD = 2;  // fragment prefetch distance, in steps
+    u32x4 kf[FD + 1], vf[FD + 1];
+    auto load = [&](int i) {
+      kf[i % (FD + 1)] = rd.k_frag(kt, 0, i);
+      vf[i % (FD + 1)] = rd.v_frag(vt, i / PDT, i % PDT);
+    };
+    s = f32x16{};
+#pragma unroll
+    for (int i = 0; i < FD; ++i) load(i);
+    // sched_barrier fences keep each step's reads FD steps ahead of its use.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < SKS; ++i) {
+      s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
+      oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
+      if (i + FD < SKS) load(i + FD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-    if (it < w_tiles) {
-      const T *kt = lds + stage * 2 * TILE;
-      const T *vt = kt + TILE;
-      f32x16 s[2] = {f32x16{}, f32x16{}};
+  auto softmax = [&](int j) {
+    const int kv0 = j * BN;
+    float x[16];  // scores of this lane's query row; element i is key kv0 + crow(i, h)
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-          s[t] = mfma32<T>(row_frag<T, D>(kt, t * 32, ks * 16, lane), qf[ks], s[t]);
+    for (int i = 0; i < 16; ++i) x[i] = s[i];
+    const bool edge = (kv0 + BN > kv_end) || keymask ||
+                      (p.causal && static_cast<int64_t>(kv0 + BN - 1) > qw + p.offset);
+    if (edge) {
+      // Key kv0 + 4h + kc(i), kc a compile-time constant.
+      const int lim = klim - kv0 - 4 * h;
+      unsigned kbits = ~0u;
+      if (keymask) {
+        const int key = kv0 + lane;
+        const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+        kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
       }
-
-      const bool edge = (kv0 + BN > kv_end) || keymask ||
-                        (p.causal && static_cast<int64_t>(kv0 + BN - 1) > qw + p.offset);
-      if (edge) {
-        unsigned long long kbits = ~0ull;
-        if (keymask) {
-          const int key = kv0 + lane;
-          const bool ok = key < p.Sk && kmask[b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3];
-          kbits = __ballot(ok);
-        }
-        const int64_t qpos = static_cast<int64_t>(qrow) + p.offset;
-        const bool causal = p.causal != 0;
 #pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const int kk = t * 32 + crow(i, h);
-            const int key = kv0 + kk;
-            const bool ok = (key < kv_end) & (!causal | (qpos >= key)) & (((kbits >> kk) & 1ull) != 0);
-            s[t][i] = ok ? s[t][i] : -INFINITY;
-          }
-        }
+      for (int i = 0; i < 16; ++i) {
+        const int kc = 8 * (i >> 2) + (i & 3);
+        const bool ok = (kc < lim) & (((kbits >> kc) & 1u) != 0);
+        x[i] = ok ? x[i] : -INFINITY;
       }
-
-      float mx = -INFINITY;
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[t][i]);
-      mx = xor32_max(mx);
-      const float m_new = fmaxf(m, mx * sl);
-      const float base = m_new == -INFINITY ? 0.f : m_new;
-      const float corr = fast_exp2(m - base);
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
+    const float mt = half_swap_max(mx) * sl;
+    if (__ballot(mt > m + kTau) != 0ull) {
+      const float m_new = fmaxf(m, mt);
+      const float corr = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
       m = m_new;
       l *= corr;
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt) oacc[dt] *= corr;
-
-      unsigned pb[4][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-          const float p0 = fast_exp2(fmaf(s[t][i], sl, -base));
-          const float p1 = fast_exp2(fmaf(s[t][i + 1], sl, -base));
-          l += p0 + p1;
-          pb[t * 2 + (i >> 3)][(i & 7) >> 1] = pack2<T>(p0, p1);
-        }
-      }
-
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 bf = {pb[ks][0], pb[ks][1], pb[ks][2], pb[ks][3]};
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-          oacc[dt] = mfma32<T>(tr_frag<T, D>(vt, ks * 16, dt * 32, lane), bf, oacc[dt]);
-      }
+      for (int dt = 0; dt < PDT; ++dt) oacc[dt] *= corr;
     }
+    const float base = m == -INFINITY ? 0.f : m;
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = fast_exp2(fmaf(x[i], sl, -base));
+      const float p1 = fast_exp2(fmaf(x[i + 1], sl, -base));
+      l += p0 + p1;  // fp32 sum of the unrounded probabilities, as the reference
+      pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
+    }
+  };
 
-    wait_vmem();
-    __syncthreads();
+  // Iteration j: issue tile j + PD, MFMA block j (PV of tile j - 1, S of tile
+  // j), softmax of tile j, then wait for tile j + 1 and barrier (stage
+  // (j + PD) % NS last held tile j - 2, read up to iteration j - 1).  Each
+  // wave's work is one straight loop, so the accumulators stay in place;
+  // iterations past the wave's last tile only keep the barrier count.
+  auto it_begin = [&](int j) {
+    if (j + PD < n_tiles) issue(j + PD);
+  };
+  auto it_end = [&](int j) {
+    wait_vm(in_flight_after(j + 1));
+    wait_lgkm0();
+    phase_barrier();
+  };
+  int j = 0;
+  if (w_tiles > 0) {
+    pb[0] = pb[1] = u32x4{0, 0, 0, 0};
+    for (; j < w_tiles; ++j) {
+      it_begin(j);
+      mfma_block(j);
+      softmax(j);
+      it_end(j);
+    }
+    it_begin(j);
+    mfma_block(j);  // PV of the last tile
+    it_end(j);
+    ++j;
+  }
+  for (; j <= n_tiles; ++j) {
+    it_begin(j);
+    it_end(j);
   }
 
   const float lt = xor32_sum(l);  // lanes c and c+32 share a query row
@@ -182,7 +364,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   T *op = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
           static_cast<int64_t>(qrow) * a.o.s2;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
+  for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = dt * 32 + g * 8 + h * 4;
