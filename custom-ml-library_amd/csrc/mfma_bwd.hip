@@ -275,26 +275,38 @@ __global__ __launch_bounds__(NTK, 1) void dkdv_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dQ: one workgroup = 128 query rows of one (b, q head); wave w owns 32 rows
-// (Q, dO rows as B operands in registers).  Key tiles of 64 stream through
-// LDS as row-major K and V: row reads feed S^T = K Q^T and dP^T = V dO^T,
-// transpose reads of K feed dQ^T = K^T dS^T.
+// dQ: one workgroup = 128 query rows of one (b, q head), 4 waves x 32 rows,
+// two workgroups per CU; a wave keeps its Q and dO rows as B operands in
+// registers.  Key tiles of 32 rows stream global -> LDS by DMA loads into a
+// 4-stage ring (issued two tiles ahead, blocked layout), one fence-free
+// barrier per tile.  Per tile j a wave runs one MFMA block -- S_j^T = K Q^T
+// and dP_j^T = V dO^T from row fragments, fused with dQ^T += K_{j-1}^T
+// dS_{j-1}^T from column fragments of the previous K tile -- then forms
+// P = exp2(S sl - lse2) and dS = P (dP - delta) on the VALU.
 // ---------------------------------------------------------------------------
 constexpr int QB = 128;  // query rows per workgroup
-constexpr int KT = 64;   // keys per tile
+constexpr int KT = 32;   // keys per tile
+constexpr int DQ_PD = 2;              // tiles issued ahead
+constexpr int DQ_NS = DQ_PD + 2;      // ring stages: tile j is read in iterations j and j + 1
 
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
-  constexpr int TILE = KT * D;
-  __shared__ __attribute__((aligned(1024))) T lds[2 * 2 * TILE];  // [stage][K | V]
+  constexpr int TILE_B = KT * D * 2;   // bytes per K (or V) tile
+  constexpr int NBLK = TILE_B / 1024;  // 1 KiB blocks per tile
+  constexpr int LPT = 2 * NBLK / NW;   // DMA loads per wave per K+V tile
+  constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
+  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
+  static_assert(SKS == 2 * PDT, "one dQ MFMA per step");
+  __shared__ __attribute__((aligned(1024))) char lds[DQ_NS * 2 * TILE_B];  // [stage][K | V]
 
   const Problem &p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_qb = (p.Sq + QB - 1) / QB;
   const int total = n_qb * p.Hq * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   const int bh = logical / n_qb;
-  const int qb = n_qb - 1 - (logical - bh * n_qb);
+  const int qb = n_qb - 1 - (logical - bh * n_qb);  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
   const int q0 = qb * QB, qw = q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);
@@ -310,14 +322,14 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int n_tiles = lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0;
   const int w_tiles = wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0;
 
-  u32x4 qf[D / 16], gf[D / 16];
-  float lse2 = 0.f, delta = 0.f;
+  u32x4 qf[SKS], gf[SKS];
+  float lse2, delta;
   {
     const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
     const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
 #pragma unroll
-    for (int ks = 0; ks < D / 16; ++ks) {
+    for (int ks = 0; ks < SKS; ++ks) {
       qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
       gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
     }
@@ -328,90 +340,152 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     delta = buf_load_f32(drs, static_cast<uint32_t>(qrow) * 4);
     lse2 = buf_load_f32(lrs, static_cast<uint32_t>(qrow) * 4);
   }
+  // Resolve these loads before the DMA loads start (the compiler's vmcnt
+  // waits do not count those).
+#pragma unroll
+  for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
+  asm volatile("" : "+v"(delta), "+v"(lse2));
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
-  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
-  auto issue = [&](int kv0, int stage) {
-    T *kt = lds + stage * 2 * TILE;
-    tile_to_lds<D, KT, NW>(krs, ks_b, kv0, kt, w, lane);
-    tile_to_lds<D, KT, NW>(vrs, vs_b, kv0, kt + TILE, w, lane);
+  const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  const uint32_t lds0 = lds_addr(lds);
+  // Wave w loads blocks e = w, w + 4, ... of the tile (K blocks first, then V):
+  // block n = (n / QG, n % QG), lane l fetches row 16 (n / QG) + l / 4, chunk
+  // 4 (n % QG) + ((l % 4) ^ ((l / 16) % 4)); n % QG = w % QG for all of them.
+  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
+  const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
+  const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
+  auto issue = [&](int tile) {
+    const uint32_t st = lds0 + (tile % DQ_NS) * 2 * TILE_B;
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = w + NW * u;
+      const int n = e < NBLK ? e : e - NBLK;
+      const uint32_t row0 = static_cast<uint32_t>(tile * KT + 16 * (n / QG));
+      if (e < NBLK) dma16(kdesc, st + n * 1024, koff, row0 * ks_b);
+      else dma16(vdesc, st + TILE_B + n * 1024, voff, row0 * vs_b);
+    }
+  };
+  auto in_flight_after = [&](int jn) {
+    const int later = min(DQ_PD - 1, n_tiles - 1 - jn);
+    return later > 0 ? later * LPT : 0;
   };
 
-  f32x16 acc[D / 32];
+  const TileReader<T, D> rd(lane);
+  f32x16 acc[PDT];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) acc[dt] = f32x16{};
+  for (int dt = 0; dt < PDT; ++dt) acc[dt] = f32x16{};
+  f32x16 s = f32x16{}, dp = f32x16{};
+  u32x4 pd[2];  // dS^T of the previous tile, packed: B operands of its 2 k-steps
   const float sl = a.sl;
-  const uint8_t *kmask = static_cast<const uint8_t *>(p.mask.data);
+  int klim = kv_end;
+  if (causal) {
+    const int64_t cl = static_cast<int64_t>(qrow) + p.offset + 1;
+    if (cl < kv_end) klim = cl < 0 ? 0 : static_cast<int>(cl);
+  }
+  const uint8_t *kmask_b =
+      keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
 
   zero_lds<NT>(lds, sizeof(lds), tid);
   __syncthreads();
-  if (n_tiles > 0) issue(0, 0);
-  wait_vmem();
+  for (int t = 0; t < DQ_PD && t < n_tiles; ++t) issue(t);
+  wait_vm(in_flight_after(0));
   __syncthreads();
 
-  for (int it = 0; it < n_tiles; ++it) {
-    const int stage = it & 1;
-    const int kv0 = it * KT;
-    if (it + 1 < n_tiles) issue(kv0 + KT, stage ^ 1);
+  // MFMA block of tile j: S_j^T, dP_j^T (k-step i each) and dQ MFMA i of the
+  // previous tile (value block i % PDT, key k-step i / PDT); fragments two
+  // steps ahead.  One code path for every block keeps the accumulators in
+  // place: the first block multiplies a zeroed stage by dS = 0, and past the
+  // wave's last tile S and dP are computed and ignored.
+  auto mfma_block = [&](int j) {
+    const char *kt = lds + (j % DQ_NS) * 2 * TILE_B;
+    const char *vt = kt + TILE_B;
+    const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * 2 * TILE_B;
+    constexpr int FD = 2;
+    u32x4 kr[FD + 1], vr[FD + 1], kc[FD + 1];
+    auto load = [&](int i) {
+      kr[i % (FD + 1)] = rd.rows(kt, 0, i);
+      vr[i % (FD + 1)] = rd.rows(vt, 0, i);
+      kc[i % (FD + 1)] = rd.cols(kp, i / PDT, i % PDT);
+    };
+    s = f32x16{};
+    dp = f32x16{};
+#pragma unroll
+    for (int i = 0; i < FD; ++i) load(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < SKS; ++i) {
+      s = mfma32<T>(kr[i % (FD + 1)], qf[i], s);
+      dp = mfma32<T>(vr[i % (FD + 1)], gf[i], dp);
+      acc[i % PDT] = mfma32<T>(kc[i % (FD + 1)], pd[i / PDT], acc[i % PDT]);
+      if (i + FD < SKS) load(i + FD);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 
-    if (it < w_tiles) {
-      const T *kt = lds + stage * 2 * TILE;
-      const T *vt = kt + TILE;
-      f32x16 s[2] = {f32x16{}, f32x16{}}, dp[2] = {f32x16{}, f32x16{}};
+  auto grad = [&](int j) {
+    const int kv0 = j * KT;
+    float x[16];
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          s[t] = mfma32<T>(row_frag<T, D>(kt, t * 32, ks * 16, lane), qf[ks], s[t]);
-          dp[t] = mfma32<T>(row_frag<T, D>(vt, t * 32, ks * 16, lane), gf[ks], dp[t]);
-        }
-      }
-      const bool edge = (kv0 + KT > kv_end) || keymask ||
-                        (causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
-      unsigned long long kbits = ~0ull;
-      if (edge && keymask) {
+    for (int i = 0; i < 16; ++i) x[i] = s[i];
+    const bool edge = (kv0 + KT > kv_end) || keymask ||
+                      (causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
+    if (edge) {
+      const int lim_l = klim - kv0 - 4 * h;
+      unsigned kbits = ~0u;
+      if (keymask) {
         const int key = kv0 + lane;
-        kbits = __ballot(key < p.Sk && kmask[b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
-      }
-      const int64_t qpos = static_cast<int64_t>(qrow) + p.offset;
-      unsigned pd[4][4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-#pragma unroll
-        for (int i = 0; i < 16; i += 2) {
-          float ds[2];
-#pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            const int kk = t * 32 + crow(i + e, h);
-            const int key = kv0 + kk;
-            const bool ok = !edge | ((key < kv_end) & (!causal | (qpos >= key)) &
-                                     (((kbits >> kk) & 1ull) != 0));
-            const float ex = fast_exp2(fmaf(s[t][i + e], sl, -lse2));
-            const float pv = ok ? ex : 0.f;
-            ds[e] = pv * (dp[t][i + e] - delta);
-          }
-          pd[t * 2 + (i >> 3)][(i & 7) >> 1] = pack2<T>(ds[0], ds[1]);
-        }
+        const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+        kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
       }
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const u32x4 bd = {pd[ks][0], pd[ks][1], pd[ks][2], pd[ks][3]};
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt)
-          acc[dt] = mfma32<T>(tr_frag<T, D>(kt, ks * 16, dt * 32, lane), bd, acc[dt]);
+      for (int i = 0; i < 16; ++i) {
+        const int kc = 8 * (i >> 2) + (i & 3);
+        const bool ok = (kc < lim_l) & (((kbits >> kc) & 1u) != 0);
+        x[i] = ok ? x[i] : -INFINITY;
       }
     }
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float p0 = fast_exp2(fmaf(x[i], sl, -lse2));
+      const float p1 = fast_exp2(fmaf(x[i + 1], sl, -lse2));
+      pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (dp[i] - delta), p1 * (dp[i + 1] - delta));
+    }
+  };
 
-    wait_vmem();
-    __syncthreads();
+  auto it_begin = [&](int j) {
+    if (j + DQ_PD < n_tiles) issue(j + DQ_PD);
+  };
+  auto it_end = [&](int j) {
+    wait_vm(in_flight_after(j + 1));
+    wait_lgkm0();
+    phase_barrier();
+  };
+  int j = 0;
+  if (w_tiles > 0) {
+    pd[0] = pd[1] = u32x4{0, 0, 0, 0};
+    for (; j < w_tiles; ++j) {
+      it_begin(j);
+      mfma_block(j);
+      grad(j);
+      it_end(j);
+    }
+    it_begin(j);
+    mfma_block(j);  // dQ of the last tile
+    it_end(j);
+    ++j;
+  }
+  for (; j <= n_tiles; ++j) {
+    it_begin(j);
+    it_end(j);
   }
 
   if (qrow >= p.Sq) return;
   T *dqp = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1 + static_cast<int64_t>(qrow) * a.dq.s2;
   const float sc = a.scale;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
+  for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = dt * 32 + g * 8 + h * 4;

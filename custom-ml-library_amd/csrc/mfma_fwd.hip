@@ -52,100 +52,6 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
 }
 
-// gfx9 s_waitcnt immediates: vmcnt(n) (0 <= n <= 7) or lgkmcnt(0), the other
-// counters at their maxima.  n is wave-uniform.
-__device__ __forceinline__ void wait_vm(int n) {
-  switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F77); break;
-  }
-}
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-// Workgroup barrier without a memory fence: outstanding global -> LDS loads
-// of later tiles stay in flight.  The scheduler may not move code across it.
-__device__ __forceinline__ void phase_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
-}
-
-// Buffer descriptor (raw, 32-bit records) as four SGPRs for inline assembly.
-__device__ __forceinline__ u32x4 make_desc(const void *base, uint32_t bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  return u32x4{static_cast<uint32_t>(a), static_cast<uint32_t>(a >> 32) & 0xFFFFu, bytes,
-               static_cast<uint32_t>(kRsrcFlags)};
-}
-
-// 16-byte global -> LDS load: lane l's bytes land at LDS address m0 + 16 l.
-// Issued as assembly so that the compiler does not treat later LDS reads as
-// depending on it (it would wait for every such load before each read); the
-// kernel orders these loads itself with s_waitcnt vmcnt + s_barrier.
-// The byte offset is voff (per lane) + soff (wave-uniform).
-__device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc),
-                 "s"(__builtin_amdgcn_readfirstlane(soff))
-               : "memory", "m0");
-}
-
-// max(x, x of lane l ^ 32) without an LDS round trip: v_permlane32_swap
-// exchanges the upper half of `a` with the lower half of `b`, so afterwards
-// {a, b} holds {own, partner} in every lane.  (Assembly: the compiler builtin
-// returns the same register for both halves when its operands are equal.)
-__device__ __forceinline__ float half_swap_max(float x) {
-  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));
-}
-
-// K / V tile layout in LDS: [BN x D] 16-bit elements cut into blocks of 16
-// rows x 4 sixteen-byte chunks (1 KiB), block (r / 16, k / 4) at
-// 1 KiB * ((r / 16) * D/32 + k / 4).  Inside a block, chunk k of row r sits at
-// slot 4 (r % 16) + ((k % 4) ^ ((r / 4) % 4)).  One DMA instruction fills one
-// block (four lanes per 64-byte row segment); K row fragments and V transpose
-// fragments are conflict-free, and every fragment address is one of four
-// per-lane bases plus a compile-time offset.
-template <typename T, int D>
-struct TileReader {
-  static constexpr int QG = D / 32;
-  uint32_t k_even, k_odd, v_lo, v_hi;  // byte offsets within a tile
-
-  __device__ __forceinline__ explicit TileReader(int lane) {
-    const int c = lane & 31, h = lane >> 5, i16 = lane & 15, g = lane >> 4;
-    const int kb = (c >> 4) * QG * 1024 + (c & 15) * 64;
-    k_even = kb + ((h ^ ((c >> 2) & 3)) << 4);
-    k_odd = kb + (((2 + h) ^ ((c >> 2) & 3)) << 4);
-    const int sel = 2 * (g & 1) + ((i16 & 3) >> 1);
-    v_lo = (((4 * h + (i16 >> 2)) * 4 + (sel ^ h)) << 4) + (i16 & 1) * 8;
-    v_hi = (((8 + 4 * h + (i16 >> 2)) * 4 + (sel ^ (h + 2))) << 4) + (i16 & 1) * 8;
-  }
-  // A operand of S^T = K Q^T: rows 32 t + c, columns 16 i + 8 h .. +7.
-  __device__ __forceinline__ u32x4 k_frag(const char *tile, int t, int i) const {
-    return ld16(tile + ((i & 1) ? k_odd : k_even) + (2 * t * QG + (i >> 1)) * 1024);
-  }
-  // A operand of O^T += V^T P^T: V^T rows 32 dt + c (value dims), k-step ks
-  // over keys in the order a C tile hands over (see crow()).
-  __device__ __forceinline__ u32x4 v_frag(const char *tile, int ks, int dt) const {
-    const char *blk = tile + (ks * QG + dt) * 1024;
-    const u32x2 a = ds_read_tr<T>(reinterpret_cast<const T *>(blk + v_lo));
-    const u32x2 b = ds_read_tr<T>(reinterpret_cast<const T *>(blk + v_hi));
-    return u32x4{a[0], a[1], b[0], b[1]};
-  }
-};
-
 template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   constexpr int TILE_B = BN * D * 2;        // bytes per K (or V) tile
@@ -264,8 +170,8 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     constexpr int FD = 2;  // fragment prefetch distance, in steps
     u32x4 kf[FD + 1], vf[FD + 1];
     auto load = [&](int i) {
-      kf[i % (FD + 1)] = rd.k_frag(kt, 0, i);
-      vf[i % (FD + 1)] = rd.v_frag(vt, i / PDT, i % PDT);
+      kf[i % (FD + 1)] = rd.rows(kt, 0, i);
+      vf[i % (FD + 1)] = rd.cols(vt, i / PDT, i % PDT);
     };
     s = f32x16{};
 #pragma unroll
