@@ -76,29 +76,41 @@ __global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
 
 // ---------------------------------------------------------------------------
 // dK / dV: one workgroup = 128 keys of one (b, kv head), 8 wavefronts.  The
-// workgroup's K and V rows stay in LDS for its whole life (B operands of
-// S = Q K^T and dP = dO V^T); query tiles of 64 rows (all query heads of the
-// group) stream through LDS as row-major Q and dO.  Wave w owns key group
-// kg = w & 3 (32 keys) and query half qh = w >> 2 (32 rows of each tile), so
-// a wave's persistent state is just its dK^T / dV^T accumulators and two
-// waves share each SIMD; the two query halves' partial sums are added
-// through LDS once at the end.  Row reads feed S and dP, transpose reads feed
-// dV^T = dO^T P and dK^T = Q^T dS.
+// workgroup's K and V rows stay in LDS for its whole life (blocked layout,
+// loaded once by DMA); query tiles of 64 rows -- Q, dO and their lse2 /
+// delta values, for every query head of the GQA group -- stream through a
+// 2-stage ring by DMA loads, one fence-free barrier per tile.  Wave w owns
+// key group kg = w % 4 (32 keys) and query half qh = w / 4 (32 rows of each
+// tile), so its persistent state is its dK^T / dV^T accumulators and two
+// waves share each SIMD; the query halves' partial sums are added through
+// LDS at the end.  Per tile a wave computes S = Q K^T and dP = dO V^T from
+// row fragments (16 MFMAs), P and dS on the VALU, then dV^T += dO^T P and
+// dK^T += Q^T dS from column fragments (16 MFMAs); fragments are prefetched
+// two steps ahead.
 // ---------------------------------------------------------------------------
 constexpr int KB = 128;   // keys per workgroup
 constexpr int QT = 64;    // query rows per tile
 constexpr int NTK = 512;  // threads of the dK/dV kernel
 constexpr int NWK = NTK / 64;
+constexpr int KV_NS = 2;  // Q / dO ring stages
 
 template <typename T, int D>
-__global__ __launch_bounds__(NTK, 1) void dkdv_kernel(BwdArgs a) {
-  constexpr int KTILE = KB * D, QTILE = QT * D;
-  __shared__ __attribute__((aligned(1024))) T kv_lds[2 * KTILE];       // K | V of the 128 keys
-  __shared__ __attribute__((aligned(1024))) T qg_lds[2 * 2 * QTILE];   // [stage][Q | dO]
-  __shared__ __attribute__((aligned(16))) float rowv[2][2 * QT];       // [stage][lse2 | delta]
+__global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
+  constexpr int KV_B = KB * D * 2;           // bytes of the K (or V) block
+  constexpr int TILE_B = QT * D * 2;         // bytes of a Q (or dO) tile
+  constexpr int KBLK = KV_B / 1024, NBLK = TILE_B / 1024;
+  constexpr int STAGE_B = 2 * TILE_B + 1024; // Q | dO | lse2 (256 B) delta (256 B), padded
+  constexpr int LPT = 2 * NBLK / NWK;        // Q + dO DMA loads per wave per tile
+  constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
+  static_assert(LPT >= 1 && LPT * NWK == 2 * NBLK, "tile loads must split evenly over the waves");
+  static_assert(2 * KBLK % NWK == 0, "K/V loads must split evenly over the waves");
+  static_assert(SKS == 2 * PDT, "one dV and one dK MFMA per step");
+  __shared__ __attribute__((aligned(1024))) char kv_lds[2 * KV_B];            // K | V
+  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B];
 
   const Problem &p = a.p;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, c = lane & 31, h = lane >> 5;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kg = w & 3, qh = w >> 2;
   const int n_kb = (p.Sk + KB - 1) / KB;
   const int total = n_kb * p.Hkv * p.B;
@@ -118,138 +130,184 @@ __global__ __launch_bounds__(NTK, 1) void dkdv_kernel(BwdArgs a) {
   // Query tiles: only rows that can see a key of this block (causal).
   int q_start = 0;
   if (causal) {
-    int64_t s = static_cast<int64_t>(k0) - p.offset;
-    q_start = s <= 0 ? 0 : static_cast<int>(s < p.Sq ? s : p.Sq);
+    const int64_t s0 = static_cast<int64_t>(k0) - p.offset;
+    q_start = s0 <= 0 ? 0 : static_cast<int>(s0 < p.Sq ? s0 : p.Sq);
     q_start = (q_start / QT) * QT;
   }
   const int n_qt = k0 < kv_end ? (p.Sq - q_start + QT - 1) / QT : 0;
   const int n_iter = n_qt * p.rep;
-  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
 
-  auto issue = [&](int itn, int stage) {
-    const int r = itn / n_qt, q0 = q_start + (itn - r * n_qt) * QT;
-    const int hq = hk * p.rep + r;
-    T *qt = qg_lds + stage * 2 * QTILE;
-    const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
-    const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
-    tile_to_lds<D, QT, NWK>(qrs, qs_b, q0, qt, w, lane);
-    tile_to_lds<D, QT, NWK>(grs, gs_b, q0, qt + QTILE, w, lane);
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
+  const uint32_t kv0 = lds_addr(kv_lds), ring0 = lds_addr(ring);
+  // Blocked layout: block n = (n / QG, n % QG); its lane l fetches row
+  // 16 (n / QG) + l / 4, chunk 4 (n % QG) + ((l % 4) ^ ((l / 16) % 4)).  A
+  // wave's blocks are w, w + 8, ..., all with n % QG = w % QG.
+  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
+  const uint32_t lrow = lane >> 2;
+  const int lpt_w = LPT + (w < 2 ? 1 : 0);  // waves 0 / 1 also load lse2 / delta
+  auto tile_of = [&](int itn, int &hq, int &q0) {
+    const int r = itn / n_qt;
+    hq = hk * p.rep + r;
+    q0 = q_start + (itn - r * n_qt) * QT;
+  };
+  auto issue = [&](int itn) {
+    int hq, q0;
+    tile_of(itn, hq, q0);
+    const uint32_t st = ring0 + (itn % KV_NS) * STAGE_B;
+    const u32x4 qdesc = make_desc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const u32x4 gdesc = make_desc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int e = w + NWK * u;
+      const int n = e < NBLK ? e : e - NBLK;
+      const uint32_t row0 = static_cast<uint32_t>(q0 + 16 * (n / QG));
+      if (e < NBLK) dma16(qdesc, st + n * 1024, lrow * qs_b + lane_chunk * 16, row0 * qs_b);
+      else dma16(gdesc, st + TILE_B + n * 1024, lrow * gs_b + lane_chunk * 16, row0 * gs_b);
+    }
     if (w < 2) {
       const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
-      const rsrc_t rrs = make_rsrc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
-      buf_load4_lds(rrs, &rowv[stage][w == 0 ? 0 : QT], static_cast<uint32_t>(q0 + lane) * 4);
+      const u32x4 rdesc = make_desc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
+      if (lane < QT / 4) dma16(rdesc, st + 2 * TILE_B + w * QT * 4, lane * 16, static_cast<uint32_t>(q0) * 4);
     }
   };
 
-  f32x16 dk_acc[D / 32], dv_acc[D / 32];
+  const TileReader<T, D> rd(lane);
+  f32x16 dk_acc[PDT], dv_acc[PDT];
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
+  for (int dt = 0; dt < PDT; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
   const float sl = a.sl;
-  const T *kt = kv_lds;
-  const T *vt = kv_lds + KTILE;
 
   zero_lds<NTK>(kv_lds, sizeof(kv_lds), tid);
-  zero_lds<NTK>(qg_lds, sizeof(qg_lds), tid);
-  zero_lds<NTK>(rowv, sizeof(rowv), tid);
+  zero_lds<NTK>(ring, sizeof(ring), tid);
   __syncthreads();
   if (n_iter > 0) {
-    const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
-    const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-    const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
-    tile_to_lds<D, KB, NWK>(krs, ks_b, k0, kv_lds, w, lane);
-    tile_to_lds<D, KB, NWK>(vrs, vs_b, k0, kv_lds + KTILE, w, lane);
-    issue(0, 0);
+    const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+    const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+#pragma unroll
+    for (int u = 0; u < 2 * KBLK / NWK; ++u) {
+      const int e = w + NWK * u;
+      const int n = e < KBLK ? e : e - KBLK;
+      const uint32_t row0 = static_cast<uint32_t>(k0 + 16 * (n / QG));
+      if (e < KBLK) dma16(kdesc, kv0 + n * 1024, lrow * ks_b + lane_chunk * 16, row0 * ks_b);
+      else dma16(vdesc, kv0 + KV_B + n * 1024, lrow * vs_b + lane_chunk * 16, row0 * vs_b);
+    }
+    issue(0);
   }
-  wait_vmem();
+  wait_vm(0);
   __syncthreads();
 
+  const char *kt = kv_lds, *vt = kv_lds + KV_B;
   for (int itn = 0; itn < n_iter; ++itn) {
-    const int stage = itn & 1;
-    const int q0 = q_start + (itn % n_qt) * QT;
+    if (itn + 1 < n_iter) issue(itn + 1);
+    const char *qt = ring + (itn % KV_NS) * STAGE_B;
+    const char *gt = qt + TILE_B;
+    const float *rv = reinterpret_cast<const float *>(qt + 2 * TILE_B);
+    int hq, q0;
+    tile_of(itn, hq, q0);
     const int qs = q0 + 32 * qh;  // first query row of this wave's half
-    if (itn + 1 < n_iter) issue(itn + 1, stage ^ 1);
 
-    // Does any (query row of this half tile, key of this wave) pair survive?
-    const bool wave_live = kw < kv_end && qs < p.Sq &&
-                           (!causal || static_cast<int64_t>(qs) + 31 + p.offset >= kw);
-    if (wave_live) {
-      const T *qt = qg_lds + stage * 2 * QTILE;
-      const T *gt = qt + QTILE;
-      const float *ll = rowv[stage];
-      const float *dl = rowv[stage] + QT;
-      const bool edge = (causal && static_cast<int64_t>(qs) + p.offset < kw + 31) ||
-                        kw + 32 > kv_end || qs + 32 > p.Sq || keymask;
-
-      f32x16 sacc = f32x16{}, dpacc = f32x16{};
+    constexpr int FD = 2;
+    // S = Q K^T, dP = dO V^T over this wave's 32 rows x 32 keys:
+    // sacc[e] = S[qs + crow(e, h)][key].  B operands are K / V row fragments.
+    f32x16 sacc = f32x16{}, dpacc = f32x16{};
+    {
+      u32x4 qa[FD + 1], ga[FD + 1], kb_[FD + 1], vb[FD + 1];
+      auto load = [&](int i) {
+        qa[i % (FD + 1)] = rd.rows(qt, qh, i);
+        ga[i % (FD + 1)] = rd.rows(gt, qh, i);
+        kb_[i % (FD + 1)] = rd.rows(kt, kg, i);
+        vb[i % (FD + 1)] = rd.rows(vt, kg, i);
+      };
 #pragma unroll
-      for (int ks = 0; ks < D / 16; ++ks) {
-        sacc = mfma32<T>(row_frag<T, D>(qt, 32 * qh, ks * 16, lane),
-                         row_frag<T, D>(kt, 32 * kg, ks * 16, lane), sacc);
-        dpacc = mfma32<T>(row_frag<T, D>(gt, 32 * qh, ks * 16, lane),
-                          row_frag<T, D>(vt, 32 * kg, ks * 16, lane), dpacc);
-      }
-      // sacc[i] = S[qs + crow(i, h)][key]
-      unsigned pp[2][4], pd[2][4];
+      for (int i = 0; i < FD; ++i) load(i);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int rq = 32 * qh + g * 8 + h * 4;
-        const float4 l4 = *reinterpret_cast<const float4 *>(ll + rq);
-        const float4 d4 = *reinterpret_cast<const float4 *>(dl + rq);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dv4[4] = {d4.x, d4.y, d4.z, d4.w};
-        float pv[4], dsv[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int i = g * 4 + e;
-          const int qrow = q0 + rq + e;
-          const bool ok = !edge | (key_live & (qrow < p.Sq) &
-                                   (!causal | (static_cast<int64_t>(qrow) + p.offset >= key)));
-          const float ex = fast_exp2(fmaf(sacc[i], sl, -lv[e]));
-          pv[e] = ok ? ex : 0.f;
-          dsv[e] = pv[e] * (dpacc[i] - dv4[e]);
-        }
-        const int ks = g >> 1, dw = (g & 1) * 2;
-        pp[ks][dw] = pack2<T>(pv[0], pv[1]);
-        pp[ks][dw + 1] = pack2<T>(pv[2], pv[3]);
-        pd[ks][dw] = pack2<T>(dsv[0], dsv[1]);
-        pd[ks][dw + 1] = pack2<T>(dsv[2], dsv[3]);
-      }
-      // dV^T += dO^T P, dK^T += Q^T dS over this wave's 32 query rows.
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const u32x4 bp = {pp[ks][0], pp[ks][1], pp[ks][2], pp[ks][3]};
-        const u32x4 bd = {pd[ks][0], pd[ks][1], pd[ks][2], pd[ks][3]};
-#pragma unroll
-        for (int dt = 0; dt < D / 32; ++dt) {
-          dv_acc[dt] = mfma32<T>(tr_frag<T, D>(gt, 32 * qh + ks * 16, dt * 32, lane), bp, dv_acc[dt]);
-          dk_acc[dt] = mfma32<T>(tr_frag<T, D>(qt, 32 * qh + ks * 16, dt * 32, lane), bd, dk_acc[dt]);
-        }
+      for (int i = 0; i < SKS; ++i) {
+        sacc = mfma32<T>(qa[i % (FD + 1)], kb_[i % (FD + 1)], sacc);
+        dpacc = mfma32<T>(ga[i % (FD + 1)], vb[i % (FD + 1)], dpacc);
+        if (i + FD < SKS) load(i + FD);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
 
-    wait_vmem();
-    __syncthreads();
+    // P = exp2(S sl - lse2), dS = P (dP - delta); rows crow(e, h) = 8 g + 4 h + e % 4.
+    const bool edge = keymask || kw + 32 > kv_end || qs + 32 > p.Sq ||
+                      (causal && static_cast<int64_t>(qs) + p.offset < kw + 31);
+    int lo = -64, hi = 64;
+    if (edge) {
+      hi = key_live ? p.Sq - qs - 4 * h : -64;
+      if (causal) {
+        const int64_t l0 = static_cast<int64_t>(key) - p.offset - qs - 4 * h;
+        lo = l0 < -64 ? -64 : (l0 > 64 ? 64 : static_cast<int>(l0));
+      }
+    }
+    u32x4 pp[2], pd[2];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 l4 = *reinterpret_cast<const float4 *>(rv + 32 * qh + 8 * g + 4 * h);
+      const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 32 * qh + 8 * g + 4 * h);
+      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+      const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
+      float pv[4], dsv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * g + r, kc = 8 * g + r;
+        const bool ok = (kc >= lo) & (kc < hi);
+        const float ex = fast_exp2(fmaf(sacc[e], sl, -lv[r]));
+        pv[r] = ok ? ex : 0.f;
+        dsv[r] = pv[r] * (dpacc[e] - dl[r]);
+      }
+      pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
+      pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
+      pd[g >> 1][(g & 1) * 2] = pack2<T>(dsv[0], dsv[1]);
+      pd[g >> 1][(g & 1) * 2 + 1] = pack2<T>(dsv[2], dsv[3]);
+    }
+
+    // dV^T += dO^T P, dK^T += Q^T dS over this wave's 32 query rows; step i:
+    // value block i % PDT, query k-step i / PDT (rows 32 qh + 16 (i / PDT) ..).
+    {
+      u32x4 gc[FD + 1], qc[FD + 1];
+      auto load = [&](int i) {
+        gc[i % (FD + 1)] = rd.cols(gt, 2 * qh + i / PDT, i % PDT);
+        qc[i % (FD + 1)] = rd.cols(qt, 2 * qh + i / PDT, i % PDT);
+      };
+#pragma unroll
+      for (int i = 0; i < FD; ++i) load(i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < SKS; ++i) {
+        dv_acc[i % PDT] = mfma32<T>(gc[i % (FD + 1)], pp[i / PDT], dv_acc[i % PDT]);
+        dk_acc[i % PDT] = mfma32<T>(qc[i % (FD + 1)], pd[i / PDT], dk_acc[i % PDT]);
+        if (i + FD < SKS) load(i + FD);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+
+    wait_vm(0);  // the next tile (issued at the top of this iteration)
+    wait_lgkm0();
+    phase_barrier();
   }
 
-  // Add the two query halves through LDS (the tile buffers are free now):
+  // Add the two query halves through LDS (the ring is free now):
   // red[kg][dt][i][lane], one pass for dK, one for dV.
-  float *red = reinterpret_cast<float *>(qg_lds);
-  static_assert(sizeof(qg_lds) >= 4 * (D / 32) * 16 * 64 * sizeof(float), "reduction buffer");
+  float *red = reinterpret_cast<float *>(ring);
+  static_assert(sizeof(ring) >= 4 * PDT * 16 * 64 * sizeof(float), "reduction buffer");
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
     if (qh == 1) {
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) red[((kg * (D / 32) + dt) * 16 + i) * 64 + lane] = acc[dt][i];
+        for (int i = 0; i < 16; ++i) red[((kg * PDT + dt) * 16 + i) * 64 + lane] = acc[dt][i];
     }
     __syncthreads();
     if (qh == 0) {
 #pragma unroll
-      for (int dt = 0; dt < D / 32; ++dt)
+      for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[dt][i] += red[((kg * (D / 32) + dt) * 16 + i) * 64 + lane];
+        for (int i = 0; i < 16; ++i) acc[dt][i] += red[((kg * PDT + dt) * 16 + i) * 64 + lane];
     }
     __syncthreads();
   }
@@ -260,7 +318,7 @@ __global__ __launch_bounds__(NTK, 1) void dkdv_kernel(BwdArgs a) {
   T *dvp = mut<T>(a.dv) + b * a.dv.s0 + hk * a.dv.s1 + static_cast<int64_t>(key) * a.dv.s2;
   const float sc = a.scale;
 #pragma unroll
-  for (int dt = 0; dt < D / 32; ++dt) {
+  for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d = dt * 32 + g * 8 + h * 4;

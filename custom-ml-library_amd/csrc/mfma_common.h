@@ -249,18 +249,38 @@ inline bool aligned16(View v) {
 // loads that the compiler does not order against LDS reads, explicit waits,
 // a fence-free barrier and the blocked K/V tile layout.
 // ---------------------------------------------------------------------------
-// gfx9 s_waitcnt immediates: vmcnt(n) (0 <= n <= 7) or lgkmcnt(0), the other
-// counters at their maxima.  n is wave-uniform.
+// gfx9 s_waitcnt immediates: vmcnt(n) with n in [0, 63] (low 4 bits in
+// [3:0], high 2 bits in [15:14]), expcnt and lgkmcnt at their maxima; or
+// lgkmcnt(0) alone.  n is wave-uniform; counts above 20 are clamped to 20,
+// which waits for more loads than asked (always safe).
+template <int N>
+__device__ __forceinline__ void wait_vm_n() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
 __device__ __forceinline__ void wait_vm(int n) {
   switch (n) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0F70); break;
-    case 1: __builtin_amdgcn_s_waitcnt(0x0F71); break;
-    case 2: __builtin_amdgcn_s_waitcnt(0x0F72); break;
-    case 3: __builtin_amdgcn_s_waitcnt(0x0F73); break;
-    case 4: __builtin_amdgcn_s_waitcnt(0x0F74); break;
-    case 5: __builtin_amdgcn_s_waitcnt(0x0F75); break;
-    case 6: __builtin_amdgcn_s_waitcnt(0x0F76); break;
-    default: __builtin_amdgcn_s_waitcnt(0x0F77); break;
+    case 0: wait_vm_n<0>(); break;
+    case 1: wait_vm_n<1>(); break;
+    case 2: wait_vm_n<2>(); break;
+    case 3: wait_vm_n<3>(); break;
+    case 4: wait_vm_n<4>(); break;
+    case 5: wait_vm_n<5>(); break;
+    case 6: wait_vm_n<6>(); break;
+    case 7: wait_vm_n<7>(); break;
+    case 8: wait_vm_n<8>(); break;
+    case 9: wait_vm_n<9>(); break;
+    case 10: wait_vm_n<10>(); break;
+    case 11: wait_vm_n<11>(); break;
+    case 12: wait_vm_n<12>(); break;
+    case 13: wait_vm_n<13>(); break;
+    case 14: wait_vm_n<14>(); break;
+    case 15: wait_vm_n<15>(); break;
+    case 16: wait_vm_n<16>(); break;
+    case 17: wait_vm_n<17>(); break;
+    case 18: wait_vm_n<18>(); break;
+    case 19: wait_vm_n<19>(); break;
+    case 20: wait_vm_n<20>(); break;
+    default: wait_vm_n<20>(); break;
   }
 }
 __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
