@@ -12,6 +12,8 @@
 // loads (one wave instruction covers 64*16 B of consecutive keys), U such
 // instructions for K and U for V are issued before any is consumed, so every
 // wave keeps 2*U KiB in flight.
+#include <type_traits>
+
 #include "mfma_common.h"
 
 namespace tsattn {
@@ -55,6 +57,35 @@ __device__ __forceinline__ void unpack8(u32x4 x, float *out) {
   const T *e = reinterpret_cast<const T *>(&x);
 #pragma unroll
   for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
+}
+
+// Sum over each aligned group of LPK lanes (the lanes holding one key row).
+// For LPK = 16 (D = 128) a DPP butterfly inside each 16-lane row: quad_perm
+// swaps within quads, then rotations by 4 and 8 lanes; no LDS traffic.
+template <int LPK>
+__device__ __forceinline__ float group_sum(float d) {
+  if constexpr (LPK == 16) {
+    auto dpp = [](float x, int ctrl_sel) {
+      const int v = __builtin_bit_cast(int, x);
+      int r;
+      switch (ctrl_sel) {
+        case 0: r = __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false); break;   // quad_perm [1,0,3,2]
+        case 1: r = __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false); break;   // quad_perm [2,3,0,1]
+        case 2: r = __builtin_amdgcn_update_dpp(0, v, 0x124, 0xF, 0xF, false); break;  // row_ror:4
+        default: r = __builtin_amdgcn_update_dpp(0, v, 0x128, 0xF, 0xF, false); break; // row_ror:8
+      }
+      return __builtin_bit_cast(float, r);
+    };
+    d += dpp(d, 0);
+    d += dpp(d, 1);
+    d += dpp(d, 2);
+    d += dpp(d, 3);
+    return d;
+  } else {
+#pragma unroll
+    for (int x = LPK / 2; x >= 1; x >>= 1) d += __shfl_xor(d, x, 64);
+    return d;
+  }
 }
 
 template <typename T, int D, int R>
@@ -105,73 +136,82 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
   const T *kbase = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1 + dc * 8;
   const T *vbase = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1 + dc * 8;
   const float log2e = kLog2e;
-  for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
-    u32x4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = kb + u * KPI + kg;
-      const bool ok = key < k_stop;
-      kr[u] = ok ? ld16(kbase + static_cast<int64_t>(key) * a.k.s2) : u32x4{0, 0, 0, 0};
-      vr[u] = ok ? ld16(vbase + static_cast<int64_t>(key) * a.v.s2) : u32x4{0, 0, 0, 0};
-    }
-    float s[U][R];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      float kf[8];
-      unpack8<T>(kr[u], kf);
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float d = 0.f;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) d = fmaf(qv[r][e], kf[e], d);
-#pragma unroll
-        for (int x = LPK / 2; x >= 1; x >>= 1) d += __shfl_xor(d, x, 64);
-        s[u][r] = d;
-      }
-    }
-    // masks: invalid keys, causal, user mask (bool or additive, any broadcast)
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int key = kb + u * KPI + kg;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const int i = r % p.Sq;
-        bool ok = key < k_stop && r < a.rows &&
-                  (!p.causal || static_cast<int64_t>(i) + p.offset >= key);
-        if (ok && masked) {
-          const int hq = hk * p.rep + r / p.Sq;
-          const int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
-                             static_cast<int64_t>(key) * p.mask.s3;
-          if (p.mask.kind == TSATTN_MASK_BOOL)
-            ok = static_cast<const uint8_t *>(p.mask.data)[mi] != 0;
-          else
-            s[u][r] += load_additive<float>(p.mask.data, mi, p.mask.dtype) * log2e;
-        }
-        if (!ok) s[u][r] = -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float mb = m[r];
-#pragma unroll
-      for (int u = 0; u < U; ++u) mb = fmaxf(mb, s[u][r]);
-      const float base = mb == -INFINITY ? 0.f : mb;
-      const float corr = fast_exp2(m[r] - base);
-      l[r] *= corr;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[r][e] *= corr;
+  // Keys past k_stop are read from row k_stop - 1 (in bounds, finite) and
+  // masked, so every load is unconditional.  K/V are streamed once: loads
+  // are non-temporal.
+  auto body = [&](auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
+      u32x4 kr[U], vr[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const float pv = fast_exp2(s[u][r] - base);
-        l[r] += pv;
-        float vf[8];
-        unpack8<T>(vr[u], vf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pv, vf[e], acc[r][e]);
+        const int key = min(kb + u * KPI + kg, k_stop - 1);
+        kr[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(kbase + static_cast<int64_t>(key) * a.k.s2));
+        vr[u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4 *>(vbase + static_cast<int64_t>(key) * a.v.s2));
       }
-      m[r] = mb;
+      float s[U][R];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float kf[8];
+        unpack8<T>(kr[u], kf);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) d = fmaf(qv[r][e], kf[e], d);
+          s[u][r] = group_sum<LPK>(d);
+        }
+      }
+      // masks: keys past the split, causal, user mask (bool or additive, any broadcast)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int key = kb + u * KPI + kg;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const int i = r % p.Sq;
+          bool ok = key < k_stop && r < a.rows &&
+                    (!p.causal || static_cast<int64_t>(i) + p.offset >= key);
+          if constexpr (MASKED) {
+            if (ok) {
+              const int hq = hk * p.rep + r / p.Sq;
+              const int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
+                                 static_cast<int64_t>(key) * p.mask.s3;
+              if (p.mask.kind == TSATTN_MASK_BOOL)
+                ok = static_cast<const uint8_t *>(p.mask.data)[mi] != 0;
+              else
+                s[u][r] += load_additive<float>(p.mask.data, mi, p.mask.dtype) * log2e;
+            }
+          }
+          if (!ok) s[u][r] = -INFINITY;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float mb = m[r];
+#pragma unroll
+        for (int u = 0; u < U; ++u) mb = fmaxf(mb, s[u][r]);
+        const float base = mb == -INFINITY ? 0.f : mb;
+        const float corr = fast_exp2(m[r] - base);
+        l[r] *= corr;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[r][e] *= corr;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float pv = fast_exp2(s[u][r] - base);
+          l[r] += pv;
+          float vf[8];
+          unpack8<T>(vr[u], vf);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pv, vf[e], acc[r][e]);
+        }
+        m[r] = mb;
+      }
     }
-  }
+  };
+  if (masked) body(std::true_type{});
+  else body(std::false_type{});
 
   // Merge the key groups of the wave (lanes dc, dc+LPK, ...), then the waves.
 #pragma unroll
@@ -217,6 +257,9 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
 }
 
 // One wave per output row (b, hq, i): combine the splits' partial states.
+// Lane s reads split s's (m, l) so the maxima and the weights exp2(m_s - M)
+// come from one round of loads; the accumulators are then summed over the
+// splits with lane d owning value columns d, d + 64, ...
 template <typename T, int D>
 __global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
   const Problem &p = a.p;
@@ -229,21 +272,38 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
   const float *base = a.ws + (static_cast<int64_t>(b * p.Hkv + hk) * a.max_splits * a.rows + r) *
                                  static_cast<int64_t>(D + 2);
   const int64_t stride = static_cast<int64_t>(a.rows) * (D + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < n; ++s) M = fmaxf(M, base[s * stride + D]);
-  const float mb = M == -INFINITY ? 0.f : M;
   constexpr int PER = (D + 63) / 64;
   float acc[PER] = {};
-  float L = 0.f;
-  for (int s = 0; s < n; ++s) {
-    const float *part = base + s * stride;
-    const float c = fast_exp2(part[D] - mb);
-    L += part[D + 1] * c;
+  float M = -INFINITY, L = 0.f;
+  for (int s0 = 0; s0 < n; s0 += 64) {  // one pass for up to 64 splits
+    const int s = s0 + lane;
+    const float ms = s < n ? base[s * stride + D] : -INFINITY;
+    const float ls = s < n ? base[s * stride + D + 1] : 0.f;
+    float mx = ms;
 #pragma unroll
-    for (int t = 0; t < PER; ++t) {
-      const int d = lane + 64 * t;
-      if (d < D) acc[t] += part[d] * c;
+    for (int x = 32; x >= 1; x >>= 1) mx = fmaxf(mx, __shfl_xor(mx, x, 64));
+    const float M2 = fmaxf(M, mx);
+    const float mb = M2 == -INFINITY ? 0.f : M2;
+    const float cold = fast_exp2(M - mb);  // rescale what earlier passes summed
+    const float cs = s < n ? fast_exp2(ms - mb) : 0.f;
+    float lsum = ls * cs;
+#pragma unroll
+    for (int x = 32; x >= 1; x >>= 1) lsum += __shfl_xor(lsum, x, 64);
+    L = L * cold + lsum;
+#pragma unroll
+    for (int t = 0; t < PER; ++t) acc[t] *= cold;
+    const int cnt = min(64, n - s0);
+#pragma unroll 4
+    for (int u = 0; u < cnt; ++u) {
+      const float c = __shfl(cs, u, 64);
+      const float *part = base + (s0 + u) * stride;
+#pragma unroll
+      for (int t = 0; t < PER; ++t) {
+        const int d = lane + 64 * t;
+        if (d < D) acc[t] = fmaf(part[d], c, acc[t]);
+      }
     }
+    M = M2;
   }
   const float inv = L > 0.f ? 1.f / L : 0.f;
   T *op = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +

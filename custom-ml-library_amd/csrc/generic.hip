@@ -393,24 +393,49 @@ hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, 
 }
 
 // Key-padding mask -> (kv_len, kv_prefix): one wave per batch row.
-__global__ __launch_bounds__(64) void key_mask_lengths_kernel(const uint8_t *mask, int64_t sb,
-                                                              int64_t sk, int K, int32_t *kv_len,
-                                                              int32_t *kv_prefix) {
-  const int b = blockIdx.x, lane = threadIdx.x;
+__global__ __launch_bounds__(256) void key_mask_lengths_kernel(const uint8_t *mask, int64_t sb,
+                                                               int64_t sk, int K, int32_t *kv_len,
+                                                               int32_t *kv_prefix) {
+  typedef unsigned u32x4_t __attribute__((ext_vector_type(4)));
+  __shared__ int red[2][4];
+  const int b = blockIdx.x, t = threadIdx.x;
+  const uint8_t *row = mask + b * sb;
   int last = -1, count = 0;
-  for (int j = lane; j < K; j += 64) {
-    if (mask[b * sb + static_cast<int64_t>(j) * sk]) {
+  int j0 = 0;
+  if (sk == 1 && reinterpret_cast<uintptr_t>(row) % 16 == 0) {
+    // 16 bytes per load; bit 7 of byte i of f is set iff byte i is nonzero.
+    const int nv = K / 16;
+    for (int v = t; v < nv; v += 256) {
+      const u32x4_t x = *reinterpret_cast<const u32x4_t *>(row + 16 * static_cast<int64_t>(v));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const unsigned f = (((x[e] & 0x7F7F7F7Fu) + 0x7F7F7F7Fu) | x[e]) & 0x80808080u;
+        count += __builtin_popcount(f);
+        if (f) last = 16 * v + 4 * e + (31 - __builtin_clz(f)) / 8;
+      }
+    }
+    j0 = nv * 16;
+  }
+  for (int j = j0 + t; j < K; j += 256) {
+    if (row[static_cast<int64_t>(j) * sk]) {
       last = j;
       ++count;
     }
   }
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) {
-    int o = __shfl_xor(last, m, 64);
+    const int o = __shfl_xor(last, m, 64);
     last = last > o ? last : o;
     count += __shfl_xor(count, m, 64);
   }
-  if (lane == 0) {
+  if ((t & 63) == 0) {
+    red[0][t >> 6] = last;
+    red[1][t >> 6] = count;
+  }
+  __syncthreads();
+  if (t == 0) {
+    last = max(max(red[0][0], red[0][1]), max(red[0][2], red[0][3]));
+    count = red[1][0] + red[1][1] + red[1][2] + red[1][3];
     kv_len[b] = last + 1;
     if (kv_prefix) kv_prefix[b] = (count == last + 1) ? 1 : 0;
   }
@@ -418,7 +443,7 @@ __global__ __launch_bounds__(64) void key_mask_lengths_kernel(const uint8_t *mas
 
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st) {
-  { Probe pr_("key_mask_lengths", st); key_mask_lengths_kernel<<<dim3(B), dim3(64), 0, st>>>(mask, sb, sk, K, kv_len, kv_prefix); }
+  { Probe pr_("key_mask_lengths", st); key_mask_lengths_kernel<<<dim3(B), dim3(256), 0, st>>>(mask, sb, sk, K, kv_len, kv_prefix); }
   return hipGetLastError();
 }
 
