@@ -16,6 +16,14 @@ time.  The JSON line also carries
   during the timed steps) against the MI355X dense bf16 MFMA peak;
 * ``decode`` -- KV-cache decode (B=64 H=32 D=128 fp16 cache, lengths
   U[512, 8192]): tokens/s and HBM GB/s with its own roofline;
+* ``prefill`` -- long-context causal prefill with a key-padding mask
+  (B=2 H=32 S=32768 D=128 bf16, valid lengths U[16384, 32768]), forward
+  only: TFLOP/s over the exact unmasked (query, key) pairs and its fraction
+  of the bf16 peak;
+* ``lm_step`` -- a 6-layer decoder LM (d_model 512, 8 heads, FFN 2048 GELU,
+  pre-LayerNorm, learned positions, vocab 32000), fp16 autocast, forward +
+  backward of next-token cross-entropy at batch 8 x 1024 tokens: step time,
+  tokens/s and the share of the step spent in the attention kernels;
 * ``cpu_baseline`` -- the NumPy oracle (a restatement of the reference's
   streaming algorithm) on a bounded sample of the same inputs, on this
   host's cores.
@@ -41,6 +49,11 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
 B, H, S, D = 16, 16, 2048, 128
 DEC_B, DEC_H, DEC_D, DEC_CAP, DEC_LO, DEC_HI = 64, 32, 128, 8192, 512, 8192
+PF_B, PF_H, PF_S, PF_D, PF_LO = 2, 32, 32768, 128, 16384
+LM_LAYERS, LM_DIM, LM_HEADS, LM_FFN, LM_VOCAB, LM_B, LM_S = 6, 512, 8, 2048, 32000, 8, 1024
+ATTN_KERNELS = ("fwd_mfma", "bwd_row_prep", "bwd_dkdv_mfma", "bwd_dq_mfma", "generic_fwd",
+                "generic_bwd_delta", "generic_bwd_dq", "generic_bwd_dkdv", "key_mask_lengths",
+                "decode_split", "decode_merge")
 
 
 def causal_fwd_flops(b, h, s, d):
@@ -56,7 +69,8 @@ def parse():
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="batch rows (of 16 heads each) in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode", "copy"], default="all",
+    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode", "prefill", "lm", "copy"],
+                    default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
 
@@ -192,6 +206,145 @@ def bench_decode(ts, torch, steps, warmup):
     }, {"q": q_raw, "k": k_raw, "v": v_raw, "lengths": lens}
 
 
+def bench_prefill(ts, torch, steps, warmup):
+    """Causal prefill over key-padded sequences; forward only (no grad)."""
+    from tensorsmith_hip import _lib
+
+    gen = torch.Generator(device="cuda").manual_seed(42)
+    shape = (PF_B, PF_H, PF_S, PF_D)
+    q, k, v = ((torch.randn(shape, generator=gen, device="cuda") * 0.5).to(torch.bfloat16)
+               for _ in range(3))
+    lengths = torch.randint(PF_LO, PF_S + 1, (PF_B,), generator=gen, device="cuda")
+    keymask = (torch.arange(PF_S, device="cuda")[None, :] < lengths[:, None])[:, None, None, :]
+    tq, tk, tv = (ts.Tensor(t, device="hip") for t in (q, k, v))
+    tm = ts.Tensor(keymask, device="hip")
+
+    def step():
+        with ts.no_grad():
+            return ts.nn.scaled_dot_product_attention(tq, tk, tv, tm, is_causal=True)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    if _lib.last_kernel_path() != _lib.PATH_MFMA:
+        raise RuntimeError("the MFMA kernel did not run for the prefill workload")
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.profile_enable(False)
+    kernels = _lib.profile_read()
+    # row i (< S) attends keys j <= i with j < L: min(i + 1, L) keys
+    pairs = 0
+    for L in lengths.cpu().tolist():
+        pairs += L * (L + 1) // 2 + (PF_S - L) * L
+    flops = 4.0 * PF_D * PF_H * pairs
+    fwd_ms = kernels["fwd_mfma"][1] / kernels["fwd_mfma"][0]
+    achieved = flops / (fwd_ms * 1e-3) / 1e12
+    return {
+        "ms_per_step": elapsed / steps * 1e3,
+        "value": flops / (elapsed / steps) / 1e12,
+        "unit": "TFLOP/s",
+        "flop_per_step": flops,
+        "kernels": {n: {"launches": c, "mean_ms": round(t / max(c, 1), 4)} for n, (c, t) in kernels.items()},
+        "roofline": {"kernel": "fwd_mfma", "bound": "mfma", "achieved": round(achieved, 1),
+                     "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4)},
+        "config": {"workload": "causal_prefill_keypad_bf16_b2h32s32768d128", "batch": PF_B,
+                   "heads": PF_H, "seq_len": PF_S, "head_dim": PF_D,
+                   "lengths": [int(x) for x in lengths.cpu().tolist()]},
+    }
+
+
+def bench_lm(ts, torch, steps, warmup):
+    """6-layer decoder LM, fp16 autocast, forward + backward, random init."""
+    from tensorsmith_hip import _lib
+
+    nn = ts.nn
+    rng = torch.Generator(device="cuda").manual_seed(42)
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln1, self.ln2 = nn.LayerNorm(LM_DIM, device="hip"), nn.LayerNorm(LM_DIM, device="hip")
+            self.attn = nn.MultiHeadAttention(LM_DIM, LM_HEADS, rotary=False, bias=True, device="hip")
+            self.up = nn.Linear(LM_DIM, LM_FFN, device="hip")
+            self.down = nn.Linear(LM_FFN, LM_DIM, device="hip")
+
+        def forward(self, x):
+            x = x + self.attn(self.ln1(x))
+            return x + self.down(nn.functional.gelu(self.up(self.ln2(x))))
+
+    class LM(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tok = nn.Embedding(LM_VOCAB, LM_DIM, device="hip")
+            self.pos = nn.Embedding(LM_S, LM_DIM, device="hip")
+            self.blocks = [Block() for _ in range(LM_LAYERS)]
+            self.ln = nn.LayerNorm(LM_DIM, device="hip")
+            self.head = nn.Linear(LM_DIM, LM_VOCAB, bias=False, device="hip")
+            for name, prm in self.named_parameters():
+                if not name.split(".")[-2].startswith("ln"):  # LayerNorm keeps gamma 1, beta 0
+                    prm._data.normal_(0.0, 0.02, generator=rng)
+
+        def forward(self, ids):
+            b, s = ids.shape
+            pos = ts.Tensor(torch.arange(s, device="cuda")[None].expand(b, s), device="hip")
+            x = self.tok(ids) + self.pos(pos)
+            for blk in self.blocks:
+                x = blk(x)
+            return self.head(self.ln(x))
+
+    model = LM()
+    ids = ts.Tensor(torch.randint(0, LM_VOCAB, (LM_B, LM_S), generator=rng, device="cuda"), device="hip")
+    tgt = ts.Tensor(torch.randint(0, LM_VOCAB, (LM_B, LM_S), generator=rng, device="cuda"), device="hip")
+
+    def step():
+        for prm in model.parameters():
+            prm.zero_grad()
+        with ts.autocast("hip"):
+            loss = nn.functional.cross_entropy(model(ids), tgt, axis=-1)
+        loss.backward()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        loss = step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.profile_enable(False)
+    kernels = _lib.profile_read()
+    ms = elapsed / steps * 1e3
+    attn_ms = sum(t for n, (c, t) in kernels.items() if n in ATTN_KERNELS) / steps
+    hd = LM_DIM // LM_HEADS
+    attn_flops = causal_fwd_flops(LM_B, LM_HEADS, LM_S, hd) * 3.5 * LM_LAYERS
+    tokens = LM_B * LM_S
+    lin_flops = 6.0 * tokens * LM_LAYERS * (4 * LM_DIM * LM_DIM + 2 * LM_DIM * LM_FFN)
+    head_flops = 6.0 * tokens * LM_DIM * LM_VOCAB
+    return {
+        "ms_per_step": ms,
+        "value": tokens / (ms * 1e-3),
+        "unit": "tokens/s",
+        "loss": float(loss.item()),
+        "attention_ms_per_step": attn_ms,
+        "attention_share": attn_ms / ms,
+        "flop_per_step": attn_flops + lin_flops + head_flops,
+        "attention_flop_per_step": attn_flops,
+        "kernels": {n: {"launches": c, "mean_ms": round(t / max(c, 1), 4)} for n, (c, t) in kernels.items()},
+        "config": {"workload": "decoder_lm_6l_d512_h8_ffn2048_v32000_b8_s1024_fp16_autocast",
+                   "layers": LM_LAYERS, "d_model": LM_DIM, "heads": LM_HEADS, "ffn": LM_FFN,
+                   "vocab": LM_VOCAB, "batch": LM_B, "seq_len": LM_S},
+    }
+
+
 def cpu_threads():
     try:
         from threadpoolctl import threadpool_info
@@ -286,6 +439,12 @@ def main():
         dec_res, _ = bench_decode(ts, torch, args.decode_steps, args.warmup)
         print(json.dumps({"decode": dec_res}), flush=True)
         return
+    if args.workload == "prefill":
+        print(json.dumps({"prefill": bench_prefill(ts, torch, 3, 1)}), flush=True)
+        return
+    if args.workload == "lm":
+        print(json.dumps({"lm_step": bench_lm(ts, torch, 5, 2)}), flush=True)
+        return
     print(f"[bench] fwd+bwd B{B} H{H} S{S} D{D} bf16: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
     main_res, host = bench_fwd_bwd(ts, torch, args.steps, args.warmup)
@@ -297,6 +456,10 @@ def main():
         return
     dec_res, dec_host = bench_decode(ts, torch, args.decode_steps, args.warmup)
     print(f"[bench] decode {dec_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
+    pf_res = bench_prefill(ts, torch, 3, 1)
+    print(f"[bench] prefill {pf_res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
+    lm_res = bench_lm(ts, torch, 5, 2)
+    print(f"[bench] lm step {lm_res['ms_per_step']:.2f} ms", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (NumPy oracle sample)", file=sys.stderr, flush=True)
@@ -322,6 +485,8 @@ def main():
         "kernels": main_res["kernels"],
         "cpu_baseline": cpu,
         "decode": dec_res,
+        "prefill": pf_res,
+        "lm_step": lm_res,
     }
     print(json.dumps(line), flush=True)
 
