@@ -97,6 +97,14 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
 
 size_t acc_size(int dtype) { return dtype == TSATTN_F64 ? sizeof(double) : sizeof(float); }
 
+// The MFMA kernels address each (b, h) slice of a view with 32-bit buffer
+// offsets and a 32-bit range bound: route only 16-byte aligned views whose
+// slice of `len` rows, plus a margin for padded tiles, stays below 2^31 bytes.
+// A zero sequence stride (a broadcast row) would make the range bound zero.
+bool mfma_view_ok(const tsattn::View &v, int64_t len) {
+  return tsattn::aligned16(v) && v.s2 > 0 && (len + 256) * v.s2 * 2 < (int64_t(1) << 31);
+}
+
 }  // namespace
 
 extern "C" {
@@ -124,8 +132,8 @@ int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsa
   hipStream_t st = static_cast<hipStream_t>(stream);
   tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v),
                vo = tsattn::make_view(out);
-  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && tsattn::aligned16(vq) &&
-      tsattn::aligned16(vk) && tsattn::aligned16(vv) && tsattn::aligned16(vo)) {
+  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && mfma_view_ok(vq, pr.Sq) &&
+      mfma_view_ok(vk, pr.Sk) && mfma_view_ok(vv, pr.Sk) && mfma_view_ok(vo, pr.Sq)) {
     g_last_path = 2;
     return hip_status(tsattn::launch_mfma_forward(pr, p->dtype, vq, vk, vv, vo,
                                                   static_cast<float *>(lse), st),
@@ -165,10 +173,10 @@ int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const ts
                vo = tsattn::make_view(out), vg = tsattn::make_view(dout),
                vdq = tsattn::make_view(dq), vdk = tsattn::make_view(dk),
                vdv = tsattn::make_view(dv);
-  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && tsattn::aligned16(vq) &&
-      tsattn::aligned16(vk) && tsattn::aligned16(vv) && tsattn::aligned16(vo) &&
-      tsattn::aligned16(vg) && tsattn::aligned16(vdq) && tsattn::aligned16(vdk) &&
-      tsattn::aligned16(vdv)) {
+  if (g_policy.load() == 0 && tsattn::mfma_supported(pr, p->dtype) && mfma_view_ok(vq, pr.Sq) &&
+      mfma_view_ok(vk, pr.Sk) && mfma_view_ok(vv, pr.Sk) && mfma_view_ok(vo, pr.Sq) &&
+      mfma_view_ok(vg, pr.Sq) && mfma_view_ok(vdq, pr.Sq) && mfma_view_ok(vdk, pr.Sk) &&
+      mfma_view_ok(vdv, pr.Sk)) {
     g_last_path = 2;
     return hip_status(tsattn::launch_mfma_backward(pr, p->dtype, vq, vk, vv, vo, vg,
                                                    static_cast<const float *>(lse), vdq, vdk,

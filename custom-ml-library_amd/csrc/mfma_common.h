@@ -126,8 +126,9 @@ struct TileRegs {
 
 // ---------------------------------------------------------------------------
 // Buffer resources: loads whose byte offset falls past `bytes` return zeros,
-// so ragged tiles need no branches.  Offsets are 32-bit: the host only routes
-// views whose per-head extent fits (mfma_extent_ok).
+// so ragged tiles need no branches.  Offsets are 32-bit: the host routes to
+// these kernels only views whose per-head slice stays below 2^31 bytes
+// (mfma_view_ok in api.hip).
 // ---------------------------------------------------------------------------
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 constexpr int kRsrcFlags = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)

@@ -152,6 +152,27 @@ def test_gqa_and_strided_views_and_dropout_rule():
         ts.nn.scaled_dot_product_attention(*tensors, backend="native", enable_gqa=True)
 
 
+def test_sequence_broadcast_keys_leave_the_mfma_path():
+    """A key/value view with sequence stride 0 (one row broadcast over the
+    sequence) is outside the MFMA kernels' buffer addressing; it must run on
+    the generic kernels and still match the oracle."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal((1, 2, 96, 64)).astype(np.float32)
+    row = rng.standard_normal((1, 2, 1, 64)).astype(np.float32)
+    kv = np.broadcast_to(row, (1, 2, 96, 64))
+    qt = T(q, "bfloat16")
+    dev = qt._data.device
+    kt = ts.Tensor(torch.from_numpy(row).to(dev, torch.bfloat16).expand(1, 2, 96, 64), device=HIP)
+    assert kt._data.stride(2) == 0
+    got = ts.nn.scaled_dot_product_attention(qt, kt, kt, is_causal=True)
+    assert _lib.last_kernel_path() == _lib.PATH_GENERIC
+    bf = lambda a: torch.from_numpy(np.ascontiguousarray(a)).bfloat16().float().numpy()
+    ref = A.sdpa(bf(q), bf(kv), bf(kv), None, True, dtype="float32", backend="dense")
+    np.testing.assert_allclose(got.numpy().astype(np.float32), ref.out, rtol=2e-2, atol=2e-2)
+
+
 def test_backward_is_deterministic():
     """Same inputs -> bitwise identical gradients (checkpoint recompute relies on it)."""
     inp = attention_inputs(2, 4, 333, 128, "bfloat16", value_scale=0.5, seed=2)
