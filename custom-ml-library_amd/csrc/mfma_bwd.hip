@@ -102,6 +102,9 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
   constexpr int STAGE_B = 2 * TILE_B + 1024; // Q | dO | lse2 (256 B) delta (256 B), padded
   constexpr int LPT = 2 * NBLK / NWK;        // Q + dO DMA loads per wave per tile
   constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
+  // workgroups resident per CU: 160 KiB of LDS, at most two by the launch bounds
+  constexpr int kLdsFit = 160 * 1024 / (2 * KV_B + KV_NS * STAGE_B);
+  constexpr int kWgPerCu = kLdsFit < 2 ? kLdsFit : 2;
   static_assert(LPT >= 1 && LPT * NWK == 2 * NBLK, "tile loads must split evenly over the waves");
   static_assert(2 * KBLK % NWK == 0, "K/V loads must split evenly over the waves");
   static_assert(SKS == 2 * PDT, "one dV and one dK MFMA per step");
@@ -115,8 +118,8 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
   const int n_kb = (p.Sk + KB - 1) / KB;
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
-  const int bh = logical / n_kb;
-  const int kb = logical - bh * n_kb;  // early key blocks see the most queries: run them first
+  int bh, kb;  // early key blocks see the most queries: run them first
+  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * kWgPerCu, bh, kb);
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * kg, key = kw + c;
   const int kv_end = kv_end_for(p, b);
@@ -363,8 +366,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int n_qb = (p.Sq + QB - 1) / QB;
   const int total = n_qb * p.Hq * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
-  const int bh = logical / n_qb;
-  const int qb = n_qb - 1 - (logical - bh * n_qb);  // long causal rows first
+  int bh, rank;
+  heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);  // 2 WG per CU
+  const int qb = n_qb - 1 - rank;  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
   const int q0 = qb * QB, qw = q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);

@@ -375,4 +375,21 @@ __device__ __forceinline__ int xcd_remap(int pid, int total) {
   return (pid & 7) * (full >> 3) + (pid >> 3);
 }
 
+// Logical id -> (head slice, work rank).  Heads are taken in groups of G;
+// inside a group the ids walk the ranks from the heaviest (rank 0: the most
+// causal work) down, cycling over the group's heads.  The tail of the grid
+// then holds only light blocks, so greedy dispatch stays near the ideal
+// makespan.  G is the number of heads whose blocks fill one XCD's resident
+// slots (`xcd_slots` = workgroups resident per XCD), so short sequences mix a
+// few heads while long ones keep one head per XCD and its K/V stream in L2.
+__device__ __forceinline__ void heavy_first(int logical, int n_blk, int n_bh, int xcd_slots,
+                                            int &bh, int &rank) {
+  const int G = max(1, xcd_slots / n_blk);
+  const int grp = logical / (G * n_blk);
+  const int in = logical - grp * G * n_blk;
+  const int heads = min(G, n_bh - grp * G);
+  rank = in / heads;
+  bh = grp * G + (in - rank * heads);
+}
+
 }  // namespace tsattn

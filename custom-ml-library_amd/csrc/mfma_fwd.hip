@@ -68,8 +68,9 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave index, in an SGPR
   const int logical = xcd_remap(blockIdx.x, a.total);
-  const int bh = logical / a.n_qblocks;
-  const int qb = a.n_qblocks - 1 - (logical - bh * a.n_qblocks);  // long causal rows first
+  int bh, rank;
+  heavy_first(logical, a.n_qblocks, a.total / a.n_qblocks, 64, bh, rank);  // 2 WG per CU
+  const int qb = a.n_qblocks - 1 - rank;  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
   const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
 
