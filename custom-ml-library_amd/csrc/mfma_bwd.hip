@@ -12,6 +12,8 @@
 //
 // Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
 // transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
+#include <type_traits>
+
 #include "mfma_common.h"
 
 namespace tsattn {
@@ -181,9 +183,8 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
   for (int dt = 0; dt < PDT; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
   const float sl = a.sl;
 
-  zero_lds<NTK>(kv_lds, sizeof(kv_lds), tid);
-  zero_lds<NTK>(ring, sizeof(ring), tid);
-  __syncthreads();
+  // No zeroing: every LDS byte the loop reads is written by a DMA load first
+  // (lanes past a buffer's range write zeros).
   if (n_iter > 0) {
     const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
     const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
@@ -246,26 +247,30 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
       }
     }
     u32x4 pp[2], pd[2];
+    // Interior tiles skip the per-element bounds (three VALU ops each).
+    auto grad = [&](auto masked) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 l4 = *reinterpret_cast<const float4 *>(rv + 32 * qh + 8 * g + 4 * h);
-      const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 32 * qh + 8 * g + 4 * h);
-      const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-      const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
-      float pv[4], dsv[4];
+      for (int g = 0; g < 4; ++g) {
+        const float4 l4 = *reinterpret_cast<const float4 *>(rv + 32 * qh + 8 * g + 4 * h);
+        const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 32 * qh + 8 * g + 4 * h);
+        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
+        const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
+        float pv[4], dsv[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e = 4 * g + r, kc = 8 * g + r;
-        const bool ok = (kc >= lo) & (kc < hi);
-        const float ex = fast_exp2(fmaf(sacc[e], sl, -lv[r]));
-        pv[r] = ok ? ex : 0.f;
-        dsv[r] = pv[r] * (dpacc[e] - dl[r]);
+        for (int r = 0; r < 4; ++r) {
+          const int e = 4 * g + r, kc = 8 * g + r;
+          pv[r] = fast_exp2(fmaf(sacc[e], sl, -lv[r]));
+          if (masked) pv[r] = (kc >= lo) & (kc < hi) ? pv[r] : 0.f;
+          dsv[r] = pv[r] * (dpacc[e] - dl[r]);
+        }
+        pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
+        pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
+        pd[g >> 1][(g & 1) * 2] = pack2<T>(dsv[0], dsv[1]);
+        pd[g >> 1][(g & 1) * 2 + 1] = pack2<T>(dsv[2], dsv[3]);
       }
-      pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
-      pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
-      pd[g >> 1][(g & 1) * 2] = pack2<T>(dsv[0], dsv[1]);
-      pd[g >> 1][(g & 1) * 2 + 1] = pack2<T>(dsv[2], dsv[3]);
-    }
+    };
+    if (edge) grad(std::true_type{});
+    else grad(std::false_type{});
 
     // dV^T += dO^T P, dK^T += Q^T dS over this wave's 32 query rows; step i:
     // value block i % PDT, query k-step i / PDT (rows 32 qh + 16 (i / PDT) ..).
@@ -292,46 +297,74 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
     phase_barrier();
   }
 
-  // Add the two query halves through LDS (the ring is free now):
-  // red[kg][dt][i][lane], one pass for dK, one for dV.
-  float *red = reinterpret_cast<float *>(ring);
-  static_assert(sizeof(ring) >= 4 * PDT * 16 * 64 * sizeof(float), "reduction buffer");
+  // Epilogue.  The loop ended on a barrier after every wave's last LDS read,
+  // so both LDS areas are free.  Slice kg of each holds, per tensor, the
+  // partial dK^T (ring) / dV^T (K/V area) of the qh = 1 wave with that kg as
+  // [dt][g][lane] float4 runs.  The qh = 0 wave adds them to its own, scales,
+  // rounds, and writes the block's rows back into the front of its slice:
+  // key row r (0..31) at r * 2D bytes, 16-byte chunk q at q ^ (r % CPR), the
+  // XOR keeping the row writes off one bank.  Then every thread stores whole
+  // 16-byte chunks of rows, so the global writes are coalesced.
+  constexpr int CPR = D / 8;                                   // 16-byte chunks per row
+  constexpr int SLICE_B = PDT * 4 * 64 * 16;                   // per wave, per tensor
+  static_assert(sizeof(ring) >= 4 * SLICE_B && sizeof(kv_lds) >= 4 * SLICE_B, "epilogue LDS");
+  static_assert(32 * 2 * D <= SLICE_B, "rows fit in a slice");
+  static_assert(KB * CPR % NTK == 0, "store chunks split evenly over the threads");
+  char *slice_k = ring + kg * SLICE_B, *slice_v = kv_lds + kg * SLICE_B;
+  if (qh == 1) {
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
-    if (qh == 1) {
+    for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-      for (int dt = 0; dt < PDT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) red[((kg * PDT + dt) * 16 + i) * 64 + lane] = acc[dt][i];
-    }
-    __syncthreads();
-    if (qh == 0) {
-#pragma unroll
-      for (int dt = 0; dt < PDT; ++dt)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) acc[dt][i] += red[((kg * PDT + dt) * 16 + i) * 64 + lane];
-    }
-    __syncthreads();
+      for (int g = 0; g < 4; ++g) {
+        const int off = ((dt * 4 + g) * 64 + lane) * 16;
+        *reinterpret_cast<float4 *>(slice_k + off) =
+            float4{dk_acc[dt][4 * g], dk_acc[dt][4 * g + 1], dk_acc[dt][4 * g + 2], dk_acc[dt][4 * g + 3]};
+        *reinterpret_cast<float4 *>(slice_v + off) =
+            float4{dv_acc[dt][4 * g], dv_acc[dt][4 * g + 1], dv_acc[dt][4 * g + 2], dv_acc[dt][4 * g + 3]};
+      }
   }
-
-  if (qh != 0 || key >= p.Sk) return;
-  // lane holds dK^T[d = 32 dt + crow(i, h)][key]
-  T *dkp = mut<T>(a.dk) + b * a.dk.s0 + hk * a.dk.s1 + static_cast<int64_t>(key) * a.dk.s2;
-  T *dvp = mut<T>(a.dv) + b * a.dv.s0 + hk * a.dv.s1 + static_cast<int64_t>(key) * a.dv.s2;
-  const float sc = a.scale;
+  __syncthreads();
+  if (qh == 0) {
 #pragma unroll
-  for (int dt = 0; dt < PDT; ++dt) {
+    for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d = dt * 32 + g * 8 + h * 4;
-      *reinterpret_cast<u32x2 *>(dkp + d) =
-          u32x2{pack2<T>(dk_acc[dt][g * 4] * sc, dk_acc[dt][g * 4 + 1] * sc),
-                pack2<T>(dk_acc[dt][g * 4 + 2] * sc, dk_acc[dt][g * 4 + 3] * sc)};
-      *reinterpret_cast<u32x2 *>(dvp + d) =
-          u32x2{pack2<T>(dv_acc[dt][g * 4], dv_acc[dt][g * 4 + 1]),
-                pack2<T>(dv_acc[dt][g * 4 + 2], dv_acc[dt][g * 4 + 3])};
-    }
+      for (int g = 0; g < 4; ++g) {
+        const int off = ((dt * 4 + g) * 64 + lane) * 16;
+        const float4 pk = *reinterpret_cast<const float4 *>(slice_k + off);
+        const float4 pv = *reinterpret_cast<const float4 *>(slice_v + off);
+        dk_acc[dt][4 * g] += pk.x, dk_acc[dt][4 * g + 1] += pk.y;
+        dk_acc[dt][4 * g + 2] += pk.z, dk_acc[dt][4 * g + 3] += pk.w;
+        dv_acc[dt][4 * g] += pv.x, dv_acc[dt][4 * g + 1] += pv.y;
+        dv_acc[dt][4 * g + 2] += pv.z, dv_acc[dt][4 * g + 3] += pv.w;
+      }
+    // lane holds dK^T[d = 32 dt + 8 g + 4 h + r][key row c]: 4 consecutive d
+    const float sc = a.scale;
+#pragma unroll
+    for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+        *reinterpret_cast<u32x2 *>(slice_k + off) =
+            u32x2{pack2<T>(dk_acc[dt][4 * g] * sc, dk_acc[dt][4 * g + 1] * sc),
+                  pack2<T>(dk_acc[dt][4 * g + 2] * sc, dk_acc[dt][4 * g + 3] * sc)};
+        *reinterpret_cast<u32x2 *>(slice_v + off) =
+            u32x2{pack2<T>(dv_acc[dt][4 * g], dv_acc[dt][4 * g + 1]),
+                  pack2<T>(dv_acc[dt][4 * g + 2], dv_acc[dt][4 * g + 3])};
+      }
+  }
+  __syncthreads();
+  T *dkb = mut<T>(a.dk) + b * a.dk.s0 + hk * a.dk.s1;
+  T *dvb = mut<T>(a.dv) + b * a.dv.s0 + hk * a.dv.s1;
+#pragma unroll
+  for (int u = 0; u < KB * CPR / NTK; ++u) {
+    const int idx = u * NTK + tid, row = idx / CPR, q = idx % CPR;
+    const int key_r = k0 + row;
+    if (key_r >= p.Sk) continue;
+    const int rr = row % 32, src = (row / 32) * SLICE_B + rr * 2 * D + ((q ^ (rr % CPR)) * 16);
+    const u32x4 vk = *reinterpret_cast<const u32x4 *>(ring + src);
+    const u32x4 vv = *reinterpret_cast<const u32x4 *>(kv_lds + src);
+    *reinterpret_cast<u32x4 *>(dkb + static_cast<int64_t>(key_r) * a.dk.s2 + q * 8) = vk;
+    *reinterpret_cast<u32x4 *>(dvb + static_cast<int64_t>(key_r) * a.dv.s2 + q * 8) = vv;
   }
 }
 
