@@ -26,7 +26,7 @@ struct BwdArgs {
   Problem p;
   View q, k, v, o, dout, dq, dk, dv;
   const float *lse;
-  float *delta;  // [rows] delta, then [rows] lse2 = safe(lse) * log2(e)
+  float *delta;  // [rows] -delta, then [rows] -safe(lse) / scale
   float sl;      // scale * log2(e)
   float scale;   // final gradient scale
 };
@@ -41,8 +41,10 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
 }
 
 // ---------------------------------------------------------------------------
-// Row pre-pass: delta = rowsum(dO * O) and lse2 = (isfinite(lse) ? lse : 0) *
-// log2(e) -- the reference's safe_lse (attention.py:231) in exp2 units.
+// Row pre-pass: nd = -rowsum(dO * O) = -delta and nl = -(isfinite(lse) ? lse
+// : 0) / scale -- the reference's safe_lse (attention.py:231) in score units.
+// Both are stored negated so the dK/dV kernel can start its S and dP
+// accumulators from them: S + nl = (S scale - lse) / scale, dP + nd = dP - delta.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
 __global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
@@ -70,60 +72,57 @@ __global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
 #pragma unroll
   for (int m = TPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
   if (row < rows && part == 0) {
-    a.delta[row] = s;
+    a.delta[row] = -s;
     const float l = a.lse[row];
-    a.delta[rows + row] = isfinite(l) ? l * kLog2e : 0.f;
+    a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
   }
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV: one workgroup = 128 keys of one (b, kv head), 8 wavefronts.  The
-// workgroup's K and V rows stay in LDS for its whole life (blocked layout,
-// loaded once by DMA); query tiles of 64 rows -- Q, dO and their lse2 /
-// delta values, for every query head of the GQA group -- stream through a
-// 2-stage ring by DMA loads, one fence-free barrier per tile.  Wave w owns
-// key group kg = w % 4 (32 keys) and query half qh = w / 4 (32 rows of each
-// tile), so its persistent state is its dK^T / dV^T accumulators and two
-// waves share each SIMD; the query halves' partial sums are added through
-// LDS at the end.  Per tile a wave computes S = Q K^T and dP = dO V^T from
-// row fragments (16 MFMAs), P and dS on the VALU, then dV^T += dO^T P and
-// dK^T += Q^T dS from column fragments (16 MFMAs); fragments are prefetched
-// two steps ahead.
+// dK / dV: one workgroup = 128 keys of one (b, kv head), 4 wavefronts, two
+// workgroups per CU.  Wave w owns keys k0 + 32 w .. + 31: it holds their K
+// and V row fragments in registers for the workgroup's life, next to its
+// dK^T / dV^T accumulators, so K and V take no LDS and no wave shares an
+// output row.  Query tiles of 32 rows -- Q, dO and their lse2 / delta values,
+// for every query head of the GQA group -- stream through a 3-stage LDS ring
+// by DMA loads issued two tiles ahead (between the first MFMA steps), one
+// fence-free barrier per tile.  Per tile a wave computes S = Q K^T and
+// dP = dO V^T (16 MFMAs, Q / dO row fragments), P and dS on the VALU, then
+// dV^T += dO^T P and dK^T += Q^T dS (16 MFMAs, column fragments).  The two
+// workgroups of a CU are not tied by barriers, so one's VALU phase overlaps
+// the other's MFMA phases, and each hides the other's prologue and epilogue.
 // ---------------------------------------------------------------------------
 constexpr int KB = 128;   // keys per workgroup
-constexpr int QT = 64;    // query rows per tile
-constexpr int NTK = 512;  // threads of the dK/dV kernel
-constexpr int NWK = NTK / 64;
-constexpr int KV_NS = 2;  // Q / dO ring stages
+constexpr int QT = 32;    // query rows per tile
+constexpr int KV_NS = 3;  // Q / dO ring stages
+constexpr int KV_PD = 2;  // tiles in flight
+#ifndef DKDV_FD
+#define DKDV_FD 1
+#endif
 
 template <typename T, int D>
-__global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
-  constexpr int KV_B = KB * D * 2;           // bytes of the K (or V) block
-  constexpr int TILE_B = QT * D * 2;         // bytes of a Q (or dO) tile
-  constexpr int KBLK = KV_B / 1024, NBLK = TILE_B / 1024;
-  constexpr int STAGE_B = 2 * TILE_B + 1024; // Q | dO | lse2 (256 B) delta (256 B), padded
-  constexpr int LPT = 2 * NBLK / NWK;        // Q + dO DMA loads per wave per tile
+__global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
+  constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
+  constexpr int NBLK = TILE_B / 1024;
+  constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | lse2 (QT floats) | delta (QT floats)
+  constexpr int LPT = 2 * NBLK / NW;          // Q + dO DMA loads per wave per tile
   constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
-  // workgroups resident per CU: 160 KiB of LDS, at most two by the launch bounds
-  constexpr int kLdsFit = 160 * 1024 / (2 * KV_B + KV_NS * STAGE_B);
-  constexpr int kWgPerCu = kLdsFit < 2 ? kLdsFit : 2;
-  static_assert(LPT >= 1 && LPT * NWK == 2 * NBLK, "tile loads must split evenly over the waves");
-  static_assert(2 * KBLK % NWK == 0, "K/V loads must split evenly over the waves");
+  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
   static_assert(SKS == 2 * PDT, "one dV and one dK MFMA per step");
-  __shared__ __attribute__((aligned(1024))) char kv_lds[2 * KV_B];            // K | V
+  static_assert(SKS == 2 * LPT, "one tile DMA part per two MFMA steps");
+  static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
   __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int kg = w & 3, qh = w >> 2;
   const int n_kb = (p.Sk + KB - 1) / KB;
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, kb;  // early key blocks see the most queries: run them first
-  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * kWgPerCu, bh, kb);
+  heavy_first(logical, n_kb, p.Hkv * p.B, 64, bh, kb);  // 2 WG per CU
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
-  const int k0 = kb * KB, kw = k0 + 32 * kg, key = kw + c;
+  const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   const bool key_live = key < kv_end &&
@@ -131,6 +130,12 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
                                          [b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
   const bool causal = p.causal != 0;
+  // Causal bounds in 32 bits: this lane's key - offset, and the first tile
+  // row at which every key of the wave is visible (q0 >= q_diag: no mask).
+  const int64_t kd64 = static_cast<int64_t>(key) - p.offset;
+  const int kdiff = kd64 < -(1 << 30) ? -(1 << 30) : static_cast<int>(kd64);
+  const int64_t qd64 = static_cast<int64_t>(kw) + 31 - p.offset;
+  const int q_diag = qd64 < -1 ? -1 : static_cast<int>(qd64);
 
   // Query tiles: only rows that can see a key of this block (causal).
   int q_start = 0;
@@ -144,38 +149,81 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
-  const uint32_t kv0 = lds_addr(kv_lds), ring0 = lds_addr(ring);
+  const uint32_t ring0 = lds_addr(ring);
   // Blocked layout: block n = (n / QG, n % QG); its lane l fetches row
   // 16 (n / QG) + l / 4, chunk 4 (n % QG) + ((l % 4) ^ ((l / 16) % 4)).  A
-  // wave's blocks are w, w + 8, ..., all with n % QG = w % QG.
+  // wave's blocks are w, w + 4, ..., all with n % QG = w % QG.
   const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
   const uint32_t lrow = lane >> 2;
-  const int lpt_w = LPT + (w < 2 ? 1 : 0);  // waves 0 / 1 also load lse2 / delta
   auto tile_of = [&](int itn, int &hq, int &q0) {
     const int r = itn / n_qt;
     hq = hk * p.rep + r;
     q0 = q_start + (itn - r * n_qt) * QT;
   };
-  auto issue = [&](int itn) {
-    int hq, q0;
-    tile_of(itn, hq, q0);
-    const uint32_t st = ring0 + (itn % KV_NS) * STAGE_B;
-    const u32x4 qdesc = make_desc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
-    const u32x4 gdesc = make_desc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
-#pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int e = w + NWK * u;
-      const int n = e < NBLK ? e : e - NBLK;
-      const uint32_t row0 = static_cast<uint32_t>(q0 + 16 * (n / QG));
-      if (e < NBLK) dma16(qdesc, st + n * 1024, lrow * qs_b + lane_chunk * 16, row0 * qs_b);
-      else dma16(gdesc, st + TILE_B + n * 1024, lrow * gs_b + lane_chunk * 16, row0 * gs_b);
-    }
-    if (w < 2) {
-      const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
-      const u32x4 rdesc = make_desc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
-      if (lane < QT / 4) dma16(rdesc, st + 2 * TILE_B + w * QT * 4, lane * 16, static_cast<uint32_t>(q0) * 4);
+  // DMA of tile itn into its ring stage, in LPT + 1 parts: part u < LPT is
+  // this wave's u-th Q / dO block, part LPT the lse2 / delta rows (waves 0, 1).
+  struct TileDma {
+    uint32_t st;
+    int q0, hq;
+    u32x4 qdesc, gdesc;
+  };
+  auto tile_dma = [&](int itn) {
+    TileDma t;
+    tile_of(itn, t.hq, t.q0);
+    t.st = ring0 + (itn % KV_NS) * STAGE_B;
+    t.qdesc = make_desc(head_ptr<T>(a.q, b, t.hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    t.gdesc = make_desc(head_ptr<T>(a.dout, b, t.hq), static_cast<uint32_t>(p.Sq) * gs_b);
+    return t;
+  };
+  // Parts u < QPARTS are Q blocks, the rest dO blocks (a compile-time split).
+  constexpr int QPARTS = NBLK / NW;
+  static_assert(NBLK % NW == 0, "Q and dO blocks split evenly over the waves");
+  const uint32_t qvoff = lrow * qs_b + lane_chunk * 16, gvoff = lrow * gs_b + lane_chunk * 16;
+  // nl (wave 0) / nd (wave 1) rows of the group's first query head
+  const float *rowv = a.delta + (static_cast<int64_t>(b) * p.Hq + hk * p.rep) * p.Sq + (w == 0 ? rows : 0);
+  auto issue_part = [&](const TileDma &t, int u) {
+    if (u < QPARTS) {
+      const int n = w + NW * u;
+      dma16(t.qdesc, t.st + n * 1024, qvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QG)) * qs_b);
+    } else if (u < LPT) {
+      const int n = w + NW * (u - QPARTS);
+      dma16(t.gdesc, t.st + TILE_B + n * 1024, gvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QG)) * gs_b);
+    } else if (w < 2) {
+      const u32x4 rdesc = make_desc(rowv + static_cast<int64_t>(t.hq - hk * p.rep) * p.Sq,
+                                    static_cast<uint32_t>(p.Sq) * 4);
+      // lane * 16, recomputed here rather than held in a register all loop
+      uint32_t loff;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(loff));
+      if (lane < QT / 4)
+        dma16(rdesc, t.st + 2 * TILE_B + w * QT * 4, loff, static_cast<uint32_t>(t.q0) * 4);
     }
   };
+  auto issue = [&](int itn) {
+    const TileDma t = tile_dma(itn);
+#pragma unroll
+    for (int u = 0; u <= LPT; ++u) issue_part(t, u);
+  };
+  // DMA loads this wave may leave in flight once tile itn has landed: those
+  // of the later tiles already issued.
+  const int parts = LPT + (w < 2 ? 1 : 0);
+  auto in_flight_after = [&](int itn) {
+    const int later = min(KV_PD - 1, n_iter - 1 - itn);
+    return later > 0 ? later * parts : 0;
+  };
+
+  // This wave's K / V row fragments (B operands of S = Q K^T, dP = dO V^T):
+  // lane (c, h) holds row key, columns 16 i + 8 h .. +7.  Keys past the cache
+  // end read as zeros.
+  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  u32x4 kf[SKS], vf[SKS];
+#pragma unroll
+  for (int i = 0; i < SKS; ++i) {
+    kf[i] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (16 * i + 8 * h) * 2);
+    vf[i] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (16 * i + 8 * h) * 2);
+  }
 
   const TileReader<T, D> rd(lane);
   f32x16 dk_acc[PDT], dv_acc[PDT];
@@ -185,83 +233,77 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
 
   // No zeroing: every LDS byte the loop reads is written by a DMA load first
   // (lanes past a buffer's range write zeros).
-  if (n_iter > 0) {
-    const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-    const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  for (int t = 0; t < KV_PD && t < n_iter; ++t) issue(t);
+  // The K / V loads were issued first, so this also waits for them; resolve
+  // them here, where the compiler's own vmcnt waits (which do not count the
+  // DMA loads) cannot land inside the loop.
+  wait_vm(n_iter > 0 ? in_flight_after(0) : 0);
 #pragma unroll
-    for (int u = 0; u < 2 * KBLK / NWK; ++u) {
-      const int e = w + NWK * u;
-      const int n = e < KBLK ? e : e - KBLK;
-      const uint32_t row0 = static_cast<uint32_t>(k0 + 16 * (n / QG));
-      if (e < KBLK) dma16(kdesc, kv0 + n * 1024, lrow * ks_b + lane_chunk * 16, row0 * ks_b);
-      else dma16(vdesc, kv0 + KV_B + n * 1024, lrow * vs_b + lane_chunk * 16, row0 * vs_b);
-    }
-    issue(0);
-  }
-  wait_vm(0);
+  for (int i = 0; i < SKS; ++i) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
   __syncthreads();
 
-  const char *kt = kv_lds, *vt = kv_lds + KV_B;
   for (int itn = 0; itn < n_iter; ++itn) {
-    if (itn + 1 < n_iter) issue(itn + 1);
+    // Tile itn + 2 is issued between the S / dP MFMA steps below, so a wave
+    // never stalls on the address unit before its first MFMA.
+    const bool prefetch = itn + KV_PD < n_iter;
+    const TileDma nxt = tile_dma(prefetch ? itn + KV_PD : itn);
     const char *qt = ring + (itn % KV_NS) * STAGE_B;
     const char *gt = qt + TILE_B;
     const float *rv = reinterpret_cast<const float *>(qt + 2 * TILE_B);
     int hq, q0;
     tile_of(itn, hq, q0);
-    const int qs = q0 + 32 * qh;  // first query row of this wave's half
 
-    constexpr int FD = 2;
-    // S = Q K^T, dP = dO V^T over this wave's 32 rows x 32 keys:
-    // sacc[e] = S[qs + crow(e, h)][key].  B operands are K / V row fragments.
-    f32x16 sacc = f32x16{}, dpacc = f32x16{};
+    constexpr int FD = DKDV_FD;
+    // S = Q K^T + nl, dP = dO V^T + nd over the tile's 32 rows x this wave's
+    // 32 keys, the accumulators starting from the rows' nl / nd values:
+    // sacc[e] = (S[q0 + crow(e, h)][key] scale - lse) / scale.
+    f32x16 sacc, dpacc;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 l4 = *reinterpret_cast<const float4 *>(rv + 8 * g + 4 * h);
+      const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 8 * g + 4 * h);
+      sacc[4 * g] = l4.x, sacc[4 * g + 1] = l4.y, sacc[4 * g + 2] = l4.z, sacc[4 * g + 3] = l4.w;
+      dpacc[4 * g] = d4.x, dpacc[4 * g + 1] = d4.y, dpacc[4 * g + 2] = d4.z, dpacc[4 * g + 3] = d4.w;
+    }
     {
-      u32x4 qa[FD + 1], ga[FD + 1], kb_[FD + 1], vb[FD + 1];
+      u32x4 qa[FD + 1], ga[FD + 1];
       auto load = [&](int i) {
-        qa[i % (FD + 1)] = rd.rows(qt, qh, i);
-        ga[i % (FD + 1)] = rd.rows(gt, qh, i);
-        kb_[i % (FD + 1)] = rd.rows(kt, kg, i);
-        vb[i % (FD + 1)] = rd.rows(vt, kg, i);
+        qa[i % (FD + 1)] = rd.rows(qt, 0, i);
+        ga[i % (FD + 1)] = rd.rows(gt, 0, i);
       };
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < SKS; ++i) {
-        sacc = mfma32<T>(qa[i % (FD + 1)], kb_[i % (FD + 1)], sacc);
-        dpacc = mfma32<T>(ga[i % (FD + 1)], vb[i % (FD + 1)], dpacc);
+        sacc = mfma32<T>(qa[i % (FD + 1)], kf[i], sacc);
+        dpacc = mfma32<T>(ga[i % (FD + 1)], vf[i], dpacc);
         if (i + FD < SKS) load(i + FD);
+        if (prefetch && (i & 1)) issue_part(nxt, i >> 1);
+        if (prefetch && i == 0) issue_part(nxt, LPT);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
 
-    // P = exp2(S sl - lse2), dS = P (dP - delta); rows crow(e, h) = 8 g + 4 h + e % 4.
-    const bool edge = keymask || kw + 32 > kv_end || qs + 32 > p.Sq ||
-                      (causal && static_cast<int64_t>(qs) + p.offset < kw + 31);
+    // P = exp2(sacc sl), dS = P dpacc; rows crow(e, h) = 8 g + 4 h + e % 4.
+    const bool edge = keymask || kw + 32 > kv_end || q0 + QT > p.Sq || (causal && q0 < q_diag);
     int lo = -64, hi = 64;
     if (edge) {
-      hi = key_live ? p.Sq - qs - 4 * h : -64;
-      if (causal) {
-        const int64_t l0 = static_cast<int64_t>(key) - p.offset - qs - 4 * h;
-        lo = l0 < -64 ? -64 : (l0 > 64 ? 64 : static_cast<int>(l0));
-      }
+      hi = key_live ? p.Sq - q0 - 4 * h : -64;
+      if (causal) lo = min(64, max(-64, kdiff - q0 - 4 * h));
     }
     u32x4 pp[2], pd[2];
     // Interior tiles skip the per-element bounds (three VALU ops each).
     auto grad = [&](auto masked) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const float4 l4 = *reinterpret_cast<const float4 *>(rv + 32 * qh + 8 * g + 4 * h);
-        const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 32 * qh + 8 * g + 4 * h);
-        const float lv[4] = {l4.x, l4.y, l4.z, l4.w};
-        const float dl[4] = {d4.x, d4.y, d4.z, d4.w};
         float pv[4], dsv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int e = 4 * g + r, kc = 8 * g + r;
-          pv[r] = fast_exp2(fmaf(sacc[e], sl, -lv[r]));
+          pv[r] = fast_exp2(sacc[e] * sl);
           if (masked) pv[r] = (kc >= lo) & (kc < hi) ? pv[r] : 0.f;
-          dsv[r] = pv[r] * (dpacc[e] - dl[r]);
+          dsv[r] = pv[r] * dpacc[e];
         }
         pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
         pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
@@ -272,13 +314,13 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
     if (edge) grad(std::true_type{});
     else grad(std::false_type{});
 
-    // dV^T += dO^T P, dK^T += Q^T dS over this wave's 32 query rows; step i:
-    // value block i % PDT, query k-step i / PDT (rows 32 qh + 16 (i / PDT) ..).
+    // dV^T += dO^T P, dK^T += Q^T dS over the tile's rows; step i: value
+    // block i % PDT, query k-step i / PDT (rows 16 (i / PDT) ..).
     {
       u32x4 gc[FD + 1], qc[FD + 1];
       auto load = [&](int i) {
-        gc[i % (FD + 1)] = rd.cols(gt, 2 * qh + i / PDT, i % PDT);
-        qc[i % (FD + 1)] = rd.cols(qt, 2 * qh + i / PDT, i % PDT);
+        gc[i % (FD + 1)] = rd.cols(gt, i / PDT, i % PDT);
+        qc[i % (FD + 1)] = rd.cols(qt, i / PDT, i % PDT);
       };
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
@@ -292,79 +334,44 @@ __global__ __launch_bounds__(NTK, 2) void dkdv_kernel(BwdArgs a) {
       }
     }
 
-    wait_vm(0);  // the next tile (issued at the top of this iteration)
+    wait_vm(in_flight_after(itn + 1));  // tile itn + 1 has landed
     wait_lgkm0();
     phase_barrier();
   }
 
   // Epilogue.  The loop ended on a barrier after every wave's last LDS read,
-  // so both LDS areas are free.  Slice kg of each holds, per tensor, the
-  // partial dK^T (ring) / dV^T (K/V area) of the qh = 1 wave with that kg as
-  // [dt][g][lane] float4 runs.  The qh = 0 wave adds them to its own, scales,
-  // rounds, and writes the block's rows back into the front of its slice:
-  // key row r (0..31) at r * 2D bytes, 16-byte chunk q at q ^ (r % CPR), the
-  // XOR keeping the row writes off one bank.  Then every thread stores whole
-  // 16-byte chunks of rows, so the global writes are coalesced.
-  constexpr int CPR = D / 8;                                   // 16-byte chunks per row
-  constexpr int SLICE_B = PDT * 4 * 64 * 16;                   // per wave, per tensor
-  static_assert(sizeof(ring) >= 4 * SLICE_B && sizeof(kv_lds) >= 4 * SLICE_B, "epilogue LDS");
-  static_assert(32 * 2 * D <= SLICE_B, "rows fit in a slice");
-  static_assert(KB * CPR % NTK == 0, "store chunks split evenly over the threads");
-  char *slice_k = ring + kg * SLICE_B, *slice_v = kv_lds + kg * SLICE_B;
-  if (qh == 1) {
+  // so the ring is free.  Each wave rounds its rows and stages them in its own
+  // slice of the ring -- key row r (0..31) at r * 2D bytes, 16-byte chunk q
+  // at q ^ (r % CPR), the XOR keeping the row writes off one bank -- then
+  // reads them back as whole 16-byte chunks of rows, so the global stores are
+  // coalesced.  dK first, then dV through the same slice.
+  constexpr int CPR = D / 8;  // 16-byte chunks per row
+  static_assert(NW * 32 * 2 * D <= KV_NS * STAGE_B, "epilogue slices fit in the ring");
+  static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
+  char *slice = ring + w * 32 * 2 * D;
+  const float sc = a.scale;
 #pragma unroll
-    for (int dt = 0; dt < PDT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int off = ((dt * 4 + g) * 64 + lane) * 16;
-        *reinterpret_cast<float4 *>(slice_k + off) =
-            float4{dk_acc[dt][4 * g], dk_acc[dt][4 * g + 1], dk_acc[dt][4 * g + 2], dk_acc[dt][4 * g + 3]};
-        *reinterpret_cast<float4 *>(slice_v + off) =
-            float4{dv_acc[dt][4 * g], dv_acc[dt][4 * g + 1], dv_acc[dt][4 * g + 2], dv_acc[dt][4 * g + 3]};
-      }
-  }
-  __syncthreads();
-  if (qh == 0) {
-#pragma unroll
-    for (int dt = 0; dt < PDT; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int off = ((dt * 4 + g) * 64 + lane) * 16;
-        const float4 pk = *reinterpret_cast<const float4 *>(slice_k + off);
-        const float4 pv = *reinterpret_cast<const float4 *>(slice_v + off);
-        dk_acc[dt][4 * g] += pk.x, dk_acc[dt][4 * g + 1] += pk.y;
-        dk_acc[dt][4 * g + 2] += pk.z, dk_acc[dt][4 * g + 3] += pk.w;
-        dv_acc[dt][4 * g] += pv.x, dv_acc[dt][4 * g + 1] += pv.y;
-        dv_acc[dt][4 * g + 2] += pv.z, dv_acc[dt][4 * g + 3] += pv.w;
-      }
-    // lane holds dK^T[d = 32 dt + 8 g + 4 h + r][key row c]: 4 consecutive d
-    const float sc = a.scale;
+  for (int pass = 0; pass < 2; ++pass) {
+    const f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
+    const float f = pass == 0 ? sc : 1.f;
+    // lane holds X^T[d = 32 dt + 8 g + 4 h + r][key row c]: 4 consecutive d
 #pragma unroll
     for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
-        *reinterpret_cast<u32x2 *>(slice_k + off) =
-            u32x2{pack2<T>(dk_acc[dt][4 * g] * sc, dk_acc[dt][4 * g + 1] * sc),
-                  pack2<T>(dk_acc[dt][4 * g + 2] * sc, dk_acc[dt][4 * g + 3] * sc)};
-        *reinterpret_cast<u32x2 *>(slice_v + off) =
-            u32x2{pack2<T>(dv_acc[dt][4 * g], dv_acc[dt][4 * g + 1]),
-                  pack2<T>(dv_acc[dt][4 * g + 2], dv_acc[dt][4 * g + 3])};
+        *reinterpret_cast<u32x2 *>(slice + off) =
+            u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
+                  pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
       }
-  }
-  __syncthreads();
-  T *dkb = mut<T>(a.dk) + b * a.dk.s0 + hk * a.dk.s1;
-  T *dvb = mut<T>(a.dv) + b * a.dv.s0 + hk * a.dv.s1;
+    const View &ov = pass == 0 ? a.dk : a.dv;
+    T *ob = mut<T>(ov) + b * ov.s0 + hk * ov.s1;
 #pragma unroll
-  for (int u = 0; u < KB * CPR / NTK; ++u) {
-    const int idx = u * NTK + tid, row = idx / CPR, q = idx % CPR;
-    const int key_r = k0 + row;
-    if (key_r >= p.Sk) continue;
-    const int rr = row % 32, src = (row / 32) * SLICE_B + rr * 2 * D + ((q ^ (rr % CPR)) * 16);
-    const u32x4 vk = *reinterpret_cast<const u32x4 *>(ring + src);
-    const u32x4 vv = *reinterpret_cast<const u32x4 *>(kv_lds + src);
-    *reinterpret_cast<u32x4 *>(dkb + static_cast<int64_t>(key_r) * a.dk.s2 + q * 8) = vk;
-    *reinterpret_cast<u32x4 *>(dvb + static_cast<int64_t>(key_r) * a.dv.s2 + q * 8) = vv;
+    for (int u = 0; u < 32 * CPR / 64; ++u) {
+      const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+      const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+      if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr;
+    }
   }
 }
 
@@ -440,6 +447,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
   asm volatile("" : "+v"(delta), "+v"(lse2));
+  lse2 *= a.sl;  // -lse in exp2 units; delta holds -delta
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
   const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
@@ -543,9 +551,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = fast_exp2(fmaf(x[i], sl, -lse2));
-      const float p1 = fast_exp2(fmaf(x[i + 1], sl, -lse2));
-      pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (dp[i] - delta), p1 * (dp[i + 1] - delta));
+      const float p0 = fast_exp2(fmaf(x[i], sl, lse2));
+      const float p1 = fast_exp2(fmaf(x[i + 1], sl, lse2));
+      pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (dp[i] + delta), p1 * (dp[i + 1] + delta));
     }
   };
 
@@ -598,7 +606,7 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
   constexpr int RPB = NT / (D / 8);
   { Probe pr_("bwd_row_prep", st); row_prep_kernel<T, D><<<dim3((rows + RPB - 1) / RPB), dim3(NT), 0, st>>>(a); }
   const int n_kb = (p.Sk + KB - 1) / KB;
-  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NTK), 0, st>>>(a); }
+  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
   const int n_qb = (p.Sq + QB - 1) / QB;
   { Probe pr_("bwd_dq_mfma", st); dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a); }
   return hipGetLastError();
