@@ -19,8 +19,10 @@
 // of the current tile on the VALU.  The two waves sharing a SIMD belong to
 // different workgroups, so one's MFMA block overlaps the other's softmax.
 // Key/value tiles stream global -> LDS by direct (DMA) buffer loads into a
-// 4-stage ring, issued two tiles ahead; the per-tile barrier is a bare
-// s_barrier (no memory fence), and each wave waits only for the next tile.
+// 4-stage ring, issued two tiles ahead and spread over the steps of the
+// MFMA block (issuing them all at once stalls every wave on the shared
+// address unit); the per-tile barrier is a bare s_barrier (no memory fence),
+// and each wave waits only for the next tile.
 //
 // Rescaling is lazy: the reference max m is raised (and O, l rescaled) only
 // when a row's max exceeds it by more than kTau (in log2 units), so P <= 2^kTau
@@ -117,16 +119,22 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
   const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
   const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
-  auto issue = [&](int tile) {
+  // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
+  constexpr int KPARTS = NBLK / NW;
+  static_assert(NBLK % NW == 0 && SKS == 2 * LPT, "one DMA part per two MFMA steps");
+  auto issue_part = [&](int tile, int u) {
     const uint32_t st = lds0 + (tile % NS) * 2 * TILE_B;
-#pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int e = w + NW * u;
-      const int n = e < NBLK ? e : e - NBLK;
-      const uint32_t row0 = static_cast<uint32_t>(tile * BN + 16 * (n / QG));
-      if (e < NBLK) dma16(kdesc, st + n * 1024, koff, row0 * ks_b);
-      else dma16(vdesc, st + TILE_B + n * 1024, voff, row0 * vs_b);
+    if (u < KPARTS) {
+      const int n = w + NW * u;
+      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * BN + 16 * (n / QG)) * ks_b);
+    } else {
+      const int n = w + NW * (u - KPARTS);
+      dma16(vdesc, st + TILE_B + n * 1024, voff, static_cast<uint32_t>(tile * BN + 16 * (n / QG)) * vs_b);
     }
+  };
+  auto issue = [&](int tile) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) issue_part(tile, u);
   };
   // Loads this wave may leave in flight once tile jn has landed: those of the
   // (at most PD - 1) later tiles already issued.
@@ -153,7 +161,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
 
-  zero_lds<NT>(lds, sizeof(lds), tid);
+  // The first MFMA block runs PV with P = 0 against the V half of stage
+  // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
+  // Every other LDS byte is written by a DMA load before it is read (lanes
+  // past the buffer range write zeros).
+  zero_lds<NT>(lds + (NS - 1) * 2 * TILE_B + TILE_B, TILE_B, tid);
   __syncthreads();
   for (int t = 0; t < PD && t < n_tiles; ++t) issue(t);
   wait_vm(in_flight_after(0));
@@ -165,7 +177,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // of step i+1 load.  One code path for every block keeps the accumulators
   // in place: the first block runs PV with P = 0 (its V stage is still the
   // zeroed LDS), and past the wave's last tile S is computed and ignored.
-  auto mfma_block = [&](int j) {
+  auto mfma_block = [&](int j, int nt) {  // nt: tile whose DMA to issue, or -1
     const char *kt = lds + (j % NS) * 2 * TILE_B;
     const char *vt = lds + ((j + NS - 1) % NS) * 2 * TILE_B + TILE_B;
     constexpr int FD = 2;  // fragment prefetch distance, in steps
@@ -184,6 +196,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
       oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
       if (i + FD < SKS) load(i + FD);
+      if (nt >= 0 && (i & 1)) issue_part(nt, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -238,9 +251,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // (j + PD) % NS last held tile j - 2, read up to iteration j - 1).  Each
   // wave's work is one straight loop, so the accumulators stay in place;
   // iterations past the wave's last tile only keep the barrier count.
-  auto it_begin = [&](int j) {
-    if (j + PD < n_tiles) issue(j + PD);
-  };
+  auto next_dma = [&](int j) { return j + PD < n_tiles ? j + PD : -1; };
   auto it_end = [&](int j) {
     wait_vm(in_flight_after(j + 1));
     wait_lgkm0();
@@ -250,37 +261,48 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   if (w_tiles > 0) {
     pb[0] = pb[1] = u32x4{0, 0, 0, 0};
     for (; j < w_tiles; ++j) {
-      it_begin(j);
-      mfma_block(j);
+      mfma_block(j, next_dma(j));
       softmax(j);
       it_end(j);
     }
-    it_begin(j);
-    mfma_block(j);  // PV of the last tile
+    mfma_block(j, next_dma(j));  // PV of the last tile
     it_end(j);
     ++j;
   }
   for (; j <= n_tiles; ++j) {
-    it_begin(j);
+    if (next_dma(j) >= 0) issue(next_dma(j));
     it_end(j);
   }
 
   const float lt = xor32_sum(l);  // lanes c and c+32 share a query row
-  if (qrow >= p.Sq) return;
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  T *op = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
-          static_cast<int64_t>(qrow) * a.o.s2;
+  // O rows leave through LDS (free after the last barrier, all loads waited
+  // for): each wave rounds its 32 rows into its own slice -- row r at r * 2D
+  // bytes, 16-byte chunk q at q ^ (r % CPR), the XOR keeping the row writes
+  // off one bank -- then reads back whole 16-byte chunks of rows, so the
+  // global stores are coalesced.  Lane holds O^T[d = 32 dt + 8 g + 4 h + r][row c].
+  constexpr int CPR = D / 8;
+  static_assert(NW * 32 * 2 * D <= NS * 2 * TILE_B, "output slices fit in the ring");
+  static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
+  char *slice = lds + w * 32 * 2 * D;
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int d = dt * 32 + g * 8 + h * 4;
-      u32x2 pk = {pack2<T>(oacc[dt][g * 4 + 0] * inv, oacc[dt][g * 4 + 1] * inv),
-                  pack2<T>(oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv)};
-      *reinterpret_cast<u32x2 *>(op + d) = pk;
+      const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+      *reinterpret_cast<u32x2 *>(slice + off) =
+          u32x2{pack2<T>(oacc[dt][g * 4 + 0] * inv, oacc[dt][g * 4 + 1] * inv),
+                pack2<T>(oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv)};
     }
   }
-  if (a.lse && h == 0)
+  T *ob = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1;
+#pragma unroll
+  for (int u = 0; u < 32 * CPR / 64; ++u) {
+    const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.o.s2 + q * 8) = vr;
+  }
+  if (a.lse && h == 0 && qrow < p.Sq)
     a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
         lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
 }
