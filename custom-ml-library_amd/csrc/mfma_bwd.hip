@@ -459,16 +459,22 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
   const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
   const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
-  auto issue = [&](int tile) {
+  // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
+  constexpr int KPARTS = NBLK / NW;
+  static_assert(NBLK % NW == 0 && SKS == 2 * LPT, "one DMA part per two MFMA steps");
+  auto issue_part = [&](int tile, int u) {
     const uint32_t st = lds0 + (tile % DQ_NS) * 2 * TILE_B;
-#pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int e = w + NW * u;
-      const int n = e < NBLK ? e : e - NBLK;
-      const uint32_t row0 = static_cast<uint32_t>(tile * KT + 16 * (n / QG));
-      if (e < NBLK) dma16(kdesc, st + n * 1024, koff, row0 * ks_b);
-      else dma16(vdesc, st + TILE_B + n * 1024, voff, row0 * vs_b);
+    if (u < KPARTS) {
+      const int n = w + NW * u;
+      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * KT + 16 * (n / QG)) * ks_b);
+    } else {
+      const int n = w + NW * (u - KPARTS);
+      dma16(vdesc, st + TILE_B + n * 1024, voff, static_cast<uint32_t>(tile * KT + 16 * (n / QG)) * vs_b);
     }
+  };
+  auto issue = [&](int tile) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) issue_part(tile, u);
   };
   auto in_flight_after = [&](int jn) {
     const int later = min(DQ_PD - 1, n_tiles - 1 - jn);
@@ -490,7 +496,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
 
-  zero_lds<NT>(lds, sizeof(lds), tid);
+  // The first MFMA block multiplies the K half of stage DQ_NS - 1 (no DMA has
+  // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
+  // LDS byte is written by a DMA load before it is read (lanes past the
+  // buffer range write zeros).
+  zero_lds<NT>(lds + (DQ_NS - 1) * 2 * TILE_B, TILE_B, tid);
   __syncthreads();
   for (int t = 0; t < DQ_PD && t < n_tiles; ++t) issue(t);
   wait_vm(in_flight_after(0));
@@ -501,7 +511,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // steps ahead.  One code path for every block keeps the accumulators in
   // place: the first block multiplies a zeroed stage by dS = 0, and past the
   // wave's last tile S and dP are computed and ignored.
-  auto mfma_block = [&](int j) {
+  auto mfma_block = [&](int j, int nt) {  // nt: tile whose DMA to issue, or -1
     const char *kt = lds + (j % DQ_NS) * 2 * TILE_B;
     const char *vt = kt + TILE_B;
     const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * 2 * TILE_B;
@@ -523,6 +533,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
       dp = mfma32<T>(vr[i % (FD + 1)], gf[i], dp);
       acc[i % PDT] = mfma32<T>(kc[i % (FD + 1)], pd[i / PDT], acc[i % PDT]);
       if (i + FD < SKS) load(i + FD);
+      if (nt >= 0 && (i & 1)) issue_part(nt, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -557,9 +568,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     }
   };
 
-  auto it_begin = [&](int j) {
-    if (j + DQ_PD < n_tiles) issue(j + DQ_PD);
-  };
+  auto next_dma = [&](int j) { return j + DQ_PD < n_tiles ? j + DQ_PD : -1; };
   auto it_end = [&](int j) {
     wait_vm(in_flight_after(j + 1));
     wait_lgkm0();
@@ -569,33 +578,45 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   if (w_tiles > 0) {
     pd[0] = pd[1] = u32x4{0, 0, 0, 0};
     for (; j < w_tiles; ++j) {
-      it_begin(j);
-      mfma_block(j);
+      mfma_block(j, next_dma(j));
       grad(j);
       it_end(j);
     }
-    it_begin(j);
-    mfma_block(j);  // dQ of the last tile
+    mfma_block(j, next_dma(j));  // dQ of the last tile
     it_end(j);
     ++j;
   }
   for (; j <= n_tiles; ++j) {
-    it_begin(j);
+    if (next_dma(j) >= 0) issue(next_dma(j));
     it_end(j);
   }
 
-  if (qrow >= p.Sq) return;
-  T *dqp = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1 + static_cast<int64_t>(qrow) * a.dq.s2;
+  // dQ rows leave through LDS (free after the last barrier, all loads waited
+  // for): each wave rounds its 32 rows into its own slice -- row r at r * 2D
+  // bytes, 16-byte chunk q at q ^ (r % CPR) -- then reads back whole 16-byte
+  // chunks of rows for coalesced stores.  Lane holds dQ^T[d = 32 dt + 8 g +
+  // 4 h + r][row c].
+  constexpr int CPR = D / 8;
+  static_assert(NW * 32 * 2 * D <= DQ_NS * 2 * TILE_B, "output slices fit in the ring");
+  static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
+  char *slice = lds + w * 32 * 2 * D;
   const float sc = a.scale;
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int d = dt * 32 + g * 8 + h * 4;
-      *reinterpret_cast<u32x2 *>(dqp + d) =
+      const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+      *reinterpret_cast<u32x2 *>(slice + off) =
           u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
                 pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
     }
+  }
+  T *ob = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1;
+#pragma unroll
+  for (int u = 0; u < 32 * CPR / 64; ++u) {
+    const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.dq.s2 + q * 8) = vr;
   }
 }
 
