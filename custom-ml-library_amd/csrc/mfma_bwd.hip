@@ -1,10 +1,10 @@
 // Attention backward for gfx950 with MFMA 32x32x16 (f16/bf16 in, fp32
 // accumulate).  Follows the reference's streaming VJP (src/tensorsmith/nn/
 // attention.py:220-247):
-//   delta_i = sum_d dO_id O_id                     (row_prep_kernel)
+//   delta_i = sum_d dO_id O_id                     (dq_kernel prologue)
 //   P_ij = exp(S_ij - LSE_i), dS_ij = P_ij (dP_ij - delta_i), dP = dO V^T
+//   dQ = scale dS K                                (dq_kernel, runs first)
 //   dV = P^T dO, dK = scale dS^T Q                 (dkdv_kernel)
-//   dQ = scale dS K                                (dq_kernel)
 // dK/dV and dQ are produced by two kernels that each own their output tile,
 // so every gradient element is written exactly once: no atomics, bitwise
 // deterministic results (checkpoint recompute reproduces them exactly).
@@ -26,7 +26,12 @@ struct BwdArgs {
   Problem p;
   View q, k, v, o, dout, dq, dk, dv;
   const float *lse;
-  float *delta;  // [rows] -delta, then [rows] -safe(lse) / scale
+  // Row values the dQ kernel writes for the dK/dV kernel: [rows] nd = -delta,
+  // then [rows] nl = -safe(lse) / scale, safe(lse) = isfinite(lse) ? lse : 0
+  // (the reference's safe_lse, attention.py:231).  Stored negated so the
+  // dK/dV kernel starts its S and dP accumulators from them:
+  // S + nl = (S scale - lse) / scale and dP + nd = dP - delta.
+  float *delta;
   float sl;      // scale * log2(e)
   float scale;   // final gradient scale
 };
@@ -41,49 +46,11 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
 }
 
 // ---------------------------------------------------------------------------
-// Row pre-pass: nd = -rowsum(dO * O) = -delta and nl = -(isfinite(lse) ? lse
-// : 0) / scale -- the reference's safe_lse (attention.py:231) in score units.
-// Both are stored negated so the dK/dV kernel can start its S and dP
-// accumulators from them: S + nl = (S scale - lse) / scale, dP + nd = dP - delta.
-// ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(NT) void row_prep_kernel(BwdArgs a) {
-  constexpr int TPR = D / 8;
-  constexpr int RPB = NT / TPR;
-  const Problem &p = a.p;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + threadIdx.x / TPR;
-  const int part = threadIdx.x % TPR;
-  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-  float s = 0.f;
-  if (row < rows) {
-    const int i = static_cast<int>(row % p.Sq);
-    const int64_t bh = row / p.Sq;
-    const int hq = static_cast<int>(bh % p.Hq), b = static_cast<int>(bh / p.Hq);
-    const T *op = static_cast<const T *>(a.o.data) + b * a.o.s0 + hq * a.o.s1 +
-                  static_cast<int64_t>(i) * a.o.s2 + part * 8;
-    const T *gp = static_cast<const T *>(a.dout.data) + b * a.dout.s0 + hq * a.dout.s1 +
-                  static_cast<int64_t>(i) * a.dout.s2 + part * 8;
-    const u32x4 ov = ld16(op), gv = ld16(gp);
-    const T *oe = reinterpret_cast<const T *>(&ov);
-    const T *ge = reinterpret_cast<const T *>(&gv);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) s += static_cast<float>(oe[e]) * static_cast<float>(ge[e]);
-  }
-#pragma unroll
-  for (int m = TPR / 2; m >= 1; m >>= 1) s += __shfl_xor(s, m, 64);
-  if (row < rows && part == 0) {
-    a.delta[row] = -s;
-    const float l = a.lse[row];
-    a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // dK / dV: one workgroup = 128 keys of one (b, kv head), 4 wavefronts, two
 // workgroups per CU.  Wave w owns keys k0 + 32 w .. + 31: it holds their K
 // and V row fragments in registers for the workgroup's life, next to its
 // dK^T / dV^T accumulators, so K and V take no LDS and no wave shares an
-// output row.  Query tiles of 32 rows -- Q, dO and their lse2 / delta values,
+// output row.  Query tiles of 32 rows -- Q, dO and their nl / nd row values,
 // for every query head of the GQA group -- stream through a 3-stage LDS ring
 // by DMA loads issued two tiles ahead (between the first MFMA steps), one
 // fence-free barrier per tile.  Per tile a wave computes S = Q K^T and
@@ -104,7 +71,7 @@ template <typename T, int D>
 __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
   constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
   constexpr int NBLK = TILE_B / 1024;
-  constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | lse2 (QT floats) | delta (QT floats)
+  constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | nl (QT floats) | nd (QT floats)
   constexpr int LPT = 2 * NBLK / NW;          // Q + dO DMA loads per wave per tile
   constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
   static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
@@ -161,7 +128,7 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
     q0 = q_start + (itn - r * n_qt) * QT;
   };
   // DMA of tile itn into its ring stage, in LPT + 1 parts: part u < LPT is
-  // this wave's u-th Q / dO block, part LPT the lse2 / delta rows (waves 0, 1).
+  // this wave's u-th Q / dO block, part LPT the nl / nd rows (waves 0, 1).
   struct TileDma {
     uint32_t st;
     int q0, hq;
@@ -425,29 +392,45 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int w_tiles = wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0;
 
   u32x4 qf[SKS], gf[SKS];
-  float lse2, delta;
+  float lse2, delta;  // -safe(lse) in exp2 units, -delta
   {
     const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
+    const uint32_t os_b = static_cast<uint32_t>(a.o.s2) * 2;
     const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+    const rsrc_t ors = make_rsrc(head_ptr<T>(a.o, b, hq), static_cast<uint32_t>(p.Sq) * os_b);
+    u32x4 of[SKS];
 #pragma unroll
     for (int ks = 0; ks < SKS; ++ks) {
       qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
       gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
+      of[ks] = buf_load16(ors, static_cast<uint32_t>(qrow) * os_b + (ks * 16 + h * 8) * 2);
     }
-    const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-    const int64_t base = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq;
-    const rsrc_t drs = make_rsrc(a.delta + base, static_cast<uint32_t>(p.Sq) * 4);
-    const rsrc_t lrs = make_rsrc(a.delta + rows + base, static_cast<uint32_t>(p.Sq) * 4);
-    delta = buf_load_f32(drs, static_cast<uint32_t>(qrow) * 4);
-    lse2 = buf_load_f32(lrs, static_cast<uint32_t>(qrow) * 4);
+    const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
+    const float l = qrow < p.Sq ? a.lse[row] : 0.f;
+    // delta = sum_d dO O in fp32; lanes c and c + 32 hold the row's two halves
+    float dsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks) {
+      const T *ge = reinterpret_cast<const T *>(&gf[ks]);
+      const T *oe = reinterpret_cast<const T *>(&of[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
+    }
+    delta = -xor32_sum(dsum);
+    const bool finite = isfinite(l);
+    lse2 = finite ? -l * kLog2e : 0.f;
+    if (h == 0 && qrow < p.Sq) {
+      const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+      a.delta[row] = delta;
+      a.delta[rows + row] = finite ? -l / a.scale : 0.f;
+    }
   }
   // Resolve these loads before the DMA loads start (the compiler's vmcnt
   // waits do not count those).
 #pragma unroll
   for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
   asm volatile("" : "+v"(delta), "+v"(lse2));
-  lse2 *= a.sl;  // -lse in exp2 units; delta holds -delta
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
   const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
@@ -623,13 +606,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
 template <typename T, int D>
 hipError_t launch(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
-  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-  constexpr int RPB = NT / (D / 8);
-  { Probe pr_("bwd_row_prep", st); row_prep_kernel<T, D><<<dim3((rows + RPB - 1) / RPB), dim3(NT), 0, st>>>(a); }
-  const int n_kb = (p.Sk + KB - 1) / KB;
-  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
+  // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   { Probe pr_("bwd_dq_mfma", st); dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a); }
+  const int n_kb = (p.Sk + KB - 1) / KB;
+  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
   return hipGetLastError();
 }
 
