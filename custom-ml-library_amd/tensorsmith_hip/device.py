@@ -109,6 +109,14 @@ def seed(value: int) -> None:
         pass
 
 
+def random_uniform(shape, value: DeviceLike = "hip"):
+    """Uniform [0, 1) float32 draws from the device generator (the reference's
+    ``device.random_uniform``, ``src/tensorsmith/device.py:276-297``)."""
+    import torch
+
+    return torch.rand(tuple(shape), dtype=torch.float32, device=device(value).torch)
+
+
 def current_stream(dev: Device) -> int:
     """Raw hipStream_t of torch's current stream on ``dev`` (0 = default)."""
     import torch

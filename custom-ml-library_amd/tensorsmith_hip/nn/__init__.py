@@ -5,10 +5,14 @@ from .attention import rotary_embedding, scaled_dot_product_attention
 from .cache import KVCache
 from .layers import GELU, Dropout, Embedding, LayerNorm, Linear
 from .module import Module, Parameter
-from .transformer import MultiHeadAttention
+from .transformer import (
+    MultiHeadAttention, RMSNorm, SiLU, SwiGLU, TransformerConfig, TransformerDecoderBlock,
+    TransformerLM, sample_logits,
+)
 
 __all__ = [
     "Dropout", "Embedding", "GELU", "KVCache", "LayerNorm", "Linear", "Module",
-    "MultiHeadAttention", "Parameter", "functional", "rotary_embedding",
-    "scaled_dot_product_attention",
+    "MultiHeadAttention", "Parameter", "RMSNorm", "SiLU", "SwiGLU", "TransformerConfig",
+    "TransformerDecoderBlock", "TransformerLM", "functional", "rotary_embedding",
+    "sample_logits", "scaled_dot_product_attention",
 ]

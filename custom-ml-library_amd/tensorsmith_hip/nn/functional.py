@@ -15,8 +15,8 @@ from ..tensor import Tensor, _sum_to_shape, is_torch
 from .attention import rotary_embedding, scaled_dot_product_attention
 
 __all__ = [
-    "cross_entropy", "dropout", "embedding", "gelu", "layer_norm", "linear", "rotary_embedding",
-    "scaled_dot_product_attention",
+    "cross_entropy", "dropout", "embedding", "gelu", "layer_norm", "linear", "rms_norm",
+    "rotary_embedding", "scaled_dot_product_attention", "silu",
 ]
 
 
@@ -77,20 +77,24 @@ def gelu(input: Tensor) -> Tensor:
     return Tensor._from_op(out, (input,), backward, "bias_gelu")
 
 
-def layer_norm(input: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float = 1e-5) -> Tensor:
-    """Layer norm over the trailing ``weight.ndim`` dims (reference ``primitives.py:67-136``)."""
+def _norm(input: Tensor, weight: Tensor, bias: Tensor | None, eps: float, rms: bool) -> Tensor:
+    """Layer / RMS norm over the trailing ``weight.ndim`` dims (reference
+    ``primitives.py:67-136``): half inputs compute in float32, the VJP uses
+    the saved normalised values and reciprocal std."""
     if eps <= 0 or not math.isfinite(eps):
         raise ValueError("eps must be positive")
     if input.shape[-weight.ndim:] != weight.shape:
         raise ValueError("normalization weight must match the trailing input dimensions")
+    if bias is not None and bias.shape != weight.shape:
+        raise ValueError("normalization bias and weight must have equal shapes")
     parents = (input, weight) if bias is None else (input, weight, bias)
     if any(p.device != input.device for p in parents):
         raise ValueError("normalization tensors must be on the same device")
-    _require_hip(input, "layer_norm")
+    _require_hip(input, "rms_norm" if rms else "layer_norm")
     axes = tuple(range(input.ndim - weight.ndim, input.ndim))
     x = _compute(input._data)
     w = weight._data.to(x.dtype)
-    centered = x - x.mean(dim=axes, keepdim=True)
+    centered = x if rms else x - x.mean(dim=axes, keepdim=True)
     rstd = 1 / (centered.square().mean(dim=axes, keepdim=True) + eps).sqrt()
     normalized = centered * rstd
     out = normalized * w
@@ -101,14 +105,40 @@ def layer_norm(input: Tensor, weight: Tensor, bias: Tensor | None = None, eps: f
     def backward(g):
         g = g.to(x.dtype)
         weighted = g * w
-        dx = rstd * (weighted - normalized * (weighted * normalized).mean(dim=axes, keepdim=True)
-                     - weighted.mean(dim=axes, keepdim=True))
+        dx = rstd * (weighted - normalized * (weighted * normalized).mean(dim=axes, keepdim=True))
+        if not rms:
+            dx = dx - rstd * weighted.mean(dim=axes, keepdim=True)
         grads = [dx.to(input.dtype), _sum_to_shape(g * normalized, weight.shape).to(weight.dtype)]
         if bias is not None:
             grads.append(_sum_to_shape(g, bias.shape).to(bias.dtype))
         return tuple(grads)
 
-    return Tensor._from_op(out, parents, backward, "layer_norm")
+    return Tensor._from_op(out, parents, backward, "rms_norm" if rms else "layer_norm")
+
+
+def layer_norm(input: Tensor, weight: Tensor, bias: Tensor | None = None, eps: float = 1e-5) -> Tensor:
+    """Layer norm (reference ``primitives.py:134-135``)."""
+    return _norm(input, weight, bias, eps, False)
+
+
+def rms_norm(input: Tensor, weight: Tensor, eps: float = 1e-6) -> Tensor:
+    """RMS norm, ``x / sqrt(mean(x^2) + eps) * weight`` (reference ``primitives.py:138-139``)."""
+    return _norm(input, weight, None, eps, True)
+
+
+def silu(input: Tensor) -> Tensor:
+    """``x * sigmoid(x)`` in float32 for half inputs (reference ``primitives.py:52-64``)."""
+    _require_hip(input, "silu")
+    import torch
+
+    x = _compute(input._data)
+    sig = torch.sigmoid(x)
+    out = (x * sig).to(input.dtype)
+
+    def backward(g):
+        return ((g.to(x.dtype) * (sig + x * sig * (1 - sig))).to(input.dtype),)
+
+    return Tensor._from_op(out, (input,), backward, "silu")
 
 
 def embedding(indices: Tensor, weight: Tensor) -> Tensor:

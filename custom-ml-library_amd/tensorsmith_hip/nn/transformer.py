@@ -1,22 +1,36 @@
-"""``MultiHeadAttention`` -- the reference's caller of the attention op.
+"""The reference's callers of the attention op: ``MultiHeadAttention`` and the
+decoder-only ``TransformerLM`` with cached generation.
 
-Same constructor, forward signature, validation and data flow as
-``src/tensorsmith/nn/transformer.py:48-155``: projections reshaped to
-``[B,S,H,D]`` and permuted to ``[B,H,S,D]`` *views* (the HIP kernels take the
-strides, so no copy is made), optional interleaved RoPE, KV-cache append with
-``causal_offset = cache.length``, then ``scaled_dot_product_attention`` with
-``backend`` (``"hip"`` added to the allowlist; ``"auto"`` picks it).
+``MultiHeadAttention`` keeps the constructor, forward signature, validation
+and data flow of ``src/tensorsmith/nn/transformer.py:48-155``: projections
+reshaped to ``[B,S,H,D]`` and permuted to ``[B,H,S,D]`` *views* (the HIP
+kernels take the strides, so no copy is made), optional interleaved RoPE,
+KV-cache append with ``causal_offset = cache.length``, then
+``scaled_dot_product_attention`` with ``backend`` (``"hip"`` added to the
+allowlist; ``"auto"`` picks it).
+
+``TransformerLM`` (``transformer.py:156-402``): pre-RMSNorm blocks with GQA /
+RoPE attention and a SwiGLU MLP, tied or separate output weights, one KV
+cache per block whose lengths roll back when a cached forward fails, and
+``generate`` -- greedy / top-k / nucleus sampling on the device, each decode
+step a one-token attention call over the caches (the split-K decode kernel).
 """
 
 from __future__ import annotations
 
 import numpy as np
 
-from ..tensor import Tensor, is_grad_enabled
+from dataclasses import dataclass
+
+from .. import device as _device
+from ..tensor import Tensor, cat, is_grad_enabled, no_grad
+from . import functional as F
 from .attention import BACKENDS, rotary_embedding, scaled_dot_product_attention
 from .cache import KVCache
-from .layers import Linear
-from .module import Module
+from .layers import Dropout, Embedding, Linear
+from .module import Module, Parameter
+
+random_uniform = _device.random_uniform
 
 
 class MultiHeadAttention(Module):
@@ -88,3 +102,246 @@ class MultiHeadAttention(Module):
             causal_offset=offset, backend=self.backend,
             enable_gqa=self.num_kv_heads != self.num_heads)
         return self.out_proj(attended.permute(0, 2, 1, 3).reshape(batch, steps, self.embed_dim))
+
+
+class RMSNorm(Module):
+    def __init__(self, dim: int, eps: float = 1e-6, device=None):
+        super().__init__()
+        if dim <= 0:
+            raise ValueError("normalization dimension must be positive")
+        self.eps = eps
+        self.weight = Parameter(Tensor(np.ones(dim, np.float32), device=device))
+
+    def forward(self, input: Tensor) -> Tensor:
+        return F.rms_norm(input, self.weight, self.eps)
+
+
+class SiLU(Module):
+    def forward(self, input: Tensor) -> Tensor:
+        return F.silu(input)
+
+
+class SwiGLU(Module):
+    def __init__(self, dim: int, hidden_dim: int, dropout: float = 0.0, device=None):
+        super().__init__()
+        self.gate = Linear(dim, hidden_dim, bias=False, device=device)
+        self.up = Linear(dim, hidden_dim, bias=False, device=device)
+        self.down = Linear(hidden_dim, dim, bias=False, device=device)
+        self.dropout = Dropout(dropout)
+
+    def forward(self, input: Tensor) -> Tensor:
+        return self.dropout(self.down(F.silu(self.gate(input)) * self.up(input)))
+
+
+class TransformerDecoderBlock(Module):
+    """Pre-RMSNorm decoder block with GQA/RoPE attention and a SwiGLU MLP."""
+
+    def __init__(self, dim: int, num_heads: int, hidden_dim: int | None = None, *,
+                 num_kv_heads=None, dropout=0.0, attention_backend="auto", device=None):
+        super().__init__()
+        self.attention_norm = RMSNorm(dim, device=device)
+        self.attention = MultiHeadAttention(dim, num_heads, num_kv_heads=num_kv_heads,
+                                            dropout=dropout, backend=attention_backend,
+                                            device=device)
+        self.residual_dropout = Dropout(dropout)
+        self.ffn_norm = RMSNorm(dim, device=device)
+        self.ffn = SwiGLU(dim, hidden_dim or 4 * dim, dropout, device)
+
+    def forward(self, input: Tensor, *, cache=None, attn_mask=None) -> Tensor:
+        hidden = input + self.residual_dropout(
+            self.attention(self.attention_norm(input), cache=cache, attn_mask=attn_mask))
+        return hidden + self.ffn(self.ffn_norm(hidden))
+
+
+@dataclass(frozen=True)
+class TransformerConfig:
+    vocab_size: int
+    dim: int = 128
+    num_heads: int = 4
+    num_layers: int = 4
+    hidden_dim: int | None = None
+    num_kv_heads: int | None = None
+    max_seq_len: int = 1024
+    dropout: float = 0.0
+    tie_weights: bool = True
+    attention_backend: str = "auto"
+    activation_checkpointing: bool = False
+
+    def __post_init__(self):
+        if min(self.vocab_size, self.dim, self.num_heads, self.num_layers, self.max_seq_len) <= 0:
+            raise ValueError("transformer dimensions must be positive")
+        if self.hidden_dim is not None and self.hidden_dim <= 0:
+            raise ValueError("hidden_dim must be positive")
+        kv = self.num_heads if self.num_kv_heads is None else self.num_kv_heads
+        if (kv <= 0 or self.dim % self.num_heads or self.num_heads % kv
+                or (self.dim // self.num_heads) % 2):
+            raise ValueError("invalid attention head configuration")
+        if not 0 <= self.dropout < 1:
+            raise ValueError("dropout must be in [0, 1)")
+        if self.attention_backend not in BACKENDS:
+            raise ValueError("invalid attention backend")
+
+
+class TransformerLM(Module):
+    """A decoder-only language model with [B,T,V] logits and cached generation.
+
+    ``activation_checkpointing`` is accepted for configuration compatibility;
+    blocks always keep their activations (same results, more memory).
+    """
+
+    def __init__(self, config: TransformerConfig, device=None):
+        super().__init__()
+        self.config = config
+        self.token_embedding = Embedding(config.vocab_size, config.dim, device=device)
+        self.embedding_dropout = Dropout(config.dropout)
+        self.blocks = [
+            TransformerDecoderBlock(config.dim, config.num_heads, config.hidden_dim,
+                                    num_kv_heads=config.num_kv_heads, dropout=config.dropout,
+                                    attention_backend=config.attention_backend, device=device)
+            for _ in range(config.num_layers)
+        ]
+        self.final_norm = RMSNorm(config.dim, device=device)
+        self.output_weight = (
+            self.token_embedding.weight if config.tie_weights else Parameter(Tensor(
+                np.random.normal(0, 0.02, (config.vocab_size, config.dim)).astype(np.float32),
+                device=device)))
+        # Embedding's generic unit variance is inappropriate for residual stacks:
+        # scaling its normal(0, 1) draw gives the reference's normal(0, 0.02).
+        self.token_embedding.weight._data = self.token_embedding.weight._data * 0.02
+
+    def forward(self, tokens: Tensor, *, caches: list[KVCache] | None = None, attn_mask=None,
+                logits_to_keep: int = 0) -> Tensor:
+        if tokens.ndim != 2 or "int" not in str(tokens.dtype) or tokens.shape[1] == 0:
+            raise ValueError("tokens must be a nonempty integer [batch, time] tensor")
+        if not isinstance(logits_to_keep, int) or not 0 <= logits_to_keep <= tokens.shape[1]:
+            raise ValueError("logits_to_keep must be between zero (all) and the input length")
+        offset = 0
+        if caches is not None:
+            if len(caches) != len(self.blocks) or len({cache.length for cache in caches}) != 1:
+                raise ValueError("provide one cache per block, all at the same sequence position")
+            if self.training or is_grad_enabled():
+                raise RuntimeError("cached decoding requires eval() and no_grad()")
+            offset = caches[0].length
+            for block, cache in zip(self.blocks, caches):
+                if cache.batch_size != tokens.shape[0] or cache.device != tokens.device:
+                    raise ValueError("cache batch/device does not match tokens")
+                if offset + tokens.shape[1] > cache.max_seq_len:
+                    raise ValueError("cache capacity exceeded")
+                attention = block.attention
+                if (cache.num_heads != attention.num_kv_heads
+                        or cache.head_dim != attention.head_dim
+                        or cache.value_dim != attention.head_dim
+                        or cache.dtype != self.token_embedding.weight.dtype):
+                    raise ValueError("cache head configuration/dtype does not match model")
+        if offset + tokens.shape[1] > self.config.max_seq_len:
+            raise ValueError("model context length exceeded")
+        hidden = self.embedding_dropout(self.token_embedding(tokens))
+        try:
+            for i, block in enumerate(self.blocks):
+                hidden = block(hidden, cache=None if caches is None else caches[i],
+                               attn_mask=attn_mask)
+            if logits_to_keep:
+                hidden = hidden[:, -logits_to_keep:, :]
+            return F.linear(self.final_norm(hidden), self.output_weight)
+        except Exception:
+            if caches is not None:
+                for cache in caches:
+                    cache.truncate(offset)
+            raise
+
+    def loss(self, tokens: Tensor, targets: Tensor, *, ignore_index=-100,
+             label_smoothing=0.0) -> Tensor:
+        return F.cross_entropy(self(tokens), targets, axis=-1, ignore_index=ignore_index,
+                               label_smoothing=label_smoothing)
+
+    def new_cache(self, batch_size: int, max_seq_len: int | None = None, *,
+                  quantized=False) -> list[KVCache]:
+        capacity = self.config.max_seq_len if max_seq_len is None else max_seq_len
+        if capacity <= 0 or capacity > self.config.max_seq_len:
+            raise ValueError("cache capacity must fit the model context")
+        return [
+            KVCache(batch_size, block.attention.num_kv_heads, block.attention.head_dim, capacity,
+                    device=self.token_embedding.weight.device,
+                    dtype=self.token_embedding.weight.dtype, quantized=quantized)
+            for block in self.blocks
+        ]
+
+    @no_grad()
+    def generate(self, prompt: Tensor, max_new_tokens: int, *, temperature=1.0,
+                 top_k: int | None = None, top_p: float = 1.0, eos_token_id: int | None = None,
+                 use_cache: bool = True, quantized_cache: bool = False) -> Tensor:
+        """Batched greedy/top-k/nucleus sampling; returns prompt plus generated tokens."""
+        if (prompt.ndim != 2 or prompt.shape[1] == 0 or max_new_tokens < 0
+                or "int" not in str(prompt.dtype)):
+            raise ValueError("invalid prompt or generation length")
+        if prompt.shape[1] + max_new_tokens > self.config.max_seq_len:
+            raise ValueError("generation exceeds the configured context length")
+        if temperature < 0 or not np.isfinite(temperature) or not 0 < top_p <= 1:
+            raise ValueError("temperature must be finite/nonnegative and top_p in (0,1]")
+        if top_k is not None and not 1 <= top_k <= self.config.vocab_size:
+            raise ValueError("top_k must be within the vocabulary")
+        if eos_token_id is not None and not 0 <= eos_token_id < self.config.vocab_size:
+            raise ValueError("eos_token_id out of range")
+        import torch
+
+        modes = [(module, module.training) for module in self.modules()]
+        try:
+            self.eval()
+            caches = (self.new_cache(prompt.shape[0], prompt.shape[1] + max_new_tokens,
+                                     quantized=quantized_cache)
+                      if use_cache and max_new_tokens else None)
+            result, current = prompt, prompt
+            finished = torch.zeros((prompt.shape[0],), dtype=torch.bool, device=prompt._data.device)
+            for _ in range(max_new_tokens):
+                logits = self(current, caches=caches, logits_to_keep=1)[:, -1, :]
+                next_token = sample_logits(logits, temperature, top_k, top_p)
+                if eos_token_id is not None:
+                    raw = next_token._data.to(prompt._data.dtype)
+                    raw = torch.where(finished, torch.full_like(raw, eos_token_id), raw)
+                    next_token = Tensor(raw, device=prompt.device)
+                    finished = finished | (raw == eos_token_id)
+                result = cat((result, next_token.astype(prompt.dtype).unsqueeze(1)), dim=1)
+                if eos_token_id is not None and bool(finished.all()):
+                    break
+                current = next_token.astype(prompt.dtype).unsqueeze(1) if caches is not None else result
+        finally:
+            for module, mode in modes:
+                module.training = mode
+        return result
+
+
+def sample_logits(logits: Tensor, temperature: float = 1.0, top_k: int | None = None,
+                  top_p: float = 1.0) -> Tensor:
+    """Device-resident sampling from [batch, vocabulary] logits (reference
+    ``transformer.py:405-437``): greedy when ``temperature == 0``, else the
+    top-k candidates in descending score order, nucleus truncation at
+    ``top_p``, and inverse-CDF selection with one uniform draw per row."""
+    if logits.ndim != 2 or temperature < 0 or not np.isfinite(temperature) or not 0 < top_p <= 1:
+        raise ValueError("invalid sampling configuration")
+    vocab = logits.shape[-1]
+    if top_k is not None and not 1 <= top_k <= vocab:
+        raise ValueError("top_k must be within the vocabulary")
+    import torch
+
+    raw = logits._data
+    if temperature == 0:
+        return Tensor(raw.argmax(dim=-1), device=logits.device)
+    scores = raw.float() / temperature
+    if top_k is not None:
+        order = torch.topk(scores, top_k, dim=-1, largest=True, sorted=True).indices
+    else:
+        order = torch.argsort(scores, dim=-1, descending=True)
+    sorted_scores = torch.gather(scores, -1, order)
+    probabilities = torch.exp(sorted_scores - sorted_scores.amax(dim=-1, keepdim=True))
+    probabilities = probabilities / probabilities.sum(dim=-1, keepdim=True)
+    if top_p < 1:
+        keep = torch.cumsum(probabilities, dim=-1) - probabilities < top_p
+        probabilities = torch.where(keep, probabilities, torch.zeros_like(probabilities))
+        probabilities = probabilities / probabilities.sum(dim=-1, keepdim=True)
+    uniform = random_uniform((logits.shape[0], 1), logits.device)
+    cumulative = torch.cumsum(probabilities, dim=-1)
+    cumulative = cumulative / cumulative[:, -1:]
+    chosen = (cumulative < uniform).sum(dim=-1)
+    chosen = torch.clamp(chosen, max=order.shape[-1] - 1)
+    rows = torch.arange(logits.shape[0], device=raw.device)
+    return Tensor(order[rows, chosen], device=logits.device)

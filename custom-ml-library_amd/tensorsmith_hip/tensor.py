@@ -387,6 +387,12 @@ class Tensor:
         axes[a], axes[b] = axes[b], axes[a]
         return self.permute(*axes)
 
+    def unsqueeze(self, dim: int) -> Tensor:
+        d = dim if dim >= 0 else dim + self.ndim + 1
+        if not 0 <= d <= self.ndim:
+            raise ValueError("unsqueeze dimension out of range")
+        return self.reshape(*self.shape[:d], 1, *self.shape[d:])
+
     def contiguous(self) -> Tensor:
         if not is_torch(self._data) or self._data.is_contiguous():
             return self
