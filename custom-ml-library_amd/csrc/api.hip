@@ -221,6 +221,62 @@ int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const t
                     "decode launch");
 }
 
+int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                               const tsattn_view *v, const tsattn_view *k_scale,
+                               const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,
+                               void *workspace, size_t workspace_bytes, void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
+      (rc = check_view(v, "value")) || (rc = check_view(k_scale, "key scale")) ||
+      (rc = check_view(v_scale, "value scale")) || (rc = check_view(out, "output")))
+    return rc;
+  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
+  if (p->mask_kind != TSATTN_MASK_NONE && !p->kv_len)
+    return fail(TSATTN_ERR_UNSUPPORTED, "int8 decode takes key-padding lengths, not general masks");
+  const tsattn::View vk = tsattn::make_view(k), vv = tsattn::make_view(v);
+  // int8 rows are read as 8-byte chunks: 8-byte aligned bases and row strides
+  auto aligned8 = [](const tsattn::View &x) {
+    return reinterpret_cast<uintptr_t>(x.data) % 8 == 0 && x.s0 % 8 == 0 && x.s1 % 8 == 0 &&
+           x.s2 % 8 == 0;
+  };
+  if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(tsattn::make_view(q)) ||
+      !aligned8(vk) || !aligned8(vv))
+    return fail(TSATTN_ERR_UNSUPPORTED,
+                "int8 decode needs <= 8 query rows per KV head, f16/bf16 queries, equal head dims "
+                "in {64,128,256} and 8-byte aligned cache rows");
+  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(TSATTN_ERR_INVALID, "decode workspace too small: %zu < %zu bytes",
+                workspace_bytes, need);
+  g_last_path = 3;
+  return hip_status(tsattn::launch_decode_int8(pr, p->dtype, tsattn::make_view(q), vk, vv,
+                                               tsattn::make_view(k_scale), tsattn::make_view(v_scale),
+                                               tsattn::make_view(out), split_len, workspace,
+                                               static_cast<hipStream_t>(stream)),
+                    "int8 decode launch");
+}
+
+int tsattn_kv_append_int8(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                          const tsattn_view *src, const tsattn_view *dst, const tsattn_view *scale,
+                          int64_t pos, void *stream) {
+  int rc;
+  if ((rc = check_view(src, "source rows")) || (rc = check_view(dst, "int8 cache")) ||
+      (rc = check_view(scale, "cache scales")))
+    return rc;
+  if (dtype != TSATTN_F32 && dtype != TSATTN_F16 && dtype != TSATTN_BF16)
+    return fail(TSATTN_ERR_INVALID, "cache rows must be f32, f16 or bf16 (got dtype %d)", dtype);
+  if (batch <= 0 || heads <= 0 || len <= 0 || dim <= 0 || pos < 0)
+    return fail(TSATTN_ERR_INVALID, "append needs positive sizes and a nonnegative position");
+  if (dim > 512) return fail(TSATTN_ERR_UNSUPPORTED, "head dims above 512 are not supported");
+  return hip_status(tsattn::launch_kv_append_int8(dtype, batch, heads, len, dim,
+                                                  tsattn::make_view(src), tsattn::make_view(dst),
+                                                  tsattn::make_view(scale), pos,
+                                                  static_cast<hipStream_t>(stream)),
+                    "int8 append launch");
+}
+
 int tsattn_key_mask_lengths(const uint8_t *mask, int64_t stride_b, int64_t stride_k,
                             int32_t batch, int32_t len_kv, int32_t *kv_len, int32_t *kv_prefix,
                             void *stream) {

@@ -12,6 +12,15 @@
 // loads (one wave instruction covers 64*16 B of consecutive keys), U such
 // instructions for K and U for V are issued before any is consumed, so every
 // wave keeps 2*U KiB in flight.
+//
+// int8 caches (the reference's quantised KVCache, src/tensorsmith/nn/
+// cache.py:73-77 and :91-98): K and V rows are int8 with one fp32 scale per
+// (b, h, key).  The same lanes read 8-byte int8 chunks and the row scales;
+// the scale of K is applied to the lane group's dot product and the scale of
+// V is folded into the probability, so dequantisation costs one multiply per
+// key instead of a pass over the cache.  The dequantised values enter the
+// math in fp32 (the reference rounds them to the cache dtype first: at most
+// half an ulp of that dtype per element).
 #include <type_traits>
 
 #include "mfma_common.h"
@@ -26,6 +35,7 @@ constexpr int kMaxRows = 8;
 struct DecArgs {
   Problem p;
   View q, k, v, o;
+  View ks, vs;  // int8 caches: fp32 row scales [B, Hkv, capacity, 1]
   float *ws;
   int split_len, max_splits, rows;  // rows = rep * Sq query rows per KV head
   float sl;                         // scale * log2(e)
@@ -59,6 +69,16 @@ __device__ __forceinline__ void unpack8(u32x4 x, float *out) {
   for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
 }
 
+__device__ __forceinline__ void unpack8_i8(u32x2 x, float *out) {
+  const int8_t *e = reinterpret_cast<const int8_t *>(&x);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
+}
+
+// Cache rows as loaded: 8 half-precision values (16 B) or 8 int8 values (8 B).
+template <bool Q8>
+using KvChunk = std::conditional_t<Q8, u32x2, u32x4>;
+
 // Sum over each aligned group of LPK lanes (the lanes holding one key row).
 // For LPK = 16 (D = 128) a DPP butterfly inside each 16-lane row: quad_perm
 // swaps within quads, then rotations by 4 and 8 lanes; no LDS traffic.
@@ -88,8 +108,9 @@ __device__ __forceinline__ float group_sum(float d) {
   }
 }
 
-template <typename T, int D, int R>
+template <typename T, int D, int R, bool Q8>
 __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
+  using KT = std::conditional_t<Q8, int8_t, T>;  // cache element type
   constexpr int LPK = D / 8;      // lanes per key row
   constexpr int KPI = 64 / LPK;   // keys per wave instruction
   constexpr int BATCH = KPI * U;  // keys per wave per batch
@@ -133,8 +154,10 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
     for (int e = 0; e < 8; ++e) acc[r][e] = 0.f;
   }
 
-  const T *kbase = static_cast<const T *>(a.k.data) + b * a.k.s0 + hk * a.k.s1 + dc * 8;
-  const T *vbase = static_cast<const T *>(a.v.data) + b * a.v.s0 + hk * a.v.s1 + dc * 8;
+  const KT *kbase = static_cast<const KT *>(a.k.data) + b * a.k.s0 + hk * a.k.s1 + dc * 8;
+  const KT *vbase = static_cast<const KT *>(a.v.data) + b * a.v.s0 + hk * a.v.s1 + dc * 8;
+  const float *ksb = Q8 ? static_cast<const float *>(a.ks.data) + b * a.ks.s0 + hk * a.ks.s1 : nullptr;
+  const float *vsb = Q8 ? static_cast<const float *>(a.vs.data) + b * a.vs.s0 + hk * a.vs.s1 : nullptr;
   const float log2e = kLog2e;
   // Keys past k_stop are read from row k_stop - 1 (in bounds, finite) and
   // masked, so every load is unconditional.  K/V are streamed once: loads
@@ -142,26 +165,33 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
   auto body = [&](auto masked_tag) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
-      u32x4 kr[U], vr[U];
+      KvChunk<Q8> kr[U], vr[U];
+      float ksc[U], vsc[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int key = min(kb + u * KPI + kg, k_stop - 1);
         kr[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(kbase + static_cast<int64_t>(key) * a.k.s2));
+            reinterpret_cast<const KvChunk<Q8> *>(kbase + static_cast<int64_t>(key) * a.k.s2));
         vr[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4 *>(vbase + static_cast<int64_t>(key) * a.v.s2));
+            reinterpret_cast<const KvChunk<Q8> *>(vbase + static_cast<int64_t>(key) * a.v.s2));
+        if constexpr (Q8) {
+          ksc[u] = ksb[static_cast<int64_t>(key) * a.ks.s2];
+          vsc[u] = vsb[static_cast<int64_t>(key) * a.vs.s2];
+        }
       }
       float s[U][R];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float kf[8];
-        unpack8<T>(kr[u], kf);
+        if constexpr (Q8) unpack8_i8(kr[u], kf);
+        else unpack8<T>(kr[u], kf);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           float d = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; ++e) d = fmaf(qv[r][e], kf[e], d);
           s[u][r] = group_sum<LPK>(d);
+          if constexpr (Q8) s[u][r] *= ksc[u];
         }
       }
       // masks: keys past the split, causal, user mask (bool or additive, any broadcast)
@@ -202,9 +232,11 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
           const float pv = fast_exp2(s[u][r] - base);
           l[r] += pv;
           float vf[8];
-          unpack8<T>(vr[u], vf);
+          if constexpr (Q8) unpack8_i8(vr[u], vf);
+          else unpack8<T>(vr[u], vf);
+          const float pw = Q8 ? pv * vsc[u] : pv;  // int8: V's row scale folded into P
 #pragma unroll
-          for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pv, vf[e], acc[r][e]);
+          for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pw, vf[e], acc[r][e]);
         }
         m[r] = mb;
       }
@@ -315,20 +347,36 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
   }
 }
 
-template <typename T, int D, int R>
+template <typename T, int D, int R, bool Q8>
 hipError_t launch_rows(const DecArgs &a, hipStream_t st) {
   const Problem &p = a.p;
-  { Probe pr_("decode_split", st); decode_split_kernel<T, D, R><<<dim3(a.max_splits, p.Hkv, p.B), dim3(NT), 0, st>>>(a); }
+  {
+    Probe pr_(Q8 ? "decode_split_int8" : "decode_split", st);
+    decode_split_kernel<T, D, R, Q8><<<dim3(a.max_splits, p.Hkv, p.B), dim3(NT), 0, st>>>(a);
+  }
   { Probe pr_("decode_merge", st); decode_merge_kernel<T, D><<<dim3(p.Hq * p.Sq, p.B), dim3(64), 0, st>>>(a); }
   return hipGetLastError();
 }
 
-template <typename T, int D>
+template <typename T, int D, bool Q8>
 hipError_t launch_dim(const DecArgs &a, hipStream_t st) {
-  if (a.rows <= 1) return launch_rows<T, D, 1>(a, st);
-  if (a.rows <= 2) return launch_rows<T, D, 2>(a, st);
-  if (a.rows <= 4) return launch_rows<T, D, 4>(a, st);
-  return launch_rows<T, D, 8>(a, st);
+  if (a.rows <= 1) return launch_rows<T, D, 1, Q8>(a, st);
+  if (a.rows <= 2) return launch_rows<T, D, 2, Q8>(a, st);
+  if (a.rows <= 4) return launch_rows<T, D, 4, Q8>(a, st);
+  return launch_rows<T, D, 8, Q8>(a, st);
+}
+
+template <bool Q8>
+hipError_t launch_any(const DecArgs &a, int dtype, hipStream_t st) {
+  const int d = a.p.Dqk;
+  if (dtype == TSATTN_BF16) {
+    if (d == 64) return launch_dim<bf16, 64, Q8>(a, st);
+    if (d == 128) return launch_dim<bf16, 128, Q8>(a, st);
+    return launch_dim<bf16, 256, Q8>(a, st);
+  }
+  if (d == 64) return launch_dim<f16, 64, Q8>(a, st);
+  if (d == 128) return launch_dim<f16, 128, Q8>(a, st);
+  return launch_dim<f16, 256, Q8>(a, st);
 }
 
 int choose_split(const Problem &p, int split_len) {
@@ -354,18 +402,20 @@ size_t decode_workspace_bytes(const Problem &p, int split_len) {
 
 hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,
                          int split_len, void *workspace, hipStream_t st) {
-  DecArgs a{p, q, k, v, o, static_cast<float *>(workspace), 0, 0, p.rep * p.Sq,
+  DecArgs a{p, q, k, v, o, View{}, View{}, static_cast<float *>(workspace), 0, 0, p.rep * p.Sq,
             static_cast<float>(p.scale) * kLog2e};
   a.split_len = choose_split(p, split_len);
   a.max_splits = (p.Sk + a.split_len - 1) / a.split_len;
-  if (dtype == TSATTN_BF16) {
-    if (p.Dqk == 64) return launch_dim<bf16, 64>(a, st);
-    if (p.Dqk == 128) return launch_dim<bf16, 128>(a, st);
-    return launch_dim<bf16, 256>(a, st);
-  }
-  if (p.Dqk == 64) return launch_dim<f16, 64>(a, st);
-  if (p.Dqk == 128) return launch_dim<f16, 128>(a, st);
-  return launch_dim<f16, 256>(a, st);
+  return launch_any<false>(a, dtype, st);
+}
+
+hipError_t launch_decode_int8(const Problem &p, int dtype, View q, View k, View v, View ks,
+                              View vs, View o, int split_len, void *workspace, hipStream_t st) {
+  DecArgs a{p, q, k, v, o, ks, vs, static_cast<float *>(workspace), 0, 0, p.rep * p.Sq,
+            static_cast<float>(p.scale) * kLog2e};
+  a.split_len = choose_split(p, split_len);
+  a.max_splits = (p.Sk + a.split_len - 1) / a.split_len;
+  return launch_any<true>(a, dtype, st);
 }
 
 }  // namespace tsattn

@@ -131,6 +131,14 @@ bool decode_supported(const Problem &p, int dtype);
 size_t decode_workspace_bytes(const Problem &p, int split_len);
 hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,
                          int split_len, void *workspace, hipStream_t st);
+// The same over an int8 cache with fp32 row scales ks / vs [B, Hkv, capacity, 1].
+hipError_t launch_decode_int8(const Problem &p, int dtype, View q, View k, View v, View ks,
+                              View vs, View o, int split_len, void *workspace, hipStream_t st);
+
+// int8 KV-cache append: rows src[b, h, t, :] (dtype f32 / f16 / bf16) are
+// quantised into dst[b, h, pos + t, :] with their scale at scale[b, h, pos + t].
+hipError_t launch_kv_append_int8(int dtype, int B, int H, int T, int D, View src, View dst,
+                                 View scale, int64_t pos, hipStream_t st);
 
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st);

@@ -229,6 +229,44 @@ def scaled_dot_product_attention(
     return Tensor._from_op(out, (query, key, value), backward, "sdpa_hip")
 
 
+def decode_int8_cache(query: Tensor, cache, *, is_causal: bool, causal_offset: int,
+                      scale: float | None = None) -> Tensor | None:
+    """Inference attention of ``query`` [B, Hq, Q, D] against an int8
+    ``KVCache``'s active prefix, dequantised inside the decode kernel
+    (``tsattn_decode_forward_int8``).  Same result as the reference's
+    ``scaled_dot_product_attention(query, *cache.get(), ...)`` (the cache
+    dequantised eagerly, ``src/tensorsmith/nn/cache.py:88-99``) up to the
+    rounding of the dequantised values to the cache dtype.  Returns None when
+    the shapes are outside the decode kernel (the caller then goes through
+    ``cache.get()``)."""
+    q = _operand(query._data)
+    b, hq, qlen, dim = q.shape
+    code = _dtype_code(q.dtype)
+    hkv = cache.num_heads
+    if (code not in (_lib.F16, _lib.BF16) or dim not in (64, 128, 256) or cache.value_dim != dim
+            or cache.head_dim != dim or hq % hkv or (hq // hkv) * qlen > 8
+            or cache.length < DECODE_MIN_KEYS or not _aligned16(q)
+            or query.device != cache.device):
+        return None
+    import torch
+
+    multiplier = 1 / math.sqrt(dim) if scale is None else scale
+    prob = _problem(b, hq, hkv, qlen, cache.length, dim, dim, code, multiplier, is_causal,
+                    causal_offset)
+    keys, values, key_scales, value_scales = cache.storage
+    out = torch.empty((b, hq, qlen, dim), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(
+        lib.tsattn_decode_forward_int8(
+            ctypes.byref(prob), _view(q), _view(keys), _view(values), _view(key_scales),
+            _view(value_scales), _view(out), 0, ctypes.c_void_p(ws.data_ptr()), nbytes,
+            ctypes.c_void_p(current_stream(query.device))),
+        "int8 decode forward")
+    return Tensor._from_op(out, (query,), None, "sdpa_hip")
+
+
 def rotary_embedding(input: Tensor, offset: int = 0, base: float = 10000.0,
                      rotary_dim: int | None = None) -> Tensor:
     """Interleaved-pair RoPE for [..., sequence, channels] with inverse-rotation VJP.

@@ -8,6 +8,12 @@ mode stores symmetric per-token/head codes with one fp32 scale each
 (``scale = max(max|x| / 127, 1e-8)``, ``q = round(x / scale)``, ``:73-77``),
 dequantised on ``get`` (``:91-98``).  The views ``get`` returns feed the decode
 kernel directly (no copy: the kernel takes the cache's strides).
+
+On the hip device an int8 append is one fused kernel
+(``tsattn_kv_append_int8``: row max, scale, rounding and both writes), and
+``MultiHeadAttention`` decodes over the int8 storage itself
+(``tsattn_decode_forward_int8`` dequantises inside the kernel) instead of
+going through ``get``.
 """
 
 from __future__ import annotations
@@ -16,6 +22,11 @@ import math
 
 import numpy as np
 
+import ctypes
+
+from .. import _lib
+from ..device import current_stream
+from .attention import _view
 from ..device import device as parse_device
 from ..tensor import Tensor, backend_dtype, is_grad_enabled, to_numpy
 
@@ -53,6 +64,11 @@ class KVCache:
 
     def append(self, key: Tensor, value: Tensor) -> tuple[Tensor, Tensor]:
         """Append a chunk after validating all shapes and capacity."""
+        self._append(key, value)
+        return self.get()
+
+    def _append(self, key: Tensor, value: Tensor) -> None:
+        """``append`` without building the returned views."""
         if key.device != self.device or value.device != self.device:
             raise ValueError("cache and key/value tensors must be on the same device")
         if is_grad_enabled() and (key.requires_grad or value.requires_grad):
@@ -68,14 +84,12 @@ class KVCache:
         window = slice(self.length, stop)
         keys, values = key._data.to(self.dtype), value._data.to(self.dtype)
         if self.quantized:
-            keys, key_scales = _quantize(keys)
-            values, value_scales = _quantize(values)
-            self._key_scales[:, :, window] = key_scales
-            self._value_scales[:, :, window] = value_scales
-        self._keys[:, :, window] = keys
-        self._values[:, :, window] = values
+            _append_int8(keys, self._keys, self._key_scales, self.length, self.device)
+            _append_int8(values, self._values, self._value_scales, self.length, self.device)
+        else:
+            self._keys[:, :, window] = keys
+            self._values[:, :, window] = values
         self.length = stop
-        return self.get()
 
     def get(self) -> tuple[Tensor, Tensor]:
         keys = self._keys[:, :, : self.length]
@@ -131,9 +145,18 @@ class KVCache:
                 f"quantized={self.quantized}, device='{self.device}')")
 
 
-def _quantize(raw):
-    import torch
+_CODES = {"torch.float32": _lib.F32, "torch.float16": _lib.F16, "torch.bfloat16": _lib.BF16}
 
-    raw = raw.float()
-    scale = torch.clamp(raw.abs().amax(dim=-1, keepdim=True) / 127, min=1e-8)
-    return torch.round(raw / scale).to(torch.int8), scale
+
+def _append_int8(rows, codes, scales, pos: int, dev) -> None:
+    """Quantise rows [B, H, T, D] (cache dtype) into codes[:, :, pos:pos+T] and
+    scales[:, :, pos:pos+T] with the fused append kernel."""
+    if rows.stride(-1) != 1:
+        rows = rows.contiguous()
+    b, h, t, d = rows.shape
+    _lib.check(
+        _lib.load().tsattn_kv_append_int8(
+            _CODES[str(rows.dtype)], b, h, t, d, ctypes.byref(_view(rows)),
+            ctypes.byref(_view(codes)), ctypes.byref(_view(scales)), pos,
+            ctypes.c_void_p(current_stream(dev))),
+        "int8 cache append")

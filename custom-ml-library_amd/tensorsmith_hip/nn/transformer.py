@@ -25,7 +25,7 @@ from dataclasses import dataclass
 from .. import device as _device
 from ..tensor import Tensor, cat, is_grad_enabled, no_grad
 from . import functional as F
-from .attention import BACKENDS, rotary_embedding, scaled_dot_product_attention
+from .attention import BACKENDS, decode_int8_cache, rotary_embedding, scaled_dot_product_attention
 from .cache import KVCache
 from .layers import Dropout, Embedding, Linear
 from .module import Module, Parameter
@@ -95,12 +95,19 @@ class MultiHeadAttention(Module):
         if self.rotary:
             q = rotary_embedding(q, offset)
             k = rotary_embedding(k, offset if context is None else 0)
+        attended = None
         if cache is not None:
-            k, v = cache.append(k, v)
-        attended = scaled_dot_product_attention(
-            q, k, v, attn_mask, self.dropout_p if self.training else 0.0, is_causal,
-            causal_offset=offset, backend=self.backend,
-            enable_gqa=self.num_kv_heads != self.num_heads)
+            cache._append(k, v)
+            if cache.quantized and attn_mask is None:
+                # decode straight over the int8 storage (dequantised in the kernel)
+                attended = decode_int8_cache(q, cache, is_causal=is_causal, causal_offset=offset)
+            if attended is None:
+                k, v = cache.get()
+        if attended is None:
+            attended = scaled_dot_product_attention(
+                q, k, v, attn_mask, self.dropout_p if self.training else 0.0, is_causal,
+                causal_offset=offset, backend=self.backend,
+                enable_gqa=self.num_kv_heads != self.num_heads)
         return self.out_proj(attended.permute(0, 2, 1, 3).reshape(batch, steps, self.embed_dim))
 
 

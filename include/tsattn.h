@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 1
+#define TSATTN_ABI_VERSION 2
 
 typedef enum {
   TSATTN_OK = 0,
@@ -153,6 +153,34 @@ size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);
 int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                           const tsattn_view *v, const tsattn_view *out, int32_t split_len,
                           void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * KV-cache decode over an int8 cache: k / v are int8 views [B, Hkv, capacity,
+ * D] with fp32 row scales k_scale / v_scale [B, Hkv, capacity, 1] -- the
+ * reference's quantised KVCache format (src/tensorsmith/nn/cache.py:48-52,
+ * :73-77).  The rows are dequantised inside the kernel (x = q * scale), where
+ * the reference dequantises the whole prefix eagerly in KVCache.get
+ * (cache.py:88-99) before the dense attention.  q / out are f16 or bf16
+ * (p->dtype); everything else is as tsattn_decode_forward, whose workspace
+ * size query applies unchanged.  A mask is accepted only as key-padding
+ * lengths (p->kv_len).
+ */
+int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                               const tsattn_view *v, const tsattn_view *k_scale,
+                               const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * KV-cache append into the int8 format (KVCache.append with quantized=True,
+ * src/tensorsmith/nn/cache.py:54-86, quantiser at :73-77): every row
+ * x = src[b, h, t, 0:dim] (dtype f32 / f16 / bf16, already the cache dtype)
+ * is stored as round_half_even(x / s) in dst[b, h, pos + t, :] (int8) with
+ * s = max(max|x| / 127, 1e-8) in scale[b, h, pos + t, 0] (fp32), in one
+ * pass.  Bit-identical to the reference's NumPy arithmetic.
+ */
+int tsattn_kv_append_int8(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                          const tsattn_view *src, const tsattn_view *dst, const tsattn_view *scale,
+                          int64_t pos, void *stream);
 
 /*
  * Boolean key mask [B, K] (strides in bytes-as-elements) -> kv_len[b] = 1 +

@@ -124,3 +124,25 @@ class generic_only:
     def __exit__(self, *exc):
         _lib.set_kernel_policy(0)
         return False
+
+
+def decode_int8(q, k8, v8, kscale, vscale, len_kv, split_len=0, **kw):
+    """tsattn_decode_forward_int8 over the first len_kv rows of int8 caches."""
+    p = problem(q, k8, v8, **kw)
+    p.len_kv = len_kv
+    out = torch.empty(q.shape[:3] + (v8.shape[3],), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    nbytes = lib.tsattn_decode_workspace(ctypes.byref(p), split_len)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.tsattn_decode_forward_int8(
+        ctypes.byref(p), view(q), view(k8), view(v8), view(kscale), view(vscale), view(out),
+        split_len, ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "int8 decode")
+    return out, lib.tsattn_last_kernel_path()
+
+
+def kv_append_int8(src, codes, scales, pos):
+    """tsattn_kv_append_int8: quantise src [B,H,T,D] into codes/scales at pos."""
+    b, h, t, d = src.shape
+    _lib.check(_lib.load().tsattn_kv_append_int8(
+        CODES[src.dtype], b, h, t, d, view(src), view(codes), view(scales), pos, stream()),
+        "int8 append")
