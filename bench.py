@@ -69,7 +69,8 @@ def parse():
     ap.add_argument("--cpu-batches", type=int, default=4,
                     help="batch rows (of 16 heads each) in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--workload", choices=["all", "fwd_bwd", "decode", "prefill", "lm", "copy"],
+    ap.add_argument("--workload",
+                    choices=["all", "fwd_bwd", "decode", "decode_int8", "prefill", "lm", "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -204,6 +205,78 @@ def bench_decode(ts, torch, steps, warmup):
                    "heads": DEC_H, "head_dim": DEC_D, "cache_capacity": DEC_CAP,
                    "lengths": "U[512,8192] seeded", "sum_len": int(lens.sum())},
     }, {"q": q_raw, "k": k_raw, "v": v_raw, "lengths": lens}
+
+
+def bench_decode_int8(ts, torch, steps, warmup, dec_inputs):
+    """The decode workload over an int8 cache (the reference's quantised
+    KVCache format): the same fp16 K/V, quantised once by the fused append
+    kernel, then decoded with the int8 split-K kernel (dequantised inside),
+    per-sequence lengths passed as kv_len."""
+    import ctypes
+
+    import numpy as np
+
+    from tensorsmith_hip import _lib
+    from tensorsmith_hip.nn.attention import _problem, _view
+
+    lib = _lib.load()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    q_raw, k_raw, v_raw = dec_inputs["q"], dec_inputs["k"], dec_inputs["v"]
+    lens = dec_inputs["lengths"]
+    shape = (DEC_B, DEC_H, DEC_CAP, DEC_D)
+    k8, v8 = (torch.empty(shape, dtype=torch.int8, device="cuda") for _ in range(2))
+    ks, vs = (torch.empty(shape[:3] + (1,), dtype=torch.float32, device="cuda") for _ in range(2))
+    for src, codes, scales in ((k_raw, k8, ks), (v_raw, v8, vs)):
+        _lib.check(lib.tsattn_kv_append_int8(_lib.F16, DEC_B, DEC_H, DEC_CAP, DEC_D,
+                                             ctypes.byref(_view(src)), ctypes.byref(_view(codes)),
+                                             ctypes.byref(_view(scales)), 0, stream), "append")
+    kv_len = torch.as_tensor(lens.astype(np.int32), device="cuda")
+    prob = _problem(DEC_B, DEC_H, DEC_H, 1, DEC_CAP, DEC_D, DEC_D, _lib.F16, 1 / math.sqrt(DEC_D),
+                    False, 0)
+    prob.kv_len = kv_len.data_ptr()
+    out = torch.empty((DEC_B, DEC_H, 1, DEC_D), dtype=torch.float16, device="cuda")
+    nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device="cuda")
+    views = [ctypes.byref(_view(t)) for t in (q_raw, k8, v8, ks, vs, out)]
+
+    def step():
+        _lib.check(lib.tsattn_decode_forward_int8(ctypes.byref(prob), *views, 0,
+                                                  ctypes.c_void_p(ws.data_ptr()), nbytes, stream),
+                   "int8 decode")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.profile_enable(False)
+    kernels = _lib.profile_read()
+    kv_bytes = float(lens.sum()) * DEC_H * (DEC_D + 4) * 2  # int8 rows + fp32 scales, K and V
+    total_bytes = kv_bytes + 2.0 * DEC_B * DEC_H * DEC_D * 2
+    ms = elapsed / steps * 1e3
+    split_ms = kernels["decode_split_int8"][1] / kernels["decode_split_int8"][0]
+    achieved = total_bytes / (split_ms * 1e-3) / 1e9
+    return {
+        "metric": "decode tokens/s (int8 cache)",
+        "value": DEC_B / (ms * 1e-3),
+        "unit": "tokens/s",
+        "ms_per_step": ms,
+        "bytes_per_step": total_bytes,
+        "kernels": {n: {"launches": c, "mean_ms": round(t / max(c, 1), 4)}
+                    for n, (c, t) in kernels.items()},
+        "roofline": {
+            "kernel": "decode_split_int8", "bound": "hbm", "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+        },
+        "config": {"workload": "decode_int8cache_f16q_b64h32d128_len512_8192", "batch": DEC_B,
+                   "heads": DEC_H, "head_dim": DEC_D, "cache_capacity": DEC_CAP},
+    }
 
 
 def bench_prefill(ts, torch, steps, warmup):
@@ -439,6 +512,11 @@ def main():
         dec_res, _ = bench_decode(ts, torch, args.decode_steps, args.warmup)
         print(json.dumps({"decode": dec_res}), flush=True)
         return
+    if args.workload == "decode_int8":
+        _, dec_host = bench_decode(ts, torch, 2, 1)
+        q8 = bench_decode_int8(ts, torch, args.decode_steps, args.warmup, dec_host)
+        print(json.dumps({"decode_int8": q8}), flush=True)
+        return
     if args.workload == "prefill":
         print(json.dumps({"prefill": bench_prefill(ts, torch, 3, 1)}), flush=True)
         return
@@ -456,6 +534,9 @@ def main():
         return
     dec_res, dec_host = bench_decode(ts, torch, args.decode_steps, args.warmup)
     print(f"[bench] decode {dec_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
+    q8_res = bench_decode_int8(ts, torch, args.decode_steps, args.warmup, dec_host)
+    print(f"[bench] int8-cache decode {q8_res['ms_per_step']:.3f} ms/step", file=sys.stderr,
+          flush=True)
     pf_res = bench_prefill(ts, torch, 3, 1)
     print(f"[bench] prefill {pf_res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
     lm_res = bench_lm(ts, torch, 5, 2)
@@ -485,6 +566,7 @@ def main():
         "kernels": main_res["kernels"],
         "cpu_baseline": cpu,
         "decode": dec_res,
+        "decode_int8": q8_res,
         "prefill": pf_res,
         "lm_step": lm_res,
     }

@@ -9,9 +9,9 @@
 // the same rescale-by-exp(m - M) rule.  Fully masked rows give 0.
 //
 // Memory layout: each key row is read by D/8 neighbouring lanes as 16-byte
-// loads (one wave instruction covers 64*16 B of consecutive keys), U such
-// instructions for K and U for V are issued before any is consumed, so every
-// wave keeps 2*U KiB in flight.
+// loads (one wave instruction covers 64*16 B of consecutive keys), kU such
+// instructions for K and kU for V are issued before any is consumed, so every
+// wave keeps 2*kU KiB in flight.
 //
 // int8 caches (the reference's quantised KVCache, src/tensorsmith/nn/
 // cache.py:73-77 and :91-98): K and V rows are int8 with one fp32 scale per
@@ -29,7 +29,7 @@ namespace tsattn {
 namespace {
 
 constexpr int NT = 256;
-constexpr int U = 4;  // key instructions in flight per batch (per operand)
+constexpr int kU = 4;  // key instructions in flight per batch (per operand, 16-byte loads)
 constexpr int kMaxRows = 8;
 
 struct DecArgs {
@@ -111,6 +111,7 @@ __device__ __forceinline__ float group_sum(float d) {
 template <typename T, int D, int R, bool Q8>
 __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
   using KT = std::conditional_t<Q8, int8_t, T>;  // cache element type
+  constexpr int U = kU;
   constexpr int LPK = D / 8;      // lanes per key row
   constexpr int KPI = 64 / LPK;   // keys per wave instruction
   constexpr int BATCH = KPI * U;  // keys per wave per batch
@@ -167,6 +168,14 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
     for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
       KvChunk<Q8> kr[U], vr[U];
       float ksc[U], vsc[U];
+      float kslot = 0.f, vslot = 0.f;
+      if constexpr (Q8) {
+        // one scale load per operand for the batch's BATCH keys: lane l takes
+        // key kb + l % BATCH; each lane then shuffles in its own keys' scales
+        const int key = min(kb + (lane % BATCH), k_stop - 1);
+        kslot = ksb[static_cast<int64_t>(key) * a.ks.s2];
+        vslot = vsb[static_cast<int64_t>(key) * a.vs.s2];
+      }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int key = min(kb + u * KPI + kg, k_stop - 1);
@@ -174,9 +183,12 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
             reinterpret_cast<const KvChunk<Q8> *>(kbase + static_cast<int64_t>(key) * a.k.s2));
         vr[u] = __builtin_nontemporal_load(
             reinterpret_cast<const KvChunk<Q8> *>(vbase + static_cast<int64_t>(key) * a.v.s2));
-        if constexpr (Q8) {
-          ksc[u] = ksb[static_cast<int64_t>(key) * a.ks.s2];
-          vsc[u] = vsb[static_cast<int64_t>(key) * a.vs.s2];
+      }
+      if constexpr (Q8) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          ksc[u] = __shfl(kslot, u * KPI + kg, 64);
+          vsc[u] = __shfl(vslot, u * KPI + kg, 64);
         }
       }
       float s[U][R];
