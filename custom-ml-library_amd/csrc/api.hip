@@ -277,6 +277,55 @@ int tsattn_kv_append_int8(int32_t dtype, int32_t batch, int32_t heads, int32_t l
                     "int8 append launch");
 }
 
+int tsattn_rope(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                int32_t rotary_dim, const tsattn_view *x, const tsattn_view *out, const void *cos,
+                const void *sin, int64_t pos0, int32_t inverse, void *stream) {
+  int rc;
+  if ((rc = check_view(x, "input")) || (rc = check_view(out, "output"))) return rc;
+  if (dtype != TSATTN_F32 && dtype != TSATTN_F16 && dtype != TSATTN_BF16)
+    return fail(TSATTN_ERR_INVALID, "RoPE rows must be f32, f16 or bf16 (got dtype %d)", dtype);
+  if (batch <= 0 || heads <= 0 || len <= 0 || dim <= 0 || pos0 < 0)
+    return fail(TSATTN_ERR_INVALID, "RoPE needs positive sizes and a nonnegative position");
+  if (rotary_dim <= 0 || rotary_dim % 2 || rotary_dim > dim || dim % 2)
+    return fail(TSATTN_ERR_INVALID, "RoPE requires a positive even rotary dimension and valid positions/base");
+  if (!cos || !sin) return fail(TSATTN_ERR_INVALID, "RoPE needs cos / sin tables");
+  return hip_status(tsattn::launch_rope(dtype, batch, heads, len, dim, rotary_dim,
+                                        tsattn::make_view(x), tsattn::make_view(out), cos, sin,
+                                        pos0, inverse, static_cast<hipStream_t>(stream)),
+                    "RoPE launch");
+}
+
+int tsattn_rope_append(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                       int32_t rotary_dim, const tsattn_view *k, const tsattn_view *v,
+                       const tsattn_view *k_cache, const tsattn_view *v_cache,
+                       const tsattn_view *k_scale, const tsattn_view *v_scale, const void *cos,
+                       const void *sin, int64_t pos, void *stream) {
+  int rc;
+  if ((rc = check_view(k, "key rows")) || (rc = check_view(v, "value rows")) ||
+      (rc = check_view(k_cache, "key cache")) || (rc = check_view(v_cache, "value cache")))
+    return rc;
+  if (!k_scale != !v_scale)
+    return fail(TSATTN_ERR_INVALID, "an int8 cache needs both key and value scales");
+  if ((k_scale && (rc = check_view(k_scale, "key scales"))) ||
+      (v_scale && (rc = check_view(v_scale, "value scales"))))
+    return rc;
+  if (dtype != TSATTN_F32 && dtype != TSATTN_F16 && dtype != TSATTN_BF16)
+    return fail(TSATTN_ERR_INVALID, "cache rows must be f32, f16 or bf16 (got dtype %d)", dtype);
+  if (batch <= 0 || heads <= 0 || len <= 0 || dim <= 0 || dim % 2 || pos < 0)
+    return fail(TSATTN_ERR_INVALID, "append needs positive sizes, an even head dim and a nonnegative position");
+  if (dim > 512) return fail(TSATTN_ERR_UNSUPPORTED, "head dims above 512 are not supported");
+  if (rotary_dim < 0 || rotary_dim % 2 || rotary_dim > dim || (rotary_dim && (!cos || !sin)))
+    return fail(TSATTN_ERR_INVALID, "RoPE requires a positive even rotary dimension and valid positions/base");
+  tsattn::View ks, vs;
+  if (k_scale) ks = tsattn::make_view(k_scale), vs = tsattn::make_view(v_scale);
+  return hip_status(tsattn::launch_rope_append(dtype, batch, heads, len, dim, rotary_dim,
+                                               tsattn::make_view(k), tsattn::make_view(v),
+                                               tsattn::make_view(k_cache), tsattn::make_view(v_cache),
+                                               k_scale ? &ks : nullptr, v_scale ? &vs : nullptr,
+                                               cos, sin, pos, static_cast<hipStream_t>(stream)),
+                    "RoPE append launch");
+}
+
 int tsattn_key_mask_lengths(const uint8_t *mask, int64_t stride_b, int64_t stride_k,
                             int32_t batch, int32_t len_kv, int32_t *kv_len, int32_t *kv_prefix,
                             void *stream) {

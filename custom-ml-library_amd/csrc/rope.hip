@@ -1,0 +1,196 @@
+// Interleaved-pair rotary position embedding (the reference's
+// rotary_embedding, src/tensorsmith/nn/attention.py:255-296) as one kernel,
+// and the same rotation fused with the KV-cache append (cache.py:54-86).
+//
+// For channel pair (2i, 2i+1) of row t: c = cos[p, i], s = sin[p, i] with
+// p = pos0 + t, taken from tables the host builds exactly as the reference
+// does (fp32 angles p * base^(-2i/dim), cos / sin, cast to the tensor
+// dtype).  The arithmetic follows the reference's per-operation rounding in
+// the tensor dtype:
+//   y0 = rnd(rnd(x0 c) + rnd(-x1 s)),  y1 = rnd(rnd(x1 c) + rnd(x0 s)),
+// rnd = round to T (for f32 each product and sum rounds once: no fused
+// multiply-add), so results are bit-identical.  `inverse` rotates by -angle
+// (the VJP, :289-294).  Channels at or past rotary_dim pass through.
+#include <type_traits>
+
+#include "mfma_common.h"
+
+namespace tsattn {
+namespace {
+
+constexpr int NT = 256;
+
+// Each product and sum rounds on its own: contraction into a fused
+// multiply-add (hipcc's default for device code) is switched off here.
+template <typename T>
+__device__ __forceinline__ T rmul(T a, T b) {
+#pragma clang fp contract(off)
+  if constexpr (std::is_same<T, float>::value) return a * b;
+  else return static_cast<T>(static_cast<float>(a) * static_cast<float>(b));
+}
+template <typename T>
+__device__ __forceinline__ T radd(T a, T b) {
+#pragma clang fp contract(off)
+  if constexpr (std::is_same<T, float>::value) return a + b;
+  else return static_cast<T>(static_cast<float>(a) + static_cast<float>(b));
+}
+
+// Rotate one row in place in registers: pairs p = lane, lane + 64, ...
+template <typename T>
+__device__ __forceinline__ void rotate_pair(T &x0, T &x1, T c, T s, bool inverse) {
+  const T sn = inverse ? static_cast<T>(-static_cast<float>(s)) : s;
+  const T y0 = radd(rmul(x0, c), rmul(static_cast<T>(-static_cast<float>(x1)), sn));
+  const T y1 = radd(rmul(x1, c), rmul(x0, sn));
+  x0 = y0;
+  x1 = y1;
+}
+
+struct RopeArgs {
+  int B, H, T, D, R;  // R = rotary dim (even, <= D)
+  View x, out;        // [B, H, T, D]
+  const void *cos, *sin;  // [*, R / 2] rows in the tensor dtype
+  int64_t pos0;
+  int inverse;
+};
+
+template <typename T>
+__global__ __launch_bounds__(NT) void rope_kernel(RopeArgs a) {
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= static_cast<int64_t>(a.B) * a.H * a.T) return;
+  const int t = static_cast<int>(row % a.T);
+  const int64_t bh = row / a.T;
+  const int h = static_cast<int>(bh % a.H), b = static_cast<int>(bh / a.H);
+  const T *x = static_cast<const T *>(a.x.data) + b * a.x.s0 + h * a.x.s1 + static_cast<int64_t>(t) * a.x.s2;
+  T *y = static_cast<T *>(const_cast<void *>(a.out.data)) + b * a.out.s0 + h * a.out.s1 +
+         static_cast<int64_t>(t) * a.out.s2;
+  const T *cr = static_cast<const T *>(a.cos) + (a.pos0 + t) * (a.R / 2);
+  const T *sr = static_cast<const T *>(a.sin) + (a.pos0 + t) * (a.R / 2);
+  for (int p = lane; 2 * p < a.D; p += 64) {
+    T x0 = x[2 * p], x1 = x[2 * p + 1];
+    if (2 * p < a.R) rotate_pair(x0, x1, cr[p], sr[p], a.inverse != 0);
+    y[2 * p] = x0;
+    y[2 * p + 1] = x1;
+  }
+}
+
+struct AppendArgs {
+  int B, H, T, D, R;      // R = 0: no rotation
+  View k, v;              // new rows [B, H, T, D]
+  View kc, vc, ks, vs;    // cache storage; ks / vs set for int8 caches
+  const void *cos, *sin;  // [*, R / 2]
+  int64_t pos;
+};
+
+// Quantise one wave-held row (PER values per lane, channels 2p, 2p + 1 for
+// p = lane + 64 j) into int8 codes + scale, as the reference (cache.py:73-77).
+template <typename T, int PER>
+__device__ __forceinline__ void store_int8_row(const T (&x)[PER][2], int D, int lane, int8_t *q,
+                                               float *scale) {
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (2 * (lane + 64 * j) < D)
+      m = fmaxf(m, fmaxf(fabsf(static_cast<float>(x[j][0])), fabsf(static_cast<float>(x[j][1]))));
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+  const float s = fmaxf(m / 127.f, 1e-8f);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int p = lane + 64 * j;
+    if (2 * p < D) {
+      q[2 * p] = static_cast<int8_t>(rintf(static_cast<float>(x[j][0]) / s));
+      q[2 * p + 1] = static_cast<int8_t>(rintf(static_cast<float>(x[j][1]) / s));
+    }
+  }
+  if (lane == 0) *scale = s;
+}
+
+template <typename T, bool Q8>
+__global__ __launch_bounds__(NT) void rope_append_kernel(AppendArgs a) {
+  constexpr int PER = 4;  // pairs per lane: D <= 512
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (NT / 64) + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= static_cast<int64_t>(a.B) * a.H * a.T) return;
+  const int t = static_cast<int>(row % a.T);
+  const int64_t bh = row / a.T;
+  const int h = static_cast<int>(bh % a.H), b = static_cast<int>(bh / a.H);
+  const int64_t tp = a.pos + t;
+  const T *kx = static_cast<const T *>(a.k.data) + b * a.k.s0 + h * a.k.s1 + static_cast<int64_t>(t) * a.k.s2;
+  const T *vx = static_cast<const T *>(a.v.data) + b * a.v.s0 + h * a.v.s1 + static_cast<int64_t>(t) * a.v.s2;
+  const T *cr = static_cast<const T *>(a.cos) + tp * (a.R / 2);
+  const T *sr = static_cast<const T *>(a.sin) + tp * (a.R / 2);
+  T kr[PER][2], vr[PER][2];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int p = lane + 64 * j;
+    kr[j][0] = kr[j][1] = vr[j][0] = vr[j][1] = static_cast<T>(0.f);
+    if (2 * p < a.D) {
+      kr[j][0] = kx[2 * p];
+      kr[j][1] = kx[2 * p + 1];
+      vr[j][0] = vx[2 * p];
+      vr[j][1] = vx[2 * p + 1];
+      if (2 * p < a.R) rotate_pair(kr[j][0], kr[j][1], cr[p], sr[p], false);
+    }
+  }
+  if constexpr (Q8) {
+    int8_t *kq = static_cast<int8_t *>(const_cast<void *>(a.kc.data)) + b * a.kc.s0 + h * a.kc.s1 + tp * a.kc.s2;
+    int8_t *vq = static_cast<int8_t *>(const_cast<void *>(a.vc.data)) + b * a.vc.s0 + h * a.vc.s1 + tp * a.vc.s2;
+    float *ksp = static_cast<float *>(const_cast<void *>(a.ks.data)) + b * a.ks.s0 + h * a.ks.s1 + tp * a.ks.s2;
+    float *vsp = static_cast<float *>(const_cast<void *>(a.vs.data)) + b * a.vs.s0 + h * a.vs.s1 + tp * a.vs.s2;
+    store_int8_row<T, PER>(kr, a.D, lane, kq, ksp);
+    store_int8_row<T, PER>(vr, a.D, lane, vq, vsp);
+  } else {
+    T *kc = static_cast<T *>(const_cast<void *>(a.kc.data)) + b * a.kc.s0 + h * a.kc.s1 + tp * a.kc.s2;
+    T *vc = static_cast<T *>(const_cast<void *>(a.vc.data)) + b * a.vc.s0 + h * a.vc.s1 + tp * a.vc.s2;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int p = lane + 64 * j;
+      if (2 * p < a.D) {
+        kc[2 * p] = kr[j][0];
+        kc[2 * p + 1] = kr[j][1];
+        vc[2 * p] = vr[j][0];
+        vc[2 * p + 1] = vr[j][1];
+      }
+    }
+  }
+}
+
+dim3 row_grid(int B, int H, int T) {
+  const int64_t rows = static_cast<int64_t>(B) * H * T;
+  return dim3(static_cast<unsigned>((rows + NT / 64 - 1) / (NT / 64)));
+}
+
+}  // namespace
+
+hipError_t launch_rope(int dtype, int B, int H, int T, int D, int R, View x, View out,
+                       const void *cos, const void *sin, int64_t pos0, int inverse, hipStream_t st) {
+  RopeArgs a{B, H, T, D, R, x, out, cos, sin, pos0, inverse};
+  Probe pr_("rope", st);
+  if (dtype == TSATTN_F32) rope_kernel<float><<<row_grid(B, H, T), NT, 0, st>>>(a);
+  else if (dtype == TSATTN_F16) rope_kernel<f16><<<row_grid(B, H, T), NT, 0, st>>>(a);
+  else rope_kernel<bf16><<<row_grid(B, H, T), NT, 0, st>>>(a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_append(int dtype, int B, int H, int T, int D, int R, View k, View v, View kc,
+                              View vc, const View *ks, const View *vs, const void *cos,
+                              const void *sin, int64_t pos, hipStream_t st) {
+  AppendArgs a{B, H, T, D, R, k, v, kc, vc, ks ? *ks : View{}, vs ? *vs : View{}, cos, sin, pos};
+  const bool q8 = ks != nullptr;
+  Probe pr_(q8 ? "rope_append_int8" : "rope_append", st);
+  const dim3 g = row_grid(B, H, T);
+  if (dtype == TSATTN_F32) {
+    if (q8) rope_append_kernel<float, true><<<g, NT, 0, st>>>(a);
+    else rope_append_kernel<float, false><<<g, NT, 0, st>>>(a);
+  } else if (dtype == TSATTN_F16) {
+    if (q8) rope_append_kernel<f16, true><<<g, NT, 0, st>>>(a);
+    else rope_append_kernel<f16, false><<<g, NT, 0, st>>>(a);
+  } else {
+    if (q8) rope_append_kernel<bf16, true><<<g, NT, 0, st>>>(a);
+    else rope_append_kernel<bf16, false><<<g, NT, 0, st>>>(a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace tsattn

@@ -140,6 +140,16 @@ hipError_t launch_decode_int8(const Problem &p, int dtype, View q, View k, View 
 hipError_t launch_kv_append_int8(int dtype, int B, int H, int T, int D, View src, View dst,
                                  View scale, int64_t pos, hipStream_t st);
 
+// Interleaved-pair RoPE of x [B, H, T, D] into out (may alias x), cos / sin
+// tables [*, R / 2] in the tensor dtype, rows pos0 .. pos0 + T - 1.
+hipError_t launch_rope(int dtype, int B, int H, int T, int D, int R, View x, View out,
+                       const void *cos, const void *sin, int64_t pos0, int inverse, hipStream_t st);
+// RoPE of the new K rows (R = 0: none) fused with the K/V cache append at
+// `pos`; ks / vs non-null for int8 caches (then quantised as the int8 append).
+hipError_t launch_rope_append(int dtype, int B, int H, int T, int D, int R, View k, View v, View kc,
+                              View vc, const View *ks, const View *vs, const void *cos,
+                              const void *sin, int64_t pos, hipStream_t st);
+
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st);
 

@@ -267,13 +267,51 @@ def decode_int8_cache(query: Tensor, cache, *, is_causal: bool, causal_offset: i
     return Tensor._from_op(out, (query,), None, "sdpa_hip")
 
 
+_ROPE_TABLES: dict = {}
+
+
+def rope_tables(base: float, dim: int, dtype, dev, length: int):
+    """Device (cos, sin) tables [L >= length, dim / 2] in ``dtype`` for
+    positions 0 .. L - 1, built as the reference builds its per-call tables
+    (``attention.py:269-279``: float32 angles, NumPy cos / sin, cast to the
+    tensor dtype); an angle depends only on its absolute position, so one
+    table serves every offset.  Grown on demand and kept per (base, dim,
+    dtype, device)."""
+    import torch
+
+    key = (float(base), int(dim), str(dtype), str(dev))
+    have = _ROPE_TABLES.get(key)
+    if have is not None and have[0].shape[0] >= length:
+        return have
+    n = max(length, 2 * (have[0].shape[0] if have is not None else 0), 256)
+    freqs = base ** (-(np.arange(0, dim, 2, dtype=np.float32)) / np.float32(dim))
+    angles = np.arange(0, n, dtype=np.float32)[:, None] * freqs[None, :]
+    made = tuple(torch.from_numpy(np.ascontiguousarray(f(angles))).to(device=dev, dtype=dtype)
+                 for f in (np.cos, np.sin))
+    _ROPE_TABLES[key] = made
+    return made
+
+
+def _rope_launch(x, out, offset: int, base: float, dim: int, inverse: bool, dev) -> None:
+    b, h, t, d = x.shape
+    cos, sin = rope_tables(base, dim, x.dtype, x.device, offset + t)
+    _lib.check(
+        _lib.load().tsattn_rope(
+            _dtype_code(x.dtype), b, h, t, d, dim, ctypes.byref(_view(x)), ctypes.byref(_view(out)),
+            ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()), offset, int(inverse),
+            ctypes.c_void_p(current_stream(dev))),
+        "RoPE")
+
+
 def rotary_embedding(input: Tensor, offset: int = 0, base: float = 10000.0,
                      rotary_dim: int | None = None) -> Tensor:
     """Interleaved-pair RoPE for [..., sequence, channels] with inverse-rotation VJP.
 
     Same contract as the reference (``src/tensorsmith/nn/attention.py:255-296``):
     pairs (2i, 2i+1) rotate by angle ``pos * base**(-2i/dim)``, positions start
-    at ``offset``, channels past ``rotary_dim`` pass through.
+    at ``offset``, channels past ``rotary_dim`` pass through.  4-D f32 / f16 /
+    bf16 inputs on the hip device run one kernel (``tsattn_rope``, bit-identical
+    to the reference's array arithmetic), forward and VJP.
     """
     if input.ndim < 2:
         raise ValueError("RoPE requires at least sequence and channel dimensions")
@@ -281,13 +319,27 @@ def rotary_embedding(input: Tensor, offset: int = 0, base: float = 10000.0,
     if dim <= 0 or dim % 2 or dim > input.shape[-1] or offset < 0 or base <= 0 or not math.isfinite(base):
         raise ValueError("RoPE requires a positive even rotary dimension and valid positions/base")
     x = input._data
+    import torch
+
+    if (input.ndim == 4 and input.shape[-1] % 2 == 0 and input.device.type == "hip"
+            and x.dtype in (torch.float32, torch.float16, torch.bfloat16)):
+        src = x if x.stride(-1) == 1 else x.contiguous()
+        out = torch.empty(src.shape, dtype=src.dtype, device=src.device)
+        _rope_launch(src, out, offset, base, dim, False, input.device)
+
+        def backward(g):
+            g = g if g.stride(-1) == 1 else g.contiguous()
+            dx = torch.empty(g.shape, dtype=g.dtype, device=g.device)
+            _rope_launch(g, dx, offset, base, dim, True, input.device)
+            return (dx,)
+
+        return Tensor._from_op(out, (input,), backward, "rope")
+
     seq = input.shape[-2]
     freqs = base ** (-(np.arange(0, dim, 2, dtype=np.float32)) / np.float32(dim))
     angles = np.arange(offset, offset + seq, dtype=np.float32)[:, None] * freqs[None, :]
     cos = np.repeat(np.cos(angles), 2, axis=-1)
     sin = np.repeat(np.sin(angles), 2, axis=-1)
-    import torch
-
     cos_t = torch.from_numpy(cos).to(device=x.device, dtype=x.dtype)
     sin_t = torch.from_numpy(sin).to(device=x.device, dtype=x.dtype)
 

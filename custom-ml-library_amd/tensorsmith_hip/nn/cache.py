@@ -69,6 +69,55 @@ class KVCache:
 
     def _append(self, key: Tensor, value: Tensor) -> None:
         """``append`` without building the returned views."""
+        stop = self._check(key, value)
+        window = slice(self.length, stop)
+        keys, values = key._data.to(self.dtype), value._data.to(self.dtype)
+        if self.quantized:
+            _append_int8(keys, self._keys, self._key_scales, self.length, self.device)
+            _append_int8(values, self._values, self._value_scales, self.length, self.device)
+        else:
+            self._keys[:, :, window] = keys
+            self._values[:, :, window] = values
+        self.length = stop
+
+    def _append_rotary(self, key: Tensor, value: Tensor, base: float = 10000.0) -> bool:
+        """Rotate ``key`` by RoPE at positions ``length ..`` and append it with
+        ``value`` in one kernel (``tsattn_rope_append``).
+
+        Same result as ``rotary_embedding(key, self.length)`` followed by
+        ``_append``: the rotation runs in the key dtype, which must be the
+        cache dtype here (else False is returned and nothing is written, so
+        the caller takes the two-step path).  Needs an even head dim
+        <= 512 equal to the value dim.
+        """
+        import torch
+
+        if (key._data.dtype != self.dtype or value._data.dtype != self.dtype
+                or self.dtype not in (torch.float32, torch.float16, torch.bfloat16)
+                or self.head_dim % 2 or self.head_dim > 512 or self.value_dim != self.head_dim):
+            return False
+        stop = self._check(key, value)
+        from .attention import rope_tables
+
+        cos, sin = rope_tables(base, self.head_dim, self.dtype, self._keys.device, stop)
+        k, v = key._data, value._data
+        k = k if k.stride(-1) == 1 else k.contiguous()
+        v = v if v.stride(-1) == 1 else v.contiguous()
+        b, h, t, d = k.shape
+        scales = ((ctypes.byref(_view(self._key_scales)), ctypes.byref(_view(self._value_scales)))
+                  if self.quantized else (None, None))
+        _lib.check(
+            _lib.load().tsattn_rope_append(
+                _CODES[str(k.dtype)], b, h, t, d, d, ctypes.byref(_view(k)), ctypes.byref(_view(v)),
+                ctypes.byref(_view(self._keys)), ctypes.byref(_view(self._values)), *scales,
+                ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()), self.length,
+                ctypes.c_void_p(current_stream(self.device))),
+            "RoPE cache append")
+        self.length = stop
+        return True
+
+    def _check(self, key: Tensor, value: Tensor) -> int:
+        """Validate an append (reference order, cache.py:54-70); return the new length."""
         if key.device != self.device or value.device != self.device:
             raise ValueError("cache and key/value tensors must be on the same device")
         if is_grad_enabled() and (key.requires_grad or value.requires_grad):
@@ -81,15 +130,7 @@ class KVCache:
         stop = self.length + key.shape[2]
         if key.shape[2] == 0 or stop > self.max_seq_len:
             raise ValueError(f"cache capacity {self.max_seq_len} exceeded or empty append")
-        window = slice(self.length, stop)
-        keys, values = key._data.to(self.dtype), value._data.to(self.dtype)
-        if self.quantized:
-            _append_int8(keys, self._keys, self._key_scales, self.length, self.device)
-            _append_int8(values, self._values, self._value_scales, self.length, self.device)
-        else:
-            self._keys[:, :, window] = keys
-            self._values[:, :, window] = values
-        self.length = stop
+        return stop
 
     def get(self) -> tuple[Tensor, Tensor]:
         keys = self._keys[:, :, : self.length]

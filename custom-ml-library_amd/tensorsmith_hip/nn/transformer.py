@@ -4,8 +4,9 @@ decoder-only ``TransformerLM`` with cached generation.
 ``MultiHeadAttention`` keeps the constructor, forward signature, validation
 and data flow of ``src/tensorsmith/nn/transformer.py:48-155``: projections
 reshaped to ``[B,S,H,D]`` and permuted to ``[B,H,S,D]`` *views* (the HIP
-kernels take the strides, so no copy is made), optional interleaved RoPE,
-KV-cache append with ``causal_offset = cache.length``, then
+kernels take the strides, so no copy is made), optional interleaved RoPE
+(one kernel per operand; with a cache, the key rotation and the K / V append
+are one kernel), KV-cache append with ``causal_offset = cache.length``, then
 ``scaled_dot_product_attention`` with ``backend`` (``"hip"`` added to the
 allowlist; ``"auto"`` picks it).
 
@@ -92,12 +93,18 @@ class MultiHeadAttention(Module):
              .permute(0, 2, 1, 3))
         v = (self.v_proj(source).reshape(batch, source.shape[1], self.num_kv_heads, self.head_dim)
              .permute(0, 2, 1, 3))
+        fused = False
         if self.rotary:
             q = rotary_embedding(q, offset)
-            k = rotary_embedding(k, offset if context is None else 0)
+            if cache is not None:
+                # rotate the new keys and write them (and the values) into the cache in one kernel
+                fused = cache._append_rotary(k, v)
+            if not fused:
+                k = rotary_embedding(k, offset if context is None else 0)
         attended = None
         if cache is not None:
-            cache._append(k, v)
+            if not fused:
+                cache._append(k, v)
             if cache.quantized and attn_mask is None:
                 # decode straight over the int8 storage (dequantised in the kernel)
                 attended = decode_int8_cache(q, cache, is_causal=is_causal, causal_offset=offset)

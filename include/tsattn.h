@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 2
+#define TSATTN_ABI_VERSION 3
 
 typedef enum {
   TSATTN_OK = 0,
@@ -181,6 +181,36 @@ int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, co
 int tsattn_kv_append_int8(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
                           const tsattn_view *src, const tsattn_view *dst, const tsattn_view *scale,
                           int64_t pos, void *stream);
+
+/*
+ * Interleaved-pair rotary position embedding (rotary_embedding, src/
+ * tensorsmith/nn/attention.py:255-296) of x [batch, heads, len, dim] into out
+ * (which may be x): channel pair (2i, 2i+1) of row t, i < rotary_dim / 2,
+ * rotates by the angle whose cosine / sine are cos[pos0 + t][i] /
+ * sin[pos0 + t][i] -- tables of rotary_dim / 2 columns in the tensor dtype,
+ * built as the reference builds them (fp32 angles, cast to the dtype).  Each
+ * product and sum rounds to the dtype as the reference's array arithmetic
+ * does, so results are bit-identical.  inverse != 0 rotates by -angle (the
+ * VJP, :289-294).  Channels from rotary_dim on pass through.
+ */
+int tsattn_rope(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                int32_t rotary_dim, const tsattn_view *x, const tsattn_view *out, const void *cos,
+                const void *sin, int64_t pos0, int32_t inverse, void *stream);
+
+/*
+ * The cached-decode step before attention in one pass: RoPE of the new key
+ * rows k (as tsattn_rope, table rows pos .. pos + len - 1; rotary_dim = 0
+ * skips it) and the append of k and v at position pos of the caches
+ * (MultiHeadAttention.forward, src/tensorsmith/nn/transformer.py:139-143 ->
+ * KVCache.append, cache.py:54-86).  k_scale / v_scale NULL: caches in the
+ * row dtype; non-NULL: int8 caches with fp32 row scales, quantised exactly as
+ * tsattn_kv_append_int8 does.
+ */
+int tsattn_rope_append(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,
+                       int32_t rotary_dim, const tsattn_view *k, const tsattn_view *v,
+                       const tsattn_view *k_cache, const tsattn_view *v_cache,
+                       const tsattn_view *k_scale, const tsattn_view *v_scale, const void *cos,
+                       const void *sin, int64_t pos, void *stream);
 
 /*
  * Boolean key mask [B, K] (strides in bytes-as-elements) -> kv_len[b] = 1 +

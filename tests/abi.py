@@ -146,3 +146,23 @@ def kv_append_int8(src, codes, scales, pos):
     _lib.check(_lib.load().tsattn_kv_append_int8(
         CODES[src.dtype], b, h, t, d, view(src), view(codes), view(scales), pos, stream()),
         "int8 append")
+
+
+def rope(x, out, cos, sin, pos0, rotary_dim, inverse=False):
+    """tsattn_rope: rotate x [B,H,T,D] into out with table rows pos0 + t."""
+    b, h, t, d = x.shape
+    _lib.check(_lib.load().tsattn_rope(
+        CODES[x.dtype], b, h, t, d, rotary_dim, view(x), view(out),
+        ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()), pos0, int(inverse),
+        stream()), "rope")
+
+
+def rope_append(k, v, kc, vc, cos, sin, pos, rotary_dim, ks=None, vs=None):
+    """tsattn_rope_append: rotate k, write k / v rows into the caches at pos
+    (int8 codes + scales when ks / vs are given)."""
+    b, h, t, d = k.shape
+    scales = tuple(None if s is None else ctypes.byref(view(s)) for s in (ks, vs))
+    _lib.check(_lib.load().tsattn_rope_append(
+        CODES[k.dtype], b, h, t, d, rotary_dim, view(k), view(v), view(kc), view(vc), *scales,
+        ctypes.c_void_p(cos.data_ptr() if cos is not None else 0),
+        ctypes.c_void_p(sin.data_ptr() if sin is not None else 0), pos, stream()), "rope append")

@@ -1,0 +1,191 @@
+"""Rotary position embedding on the device (needs an MI355X).
+
+* ``tsattn_rope``: bit-exact against the oracle's restatement of the
+  reference's rotary_embedding (src/tensorsmith/nn/attention.py:255-296) for
+  f32 / f16 / bf16, full and partial rotary dims, odd pair counts past one
+  wave (D = 130), position offsets and strided (permuted) sources; the
+  inverse rotation is bit-exact against the oracle's VJP rotation.
+* The mirror's ``rotary_embedding`` runs that kernel forward and backward
+  (timing probe) with the same bits.
+* ``tsattn_rope_append``: the new key rows rotated and both K and V written
+  into the cache rows at ``pos`` -- bit-exact against oracle rope followed by
+  a plain copy (fp caches) or by the oracle's restatement of the reference
+  quantiser (cache.py:73-77, int8 caches); rows outside the window untouched.
+* Model level: cached TransformerLM decoding through the fused kernel gives
+  bit-identical logits and cache contents to the two-step path
+  (rotary_embedding, then append), fp16 and int8 caches.
+"""
+
+from __future__ import annotations
+
+from unittest.mock import patch
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("no GPU", allow_module_level=True)
+
+import abi  # noqa: E402
+import tensorsmith_hip as ts  # noqa: E402
+from oracle import attention as A  # noqa: E402
+from oracle import rope as R  # noqa: E402
+from oracle.halfprec import round_to  # noqa: E402
+from tensorsmith_hip import _lib, nn  # noqa: E402
+from tensorsmith_hip.nn.cache import KVCache  # noqa: E402
+
+DTYPES = ["float32", "float16", "bfloat16"]
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def tables(n, rdim, dtype):
+    cos, sin = R.tables(n, rdim)
+    return abi.dev_tensor(round_to(cos, dtype), dtype), abi.dev_tensor(round_to(sin, dtype), dtype)
+
+
+def rows(rng, shape, dtype, scale=2.0):
+    return round_to(rng.standard_normal(shape).astype(np.float32) * scale, dtype)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim,rdim", [(64, 64), (130, 130), (256, 96), (6, 4)])
+@pytest.mark.parametrize("offset", [0, 37])
+@pytest.mark.parametrize("inverse", [False, True])
+def test_rope_kernel_is_bit_exact(dtype, dim, rdim, offset, inverse):
+    say(f"rope {dtype} D{dim} R{rdim} offset {offset} inverse {inverse}")
+    rng = np.random.default_rng(dim + offset)
+    b, h, t = 2, 3, 9
+    x = rows(rng, (b, t, h, dim), dtype)
+    src = abi.dev_tensor(x, dtype).permute(0, 2, 1, 3)  # [B,H,T,D] strided view
+    out = torch.full((b, h, t, dim), 7.0, dtype=src.dtype, device="cuda")
+    cos, sin = tables(offset + t + 3, rdim, dtype)
+    abi.rope(src, out, cos, sin, offset, rdim, inverse)
+    want = R.rope(x.transpose(0, 2, 1, 3), offset, rotary_dim=rdim, dtype=dtype, inverse=inverse)
+    np.testing.assert_array_equal(abi.host(out), want)
+
+
+def test_rope_then_inverse_is_the_identity_up_to_rounding():
+    rng = np.random.default_rng(3)
+    x = rows(rng, (1, 4, 33, 128), "float32")
+    src = abi.dev_tensor(x, "float32")
+    mid, back = torch.empty_like(src), torch.empty_like(src)
+    cos, sin = tables(1000, 128, "float32")
+    abi.rope(src, mid, cos, sin, 900, 128)
+    abi.rope(mid, back, cos, sin, 900, 128, inverse=True)
+    np.testing.assert_allclose(abi.host(back), x, rtol=0, atol=4e-6 * np.abs(x).max())
+    assert np.abs(abi.host(mid) - x).max() > 0.1  # it did rotate
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_mirror_rotary_embedding_runs_the_kernel_forward_and_backward(dtype):
+    say(f"rotary_embedding mirror {dtype}")
+    rng = np.random.default_rng(11)
+    x = rows(rng, (2, 4, 17, 64), dtype)
+    g = rows(rng, (2, 4, 17, 64), dtype, 1.0)
+    xt = ts.tensor(x, device="hip", dtype=dtype, requires_grad=True)
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    y = nn.functional.rotary_embedding(xt, 5, rotary_dim=48)
+    y.backward(ts.tensor(g, device="hip", dtype=dtype))
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert probes["rope"][0] == 2
+    np.testing.assert_array_equal(y.numpy().astype(np.float32),
+                                  R.rope(x, 5, rotary_dim=48, dtype=dtype))
+    np.testing.assert_array_equal(xt.grad.numpy().astype(np.float32),
+                                  R.rope(g, 5, rotary_dim=48, dtype=dtype, inverse=True))
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("dim,rdim", [(64, 64), (130, 66), (512, 512), (128, 0)])
+@pytest.mark.parametrize("quantized", [False, True])
+def test_rope_append_is_bit_exact(dtype, dim, rdim, quantized):
+    say(f"rope append {dtype} D{dim} R{rdim} int8 {quantized}")
+    rng = np.random.default_rng(dim + rdim)
+    b, h, t, pos, cap = 2, 3, 5, 6, 16
+    k = rows(rng, (b, t, h, dim), dtype)
+    v = rows(rng, (b, t, h, dim), dtype)
+    k[1, 2] = 0.0  # all-zero rows: scale 1e-8 in an int8 cache
+    kd = abi.dev_tensor(k, dtype).permute(0, 2, 1, 3)
+    vd = abi.dev_tensor(v, dtype).permute(0, 2, 1, 3)
+    cos, sin = tables(cap, rdim, dtype) if rdim else (None, None)
+    store = torch.int8 if quantized else kd.dtype
+    kc = torch.zeros((b, h, cap, dim), dtype=store, device="cuda")
+    vc = torch.zeros((b, h, cap, dim), dtype=store, device="cuda")
+    ks = torch.ones((b, h, cap, 1), dtype=torch.float32, device="cuda") if quantized else None
+    vs = torch.ones((b, h, cap, 1), dtype=torch.float32, device="cuda") if quantized else None
+    abi.rope_append(kd, vd, kc, vc, cos, sin, pos, rdim, ks, vs)
+    kr = k.transpose(0, 2, 1, 3)
+    vr = v.transpose(0, 2, 1, 3)
+    if rdim:
+        kr = R.rope(kr, pos, rotary_dim=rdim, dtype=dtype)
+    win = slice(pos, pos + t)
+    if quantized:
+        for cache, scale, want in ((kc, ks, kr), (vc, vs, vr)):
+            q, s = A.quantize_int8(want)
+            np.testing.assert_array_equal(cache[:, :, win].cpu().numpy(), q)
+            np.testing.assert_array_equal(scale[:, :, win].cpu().numpy(), s)
+            assert (scale[:, :, :pos] == 1).all() and (scale[:, :, pos + t:] == 1).all()
+    else:
+        np.testing.assert_array_equal(abi.host(kc[:, :, win]), kr)
+        np.testing.assert_array_equal(abi.host(vc[:, :, win]), vr)
+    for cache in (kc, vc):
+        assert (cache[:, :, :pos] == 0).all() and (cache[:, :, pos + t:] == 0).all()
+
+
+def test_rope_append_rejects_what_it_cannot_hold():
+    x = torch.zeros((1, 1, 1, 514), dtype=torch.float16, device="cuda")
+    cos, sin = tables(4, 514, "float16")
+    with pytest.raises(Exception, match="512"):
+        abi.rope_append(x, x, x, x, cos, sin, 0, 514)
+    y = torch.zeros((1, 1, 1, 64), dtype=torch.float16, device="cuda")
+    with pytest.raises(Exception, match="rotary"):
+        abi.rope_append(y, y, y, y, cos, sin, 0, 63)
+    with pytest.raises(Exception, match="rotary"):
+        abi.rope(y, y, cos, sin, 0, 66)
+    with pytest.raises(Exception, match="both"):
+        abi.rope_append(y, y, y, y, cos, sin, 0, 64, ks=torch.ones((1, 1, 1, 1), device="cuda"),
+                        vs=None)
+
+
+@pytest.mark.parametrize("quantized", [False, True])
+def test_fused_cached_decode_is_bitwise_the_two_step_path(quantized):
+    say(f"LM fused RoPE append int8 {quantized}")
+    ts.seed(21)
+    cfg = nn.TransformerConfig(61, dim=256, num_heads=4, num_kv_heads=2, num_layers=2,
+                               max_seq_len=64)
+    model = nn.TransformerLM(cfg, device="hip").eval()
+    model.to(dtype="float16")
+    tokens = ts.tensor(np.random.default_rng(21).integers(0, 61, (2, 24)), device="hip")
+    fused_calls = []
+    original = KVCache._append_rotary
+
+    def counting(self, *args, **kw):
+        done = original(self, *args, **kw)
+        fused_calls.append(done)
+        return done
+
+    def run():
+        caches = model.new_cache(2, quantized=quantized)
+        parts = [model(tokens[:, :20], caches=caches).numpy()]
+        for t in range(20, 24):
+            parts.append(model(tokens[:, t:t + 1], caches=caches).numpy())
+        return np.concatenate(parts, axis=1), [c.storage for c in caches]
+
+    with ts.no_grad():
+        with patch.object(KVCache, "_append_rotary", counting):
+            got, got_store = run()
+        with patch.object(KVCache, "_append_rotary", lambda self, *a, **k: False):
+            want, want_store = run()
+    assert fused_calls and all(fused_calls)
+    np.testing.assert_array_equal(got, want)
+    for a, b in zip(got_store, want_store):
+        for x, y in zip(a, b):
+            if x is not None:
+                assert torch.equal(x, y)

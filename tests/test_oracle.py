@@ -209,3 +209,49 @@ def test_inputs_recipe_is_seeded_and_ordered():
     assert np.array_equal(a.lengths, rng.integers(3, 9, size=2))
     assert math.isclose(float(np.std(attention_inputs(1, 1, 64, 64, "float32",
                                                       value_scale=0.5).q)), 0.5, rel_tol=0.1)
+
+
+# ---------------------------------------------------------------------------
+# RoPE oracle (reference attention.py:255-296), pinned by what the
+# mathematics fixes rather than by retyping the formula.
+# ---------------------------------------------------------------------------
+from oracle import rope as R  # noqa: E402
+
+
+def test_rope_position_zero_is_identity_and_tail_passes_through():
+    x = np.random.default_rng(1).standard_normal((2, 3, 5, 16)).astype(np.float32)
+    y = R.rope(x, offset=0, rotary_dim=12)
+    np.testing.assert_array_equal(y[..., 0, :], x[..., 0, :])  # cos 0 = 1, sin 0 = 0
+    np.testing.assert_array_equal(y[..., 12:], x[..., 12:])    # channels past rotary_dim
+
+
+def test_rope_f32_is_complex_multiplication():
+    """(x0 + i x1) * exp(i theta) in float64 on the same float32 cos / sin:
+    each component rounds twice (products, then the sum) in float32."""
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((4, 7, 32)).astype(np.float32)
+    y = R.rope(x, offset=11, base=500.0)
+    c, s = R.tables(7, 32, 500.0, 11)
+    z = (x[..., 0::2].astype(np.float64) + 1j * x[..., 1::2]) * (c.astype(np.float64) + 1j * s)
+    np.testing.assert_allclose(y[..., 0::2], z.real, rtol=0, atol=4e-7 * np.abs(x).max())
+    np.testing.assert_allclose(y[..., 1::2], z.imag, rtol=0, atol=4e-7 * np.abs(x).max())
+
+
+@pytest.mark.parametrize("dtype,tol", [("float32", 1e-6), ("float16", 2e-3), ("bfloat16", 1.6e-2)])
+def test_rope_inverse_undoes_rotation_and_keeps_pair_norms(dtype, tol):
+    from oracle.halfprec import round_to
+
+    x = round_to(np.random.default_rng(3).standard_normal((3, 9, 64)), dtype)
+    y = R.rope(x, offset=100, dtype=dtype)
+    back = R.rope(y, offset=100, dtype=dtype, inverse=True)
+    np.testing.assert_allclose(back, x, atol=tol * 4, rtol=tol * 4)
+    n0 = np.hypot(x[..., 0::2], x[..., 1::2])
+    n1 = np.hypot(y[..., 0::2], y[..., 1::2])
+    np.testing.assert_allclose(n1, n0, rtol=tol * 2, atol=tol * 2)
+
+
+def test_rope_rows_depend_only_on_absolute_position():
+    x = np.random.default_rng(4).standard_normal((1, 1, 8, 16)).astype(np.float32)
+    whole = R.rope(x, offset=3)
+    for t in range(8):
+        np.testing.assert_array_equal(R.rope(x[..., t:t + 1, :], offset=3 + t), whole[..., t:t + 1, :])
