@@ -12,6 +12,10 @@
 //
 // Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
 // transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
+//
+// Masks (template MK) as in the forward: a key mask reduced to lengths, or a
+// general boolean / additive mask read per (query row, key) on every tile
+// (additive: P = exp(S scale + mask - LSE)).
 #include <type_traits>
 
 #include "mfma_common.h"
@@ -67,7 +71,7 @@ constexpr int KV_PD = 2;  // tiles in flight
 #define DKDV_FD 1
 #endif
 
-template <typename T, int D>
+template <typename T, int D, int MK>
 __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
   constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
   constexpr int NBLK = TILE_B / 1024;
@@ -91,7 +95,8 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
-  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  const bool keymask =
+      MK == 0 && p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   const bool key_live = key < kv_end &&
                         (!keymask || static_cast<const uint8_t *>(p.mask.data)
                                          [b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
@@ -253,7 +258,8 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
     }
 
     // P = exp2(sacc sl), dS = P dpacc; rows crow(e, h) = 8 g + 4 h + e % 4.
-    const bool edge = keymask || kw + 32 > kv_end || q0 + QT > p.Sq || (causal && q0 < q_diag);
+    const bool edge = MK != 0 || keymask || kw + 32 > kv_end || q0 + QT > p.Sq ||
+                      (causal && q0 < q_diag);
     int lo = -64, hi = 64;
     if (edge) {
       hi = key_live ? p.Sq - q0 - 4 * h : -64;
@@ -261,15 +267,30 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
     }
     u32x4 pp[2], pd[2];
     // Interior tiles skip the per-element bounds (three VALU ops each).
+    // A general mask: element (b, hq, q0 + 4h + kc, key), kc along the rows.
     auto grad = [&](auto masked) {
+      float xs[16];
+      if constexpr (MK != 0) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xs[e] = sacc[e];
+        const int64_t m0 = b * p.mask.s0 + hq * p.mask.s1 +
+                           static_cast<int64_t>(q0 + 4 * h) * p.mask.s2 +
+                           static_cast<int64_t>(key) * p.mask.s3;
+        mask_scores<MK>(xs, p.mask, m0, p.mask.s2, lo, hi, sl);
+      }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float pv[4], dsv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int e = 4 * g + r, kc = 8 * g + r;
-          pv[r] = fast_exp2(sacc[e] * sl);
-          if (masked) pv[r] = (kc >= lo) & (kc < hi) ? pv[r] : 0.f;
+          if constexpr (MK == 0) {
+            pv[r] = fast_exp2(sacc[e] * sl);
+            if (masked) pv[r] = ((kc >= lo) & (kc < hi)) ? pv[r] : 0.f;
+          } else {
+            // -inf where disallowed; additive-masked scores arrive scaled
+            pv[r] = fast_exp2(MK == 2 ? xs[e] : xs[e] * sl);
+          }
           dsv[r] = pv[r] * dpacc[e];
         }
         pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
@@ -357,7 +378,7 @@ constexpr int KT = 32;   // keys per tile
 constexpr int DQ_PD = 2;              // tiles issued ahead
 constexpr int DQ_NS = DQ_PD + 2;      // ring stages: tile j is read in iterations j and j + 1
 
-template <typename T, int D>
+template <typename T, int D, int MK>
 __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   constexpr int TILE_B = KT * D * 2;   // bytes per K (or V) tile
   constexpr int NBLK = TILE_B / 1024;  // 1 KiB blocks per tile
@@ -379,7 +400,8 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
   const int q0 = qb * QB, qw = q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);
-  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  const bool keymask =
+      MK == 0 && p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   const bool causal = p.causal != 0;
 
   int64_t lim = kv_end, wlim = kv_end;
@@ -478,6 +500,10 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
+  // General mask: element (b, hq, qrow, 0); rows past Sq read nothing.
+  const int64_t mrow = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(qrow) * p.mask.s2;
+  if (MK != 0 && qrow >= p.Sq) klim = 0;
+  const float slx = MK == 2 ? 1.f : sl;  // additive-masked scores arrive scaled
 
   // The first MFMA block multiplies the K half of stage DQ_NS - 1 (no DMA has
   // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
@@ -526,27 +552,32 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = s[i];
-    const bool edge = (kv0 + KT > kv_end) || keymask ||
+    const bool edge = MK != 0 || (kv0 + KT > kv_end) || keymask ||
                       (causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
     if (edge) {
       const int lim_l = klim - kv0 - 4 * h;
-      unsigned kbits = ~0u;
-      if (keymask) {
-        const int key = kv0 + lane;
-        const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
-        kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
-      }
+      if constexpr (MK == 0) {
+        unsigned kbits = ~0u;
+        if (keymask) {
+          const int key = kv0 + lane;
+          const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+          kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
+        }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kc = 8 * (i >> 2) + (i & 3);
-        const bool ok = (kc < lim_l) & (((kbits >> kc) & 1u) != 0);
-        x[i] = ok ? x[i] : -INFINITY;
+        for (int i = 0; i < 16; ++i) {
+          const int kc = 8 * (i >> 2) + (i & 3);
+          const bool ok = (kc < lim_l) & (((kbits >> kc) & 1u) != 0);
+          x[i] = ok ? x[i] : -INFINITY;
+        }
+      } else {
+        const int64_t m0 = mrow + static_cast<int64_t>(kv0 + 4 * h) * p.mask.s3;
+        mask_scores<MK>(x, p.mask, m0, p.mask.s3, -64, lim_l, sl);
       }
     }
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = fast_exp2(fmaf(x[i], sl, lse2));
-      const float p1 = fast_exp2(fmaf(x[i + 1], sl, lse2));
+      const float p0 = fast_exp2(fmaf(x[i], slx, lse2));
+      const float p1 = fast_exp2(fmaf(x[i + 1], slx, lse2));
       pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (dp[i] + delta), p1 * (dp[i + 1] + delta));
     }
   };
@@ -603,14 +634,28 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
-template <typename T, int D>
-hipError_t launch(const BwdArgs &a, hipStream_t st) {
+template <typename T, int D, int MK>
+void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
-  { Probe pr_("bwd_dq_mfma", st); dq_kernel<T, D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a); }
+  {
+    Probe pr_(MK ? "bwd_dq_mfma_masked" : "bwd_dq_mfma", st);
+    dq_kernel<T, D, MK><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+  }
   const int n_kb = (p.Sk + KB - 1) / KB;
-  { Probe pr_("bwd_dkdv_mfma", st); dkdv_kernel<T, D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a); }
+  {
+    Probe pr_(MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma", st);
+    dkdv_kernel<T, D, MK><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+  }
+}
+
+template <typename T, int D>
+hipError_t launch(const BwdArgs &a, hipStream_t st) {
+  const int mk = mfma_mask_mode(a.p);
+  if (mk == 1) launch_mk<T, D, 1>(a, st);
+  else if (mk == 2) launch_mk<T, D, 2>(a, st);
+  else launch_mk<T, D, 0>(a, st);
   return hipGetLastError();
 }
 

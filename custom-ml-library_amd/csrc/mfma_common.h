@@ -59,6 +59,48 @@ __device__ __forceinline__ constexpr int crow(int i, int h) { return ((i >> 2) <
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// A general mask over the 16 scores of a lane's accumulator (MK = 1 boolean,
+// MK = 2 additive).  Score i sits at mask element m0 + kc(i) * stride with
+// kc(i) = 8 (i / 4) + i % 4 (the accumulator row pattern with the lane half
+// folded into m0); it is allowed iff lo <= kc < hi and the mask allows it.
+// Elements outside [lo, hi) are never read.  Disallowed scores become -inf;
+// with an additive mask the allowed ones become x sl + mask log2(e), i.e.
+// (scores * scale + mask) in log2 units, already scaled.
+template <typename M>
+__device__ __forceinline__ void add_mask16(float (&x)[16], const void *data, int64_t m0,
+                                           int64_t stride, int lo, int hi, float sl) {
+  const M *mp = static_cast<const M *>(data) + m0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int kc = 8 * (i >> 2) + (i & 3);
+    const bool ok = (kc >= lo) & (kc < hi);
+    float mv = 0.f;
+    if (ok) mv = static_cast<float>(mp[kc * stride]);
+    x[i] = ok ? fmaf(x[i], sl, mv * kLog2e) : -INFINITY;
+  }
+}
+
+template <int MK>
+__device__ __forceinline__ void mask_scores(float (&x)[16], const MaskDesc &m, int64_t m0,
+                                            int64_t stride, int lo, int hi, float sl) {
+  if constexpr (MK == 1) {
+    const uint8_t *mb = static_cast<const uint8_t *>(m.data) + m0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kc = 8 * (i >> 2) + (i & 3);
+      bool ok = (kc >= lo) & (kc < hi);
+      if (ok) ok = mb[kc * stride] != 0;
+      x[i] = ok ? x[i] : -INFINITY;
+    }
+  } else if (m.dtype == TSATTN_F16) {
+    add_mask16<f16>(x, m.data, m0, stride, lo, hi, sl);
+  } else if (m.dtype == TSATTN_BF16) {
+    add_mask16<bf16>(x, m.data, m0, stride, lo, hi, sl);
+  } else {
+    add_mask16<float>(x, m.data, m0, stride, lo, hi, sl);
+  }
+}
+
 __device__ __forceinline__ float xor32_max(float x) {
   float y = __shfl_xor(x, 32, 64);
   return fmaxf(x, y);

@@ -27,6 +27,11 @@
 // Rescaling is lazy: the reference max m is raised (and O, l rescaled) only
 // when a row's max exceeds it by more than kTau (in log2 units), so P <= 2^kTau
 // and most tiles skip the rescale.  O / l and the LSE are exact for any m.
+//
+// Masks (template MK): a key mask reduced to per-row lengths costs one ballot
+// per tile; a general boolean or additive mask (MK = 1 / 2) is read per
+// (query row, key) from its broadcast strides on every tile, an additive one
+// entering as scores * scale + mask (attention.py:105-107) in log2 units.
 #include "mfma_common.h"
 
 namespace tsattn {
@@ -54,7 +59,7 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
 }
 
-template <typename T, int D>
+template <typename T, int D, int MK>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   constexpr int TILE_B = BN * D * 2;        // bytes per K (or V) tile
   constexpr int NBLK = TILE_B / 1024;       // 1 KiB blocks per tile
@@ -77,7 +82,8 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
 
   const int kv_end = kv_end_for(p, b);
-  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  const bool keymask =
+      MK == 0 && p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
 
   // Key tiles of the workgroup (all its rows) and of this wave.
   int64_t lim = kv_end, wlim = kv_end;
@@ -160,6 +166,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   }
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
+  // General mask: element (b, hq, qrow, 0); rows past Sq read nothing.
+  const int64_t mrow = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(qrow) * p.mask.s2;
+  if (MK != 0 && qrow >= p.Sq) klim = 0;
+  // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
+  const float slx = MK == 2 ? 1.f : a.sl;
 
   // The first MFMA block runs PV with P = 0 against the V half of stage
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
@@ -206,28 +217,33 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     float x[16];  // scores of this lane's query row; element i is key kv0 + crow(i, h)
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = s[i];
-    const bool edge = (kv0 + BN > kv_end) || keymask ||
+    const bool edge = MK != 0 || (kv0 + BN > kv_end) || keymask ||
                       (p.causal && static_cast<int64_t>(kv0 + BN - 1) > qw + p.offset);
     if (edge) {
       // Key kv0 + 4h + kc(i), kc a compile-time constant.
       const int lim = klim - kv0 - 4 * h;
-      unsigned kbits = ~0u;
-      if (keymask) {
-        const int key = kv0 + lane;
-        const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
-        kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
-      }
+      if constexpr (MK == 0) {
+        unsigned kbits = ~0u;
+        if (keymask) {
+          const int key = kv0 + lane;
+          const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+          kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
+        }
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kc = 8 * (i >> 2) + (i & 3);
-        const bool ok = (kc < lim) & (((kbits >> kc) & 1u) != 0);
-        x[i] = ok ? x[i] : -INFINITY;
+        for (int i = 0; i < 16; ++i) {
+          const int kc = 8 * (i >> 2) + (i & 3);
+          const bool ok = (kc < lim) & (((kbits >> kc) & 1u) != 0);
+          x[i] = ok ? x[i] : -INFINITY;
+        }
+      } else {
+        const int64_t m0 = mrow + static_cast<int64_t>(kv0 + 4 * h) * p.mask.s3;
+        mask_scores<MK>(x, p.mask, m0, p.mask.s3, -64, lim, sl);
       }
     }
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
-    const float mt = half_swap_max(mx) * sl;
+    const float mt = half_swap_max(mx) * slx;
     if (__ballot(mt > m + kTau) != 0ull) {
       const float m_new = fmaxf(m, mt);
       const float corr = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
@@ -239,8 +255,8 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     const float base = m == -INFINITY ? 0.f : m;
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = fast_exp2(fmaf(x[i], sl, -base));
-      const float p1 = fast_exp2(fmaf(x[i + 1], sl, -base));
+      const float p0 = fast_exp2(fmaf(x[i], slx, -base));
+      const float p1 = fast_exp2(fmaf(x[i + 1], slx, -base));
       l += p0 + p1;  // fp32 sum of the unrounded probabilities, as the reference
       pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
     }
@@ -309,7 +325,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 
 template <typename T, int D>
 hipError_t launch(const FwdArgs &a, hipStream_t st) {
-  { Probe pr_("fwd_mfma", st); fwd_kernel<T, D><<<dim3(a.total), dim3(NT), 0, st>>>(a); }
+  const int mk = mfma_mask_mode(a.p);
+  Probe pr_(mk ? "fwd_mfma_masked" : "fwd_mfma", st);
+  if (mk == 1) fwd_kernel<T, D, 1><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 2) fwd_kernel<T, D, 2><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else fwd_kernel<T, D, 0><<<dim3(a.total), dim3(NT), 0, st>>>(a);
   return hipGetLastError();
 }
 
@@ -319,9 +339,8 @@ bool mfma_supported(const Problem &p, int dtype) {
   if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
   if (p.Dqk != p.Dv || (p.Dqk != 64 && p.Dqk != 128)) return false;
   if (!(p.scale > 0.0)) return false;
-  if (p.mask.kind == TSATTN_MASK_NONE) return true;
-  // key masks [B,1,1,K] with their derived lengths
-  return p.mask.kind == TSATTN_MASK_BOOL && p.mask.s1 == 0 && p.mask.s2 == 0 && p.kv_len != nullptr;
+  if (p.mask.kind != TSATTN_MASK_ADDITIVE) return true;
+  return p.mask.dtype == TSATTN_F32 || p.mask.dtype == TSATTN_F16 || p.mask.dtype == TSATTN_BF16;
 }
 
 hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,

@@ -76,6 +76,16 @@ struct Problem {
   MaskDesc mask;
 };
 
+// Mask handling of the MFMA kernels (a template parameter): 0 = none, or a
+// key mask [B,1,1,K] reduced to kv_len / kv_prefix; 1 = any other boolean
+// mask, read per (row, key) from its strides; 2 = an additive mask, read the
+// same way and added to the scaled scores.
+inline int mfma_mask_mode(const Problem &p) {
+  if (p.mask.kind == TSATTN_MASK_BOOL)
+    return p.mask.s1 == 0 && p.mask.s2 == 0 && p.kv_len != nullptr ? 0 : 1;
+  return p.mask.kind == TSATTN_MASK_ADDITIVE ? 2 : 0;
+}
+
 // Valid keys for batch row b: [0, kv_end).
 __device__ __forceinline__ int kv_end_for(const Problem &p, int b) {
   int e = p.Sk;
@@ -117,8 +127,8 @@ hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, 
                                    View dout, const void *lse, View dq, View dk, View dv,
                                    void *delta, hipStream_t st);
 
-// MFMA kernels: f16 / bf16, dim_qk == dim_v in {64, 128}, scale > 0,
-// no mask other than a key mask [B,1,1,K] (+ kv_len / kv_prefix).
+// MFMA kernels: f16 / bf16, dim_qk == dim_v in {64, 128}, scale > 0; any
+// boolean mask, or an additive mask in f32 / f16 / bf16.
 bool mfma_supported(const Problem &p, int dtype);
 hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,
                                float *lse, hipStream_t st);

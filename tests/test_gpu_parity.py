@@ -192,6 +192,91 @@ def test_mfma_key_padding_mask(prefix):
         check_half(abi.host(got), want, dtype, "g", n)
 
 
+# General masks on the MFMA kernels: boolean masks of any broadcast shape
+# (read per row and key) and additive masks in f32 / f16 / bf16, with causal
+# windows, offsets, GQA and fully masked rows (O = 0, LSE = -inf, zero grads).
+MASK_CASES = [
+    # (id, dtype, B, Hq, Hkv, Sq, Sk, D, causal, offset, mask shape, mask dtype)
+    ("bool-qk-causal", "bfloat16", 2, 2, 2, 200, 333, 128, True, 133, (200, 333), "bool"),
+    ("bool-b1qk-gqa", "float16", 2, 4, 2, 160, 190, 64, False, 0, (2, 1, 160, 190), "bool"),
+    ("bool-1h1k", "bfloat16", 2, 3, 3, 129, 257, 128, False, 0, (1, 3, 1, 257), "bool"),
+    ("add-f32-1hqk-causal", "float16", 1, 2, 2, 300, 300, 128, True, 0, (1, 2, 300, 300), "float32"),
+    ("add-bf16-qk", "bfloat16", 2, 2, 1, 77, 150, 64, True, 73, (77, 150), "bfloat16"),
+    ("add-f16-keybias", "float16", 3, 2, 2, 96, 200, 128, False, 0, (3, 1, 1, 200), "float16"),
+]
+
+
+def _mask(rng, shape, mdtype, sq):
+    if mdtype == "bool":
+        m = rng.random(shape) > 0.3
+        if len(shape) >= 2 and shape[-2] == sq:
+            m[..., 5, :] = False  # a fully masked query row
+        return m
+    m = (rng.standard_normal(shape) * 1.5).astype(np.float32)
+    m[rng.random(shape) < 0.2] = -np.inf
+    if len(shape) >= 2 and shape[-2] == sq:
+        m[..., 7, :] = -np.inf  # a fully masked query row
+    return round_to(m, mdtype)
+
+
+@pytest.mark.parametrize("case", MASK_CASES, ids=lambda c: c[0])
+def test_mfma_general_masks(case):
+    _, dtype, b, hq, hkv, sq, sk, d, causal, off, mshape, mdtype = case
+    say(f"mfma general mask {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=21)
+    rng = np.random.default_rng(sq + sk)
+    mask = _mask(rng, mshape, mdtype, sq)
+    ref = _oracle(inp, dtype, causal, off, mask=mask, gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    tm = (torch.from_numpy(mask).cuda() if mdtype == "bool"
+          else abi.dev_tensor(mask, mdtype))
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    out, lse, path = abi.forward(q, k, v, causal=causal, offset=off, mask=tm)
+    assert path == _lib.PATH_MFMA
+    dq, dk, dv, bpath = abi.backward(q, k, v, out, g, lse, causal=causal, offset=off, mask=tm)
+    assert bpath == _lib.PATH_MFMA
+    torch.cuda.synchronize()
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert {"fwd_mfma_masked", "bwd_dq_mfma_masked", "bwd_dkdv_mfma_masked"} <= set(probes)
+    check_half(abi.host(out), ref.out, dtype, "o", "O")
+    check_lse(abi.host(lse), ref.lse, "LSE")
+    rdq, rdk, rdv = ref.backward_compute(inp.do)
+    check_half(abi.host(dq), rdq, dtype, "g", "dQ")
+    check_half(abi.host(dk), rdk, dtype, "g", "dK")
+    check_half(abi.host(dv), rdv, dtype, "g", "dV")
+    if mshape[-2] == sq:  # the fully masked row: O = 0, LSE = -inf, dQ = 0
+        row = 5 if mdtype == "bool" else 7
+        assert (abi.host(out)[:, :, row] == 0).all()
+        assert np.isneginf(abi.host(lse)[:, :, row]).all()
+        assert (abi.host(dq)[:, :, row] == 0).all()
+
+
+def test_mfma_key_mask_without_lengths_reads_the_mask():
+    """A [B,1,1,K] boolean mask passed without kv_len runs the general-mask
+    kernels and agrees with the length-reduced path."""
+    dtype = "bfloat16"
+    inp = attention_inputs(2, 2, 150, 128, dtype, value_scale=0.5, seed=4)
+    keymask = np.ones((2, 150), dtype=bool)
+    keymask[0, 100:] = False
+    keymask[1, [3, 77, 149]] = False
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    km = torch.from_numpy(keymask).cuda()
+    m4 = km[:, None, None, :]
+    out_g, lse_g, _ = abi.forward(q, k, v, causal=True, mask=m4)
+    grads_g = abi.backward(q, k, v, out_g, g, lse_g, causal=True, mask=m4)[:3]
+    kv_len, kv_prefix = abi.key_lengths(km)
+    out_l, lse_l, _ = abi.forward(q, k, v, causal=True, mask=m4, kv_len=kv_len, kv_prefix=kv_prefix)
+    grads_l = abi.backward(q, k, v, out_l, g, lse_l, causal=True, mask=m4, kv_len=kv_len,
+                           kv_prefix=kv_prefix)[:3]
+    torch.cuda.synchronize()
+    # same tiles, same arithmetic on every allowed score: identical results
+    assert torch.equal(out_g, out_l) and torch.equal(lse_g, lse_l)
+    for a_, b_ in zip(grads_g, grads_l):
+        assert torch.equal(a_, b_)
+
+
 # ---------------------------------------------------------------------------
 # Decode kernel
 # ---------------------------------------------------------------------------
