@@ -71,8 +71,14 @@ constexpr int KV_PD = 2;  // tiles in flight
 #define DKDV_FD 1
 #endif
 
+// Workgroups per CU: two, except the general-mask kernel at D = 128, whose
+// mask registers do not fit beside the two-workgroup register budget; alone
+// on its CU it has the accumulation registers as well.
+template <int D, int MK>
+constexpr int dkdv_wg_per_cu() { return MK != 0 && D > 64 ? 1 : 2; }
+
 template <typename T, int D, int MK>
-__global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
+__global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(BwdArgs a) {
   constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
   constexpr int NBLK = TILE_B / 1024;
   constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | nl (QT floats) | nd (QT floats)
@@ -91,7 +97,7 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, kb;  // early key blocks see the most queries: run them first
-  heavy_first(logical, n_kb, p.Hkv * p.B, 64, bh, kb);  // 2 WG per CU
+  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<D, MK>(), bh, kb);  // slots per XCD
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
@@ -226,6 +232,21 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
     tile_of(itn, hq, q0);
 
     constexpr int FD = DKDV_FD;
+    // A general mask: this tile's elements (b, hq, q0 + 4h + kc, key), kc
+    // along the rows, fetched before the S / dP MFMAs (their latency hides
+    // under them) and before the next tile's DMA parts issued among those, so
+    // that the wait for them leaves the parts in flight.
+    MaskFetch mf;
+    if constexpr (MK != 0) {
+      constexpr int mes = mask_bytes<MK>();
+      const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * mes;
+      const u32x4 mdesc = make_desc(
+          static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + hq * p.mask.s1) * mes,
+          static_cast<uint32_t>(extent));
+      const int64_t off0 = (static_cast<int64_t>(q0 + 4 * h) * p.mask.s2 +
+                            static_cast<int64_t>(key) * p.mask.s3) * mes;
+      mf.issue<mes>(mdesc, static_cast<uint32_t>(off0), static_cast<uint32_t>(p.mask.s2 * mes));
+    }
     // S = Q K^T + nl, dP = dO V^T + nd over the tile's 32 rows x this wave's
     // 32 keys, the accumulators starting from the rows' nl / nd values:
     // sacc[e] = (S[q0 + crow(e, h)][key] scale - lse) / scale.
@@ -267,16 +288,17 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
     }
     u32x4 pp[2], pd[2];
     // Interior tiles skip the per-element bounds (three VALU ops each).
-    // A general mask: element (b, hq, q0 + 4h + kc, key), kc along the rows.
     auto grad = [&](auto masked) {
       float xs[16];
       if constexpr (MK != 0) {
+        // The mask loads; the next tile's Q / dO parts stay in flight (waves 0
+        // and 1 also wait for their row-value part, the first one issued).
+        if (prefetch) wait_vm_n<LPT>();
+        else wait_vm_n<0>();
+        mf.resolve();
 #pragma unroll
         for (int e = 0; e < 16; ++e) xs[e] = sacc[e];
-        const int64_t m0 = b * p.mask.s0 + hq * p.mask.s1 +
-                           static_cast<int64_t>(q0 + 4 * h) * p.mask.s2 +
-                           static_cast<int64_t>(key) * p.mask.s3;
-        mask_scores<MK>(xs, p.mask, m0, p.mask.s2, lo, hi, sl);
+        mask_scores<MK>(xs, mf, p.mask.dtype, lo, hi, sl);
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
@@ -289,7 +311,7 @@ __global__ __launch_bounds__(NT, 2) void dkdv_kernel(BwdArgs a) {
             if (masked) pv[r] = ((kc >= lo) & (kc < hi)) ? pv[r] : 0.f;
           } else {
             // -inf where disallowed; additive-masked scores arrive scaled
-            pv[r] = fast_exp2(MK == 2 ? xs[e] : xs[e] * sl);
+            pv[r] = fast_exp2(MK >= 2 ? xs[e] : xs[e] * sl);
           }
           dsv[r] = pv[r] * dpacc[e];
         }
@@ -500,10 +522,21 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
-  // General mask: element (b, hq, qrow, 0); rows past Sq read nothing.
-  const int64_t mrow = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(qrow) * p.mask.s2;
-  if (MK != 0 && qrow >= p.Sq) klim = 0;
-  const float slx = MK == 2 ? 1.f : sl;  // additive-masked scores arrive scaled
+  // General mask: the (b, hq) slice as a buffer; this lane reads row qrow.
+  // Rows past Sq use none of what they read.
+  constexpr int mes = mask_bytes<MK>();
+  u32x4 mdesc{};
+  uint32_t mrow = 0, mstep = 0;
+  if constexpr (MK != 0) {
+    const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * mes;
+    mdesc = make_desc(static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + hq * p.mask.s1) * mes,
+                      static_cast<uint32_t>(extent));
+    mrow = static_cast<uint32_t>(static_cast<int64_t>(qrow) * p.mask.s2 * mes);
+    mstep = static_cast<uint32_t>(p.mask.s3 * mes);
+    if (qrow >= p.Sq) klim = 0;
+  }
+  MaskFetch mf;
+  const float slx = MK >= 2 ? 1.f : sl;  // additive-masked scores arrive scaled
 
   // The first MFMA block multiplies the K half of stage DQ_NS - 1 (no DMA has
   // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
@@ -520,7 +553,10 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // steps ahead.  One code path for every block keeps the accumulators in
   // place: the first block multiplies a zeroed stage by dS = 0, and past the
   // wave's last tile S and dP are computed and ignored.
-  auto mfma_block = [&](int j, int nt) {  // nt: tile whose DMA to issue, or -1
+  // fetch: also load tile j's mask elements, before the DMA parts.
+  auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
+    if constexpr (MK != 0)
+      if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * KT + 4 * h) * mstep, mstep);
     const char *kt = lds + (j % DQ_NS) * 2 * TILE_B;
     const char *vt = kt + TILE_B;
     const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * 2 * TILE_B;
@@ -547,7 +583,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     }
   };
 
-  auto grad = [&](int j) {
+  auto grad = [&](int j, int nt) {
     const int kv0 = j * KT;
     float x[16];
 #pragma unroll
@@ -570,8 +606,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
           x[i] = ok ? x[i] : -INFINITY;
         }
       } else {
-        const int64_t m0 = mrow + static_cast<int64_t>(kv0 + 4 * h) * p.mask.s3;
-        mask_scores<MK>(x, p.mask, m0, p.mask.s3, -64, lim_l, sl);
+        wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
+        mf.resolve();
+        mask_scores<MK>(x, mf, p.mask.dtype, -64, lim_l, sl);
       }
     }
 #pragma unroll
@@ -592,11 +629,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   if (w_tiles > 0) {
     pd[0] = pd[1] = u32x4{0, 0, 0, 0};
     for (; j < w_tiles; ++j) {
-      mfma_block(j, next_dma(j));
-      grad(j);
+      mfma_block(j, next_dma(j), true);
+      grad(j, next_dma(j));
       it_end(j);
     }
-    mfma_block(j, next_dma(j));  // dQ of the last tile
+    mfma_block(j, next_dma(j), false);  // dQ of the last tile
     it_end(j);
     ++j;
   }
@@ -655,6 +692,7 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
   const int mk = mfma_mask_mode(a.p);
   if (mk == 1) launch_mk<T, D, 1>(a, st);
   else if (mk == 2) launch_mk<T, D, 2>(a, st);
+  else if (mk == 3) launch_mk<T, D, 3>(a, st);
   else launch_mk<T, D, 0>(a, st);
   return hipGetLastError();
 }

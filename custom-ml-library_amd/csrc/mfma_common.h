@@ -60,44 +60,64 @@ __device__ __forceinline__ constexpr int crow(int i, int h) { return ((i >> 2) <
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // A general mask over the 16 scores of a lane's accumulator (MK = 1 boolean,
-// MK = 2 additive).  Score i sits at mask element m0 + kc(i) * stride with
-// kc(i) = 8 (i / 4) + i % 4 (the accumulator row pattern with the lane half
-// folded into m0); it is allowed iff lo <= kc < hi and the mask allows it.
-// Elements outside [lo, hi) are never read.  Disallowed scores become -inf;
-// with an additive mask the allowed ones become x sl + mask log2(e), i.e.
-// (scores * scale + mask) in log2 units, already scaled.
-template <typename M>
-__device__ __forceinline__ void add_mask16(float (&x)[16], const void *data, int64_t m0,
-                                           int64_t stride, int lo, int hi, float sl) {
-  const M *mp = static_cast<const M *>(data) + m0;
+// 2 additive f32, 3 additive f16 / bf16).  Score i sits at mask byte offset
+// off0 + kc(i) * step with kc(i) = 8 (i / 4) + i % 4 (the accumulator row
+// pattern, the lane half folded into off0).
+//
+// The 16 elements are fetched by buffer loads issued as assembly at the start
+// of a tile's MFMA block, so their latency hides under it: the compiler does
+// not see these loads and adds no wait for them (its waits would also wait for
+// the DMA loads issued after them).  The kernel waits with wait_vm(n), n = the
+// loads it issued since, then resolve()s the registers.  The load width is a
+// compile-time constant: no branch separates a load from its wait.  Offsets past the
+// buffer range read as zero; elements the kernel does not allow are not used.
+struct MaskFetch {
+  uint32_t v[16];
+
+  template <int BYTES>
+  __device__ __forceinline__ void issue(u32x4 desc, uint32_t off0, uint32_t step) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint32_t off = off0 + static_cast<uint32_t>(8 * (i >> 2) + (i & 3)) * step;
+      if constexpr (BYTES == 1)
+        asm volatile("buffer_load_ubyte %0, %1, %2, 0 offen" : "=v"(v[i]) : "v"(off), "s"(desc) : "memory");
+      else if constexpr (BYTES == 2)
+        asm volatile("buffer_load_ushort %0, %1, %2, 0 offen" : "=v"(v[i]) : "v"(off), "s"(desc) : "memory");
+      else
+        asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v[i]) : "v"(off), "s"(desc) : "memory");
+    }
+  }
+  __device__ __forceinline__ void resolve() {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(v[i]));
+  }
+};
+
+// Bytes per mask element of mask mode MK (1 boolean, 2 additive f32,
+// 3 additive f16 / bf16).
+template <int MK>
+constexpr int mask_bytes() { return MK == 1 ? 1 : (MK == 2 ? 4 : 2); }
+
+// Apply fetched mask elements: score i is allowed iff lo <= kc(i) < hi and
+// the mask allows it; disallowed scores become -inf.  With an additive mask
+// the allowed ones become x sl + mask log2(e), i.e. (scores * scale + mask)
+// in log2 units, already scaled.
+template <int MK>
+__device__ __forceinline__ void mask_scores(float (&x)[16], const MaskFetch &mf, int mdtype,
+                                            int lo, int hi, float sl) {
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     const int kc = 8 * (i >> 2) + (i & 3);
-    const bool ok = (kc >= lo) & (kc < hi);
-    float mv = 0.f;
-    if (ok) mv = static_cast<float>(mp[kc * stride]);
-    x[i] = ok ? fmaf(x[i], sl, mv * kLog2e) : -INFINITY;
-  }
-}
-
-template <int MK>
-__device__ __forceinline__ void mask_scores(float (&x)[16], const MaskDesc &m, int64_t m0,
-                                            int64_t stride, int lo, int hi, float sl) {
-  if constexpr (MK == 1) {
-    const uint8_t *mb = static_cast<const uint8_t *>(m.data) + m0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int kc = 8 * (i >> 2) + (i & 3);
-      bool ok = (kc >= lo) & (kc < hi);
-      if (ok) ok = mb[kc * stride] != 0;
-      x[i] = ok ? x[i] : -INFINITY;
+    const bool in = (kc >= lo) & (kc < hi);
+    if constexpr (MK == 1) {
+      x[i] = in && mf.v[i] != 0u ? x[i] : -INFINITY;
+    } else {
+      float mv;
+      if constexpr (MK == 2) mv = __builtin_bit_cast(float, mf.v[i]);
+      else if (mdtype == TSATTN_BF16) mv = __builtin_bit_cast(float, mf.v[i] << 16);
+      else mv = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(mf.v[i])));
+      x[i] = in ? fmaf(x[i], sl, mv * kLog2e) : -INFINITY;
     }
-  } else if (m.dtype == TSATTN_F16) {
-    add_mask16<f16>(x, m.data, m0, stride, lo, hi, sl);
-  } else if (m.dtype == TSATTN_BF16) {
-    add_mask16<bf16>(x, m.data, m0, stride, lo, hi, sl);
-  } else {
-    add_mask16<float>(x, m.data, m0, stride, lo, hi, sl);
   }
 }
 

@@ -31,7 +31,8 @@
 // Masks (template MK): a key mask reduced to per-row lengths costs one ballot
 // per tile; a general boolean or additive mask (MK = 1 / 2) is read per
 // (query row, key) from its broadcast strides on every tile, an additive one
-// entering as scores * scale + mask (attention.py:105-107) in log2 units.
+// entering as scores * scale + mask (attention.py:105-107) in log2 units
+// (MK = 2 for an f32 mask, 3 for f16 / bf16).
 #include "mfma_common.h"
 
 namespace tsattn {
@@ -166,11 +167,22 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   }
   const uint8_t *kmask_b =
       keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
-  // General mask: element (b, hq, qrow, 0); rows past Sq read nothing.
-  const int64_t mrow = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(qrow) * p.mask.s2;
-  if (MK != 0 && qrow >= p.Sq) klim = 0;
+  // General mask: the (b, hq) slice as a buffer; this lane reads row qrow.
+  // Rows past Sq use none of what they read.
+  constexpr int mes = mask_bytes<MK>();
+  u32x4 mdesc{};
+  uint32_t mrow = 0, mstep = 0;
+  if constexpr (MK != 0) {
+    const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * mes;
+    mdesc = make_desc(static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + hq * p.mask.s1) * mes,
+                      static_cast<uint32_t>(extent));
+    mrow = static_cast<uint32_t>(static_cast<int64_t>(qrow) * p.mask.s2 * mes);
+    mstep = static_cast<uint32_t>(p.mask.s3 * mes);
+    if (qrow >= p.Sq) klim = 0;
+  }
+  MaskFetch mf;
   // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
-  const float slx = MK == 2 ? 1.f : a.sl;
+  const float slx = MK >= 2 ? 1.f : a.sl;
 
   // The first MFMA block runs PV with P = 0 against the V half of stage
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
@@ -188,7 +200,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // of step i+1 load.  One code path for every block keeps the accumulators
   // in place: the first block runs PV with P = 0 (its V stage is still the
   // zeroed LDS), and past the wave's last tile S is computed and ignored.
-  auto mfma_block = [&](int j, int nt) {  // nt: tile whose DMA to issue, or -1
+  // fetch: also load tile j's mask elements (before the DMA parts, so that
+  // the softmax can wait for them and leave those parts in flight).
+  auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
+    if constexpr (MK != 0)
+      if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * BN + 4 * h) * mstep, mstep);
     const char *kt = lds + (j % NS) * 2 * TILE_B;
     const char *vt = lds + ((j + NS - 1) % NS) * 2 * TILE_B + TILE_B;
     constexpr int FD = 2;  // fragment prefetch distance, in steps
@@ -212,7 +228,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     }
   };
 
-  auto softmax = [&](int j) {
+  auto softmax = [&](int j, int nt) {
     const int kv0 = j * BN;
     float x[16];  // scores of this lane's query row; element i is key kv0 + crow(i, h)
 #pragma unroll
@@ -236,8 +252,9 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
           x[i] = ok ? x[i] : -INFINITY;
         }
       } else {
-        const int64_t m0 = mrow + static_cast<int64_t>(kv0 + 4 * h) * p.mask.s3;
-        mask_scores<MK>(x, p.mask, m0, p.mask.s3, -64, lim, sl);
+        wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
+        mf.resolve();
+        mask_scores<MK>(x, mf, p.mask.dtype, -64, lim, sl);
       }
     }
     float mx = -INFINITY;
@@ -277,11 +294,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   if (w_tiles > 0) {
     pb[0] = pb[1] = u32x4{0, 0, 0, 0};
     for (; j < w_tiles; ++j) {
-      mfma_block(j, next_dma(j));
-      softmax(j);
+      mfma_block(j, next_dma(j), true);
+      softmax(j, next_dma(j));
       it_end(j);
     }
-    mfma_block(j, next_dma(j));  // PV of the last tile
+    mfma_block(j, next_dma(j), false);  // PV of the last tile
     it_end(j);
     ++j;
   }
@@ -329,6 +346,7 @@ hipError_t launch(const FwdArgs &a, hipStream_t st) {
   Probe pr_(mk ? "fwd_mfma_masked" : "fwd_mfma", st);
   if (mk == 1) fwd_kernel<T, D, 1><<<dim3(a.total), dim3(NT), 0, st>>>(a);
   else if (mk == 2) fwd_kernel<T, D, 2><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 3) fwd_kernel<T, D, 3><<<dim3(a.total), dim3(NT), 0, st>>>(a);
   else fwd_kernel<T, D, 0><<<dim3(a.total), dim3(NT), 0, st>>>(a);
   return hipGetLastError();
 }
@@ -339,8 +357,17 @@ bool mfma_supported(const Problem &p, int dtype) {
   if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
   if (p.Dqk != p.Dv || (p.Dqk != 64 && p.Dqk != 128)) return false;
   if (!(p.scale > 0.0)) return false;
-  if (p.mask.kind != TSATTN_MASK_ADDITIVE) return true;
-  return p.mask.dtype == TSATTN_F32 || p.mask.dtype == TSATTN_F16 || p.mask.dtype == TSATTN_BF16;
+  if (p.mask.kind == TSATTN_MASK_ADDITIVE && p.mask.dtype != TSATTN_F32 &&
+      p.mask.dtype != TSATTN_F16 && p.mask.dtype != TSATTN_BF16)
+    return false;
+  const int mk = mfma_mask_mode(p);
+  if (mk == 0) return true;
+  // General masks are read with 32-bit byte offsets inside each (b, h) slice,
+  // rows and keys padded to whole tiles.
+  const MaskDesc &m = p.mask;
+  if (m.s0 < 0 || m.s1 < 0 || m.s2 < 0 || m.s3 < 0) return false;
+  const int64_t es = mk == 1 ? 1 : (mk == 2 ? 4 : 2);
+  return ((p.Sq + 128) * m.s2 + (p.Sk + 128) * m.s3 + 1) * es < (int64_t(1) << 31);
 }
 
 hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,

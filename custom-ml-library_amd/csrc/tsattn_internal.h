@@ -78,12 +78,13 @@ struct Problem {
 
 // Mask handling of the MFMA kernels (a template parameter): 0 = none, or a
 // key mask [B,1,1,K] reduced to kv_len / kv_prefix; 1 = any other boolean
-// mask, read per (row, key) from its strides; 2 = an additive mask, read the
-// same way and added to the scaled scores.
+// mask, read per (row, key) from its strides; 2 / 3 = an additive f32 /
+// (f16 or bf16) mask, read the same way and added to the scaled scores.
 inline int mfma_mask_mode(const Problem &p) {
   if (p.mask.kind == TSATTN_MASK_BOOL)
     return p.mask.s1 == 0 && p.mask.s2 == 0 && p.kv_len != nullptr ? 0 : 1;
-  return p.mask.kind == TSATTN_MASK_ADDITIVE ? 2 : 0;
+  if (p.mask.kind != TSATTN_MASK_ADDITIVE) return 0;
+  return p.mask.dtype == TSATTN_F32 ? 2 : 3;
 }
 
 // Valid keys for batch row b: [0, kv_end).
