@@ -105,30 +105,34 @@ bool mfma_view_ok(const tsattn::View &v, int64_t len) {
   return tsattn::aligned16(v) && v.s2 > 0 && (len + 256) * v.s2 * 2 < (int64_t(1) << 31);
 }
 
-}  // namespace
-
-extern "C" {
-
-int tsattn_abi_version(void) { return TSATTN_ABI_VERSION; }
-
-const char *tsattn_last_error(void) { return g_error; }
-
-int tsattn_set_kernel_policy(int policy) {
-  if (policy < 0 || policy > 1) return fail(TSATTN_ERR_INVALID, "unknown kernel policy %d", policy);
-  g_policy.store(policy);
+// The forward / backward behind the plain and the RoPE entry points.  With a
+// RoPE descriptor only the MFMA kernels apply (they fold the rotation in).
+int check_rope(const tsattn_rope_desc *r, const tsattn::Problem &pr, tsattn::RopeDesc *out) {
+  if (!r->cos || !r->sin) return fail(TSATTN_ERR_INVALID, "RoPE needs cos / sin tables");
+  if (r->rotary_dim <= 0 || r->rotary_dim % 2 || r->rotary_dim > pr.Dqk || r->q_pos0 < 0 ||
+      r->k_pos0 < 0)
+    return fail(TSATTN_ERR_INVALID,
+                "RoPE requires a positive even rotary dimension and valid positions/base");
+  *out = tsattn::RopeDesc{r->cos, r->sin, r->rotary_dim, r->q_pos0, r->k_pos0};
   return TSATTN_OK;
 }
 
-int tsattn_last_kernel_path(void) { return g_last_path; }
+int rope_unsupported() {
+  return fail(TSATTN_ERR_UNSUPPORTED,
+              "RoPE folded into attention needs the MFMA kernels (f16/bf16, dim_qk == dim_v in "
+              "{64, 128}, 16-byte aligned views); rotate with tsattn_rope instead");
+}
 
-int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
-                        const tsattn_view *v, const tsattn_view *out, void *lse, void *stream) {
+int sdpa_forward(const tsattn_problem *p, const tsattn_rope_desc *rope, const tsattn_view *q,
+                 const tsattn_view *k, const tsattn_view *v, const tsattn_view *out, void *lse,
+                 void *stream) {
   tsattn::Problem pr;
   int rc = check_problem(p, &pr);
   if (rc) return rc;
   if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
       (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
     return rc;
+  if (rope && (rc = check_rope(rope, pr, &pr.rope))) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v),
                vo = tsattn::make_view(out);
@@ -139,22 +143,29 @@ int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsa
                                                   static_cast<float *>(lse), st),
                       "mfma forward launch");
   }
+  if (rope) return rope_unsupported();
   g_last_path = 1;
   return hip_status(tsattn::launch_generic_forward(pr, p->dtype, vq, vk, vv, vo, lse, st),
                     "generic forward launch");
 }
 
-size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p) {
+size_t backward_workspace(const tsattn_problem *p) {
   if (!p || p->batch <= 0 || p->heads_q <= 0 || p->len_q <= 0) return 0;
   // row deltas, then (MFMA path) the row LSE in log2 units
   return 2 * static_cast<size_t>(p->batch) * p->heads_q * p->len_q * acc_size(p->dtype);
 }
 
-int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
-                         const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,
-                         const void *lse, const tsattn_view *dq, const tsattn_view *dk,
-                         const tsattn_view *dv, void *workspace, size_t workspace_bytes,
-                         void *stream) {
+// Row values (as above), then the rotated query rows the dK/dV kernel reads.
+size_t rope_backward_workspace(const tsattn::Problem &pr) {
+  return tsattn::mfma_rope_stage_offset(pr) +
+         static_cast<size_t>(pr.B) * pr.Hq * pr.Sq * pr.Dqk * 2;
+}
+
+int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const tsattn_view *q,
+                  const tsattn_view *k, const tsattn_view *v, const tsattn_view *out,
+                  const tsattn_view *dout, const void *lse, const tsattn_view *dq,
+                  const tsattn_view *dk, const tsattn_view *dv, void *workspace,
+                  size_t workspace_bytes, void *stream) {
   tsattn::Problem pr;
   int rc = check_problem(p, &pr);
   if (rc) return rc;
@@ -164,7 +175,8 @@ int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const ts
       (rc = check_view(dk, "dk")) || (rc = check_view(dv, "dv")))
     return rc;
   if (!lse) return fail(TSATTN_ERR_INVALID, "backward needs the saved LSE");
-  const size_t need = tsattn_sdpa_backward_workspace(p);
+  if (rope && (rc = check_rope(rope, pr, &pr.rope))) return rc;
+  const size_t need = rope ? rope_backward_workspace(pr) : backward_workspace(p);
   if (!workspace || workspace_bytes < need)
     return fail(TSATTN_ERR_INVALID, "backward workspace too small: %zu < %zu bytes",
                 workspace_bytes, need);
@@ -183,10 +195,66 @@ int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const ts
                                                    vdv, static_cast<float *>(workspace), st),
                       "mfma backward launch");
   }
+  if (rope) return rope_unsupported();
   g_last_path = 1;
   return hip_status(tsattn::launch_generic_backward(pr, p->dtype, vq, vk, vv, vo, vg, lse, vdq,
                                                     vdk, vdv, workspace, st),
                     "generic backward launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int tsattn_abi_version(void) { return TSATTN_ABI_VERSION; }
+
+const char *tsattn_last_error(void) { return g_error; }
+
+int tsattn_set_kernel_policy(int policy) {
+  if (policy < 0 || policy > 1) return fail(TSATTN_ERR_INVALID, "unknown kernel policy %d", policy);
+  g_policy.store(policy);
+  return TSATTN_OK;
+}
+
+int tsattn_last_kernel_path(void) { return g_last_path; }
+
+int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                        const tsattn_view *v, const tsattn_view *out, void *lse, void *stream) {
+  return sdpa_forward(p, nullptr, q, k, v, out, lse, stream);
+}
+
+int tsattn_sdpa_forward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                             const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                             const tsattn_view *out, void *lse, void *stream) {
+  if (!rope) return fail(TSATTN_ERR_INVALID, "RoPE descriptor is NULL");
+  return sdpa_forward(p, rope, q, k, v, out, lse, stream);
+}
+
+size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p) { return backward_workspace(p); }
+
+size_t tsattn_sdpa_backward_rope_workspace(const tsattn_problem *p) {
+  tsattn::Problem pr;
+  if (check_problem(p, &pr)) return 0;
+  return rope_backward_workspace(pr);
+}
+
+int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
+                         const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,
+                         const void *lse, const tsattn_view *dq, const tsattn_view *dk,
+                         const tsattn_view *dv, void *workspace, size_t workspace_bytes,
+                         void *stream) {
+  return sdpa_backward(p, nullptr, q, k, v, out, dout, lse, dq, dk, dv, workspace,
+                       workspace_bytes, stream);
+}
+
+int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                              const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                              const tsattn_view *out, const tsattn_view *dout, const void *lse,
+                              const tsattn_view *dq, const tsattn_view *dk, const tsattn_view *dv,
+                              void *workspace, size_t workspace_bytes, void *stream) {
+  if (!rope) return fail(TSATTN_ERR_INVALID, "RoPE descriptor is NULL");
+  return sdpa_backward(p, rope, q, k, v, out, dout, lse, dq, dk, dv, workspace, workspace_bytes,
+                       stream);
 }
 
 size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len) {

@@ -13,12 +13,18 @@
 // Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
 // transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
 //
+// RoPE (Problem::rope, R > 0): the dQ prologue rotates the query fragments
+// as the forward did; the dQ and dK epilogues apply the inverse rotation to
+// the rounded gradients, so they are those of the unrotated queries and keys
+// (bit-identical to a separate inverse tsattn_rope).
+//
 // Masks (template MK) as in the forward: a key mask reduced to lengths, or a
 // general boolean / additive mask read per (query row, key) on every tile
 // (additive: P = exp(S scale + mask - LSE)).
 #include <type_traits>
 
 #include "mfma_common.h"
+#include "rope_math.h"
 
 namespace tsattn {
 namespace {
@@ -29,6 +35,9 @@ constexpr int NW = NT / 64;
 struct BwdArgs {
   Problem p;
   View q, k, v, o, dout, dq, dk, dv;
+  // The queries the dK/dV kernel reads: q, or with RoPE folded in the rotated
+  // rows the dQ kernel stages in the workspace ([B, Hq, Sq, D] contiguous).
+  View qk;
   const float *lse;
   // Row values the dQ kernel writes for the dK/dV kernel: [rows] nd = -delta,
   // then [rows] nl = -safe(lse) / scale, safe(lse) = isfinite(lse) ? lse : 0
@@ -125,7 +134,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
   const int n_qt = k0 < kv_end ? (p.Sq - q_start + QT - 1) / QT : 0;
   const int n_iter = n_qt * p.rep;
 
-  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
+  const uint32_t qs_b = static_cast<uint32_t>(a.qk.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
   const uint32_t ring0 = lds_addr(ring);
   // Blocked layout: block n = (n / QG, n % QG); its lane l fetches row
@@ -149,7 +158,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
     TileDma t;
     tile_of(itn, t.hq, t.q0);
     t.st = ring0 + (itn % KV_NS) * STAGE_B;
-    t.qdesc = make_desc(head_ptr<T>(a.q, b, t.hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    t.qdesc = make_desc(head_ptr<T>(a.qk, b, t.hq), static_cast<uint32_t>(p.Sq) * qs_b);
     t.gdesc = make_desc(head_ptr<T>(a.dout, b, t.hq), static_cast<uint32_t>(p.Sq) * gs_b);
     return t;
   };
@@ -360,6 +369,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
   char *slice = ring + w * 32 * 2 * D;
   const float sc = a.scale;
+  const bool rope_keys = p.rope.R > 0 && kw + c < p.Sk;
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     const f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
@@ -370,9 +380,13 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
-        *reinterpret_cast<u32x2 *>(slice + off) =
-            u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
-                  pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
+        u32x2 y = u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
+                        pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
+        // RoPE folded in: dK of the unrotated keys = the inverse rotation of
+        // the rounded dK, key position kpos0 + kw + c.
+        if (pass == 0 && rope_keys)
+          rotate_words<T, 2>(y, p.rope, p.rope.kpos0 + kw + c, 16 * dt + 4 * g + 2 * h, true);
+        *reinterpret_cast<u32x2 *>(slice + off) = y;
       }
     const View &ov = pass == 0 ? a.dk : a.dv;
     T *ob = mut<T>(ov) + b * ov.s0 + hk * ov.s1;
@@ -449,6 +463,16 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
       qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
       gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
       of[ks] = buf_load16(ors, static_cast<uint32_t>(qrow) * os_b + (ks * 16 + h * 8) * 2);
+    }
+    // RoPE folded in: rotate the query fragments as the forward did, and
+    // stage the rotated rows for the dK/dV kernel.
+    if (p.rope.R > 0 && qrow < p.Sq) {
+      T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+#pragma unroll
+      for (int ks = 0; ks < SKS; ++ks) {
+        rotate_words<T, 4>(qf[ks], p.rope, p.rope.qpos0 + qrow, 8 * ks + 4 * h, false);
+        *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
+      }
     }
     const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
     const float l = qrow < p.Sq ? a.lse[row] : 0.f;
@@ -652,14 +676,19 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
   char *slice = lds + w * 32 * 2 * D;
   const float sc = a.scale;
+  const bool rope_rows = p.rope.R > 0 && qw + c < p.Sq;
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
-      *reinterpret_cast<u32x2 *>(slice + off) =
-          u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
-                pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
+      u32x2 y = u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
+                      pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
+      // RoPE folded in: dQ of the unrotated queries = the inverse rotation of
+      // the rounded dQ (rotary_embedding's VJP), channels 32 dt + 8 g + 4 h ..
+      if (rope_rows)
+        rotate_words<T, 2>(y, p.rope, p.rope.qpos0 + qw + c, 16 * dt + 4 * g + 2 * h, true);
+      *reinterpret_cast<u32x2 *>(slice + off) = y;
     }
   }
   T *ob = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1;
@@ -699,10 +728,22 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
 
 }  // namespace
 
+size_t mfma_rope_stage_offset(const Problem &p) {
+  const size_t rows = static_cast<size_t>(p.B) * p.Hq * p.Sq;
+  return (2 * rows * sizeof(float) + 255) / 256 * 256;
+}
+
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
                                 View dout, const float *lse, View dq, View dk, View dv,
                                 float *delta, hipStream_t st) {
-  BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, lse, delta,
+  View qk = q;
+  if (p.rope.R > 0) {
+    // rotated query rows staged after the row values, 256-byte aligned
+    const int64_t D = p.Dqk;
+    qk = View{reinterpret_cast<char *>(delta) + mfma_rope_stage_offset(p),
+              static_cast<int64_t>(p.Hq) * p.Sq * D, static_cast<int64_t>(p.Sq) * D, D};
+  }
+  BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
             static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale)};
   if (dtype == TSATTN_BF16) return p.Dqk == 128 ? launch<bf16, 128>(a, st) : launch<bf16, 64>(a, st);
   return p.Dqk == 128 ? launch<f16, 128>(a, st) : launch<f16, 64>(a, st);

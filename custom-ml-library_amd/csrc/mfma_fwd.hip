@@ -28,12 +28,16 @@
 // when a row's max exceeds it by more than kTau (in log2 units), so P <= 2^kTau
 // and most tiles skip the rescale.  O / l and the LSE are exact for any m.
 //
+// RoPE (Problem::rope, R > 0): the prologue rotates the query fragments it
+// loads (the keys come rotated), bit-identical to a separate tsattn_rope.
+//
 // Masks (template MK): a key mask reduced to per-row lengths costs one ballot
 // per tile; a general boolean or additive mask (MK = 1 / 2) is read per
 // (query row, key) from its broadcast strides on every tile, an additive one
 // entering as scores * scale + mask (attention.py:105-107) in log2 units
 // (MK = 2 for an f32 mask, 3 for f16 / bf16).
 #include "mfma_common.h"
+#include "rope_math.h"
 
 namespace tsattn {
 namespace {
@@ -110,6 +114,13 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int ks = 0; ks < SKS; ++ks)
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+  // RoPE folded in: rotate the lane's channels 16 ks + 8 h .. + 7 (pairs
+  // 8 ks + 4 h ..) by position qpos0 + qrow, exactly as tsattn_rope would.
+  if (p.rope.R > 0 && qrow < p.Sq) {
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks)
+      rotate_words<T, 4>(qf[ks], p.rope, p.rope.qpos0 + qrow, 8 * ks + 4 * h, false);
+  }
   // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
   // DMA loads below, so a first use of qf inside the main loop would make it
   // wait there for tiles still in flight.

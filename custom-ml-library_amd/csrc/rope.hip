@@ -5,45 +5,16 @@
 // For channel pair (2i, 2i+1) of row t: c = cos[p, i], s = sin[p, i] with
 // p = pos0 + t, taken from tables the host builds exactly as the reference
 // does (fp32 angles p * base^(-2i/dim), cos / sin, cast to the tensor
-// dtype).  The arithmetic follows the reference's per-operation rounding in
-// the tensor dtype:
-//   y0 = rnd(rnd(x0 c) + rnd(-x1 s)),  y1 = rnd(rnd(x1 c) + rnd(x0 s)),
-// rnd = round to T (for f32 each product and sum rounds once: no fused
-// multiply-add), so results are bit-identical.  `inverse` rotates by -angle
+// dtype); the rotation rounds as the reference's array arithmetic
+// (rope_math.h), so results are bit-identical.  `inverse` rotates by -angle
 // (the VJP, :289-294).  Channels at or past rotary_dim pass through.
-#include <type_traits>
-
 #include "mfma_common.h"
+#include "rope_math.h"
 
 namespace tsattn {
 namespace {
 
 constexpr int NT = 256;
-
-// Each product and sum rounds on its own: contraction into a fused
-// multiply-add (hipcc's default for device code) is switched off here.
-template <typename T>
-__device__ __forceinline__ T rmul(T a, T b) {
-#pragma clang fp contract(off)
-  if constexpr (std::is_same<T, float>::value) return a * b;
-  else return static_cast<T>(static_cast<float>(a) * static_cast<float>(b));
-}
-template <typename T>
-__device__ __forceinline__ T radd(T a, T b) {
-#pragma clang fp contract(off)
-  if constexpr (std::is_same<T, float>::value) return a + b;
-  else return static_cast<T>(static_cast<float>(a) + static_cast<float>(b));
-}
-
-// Rotate one row in place in registers: pairs p = lane, lane + 64, ...
-template <typename T>
-__device__ __forceinline__ void rotate_pair(T &x0, T &x1, T c, T s, bool inverse) {
-  const T sn = inverse ? static_cast<T>(-static_cast<float>(s)) : s;
-  const T y0 = radd(rmul(x0, c), rmul(static_cast<T>(-static_cast<float>(x1)), sn));
-  const T y1 = radd(rmul(x1, c), rmul(x0, sn));
-  x0 = y0;
-  x1 = y1;
-}
 
 struct RopeArgs {
   int B, H, T, D, R;  // R = rotary dim (even, <= D)

@@ -66,6 +66,15 @@ struct MaskDesc {
   int64_t s0, s1, s2, s3;
 };
 
+// RoPE folded into the MFMA attention kernels: cos / sin tables [*, R / 2]
+// in the tensor dtype; query row i at position qpos0 + i, key row j at
+// kpos0 + j.  R = 0: none.
+struct RopeDesc {
+  const void *cos, *sin;
+  int R;
+  int64_t qpos0, kpos0;
+};
+
 struct Problem {
   int B, Hq, Hkv, Sq, Sk, Dqk, Dv, rep;
   double scale;
@@ -74,6 +83,7 @@ struct Problem {
   const int32_t *kv_len;
   const int32_t *kv_prefix;
   MaskDesc mask;
+  RopeDesc rope;
 };
 
 // Mask handling of the MFMA kernels (a template parameter): 0 = none, or a
@@ -136,6 +146,9 @@ hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
                                 View dout, const float *lse, View dq, View dk, View dv,
                                 float *delta, hipStream_t st);
+// With RoPE folded in (p.rope.R > 0) the backward workspace also holds the
+// rotated query rows [B, Hq, Sq, Dqk] (16-bit) from this byte offset on.
+size_t mfma_rope_stage_offset(const Problem &p);
 
 // Split-K decode.
 bool decode_supported(const Problem &p, int dtype);

@@ -16,7 +16,7 @@ from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_native" / "libtsattn.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, F16, BF16, F64, BOOL, I8 = 0, 1, 2, 3, 4, 5
@@ -53,8 +53,21 @@ class Problem(ctypes.Structure):
     ]
 
 
+class RopeDesc(ctypes.Structure):
+    """``tsattn_rope_desc``: cos / sin tables, rotary dim, query / key positions."""
+
+    _fields_ = [
+        ("cos", c_void_p),
+        ("sin", c_void_p),
+        ("rotary_dim", c_int32),
+        ("q_pos0", c_int64),
+        ("k_pos0", c_int64),
+    ]
+
+
 _PV = POINTER(View)
 _PP = POINTER(Problem)
+_PR = POINTER(RopeDesc)
 
 # name -> (restype, argtypes); exactly the symbols include/tsattn.h declares
 SIGNATURES = {
@@ -67,6 +80,13 @@ SIGNATURES = {
     "tsattn_sdpa_backward": (
         c_int,
         [_PP, _PV, _PV, _PV, _PV, _PV, c_void_p, _PV, _PV, _PV, c_void_p, c_size_t, c_void_p],
+    ),
+    "tsattn_sdpa_forward_rope": (c_int, [_PP, _PR, _PV, _PV, _PV, _PV, c_void_p, c_void_p]),
+    "tsattn_sdpa_backward_rope_workspace": (c_size_t, [_PP]),
+    "tsattn_sdpa_backward_rope": (
+        c_int,
+        [_PP, _PR, _PV, _PV, _PV, _PV, _PV, c_void_p, _PV, _PV, _PV, c_void_p, c_size_t,
+         c_void_p],
     ),
     "tsattn_decode_workspace": (c_size_t, [_PP, c_int32]),
     "tsattn_decode_forward": (

@@ -83,6 +83,7 @@ def scaled_dot_product_attention(
     backend: str = "auto",
     block_size: int = 64,
     enable_gqa: bool = False,
+    _rope: tuple | None = None,
 ) -> Tensor:
     """Attention for [batch, heads, sequence, channels] tensors.
 
@@ -91,6 +92,15 @@ def scaled_dot_product_attention(
     absolute position of the first query in a cached key sequence.
     ``block_size`` is accepted for signature compatibility; the kernels use
     their own tiles.
+
+    ``_rope = (q_pos0, k_pos0, base)`` (used by ``MultiHeadAttention``, not
+    part of the reference signature): query and key are *unrotated*; the
+    result and gradients are those of ``rotary_embedding(query, q_pos0)`` and
+    ``rotary_embedding(key, k_pos0)`` fed to this function, bit for bit.  The
+    keys are rotated once by the RoPE kernel; the query rotation and both
+    inverse rotations of the gradients run inside the MFMA kernels
+    (``tsattn_sdpa_forward_rope`` / ``_backward_rope``), with separate RoPE
+    kernels where those do not apply.
     """
     # --- the reference's validation, same order and messages (:36-62) ---
     if any(t.ndim != 4 for t in (query, key, value)):
@@ -170,6 +180,18 @@ def scaled_dot_product_attention(
     stream = ctypes.c_void_p(current_stream(query.device))
     recording = is_grad_enabled() and any(t.requires_grad for t in (query, key, value))
     out = torch.empty((b, hq, qlen, dim_v), dtype=q.dtype, device=tdev)
+    rope = None  # (descriptor, tables) when the kernels fold the query rotation in
+    if _rope is not None:
+        q_pos0, k_pos0, base = _rope
+        if (dim % 2 or q_pos0 < 0 or k_pos0 < 0 or base <= 0 or not math.isfinite(base)
+                or q.dtype not in (torch.float32, torch.float16, torch.bfloat16)):
+            raise ValueError("RoPE requires a positive even rotary dimension and valid positions/base")
+        k = _rope_rows(k, k_pos0, base, dim, False, query.device)
+        tables = rope_tables(base, dim, q.dtype, tdev, max(q_pos0 + qlen, k_pos0 + klen))
+        desc = _lib.RopeDesc()
+        desc.cos, desc.sin = tables[0].data_ptr(), tables[1].data_ptr()
+        desc.rotary_dim, desc.q_pos0, desc.k_pos0 = dim, q_pos0, k_pos0
+        rope = (desc, tables)
     vq, vk, vv, vo = _view(q), _view(k), _view(v), _view(out)
 
     use_decode = (
@@ -182,6 +204,9 @@ def scaled_dot_product_attention(
         and all(_aligned16(t) for t in (q, k, v))
     )
     if use_decode:
+        if rope is not None:
+            q = _rope_rows(q, q_pos0, base, dim, False, query.device)
+            vq = _view(q)
         nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
         _lib.check(
@@ -197,13 +222,19 @@ def scaled_dot_product_attention(
     if recording:
         lse_dtype = torch.float64 if code == _lib.F64 else torch.float32
         lse = torch.empty((b, hq, qlen), dtype=lse_dtype, device=tdev)
-    _lib.check(
-        lib.tsattn_sdpa_forward(
-            ctypes.byref(prob), vq, vk, vv, vo,
-            ctypes.c_void_p(None if lse is None else lse.data_ptr()), stream,
-        ),
-        "attention forward",
-    )
+    lse_ptr = ctypes.c_void_p(None if lse is None else lse.data_ptr())
+    fused = False
+    if rope is not None:
+        try:
+            _lib.check(lib.tsattn_sdpa_forward_rope(ctypes.byref(prob), ctypes.byref(rope[0]), vq, vk,
+                                                    vv, vo, lse_ptr, stream), "attention forward")
+            fused = True
+        except NotImplementedError:  # not an MFMA problem: rotate the queries separately
+            q = _rope_rows(q, q_pos0, base, dim, False, query.device)
+            vq = _view(q)
+    if not fused:
+        _lib.check(lib.tsattn_sdpa_forward(ctypes.byref(prob), vq, vk, vv, vo, lse_ptr, stream),
+                   "attention forward")
     if not recording:
         return Tensor._from_op(out, (query, key, value), None, "sdpa_hip")
 
@@ -214,16 +245,20 @@ def scaled_dot_product_attention(
         dq = torch.empty(q.shape, dtype=q.dtype, device=tdev)
         dk = torch.empty(k.shape, dtype=k.dtype, device=tdev)
         dv = torch.empty(v.shape, dtype=v.dtype, device=tdev)
-        nbytes = lib.tsattn_sdpa_backward_workspace(ctypes.byref(prob))
+        nbytes = (lib.tsattn_sdpa_backward_rope_workspace if fused
+                  else lib.tsattn_sdpa_backward_workspace)(ctypes.byref(prob))
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
-        _lib.check(
-            lib.tsattn_sdpa_backward(
-                ctypes.byref(prob), vq, vk, vv, vo, _view(g), ctypes.c_void_p(lse.data_ptr()),
-                _view(dq), _view(dk), _view(dv), ctypes.c_void_p(ws.data_ptr()), nbytes,
-                ctypes.c_void_p(current_stream(query.device)),
-            ),
-            "attention backward",
-        )
+        args = (vq, vk, vv, vo, _view(g), ctypes.c_void_p(lse.data_ptr()), _view(dq), _view(dk),
+                _view(dv), ctypes.c_void_p(ws.data_ptr()), nbytes,
+                ctypes.c_void_p(current_stream(query.device)))
+        if fused:  # gradients of the unrotated queries and keys, straight from the kernels
+            _lib.check(lib.tsattn_sdpa_backward_rope(ctypes.byref(prob), ctypes.byref(rope[0]), *args),
+                       "attention backward")
+            return dq, dk, dv
+        _lib.check(lib.tsattn_sdpa_backward(ctypes.byref(prob), *args), "attention backward")
+        if rope is not None:  # rotary_embedding's VJP on both
+            dq = _rope_rows(dq, q_pos0, base, dim, True, query.device)
+            dk = _rope_rows(dk, k_pos0, base, dim, True, query.device)
         return dq, dk, dv
 
     return Tensor._from_op(out, (query, key, value), backward, "sdpa_hip")
@@ -301,6 +336,16 @@ def _rope_launch(x, out, offset: int, base: float, dim: int, inverse: bool, dev)
             ctypes.c_void_p(cos.data_ptr()), ctypes.c_void_p(sin.data_ptr()), offset, int(inverse),
             ctypes.c_void_p(current_stream(dev))),
         "RoPE")
+
+
+def _rope_rows(x, offset: int, base: float, dim: int, inverse: bool, dev):
+    """RoPE (or its inverse) of a raw [B, H, T, D] device array into a new one."""
+    import torch
+
+    src = x if x.stride(-1) == 1 else x.contiguous()
+    out = torch.empty(src.shape, dtype=src.dtype, device=src.device)
+    _rope_launch(src, out, offset, base, dim, inverse, dev)
+    return out
 
 
 def rotary_embedding(input: Tensor, offset: int = 0, base: float = 10000.0,

@@ -5,8 +5,11 @@ decoder-only ``TransformerLM`` with cached generation.
 and data flow of ``src/tensorsmith/nn/transformer.py:48-155``: projections
 reshaped to ``[B,S,H,D]`` and permuted to ``[B,H,S,D]`` *views* (the HIP
 kernels take the strides, so no copy is made), optional interleaved RoPE
-(one kernel per operand; with a cache, the key rotation and the K / V append
-are one kernel), KV-cache append with ``causal_offset = cache.length``, then
+(without a cache the attention kernels rotate the queries in their prologue
+and rotate the query / key gradients back in their epilogues, the keys taking
+one RoPE kernel; with a cache, one RoPE kernel for the queries and one kernel
+for the key rotation and the K / V append), KV-cache append with
+``causal_offset = cache.length``, then
 ``scaled_dot_product_attention`` with ``backend`` (``"hip"`` added to the
 allowlist; ``"auto"`` picks it).
 
@@ -94,13 +97,16 @@ class MultiHeadAttention(Module):
         v = (self.v_proj(source).reshape(batch, source.shape[1], self.num_kv_heads, self.head_dim)
              .permute(0, 2, 1, 3))
         fused = False
-        if self.rotary:
+        rope = None
+        if self.rotary and cache is None:
+            # the attention kernels rotate the queries (and the gradients) themselves
+            rope = (offset, offset if context is None else 0, 10000.0)
+        elif self.rotary:
             q = rotary_embedding(q, offset)
-            if cache is not None:
-                # rotate the new keys and write them (and the values) into the cache in one kernel
-                fused = cache._append_rotary(k, v)
+            # rotate the new keys and write them (and the values) into the cache in one kernel
+            fused = cache._append_rotary(k, v)
             if not fused:
-                k = rotary_embedding(k, offset if context is None else 0)
+                k = rotary_embedding(k, offset)
         attended = None
         if cache is not None:
             if not fused:
@@ -114,7 +120,7 @@ class MultiHeadAttention(Module):
             attended = scaled_dot_product_attention(
                 q, k, v, attn_mask, self.dropout_p if self.training else 0.0, is_causal,
                 causal_offset=offset, backend=self.backend,
-                enable_gqa=self.num_kv_heads != self.num_heads)
+                enable_gqa=self.num_kv_heads != self.num_heads, _rope=rope)
         return self.out_proj(attended.permute(0, 2, 1, 3).reshape(batch, steps, self.embed_dim))
 
 

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 3
+#define TSATTN_ABI_VERSION 4
 
 typedef enum {
   TSATTN_OK = 0,
@@ -137,6 +137,54 @@ int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const ts
                          const void *lse, const tsattn_view *dq, const tsattn_view *dk,
                          const tsattn_view *dv, void *workspace, size_t workspace_bytes,
                          void *stream);
+
+/*
+ * RoPE folded into the attention kernels.  cos / sin: device tables
+ * [L, rotary_dim / 2] in the tensor dtype whose row p holds the angles of
+ * position p, built as the reference builds its per-call table
+ * (src/tensorsmith/nn/attention.py:269-279: float32 angles
+ * p * base^(-2i / rotary_dim), NumPy cos / sin, cast to the dtype); query
+ * row i sits at position q_pos0 + i, key row j at k_pos0 + j, and the tables
+ * must hold those rows.
+ */
+typedef struct tsattn_rope_desc {
+  const void *cos;
+  const void *sin;
+  int32_t rotary_dim; /* even, 0 < rotary_dim <= dim_qk; later channels pass through */
+  int64_t q_pos0;
+  int64_t k_pos0;
+} tsattn_rope_desc;
+
+/*
+ * rotary_embedding(q, q_pos0) then scaled_dot_product_attention, the step
+ * MultiHeadAttention takes (src/tensorsmith/nn/transformer.py:138-149), with
+ * the query rotation done in the kernel prologue: `q` holds the unrotated
+ * queries, `k` the keys already rotated (tsattn_rope).  Bit-identical to
+ * tsattn_rope on q followed by tsattn_sdpa_forward.  Only problems the MFMA
+ * kernels take (f16/bf16, dim_qk == dim_v in {64, 128}, 16-byte aligned
+ * views); others return TSATTN_ERR_UNSUPPORTED (rotate with tsattn_rope).
+ */
+int tsattn_sdpa_forward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                             const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                             const tsattn_view *out, void *lse, void *stream);
+
+/* Bytes of scratch tsattn_sdpa_backward_rope needs: the row values of
+ * tsattn_sdpa_backward plus the rotated query rows the dK/dV kernel reads. */
+size_t tsattn_sdpa_backward_rope_workspace(const tsattn_problem *p);
+
+/*
+ * Its VJP, with rotary_embedding's VJP (attention.py:289-294) folded in:
+ * `q` unrotated, `k` rotated, as in the forward; dq and dk are the gradients
+ * of the unrotated queries and keys -- the dQ and dK epilogues round the
+ * gradients to the tensor dtype and rotate them back (positions q_pos0 + i,
+ * k_pos0 + j), bit-identical to tsattn_sdpa_backward followed by an inverse
+ * tsattn_rope on dq and dk.  Workspace: tsattn_sdpa_backward_rope_workspace.
+ */
+int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                              const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                              const tsattn_view *out, const tsattn_view *dout, const void *lse,
+                              const tsattn_view *dq, const tsattn_view *dk, const tsattn_view *dv,
+                              void *workspace, size_t workspace_bytes, void *stream);
 
 /* Bytes of scratch tsattn_decode_forward needs for `split_len` keys per split. */
 size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);

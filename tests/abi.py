@@ -166,3 +166,36 @@ def rope_append(k, v, kc, vc, cos, sin, pos, rotary_dim, ks=None, vs=None):
         CODES[k.dtype], b, h, t, d, rotary_dim, view(k), view(v), view(kc), view(vc), *scales,
         ctypes.c_void_p(cos.data_ptr() if cos is not None else 0),
         ctypes.c_void_p(sin.data_ptr() if sin is not None else 0), pos, stream()), "rope append")
+
+
+def rope_desc(cos, sin, rotary_dim, q_pos0, k_pos0):
+    d = _lib.RopeDesc()
+    d.cos, d.sin = cos.data_ptr(), sin.data_ptr()
+    d.rotary_dim, d.q_pos0, d.k_pos0 = rotary_dim, q_pos0, k_pos0
+    return d
+
+
+def forward_rope(q, k, v, desc, **kw):
+    """tsattn_sdpa_forward_rope: q unrotated, k rotated."""
+    p = problem(q, k, v, **kw)
+    out = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device)
+    lse = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device)
+    lib = _lib.load()
+    _lib.check(lib.tsattn_sdpa_forward_rope(ctypes.byref(p), ctypes.byref(desc), view(q), view(k),
+                                            view(v), view(out), ctypes.c_void_p(lse.data_ptr()),
+                                            stream()), "forward rope")
+    return out, lse, lib.tsattn_last_kernel_path()
+
+
+def backward_rope(q, k, v, out, g, lse, desc, **kw):
+    """tsattn_sdpa_backward_rope: gradients of the unrotated q and k."""
+    p = problem(q, k, v, **kw)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    lib = _lib.load()
+    nbytes = lib.tsattn_sdpa_backward_rope_workspace(ctypes.byref(p))
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
+    _lib.check(lib.tsattn_sdpa_backward_rope(
+        ctypes.byref(p), ctypes.byref(desc), view(q), view(k), view(v), view(out), view(g),
+        ctypes.c_void_p(lse.data_ptr()), view(dq), view(dk), view(dv),
+        ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "backward rope")
+    return dq, dk, dv

@@ -14,6 +14,14 @@
 * Model level: cached TransformerLM decoding through the fused kernel gives
   bit-identical logits and cache contents to the two-step path
   (rotary_embedding, then append), fp16 and int8 caches.
+* RoPE folded into the MFMA attention kernels
+  (``tsattn_sdpa_forward_rope`` / ``_backward_rope``): O, LSE, dQ, dK, dV
+  bit-identical to the unfused chain (tsattn_rope on q and k, attention,
+  inverse tsattn_rope on dq and dk) -- partial rotary dims, GQA, causal
+  offsets, distinct query / key positions, general masks; problems outside
+  the MFMA kernels refuse with ERR_UNSUPPORTED; MultiHeadAttention training
+  steps give bit-identical outputs and gradients through the fused path and
+  through rotary_embedding + attention.
 """
 
 from __future__ import annotations
@@ -189,3 +197,122 @@ def test_fused_cached_decode_is_bitwise_the_two_step_path(quantized):
         for x, y in zip(a, b):
             if x is not None:
                 assert torch.equal(x, y)
+
+
+FUSED_CASES = [
+    # (dtype, B, Hq, Hkv, Sq, Sk, D, R, causal, offset, q_pos0, k_pos0)
+    ("bfloat16", 2, 2, 2, 200, 200, 128, 128, True, 0, 0, 0),
+    ("float16", 1, 4, 2, 130, 257, 64, 64, True, 127, 127, 0),
+    ("bfloat16", 2, 2, 1, 77, 150, 128, 64, False, 0, 9, 3),
+    ("float16", 1, 2, 2, 256, 256, 128, 96, True, 0, 5, 5),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_rope_folded_into_attention_is_bitwise_the_unfused_chain(case):
+    dtype, b, hq, hkv, sq, sk, d, r, causal, off, qp, kp = case
+    say(f"fused rope attention {case}")
+    rng = np.random.default_rng(sq + d)
+    q, k, v, g = (abi.dev_tensor(rows(rng, shape, dtype, 0.7), dtype)
+                  for shape in ((b, hq, sq, d), (b, hkv, sk, d), (b, hkv, sk, d), (b, hq, sq, d)))
+    cos, sin = tables(max(qp + sq, kp + sk) + 1, r, dtype)
+    rot = lambda x, pos, inv=False: _rot(x, cos, sin, pos, r, inv)
+    k_rot = rot(k, kp)
+    kw = dict(causal=causal, offset=off)
+    # unfused chain
+    out_u, lse_u, _ = abi.forward(rot(q, qp), k_rot, v, **kw)
+    dq_r, dk_r, dv_u, _ = abi.backward(rot(q, qp), k_rot, v, out_u, g, lse_u, **kw)
+    dq_u, dk_u = rot(dq_r, qp, True), rot(dk_r, kp, True)
+    # folded
+    desc = abi.rope_desc(cos, sin, r, qp, kp)
+    out_f, lse_f, path = abi.forward_rope(q, k_rot, v, desc, **kw)
+    assert path == _lib.PATH_MFMA
+    dq_f, dk_f, dv_f = abi.backward_rope(q, k_rot, v, out_f, g, lse_f, desc, **kw)
+    torch.cuda.synchronize()
+    for name, a_, b_ in (("O", out_f, out_u), ("LSE", lse_f, lse_u), ("dQ", dq_f, dq_u),
+                         ("dK", dk_f, dk_u), ("dV", dv_f, dv_u)):
+        assert torch.equal(a_, b_), name
+
+
+def _rot(x, cos, sin, pos, r, inverse):
+    out = torch.empty_like(x)
+    abi.rope(x, out, cos, sin, pos, r, inverse)
+    return out
+
+
+def test_rope_folded_with_a_general_mask():
+    dtype, b, h, s, d = "bfloat16", 2, 2, 150, 128
+    rng = np.random.default_rng(7)
+    q, k, v, g = (abi.dev_tensor(rows(rng, (b, h, s, d), dtype, 0.7), dtype) for _ in range(4))
+    mask = torch.from_numpy(rng.random((s, s)) > 0.2).cuda()
+    cos, sin = tables(s + 1, d, dtype)
+    k_rot = _rot(k, cos, sin, 0, d, False)
+    out_u, lse_u, _ = abi.forward(_rot(q, cos, sin, 0, d, False), k_rot, v, causal=True, mask=mask)
+    grads_u = abi.backward(_rot(q, cos, sin, 0, d, False), k_rot, v, out_u, g, lse_u, causal=True,
+                           mask=mask)[:3]
+    desc = abi.rope_desc(cos, sin, d, 0, 0)
+    out_f, lse_f, _ = abi.forward_rope(q, k_rot, v, desc, causal=True, mask=mask)
+    dq_f, dk_f, dv_f = abi.backward_rope(q, k_rot, v, out_f, g, lse_f, desc, causal=True, mask=mask)
+    torch.cuda.synchronize()
+    assert torch.equal(out_f, out_u) and torch.equal(lse_f, lse_u)
+    assert torch.equal(dq_f, _rot(grads_u[0], cos, sin, 0, d, True))
+    assert torch.equal(dk_f, _rot(grads_u[1], cos, sin, 0, d, True))
+    assert torch.equal(dv_f, grads_u[2])
+
+
+def test_rope_folded_refuses_problems_outside_the_mfma_kernels():
+    q = torch.zeros((1, 1, 8, 32), dtype=torch.float32, device="cuda")
+    cos, sin = tables(9, 32, "float32")
+    desc = abi.rope_desc(cos, sin, 32, 0, 0)
+    with pytest.raises(NotImplementedError, match="tsattn_rope"):
+        abi.forward_rope(q, q, q, desc)
+    h = torch.zeros((1, 1, 8, 96), dtype=torch.float16, device="cuda")  # D = 96: not an MFMA shape
+    c16, s16 = tables(9, 96, "float16")
+    with pytest.raises(NotImplementedError):
+        abi.forward_rope(h, h, h, abi.rope_desc(c16, s16, 96, 0, 0))
+    with pytest.raises(ValueError, match="rotary"):
+        abi.forward_rope(h, h, h, abi.rope_desc(c16, s16, 97, 0, 0))
+
+
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_attention_module_fused_rope_is_bitwise_the_two_step_path(dtype):
+    from tensorsmith_hip.nn import attention as attn_mod
+    from tensorsmith_hip.nn import transformer as tr_mod
+
+    say(f"MHA fused rope {dtype}")
+    plain = attn_mod.scaled_dot_product_attention
+
+    def two_step(q, k, v, *args, _rope=None, **kw):
+        if _rope is not None:
+            q = attn_mod.rotary_embedding(q, _rope[0], _rope[2])
+            k = attn_mod.rotary_embedding(k, _rope[1], _rope[2])
+        return plain(q, k, v, *args, **kw)
+
+    def step(patched):
+        ts.seed(5)
+        mha = nn.MultiHeadAttention(256, 2, num_kv_heads=1, device="hip")
+        mha.to(dtype=dtype)
+        x = ts.tensor(np.random.default_rng(5).standard_normal((2, 96, 256)).astype(np.float32),
+                      device="hip", dtype=dtype, requires_grad=True)
+        _lib.profile_enable(True)
+        _lib.profile_reset()
+        gy = ts.tensor(np.random.default_rng(6).standard_normal((2, 96, 256)).astype(np.float32),
+                       device="hip", dtype=dtype)
+        if patched:
+            with patch.object(tr_mod, "scaled_dot_product_attention", two_step):
+                y = mha(x, is_causal=True)
+                y.backward(gy)
+        else:
+            y = mha(x, is_causal=True)
+            y.backward(gy)
+        probes = _lib.profile_read()
+        _lib.profile_enable(False)
+        grads = [p.grad.numpy() for p in mha.parameters()] + [x.grad.numpy()]
+        return y.numpy(), grads, probes
+
+    y_f, g_f, probes_f = step(False)
+    y_u, g_u, probes_u = step(True)
+    assert probes_f["rope"][0] == 1 and probes_u["rope"][0] == 4  # keys only / q, k and both VJPs
+    np.testing.assert_array_equal(y_f, y_u)
+    for a_, b_ in zip(g_f, g_u):
+        np.testing.assert_array_equal(a_, b_)
