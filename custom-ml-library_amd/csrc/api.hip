@@ -113,6 +113,12 @@ int check_rope(const tsattn_rope_desc *r, const tsattn::Problem &pr, tsattn::Rop
       r->k_pos0 < 0)
     return fail(TSATTN_ERR_INVALID,
                 "RoPE requires a positive even rotary dimension and valid positions/base");
+  if (r->rotary_dim % 8)
+    return fail(TSATTN_ERR_UNSUPPORTED,
+                "RoPE folded into attention needs a rotary dim divisible by 8 (got %d); rotate "
+                "with tsattn_rope instead", r->rotary_dim);
+  if (reinterpret_cast<uintptr_t>(r->cos) % 8 || reinterpret_cast<uintptr_t>(r->sin) % 8)
+    return fail(TSATTN_ERR_UNSUPPORTED, "RoPE tables must be 8-byte aligned; rotate with tsattn_rope instead");
   *out = tsattn::RopeDesc{r->cos, r->sin, r->rotary_dim, r->q_pos0, r->k_pos0};
   return TSATTN_OK;
 }

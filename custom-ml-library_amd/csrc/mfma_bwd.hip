@@ -369,7 +369,6 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
   char *slice = ring + w * 32 * 2 * D;
   const float sc = a.scale;
-  const bool rope_keys = p.rope.R > 0 && kw + c < p.Sk;
 #pragma unroll
   for (int pass = 0; pass < 2; ++pass) {
     const f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
@@ -380,21 +379,32 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
-        u32x2 y = u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
-                        pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
-        // RoPE folded in: dK of the unrotated keys = the inverse rotation of
-        // the rounded dK, key position kpos0 + kw + c.
-        if (pass == 0 && rope_keys)
-          rotate_words<T, 2>(y, p.rope, p.rope.kpos0 + kw + c, 16 * dt + 4 * g + 2 * h, true);
-        *reinterpret_cast<u32x2 *>(slice + off) = y;
+        *reinterpret_cast<u32x2 *>(slice + off) =
+            u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
+                  pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
       }
     const View &ov = pass == 0 ? a.dk : a.dv;
     T *ob = mut<T>(ov) + b * ov.s0 + hk * ov.s1;
+    u32x4 vr[32 * CPR / 64];
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-      const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
-      if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr;
+      vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+    }
+    // RoPE folded in: dK of the unrotated keys = the inverse rotation of the
+    // rounded dK, key position kpos0 + kw + r, one 16-byte row chunk at a time.
+    if (pass == 0 && p.rope.R > 0) {
+#pragma unroll
+      for (int u = 0; u < 32 * CPR / 64; ++u) {
+        const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+        const int key = kw + r < p.Sk ? kw + r : p.Sk - 1;  // rows past Sk: not stored
+        rotate_chunk<T>(vr[u], p.rope, p.rope.kpos0 + key, 4 * q, true);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 32 * CPR / 64; ++u) {
+      const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+      if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr[u];
     }
   }
 }
@@ -466,12 +476,14 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     }
     // RoPE folded in: rotate the query fragments as the forward did, and
     // stage the rotated rows for the dK/dV kernel.
-    if (p.rope.R > 0 && qrow < p.Sq) {
-      T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+    if (p.rope.R > 0) {
+      const int64_t row = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
 #pragma unroll
-      for (int ks = 0; ks < SKS; ++ks) {
-        rotate_words<T, 4>(qf[ks], p.rope, p.rope.qpos0 + qrow, 8 * ks + 4 * h, false);
-        *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
+      for (int ks = 0; ks < SKS; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
+      if (qrow < p.Sq) {
+        T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+#pragma unroll
+        for (int ks = 0; ks < SKS; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
       }
     }
     const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
@@ -676,27 +688,37 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
   char *slice = lds + w * 32 * 2 * D;
   const float sc = a.scale;
-  const bool rope_rows = p.rope.R > 0 && qw + c < p.Sq;
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
-      u32x2 y = u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
-                      pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
-      // RoPE folded in: dQ of the unrotated queries = the inverse rotation of
-      // the rounded dQ (rotary_embedding's VJP), channels 32 dt + 8 g + 4 h ..
-      if (rope_rows)
-        rotate_words<T, 2>(y, p.rope, p.rope.qpos0 + qw + c, 16 * dt + 4 * g + 2 * h, true);
-      *reinterpret_cast<u32x2 *>(slice + off) = y;
+      *reinterpret_cast<u32x2 *>(slice + off) =
+          u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
+                pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
     }
   }
   T *ob = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1;
+  u32x4 vr[32 * CPR / 64];
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
     const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
-    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.dq.s2 + q * 8) = vr;
+    vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+  }
+  // RoPE folded in: dQ of the unrotated queries = the inverse rotation of the
+  // rounded dQ (rotary_embedding's VJP), one 16-byte row chunk at a time.
+  if (p.rope.R > 0) {
+#pragma unroll
+    for (int u = 0; u < 32 * CPR / 64; ++u) {
+      const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+      const int row = qw + r < p.Sq ? qw + r : p.Sq - 1;  // rows past Sq: not stored
+      rotate_chunk<T>(vr[u], p.rope, p.rope.qpos0 + row, 4 * q, true);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < 32 * CPR / 64; ++u) {
+    const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.dq.s2 + q * 8) = vr[u];
   }
 }
 

@@ -116,10 +116,10 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
   // RoPE folded in: rotate the lane's channels 16 ks + 8 h .. + 7 (pairs
   // 8 ks + 4 h ..) by position qpos0 + qrow, exactly as tsattn_rope would.
-  if (p.rope.R > 0 && qrow < p.Sq) {
+  if (p.rope.R > 0) {
+    const int64_t row = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
 #pragma unroll
-    for (int ks = 0; ks < SKS; ++ks)
-      rotate_words<T, 4>(qf[ks], p.rope, p.rope.qpos0 + qrow, 8 * ks + 4 * h, false);
+    for (int ks = 0; ks < SKS; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
   }
   // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
   // DMA loads below, so a first use of qf inside the main loop would make it

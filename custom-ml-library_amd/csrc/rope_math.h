@@ -13,7 +13,7 @@
 
 #include <type_traits>
 
-#include "tsattn_internal.h"
+#include "mfma_common.h"
 
 namespace tsattn {
 
@@ -50,17 +50,30 @@ __device__ __forceinline__ unsigned rotate_word(unsigned w, T c, T s, bool inver
          (static_cast<unsigned>(__builtin_bit_cast(uint16_t, x1)) << 16);
 }
 
-// Rotate the N pairs packed in words w[0 .. N) -- pair p0 + m in word m --
-// by row `row` of the descriptor's [*, R / 2] tables; pairs at or past R / 2
-// pass through (and read no table entry).
-template <typename T, int N, typename W>
-__device__ __forceinline__ void rotate_words(W &w, const RopeDesc &r, int64_t row, int p0,
+// Rotate one 16-byte chunk of a row -- 4 pairs packed in x, pairs p0 .. p0 + 3
+// (p0 a multiple of 4) -- by row `row` of the descriptor's [*, R / 2] tables,
+// R a multiple of 8 so that a chunk is wholly inside or outside the rotated
+// channels.  The table loads are unconditional 8-byte loads (the pair index
+// clamped into range, the result selected), so a run of chunks issues all
+// its loads before the first use instead of one guarded load at a time.
+template <typename T>
+__device__ __forceinline__ void rotate_chunk(u32x4 &x, const RopeDesc &r, int64_t row, int p0,
                                              bool inverse) {
-  const T *cr = static_cast<const T *>(r.cos) + row * (r.R / 2);
-  const T *sr = static_cast<const T *>(r.sin) + row * (r.R / 2);
+  const int half = r.R / 2;
+  const int pc = p0 < half ? p0 : half - 4;
+  const int64_t at = row * half + pc;
+  const u32x2 cw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(r.cos) + at);
+  const u32x2 sw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(r.sin) + at);
+  u32x4 y;
 #pragma unroll
-  for (int m = 0; m < N; ++m)
-    if (2 * (p0 + m) < r.R) w[m] = rotate_word<T>(w[m], cr[p0 + m], sr[p0 + m], inverse);
+  for (int m = 0; m < 4; ++m) {
+    const unsigned c2 = cw[m >> 1], s2 = sw[m >> 1];
+    const int sh = (m & 1) * 16;
+    const T c = __builtin_bit_cast(T, static_cast<uint16_t>(c2 >> sh));
+    const T s = __builtin_bit_cast(T, static_cast<uint16_t>(s2 >> sh));
+    y[m] = rotate_word<T>(x[m], c, s, inverse);
+  }
+  if (p0 < half) x = y;
 }
 
 }  // namespace tsattn
