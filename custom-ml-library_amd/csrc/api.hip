@@ -64,6 +64,8 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
     if (p->mask_kind == TSATTN_MASK_ADDITIVE && !is_float_dtype(p->mask_dtype))
       return fail(TSATTN_ERR_INVALID, "attention masks must be boolean or floating point");
   }
+  if (!(p->dropout_p >= 0.0 && p->dropout_p < 1.0))
+    return fail(TSATTN_ERR_INVALID, "invalid dropout probability, block size, or causal offset");
   if (p->dim_qk > 512 || p->dim_v > 512)
     return fail(TSATTN_ERR_UNSUPPORTED, "head dims above 512 are not supported (got %d/%d)",
                 p->dim_qk, p->dim_v);
@@ -91,6 +93,17 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
   q.mask.s1 = p->heads_q == 1 ? 0 : p->mask.stride[1];
   q.mask.s2 = p->len_q == 1 ? 0 : p->mask.stride[2];
   q.mask.s3 = p->len_kv == 1 ? 0 : p->mask.stride[3];
+  if (p->dropout_p > 0.0) {
+    // keep iff word >= round-half-even(65536 p); kept values times f32(1) / f32(1 - p)
+    q.drop.on = 1;
+    q.drop.thr = static_cast<uint32_t>(fmin(nearbyint(p->dropout_p * 65536.0), 65536.0));
+    q.drop.scale = 1.0f / static_cast<float>(1.0 - p->dropout_p);
+    q.drop.scale64 = 1.0 / (1.0 - p->dropout_p);
+    q.drop.k0 = p->dropout_key[0];
+    q.drop.k1 = p->dropout_key[1];
+    q.drop.c0 = p->dropout_counter + 1;
+    q.drop.c1 = q.drop.c0 == 0 ? 1 : 0;
+  }
   *out = q;
   return TSATTN_OK;
 }
@@ -263,6 +276,15 @@ int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *r
                        stream);
 }
 
+int tsattn_dropout_keep(const tsattn_problem *p, uint8_t *out, void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if (!out) return fail(TSATTN_ERR_INVALID, "output pointer is NULL");
+  return hip_status(tsattn::launch_dropout_keep(pr, out, static_cast<hipStream_t>(stream)),
+                    "dropout keep launch");
+}
+
 size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len) {
   tsattn::Problem pr;
   if (check_problem(p, &pr)) return 0;
@@ -275,6 +297,8 @@ int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const t
   tsattn::Problem pr;
   int rc = check_problem(p, &pr);
   if (rc) return rc;
+  if (pr.drop.on)
+    return fail(TSATTN_ERR_UNSUPPORTED, "the decode kernel does not drop (inference only)");
   if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
       (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
     return rc;
@@ -302,6 +326,8 @@ int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, co
   tsattn::Problem pr;
   int rc = check_problem(p, &pr);
   if (rc) return rc;
+  if (pr.drop.on)
+    return fail(TSATTN_ERR_UNSUPPORTED, "the decode kernel does not drop (inference only)");
   if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
       (rc = check_view(v, "value")) || (rc = check_view(k_scale, "key scale")) ||
       (rc = check_view(v_scale, "value scale")) || (rc = check_view(out, "output")))

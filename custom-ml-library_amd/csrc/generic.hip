@@ -7,8 +7,10 @@
 // broadcast shape, any scale sign.  Same recurrence as the reference's
 // streaming backend (src/tensorsmith/nn/attention.py:175-198) and its VJP
 // (:220-244): running max / sum / accumulator per row over 64-key chunks, and
-// P recomputed from the saved LSE in the backward.
-#include "tsattn_internal.h"
+// P recomputed from the saved LSE in the backward.  Dropout as the dense
+// backend (:140-144, :210-217): P V takes P * mask, dS = P (dP * mask -
+// delta), the mask regenerated per element from the problem's Philox stream.
+#include "philox.h"
 
 namespace tsattn {
 namespace {
@@ -66,6 +68,15 @@ __device__ __forceinline__ A score(const Problem &p, const A *qrow, const T *kro
   return s;
 }
 
+// Dropout mask value of element (row, j): 0, or the keep scale in the
+// compute type (the reference's keep.astype(compute dtype) / (1 - p)).
+template <typename A>
+__device__ __forceinline__ A drop_factor(const Problem &p, int64_t row, int j) {
+  if (!p.drop.on) return A(1);
+  const A scale = sizeof(A) == 8 ? static_cast<A>(p.drop.scale64) : static_cast<A>(p.drop.scale);
+  return dropout_keeps_one(p, row, j) ? scale : A(0);
+}
+
 template <typename T>
 __device__ __forceinline__ const T *row_ptr(View v, int b, int h, int s) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1 + static_cast<int64_t>(s) * v.s2;
@@ -116,11 +127,11 @@ __global__ __launch_bounds__(256) void generic_forward_kernel(Problem p, View q,
     const A base = isfinite(m_new) ? m_new : A(0);
     const A corr = exp_acc(m - base);
     const A pj = exp_acc(s - base);
-    l = l * corr + wave_sum(pj);
+    l = l * corr + wave_sum(pj);  // the denominator sums the undropped P
     m = m_new;
 #pragma unroll
     for (int t = 0; t < kMaxDimSlots; ++t) acc[t] *= corr;
-    pbuf[lane] = pj;
+    pbuf[lane] = p.drop.on ? pj * drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i, j) : pj;
     __syncthreads();
     const int n = (stop - j0) < kChunk ? static_cast<int>(stop - j0) : kChunk;
     for (int jj = 0; jj < n; ++jj) {
@@ -212,6 +223,7 @@ __global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View
         const T *vrow = row_ptr<T>(v, b, hk, j);
         A dp = 0;
         for (int d = 0; d < p.Dv; ++d) dp += grow[d] * to_acc<A>(vrow[d]);
+        if (p.drop.on) dp *= drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i, j);
         ds = pij * (dp - row_delta) * scale;
       }
     }
@@ -308,7 +320,9 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
             const T *gp = row_ptr<T>(dout, b, hq, i);
             A dp = 0;
             for (int d = 0; d < p.Dv; ++d) dp += to_acc<A>(gp[d]) * vrow[d];
-            ds = pij * (dp - delta[rr]) * scale;
+            const A f = drop_factor<A>(p, rr, j);  // rr = the query row's index
+            ds = pij * (dp * f - delta[rr]) * scale;
+            pij *= f;  // dV takes P * mask
           }
         }
       }

@@ -13,6 +13,11 @@
 // Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
 // transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
 //
+// Dropout (template DR): the mask is regenerated from the problem's Philox
+// stream (philox.h) in both kernels: dV = (P * mask)^T dO and
+// dS = P (dP * mask - delta) (attention.py:210-217; delta = rowsum(dO O)
+// already holds the mask through O).
+//
 // RoPE (Problem::rope, R > 0): the dQ prologue rotates the query fragments
 // as the forward did; the dQ and dK epilogues apply the inverse rotation to
 // the rounded gradients, so they are those of the unrotated queries and keys
@@ -24,6 +29,7 @@
 #include <type_traits>
 
 #include "mfma_common.h"
+#include "philox.h"
 #include "rope_math.h"
 
 namespace tsattn {
@@ -83,11 +89,11 @@ constexpr int KV_PD = 2;  // tiles in flight
 // Workgroups per CU: two, except the general-mask kernel at D = 128, whose
 // mask registers do not fit beside the two-workgroup register budget; alone
 // on its CU it has the accumulation registers as well.
-template <int D, int MK>
-constexpr int dkdv_wg_per_cu() { return MK != 0 && D > 64 ? 1 : 2; }
+template <int D, int MK, bool DR>
+constexpr int dkdv_wg_per_cu() { return (MK != 0 || DR) && D > 64 ? 1 : 2; }
 
-template <typename T, int D, int MK>
-__global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(BwdArgs a) {
+template <typename T, int D, int MK, bool DR>
+__global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel(BwdArgs a) {
   constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
   constexpr int NBLK = TILE_B / 1024;
   constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | nl (QT floats) | nd (QT floats)
@@ -97,7 +103,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
   static_assert(SKS == 2 * PDT, "one dV and one dK MFMA per step");
   static_assert(SKS == 2 * LPT, "one tile DMA part per two MFMA steps");
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
-  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B];
+  // Q / dO ring; with dropout each wave's 32 x 32 tile of dropout words after it
+  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B + (DR ? NW * 2048 : 0)];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -106,7 +113,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, kb;  // early key blocks see the most queries: run them first
-  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<D, MK>(), bh, kb);  // slots per XCD
+  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<D, MK, DR>(), bh, kb);  // slots per XCD
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
@@ -263,7 +270,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const float4 l4 = *reinterpret_cast<const float4 *>(rv + 8 * g + 4 * h);
-      const float4 d4 = *reinterpret_cast<const float4 *>(rv + QT + 8 * g + 4 * h);
+      const float4 d4 = DR ? float4{0.f, 0.f, 0.f, 0.f}  // dropout: dP alone, nd added later
+                           : *reinterpret_cast<const float4 *>(rv + QT + 8 * g + 4 * h);
       sacc[4 * g] = l4.x, sacc[4 * g + 1] = l4.y, sacc[4 * g + 2] = l4.z, sacc[4 * g + 3] = l4.w;
       dpacc[4 * g] = d4.x, dpacc[4 * g + 1] = d4.y, dpacc[4 * g + 2] = d4.z, dpacc[4 * g + 3] = d4.w;
     }
@@ -296,6 +304,20 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
       if (causal) lo = min(64, max(-64, kdiff - q0 - 4 * h));
     }
     u32x4 pp[2], pd[2];
+    // Dropout: lane (c, h) draws the 16 words of row q0 + c, keys kw + 16 h ..,
+    // into the wave's 32 x 32 word tile in LDS; lane (c, h) then reads its key
+    // c at rows 8 g + 4 h + r.  dV takes P * mask, dS = P (dP * mask - delta).
+    const uint16_t *dtile = reinterpret_cast<const uint16_t *>(ring + KV_NS * STAGE_B + w * 2048);
+    if constexpr (DR) {
+      uint64_t blk[4];
+      dropout_block(p.drop,
+                    dropout_block_index(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + q0 + c,
+                                        kw + 16 * h),
+                    blk);
+      uint64_t *dst = reinterpret_cast<uint64_t *>(ring + KV_NS * STAGE_B + w * 2048 + c * 64 + h * 32);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) dst[m] = blk[m];
+    }
     // Interior tiles skip the per-element bounds (three VALU ops each).
     auto grad = [&](auto masked) {
       float xs[16];
@@ -322,7 +344,14 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK>())) void dkdv_kernel(Bwd
             // -inf where disallowed; additive-masked scores arrive scaled
             pv[r] = fast_exp2(MK >= 2 ? xs[e] : xs[e] * sl);
           }
-          dsv[r] = pv[r] * dpacc[e];
+          if constexpr (DR) {
+            const bool keep = dtile[(8 * g + 4 * h + r) * 32 + c] >= p.drop.thr;
+            const float nd = rv[QT + 8 * g + 4 * h + r];
+            dsv[r] = pv[r] * (keep ? fmaf(dpacc[e], p.drop.scale, nd) : nd);
+            pv[r] = keep ? pv[r] * p.drop.scale : 0.f;
+          } else {
+            dsv[r] = pv[r] * dpacc[e];
+          }
         }
         pp[g >> 1][(g & 1) * 2] = pack2<T>(pv[0], pv[1]);
         pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
@@ -424,7 +453,7 @@ constexpr int KT = 32;   // keys per tile
 constexpr int DQ_PD = 2;              // tiles issued ahead
 constexpr int DQ_NS = DQ_PD + 2;      // ring stages: tile j is read in iterations j and j + 1
 
-template <typename T, int D, int MK>
+template <typename T, int D, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   constexpr int TILE_B = KT * D * 2;   // bytes per K (or V) tile
   constexpr int NBLK = TILE_B / 1024;  // 1 KiB blocks per tile
@@ -647,11 +676,20 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim_l, sl);
       }
     }
+    // Dropout: dS = P (dP * mask - delta) (attention.py:215-217).
+    uint64_t dw[4];
+    if constexpr (DR)
+      dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = fast_exp2(fmaf(x[i], slx, lse2));
       const float p1 = fast_exp2(fmaf(x[i + 1], slx, lse2));
-      pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (dp[i] + delta), p1 * (dp[i + 1] + delta));
+      float d0 = dp[i], d1 = dp[i + 1];
+      if constexpr (DR) {
+        d0 = dropout_keeps(p.drop, dw, i) ? d0 * p.drop.scale : 0.f;
+        d1 = dropout_keeps(p.drop, dw, i + 1) ? d1 * p.drop.scale : 0.f;
+      }
+      pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (d0 + delta), p1 * (d1 + delta));
     }
   };
 
@@ -722,29 +760,35 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
-template <typename T, int D, int MK>
+template <typename T, int D, int MK, bool DR>
 void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   {
-    Probe pr_(MK ? "bwd_dq_mfma_masked" : "bwd_dq_mfma", st);
-    dq_kernel<T, D, MK><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+    Probe pr_(DR ? "bwd_dq_mfma_dropout" : (MK ? "bwd_dq_mfma_masked" : "bwd_dq_mfma"), st);
+    dq_kernel<T, D, MK, DR><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
   }
   const int n_kb = (p.Sk + KB - 1) / KB;
   {
-    Probe pr_(MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma", st);
-    dkdv_kernel<T, D, MK><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+    Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
+    dkdv_kernel<T, D, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
   }
+}
+
+template <typename T, int D, bool DR>
+void launch_dr(const BwdArgs &a, int mk, hipStream_t st) {
+  if (mk == 1) launch_mk<T, D, 1, DR>(a, st);
+  else if (mk == 2) launch_mk<T, D, 2, DR>(a, st);
+  else if (mk == 3) launch_mk<T, D, 3, DR>(a, st);
+  else launch_mk<T, D, 0, DR>(a, st);
 }
 
 template <typename T, int D>
 hipError_t launch(const BwdArgs &a, hipStream_t st) {
   const int mk = mfma_mask_mode(a.p);
-  if (mk == 1) launch_mk<T, D, 1>(a, st);
-  else if (mk == 2) launch_mk<T, D, 2>(a, st);
-  else if (mk == 3) launch_mk<T, D, 3>(a, st);
-  else launch_mk<T, D, 0>(a, st);
+  if (a.p.drop.on) launch_dr<T, D, true>(a, mk, st);
+  else launch_dr<T, D, false>(a, mk, st);
   return hipGetLastError();
 }
 

@@ -386,6 +386,17 @@ __device__ __forceinline__ float half_swap_max(float x) {
   return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
+// The value x of the partner lane l ^ 32 (v_permlane32_swap, as above).
+__device__ __forceinline__ unsigned partner32(unsigned x, int h) {
+  unsigned a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return h ? a : b;
+}
+__device__ __forceinline__ uint64_t partner64(uint64_t x, int h) {
+  return static_cast<uint64_t>(partner32(static_cast<unsigned>(x), h)) |
+         (static_cast<uint64_t>(partner32(static_cast<unsigned>(x >> 32), h)) << 32);
+}
+
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));

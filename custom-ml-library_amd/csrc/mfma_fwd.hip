@@ -28,6 +28,10 @@
 // when a row's max exceeds it by more than kTau (in log2 units), so P <= 2^kTau
 // and most tiles skip the rescale.  O / l and the LSE are exact for any m.
 //
+// Dropout (template DR): the probabilities fed to PV are multiplied by the
+// keep mask the problem's Philox stream gives (philox.h) -- regenerated, not
+// stored -- while the softmax denominator sums the undropped ones.
+//
 // RoPE (Problem::rope, R > 0): the prologue rotates the query fragments it
 // loads (the keys come rotated), bit-identical to a separate tsattn_rope.
 //
@@ -37,6 +41,7 @@
 // entering as scores * scale + mask (attention.py:105-107) in log2 units
 // (MK = 2 for an f32 mask, 3 for f16 / bf16).
 #include "mfma_common.h"
+#include "philox.h"
 #include "rope_math.h"
 
 namespace tsattn {
@@ -64,7 +69,7 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
 }
 
-template <typename T, int D, int MK>
+template <typename T, int D, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   constexpr int TILE_B = BN * D * 2;        // bytes per K (or V) tile
   constexpr int NBLK = TILE_B / 1024;       // 1 KiB blocks per tile
@@ -281,11 +286,20 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       for (int dt = 0; dt < PDT; ++dt) oacc[dt] *= corr;
     }
     const float base = m == -INFINITY ? 0.f : m;
+    // Dropout: the denominator sums the undropped probabilities (the
+    // reference normalises first, attention.py:139-144); PV takes P * mask.
+    uint64_t dw[4];
+    if constexpr (DR)
+      dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      const float p0 = fast_exp2(fmaf(x[i], slx, -base));
-      const float p1 = fast_exp2(fmaf(x[i + 1], slx, -base));
+      float p0 = fast_exp2(fmaf(x[i], slx, -base));
+      float p1 = fast_exp2(fmaf(x[i + 1], slx, -base));
       l += p0 + p1;  // fp32 sum of the unrounded probabilities, as the reference
+      if constexpr (DR) {
+        p0 = dropout_keeps(p.drop, dw, i) ? p0 * p.drop.scale : 0.f;
+        p1 = dropout_keeps(p.drop, dw, i + 1) ? p1 * p.drop.scale : 0.f;
+      }
       pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
     }
   };
@@ -351,14 +365,21 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
         lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
 }
 
+template <typename T, int D, bool DR>
+void launch_dr(const FwdArgs &a, int mk, hipStream_t st) {
+  if (mk == 1) fwd_kernel<T, D, 1, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 2) fwd_kernel<T, D, 2, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 3) fwd_kernel<T, D, 3, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else fwd_kernel<T, D, 0, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+}
+
 template <typename T, int D>
 hipError_t launch(const FwdArgs &a, hipStream_t st) {
   const int mk = mfma_mask_mode(a.p);
-  Probe pr_(mk ? "fwd_mfma_masked" : "fwd_mfma", st);
-  if (mk == 1) fwd_kernel<T, D, 1><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 2) fwd_kernel<T, D, 2><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 3) fwd_kernel<T, D, 3><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else fwd_kernel<T, D, 0><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  const bool dr = a.p.drop.on != 0;
+  Probe pr_(dr ? "fwd_mfma_dropout" : (mk ? "fwd_mfma_masked" : "fwd_mfma"), st);
+  if (dr) launch_dr<T, D, true>(a, mk, st);
+  else launch_dr<T, D, false>(a, mk, st);
   return hipGetLastError();
 }
 

@@ -75,6 +75,18 @@ struct RopeDesc {
   int64_t qpos0, kpos0;
 };
 
+// Attention dropout (on = 0: none): keep a 16-bit word w iff w >= thr, kept
+// probabilities times `scale` (f32 compute) / `scale64` (f64 compute), the
+// reference's keep.astype(compute dtype) / (1 - p); Philox key (k0, k1) and
+// first block counter (c0, c1) = the stream counter + 1 (128 bits).
+struct DropDesc {
+  int on;
+  uint32_t thr;
+  float scale;
+  double scale64;
+  uint64_t k0, k1, c0, c1;
+};
+
 struct Problem {
   int B, Hq, Hkv, Sq, Sk, Dqk, Dv, rep;
   double scale;
@@ -84,6 +96,7 @@ struct Problem {
   const int32_t *kv_prefix;
   MaskDesc mask;
   RopeDesc rope;
+  DropDesc drop;
 };
 
 // Mask handling of the MFMA kernels (a template parameter): 0 = none, or a
@@ -173,6 +186,9 @@ hipError_t launch_rope(int dtype, int B, int H, int T, int D, int R, View x, Vie
 hipError_t launch_rope_append(int dtype, int B, int H, int T, int D, int R, View k, View v, View kc,
                               View vc, const View *ks, const View *vs, const void *cos,
                               const void *sin, int64_t pos, hipStream_t st);
+
+// The dropout keep mask of problem p as a contiguous [B, Hq, Sq, Sk] uint8 array.
+hipError_t launch_dropout_keep(const Problem &p, uint8_t *out, hipStream_t st);
 
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st);

@@ -133,10 +133,12 @@ def scaled_dot_product_attention(
         raise RuntimeError(
             "tensorsmith_hip runs attention on hip devices only; move the tensors to 'hip'"
         )
+    # the reference drops only in its dense backend, which "auto" selects when
+    # dropping (attention.py:77-84); "hip" drops on the kernels as well
+    if dropout_p and backend in ("streaming", "native"):
+        raise ValueError("attention dropout currently requires the dense backend")
     if backend == "native":
         raise ValueError("native attention requires Metal and equal query/value head dimensions")
-    if dropout_p:
-        raise ValueError("attention dropout currently requires the dense backend")
 
     code = _dtype_code(query.dtype)
     q, k, v = (_operand(t._data) for t in (query, key, value))
@@ -144,6 +146,14 @@ def scaled_dot_product_attention(
 
     tdev = q.device
     prob = _problem(b, hq, hkv, qlen, klen, dim, dim_v, code, multiplier, is_causal, causal_offset)
+    if dropout_p:
+        # a fresh 128-bit Philox key per call from the host stream (ts.seed);
+        # the backward regenerates the same keep mask from it
+        key_bytes = np.random.bytes(16)
+        prob.dropout_p = float(dropout_p)
+        prob.dropout_key[0] = int.from_bytes(key_bytes[:8], "little")
+        prob.dropout_key[1] = int.from_bytes(key_bytes[8:], "little")
+        prob.dropout_counter = 0
     keep = []  # device buffers the launch reads, alive until the call returns
 
     if attn_mask is not None:
@@ -196,6 +206,7 @@ def scaled_dot_product_attention(
 
     use_decode = (
         not recording
+        and not dropout_p
         and code in (_lib.F16, _lib.BF16)
         and dim == dim_v
         and dim in (64, 128, 256)

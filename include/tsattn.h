@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 4
+#define TSATTN_ABI_VERSION 5
 
 typedef enum {
   TSATTN_OK = 0,
@@ -79,6 +79,19 @@ typedef struct tsattn_problem {
   int32_t mask_kind;  /* tsattn_mask_kind */
   int32_t mask_dtype; /* TSATTN_BOOL, or the additive mask's float type */
   tsattn_view mask;   /* broadcast to [B, Hq, Sq, Sk] */
+  /*
+   * Attention dropout (src/tensorsmith/nn/attention.py:140-144): probability
+   * p in [0, 1) (0 = none) and the counter-based stream it draws from.
+   * Element (b, h, i, j) takes 16-bit word L = ((b Hq + h) Sq + i) Sk16 + j
+   * (Sk16 = len_kv rounded up to 16) of the raw Philox4x64-10 stream of
+   * numpy.random.Philox(key = key[0] + 2^64 key[1], counter = counter)
+   * viewed as little-endian uint16, and is kept iff word >= round(65536 p);
+   * kept probabilities scale by float32(1) / float32(1 - p).  The backward
+   * regenerates the same mask from the same key and counter.
+   */
+  double dropout_p;
+  uint64_t dropout_key[2];
+  uint64_t dropout_counter;
 } tsattn_problem;
 
 /* ABI version of the loaded library (== TSATTN_ABI_VERSION). */
@@ -185,6 +198,15 @@ int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *r
                               const tsattn_view *out, const tsattn_view *dout, const void *lse,
                               const tsattn_view *dq, const tsattn_view *dk, const tsattn_view *dv,
                               void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * The keep mask the attention kernels draw for problem `p` (its dropout
+ * fields and sizes): out[b, h, i, j] = 1 if kept, else 0, as a contiguous
+ * [B, Hq, Sq, Sk] uint8 array.  The reference's dense backend holds this mask
+ * explicitly (attention.py:141-143); this materialises the one the hip
+ * kernels regenerate, for inspection and tests.
+ */
+int tsattn_dropout_keep(const tsattn_problem *p, uint8_t *out, void *stream);
 
 /* Bytes of scratch tsattn_decode_forward needs for `split_len` keys per split. */
 size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);

@@ -11,9 +11,8 @@ Follows ``src/tensorsmith/nn/attention.py`` of the reference line for line in
 * GQA expansion and group reduction      ``attention.py:93-100,245-247``
 
 Half inputs are carried as float32 arrays holding exactly-representable
-values (see ``oracle.halfprec``).  Dropout is not restated: the HIP backend
-rejects ``dropout_p > 0`` exactly like the reference's ``streaming`` backend
-(``attention.py:83-84``).
+values (see ``oracle.halfprec``).  Dropout (dense backend, ``:140-144``) is
+restated in ``oracle.dropout`` with the hip kernels' counter-based mask.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this module.

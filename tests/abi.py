@@ -44,7 +44,7 @@ def stream():
 
 
 def problem(q, k, v, *, causal=False, offset=0, scale=None, mask=None, kv_len=None,
-            kv_prefix=None):
+            kv_prefix=None, dropout=None):
     b, hq, sq, d = q.shape
     p = _lib.Problem()
     p.dtype = CODES[q.dtype]
@@ -56,6 +56,11 @@ def problem(q, k, v, *, causal=False, offset=0, scale=None, mask=None, kv_len=No
     p.kv_len = None if kv_len is None else kv_len.data_ptr()
     p.kv_prefix = None if kv_prefix is None else kv_prefix.data_ptr()
     p.mask_kind = _lib.MASK_NONE
+    if dropout is not None:  # (p, 128-bit key, counter)
+        p.dropout_p = dropout[0]
+        p.dropout_key[0] = dropout[1] & (2**64 - 1)
+        p.dropout_key[1] = dropout[1] >> 64
+        p.dropout_counter = dropout[2]
     if mask is not None:
         m = torch.broadcast_to(mask, (b, hq, sq, k.shape[2]))
         if m.dtype == torch.bool:
@@ -199,3 +204,12 @@ def backward_rope(q, k, v, out, g, lse, desc, **kw):
         ctypes.c_void_p(lse.data_ptr()), view(dq), view(dk), view(dv),
         ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "backward rope")
     return dq, dk, dv
+
+
+def dropout_keep(q, k, v, **kw):
+    """tsattn_dropout_keep: the [B, Hq, Sq, Sk] uint8 keep mask of the problem."""
+    p = problem(q, k, v, **kw)
+    out = torch.empty((p.batch, p.heads_q, p.len_q, p.len_kv), dtype=torch.uint8, device=q.device)
+    _lib.check(_lib.load().tsattn_dropout_keep(ctypes.byref(p), ctypes.c_void_p(out.data_ptr()),
+                                               stream()), "dropout keep")
+    return out

@@ -146,8 +146,13 @@ def test_gqa_and_strided_views_and_dropout_rule():
     dense = ts.nn.scaled_dot_product_attention(*(ts.Tensor(view._data.contiguous(), device=HIP)
                                                  for _ in range(3)), is_causal=True)
     np.testing.assert_array_equal(got.numpy(), dense.numpy())
+    # dropout: the reference's rule (attention.py:77-84) -- dense drops,
+    # streaming raises; these fp32 inputs drop on the generic kernels
     with pytest.raises(ValueError, match="dense"):
-        ts.nn.scaled_dot_product_attention(*tensors, dropout_p=0.1, enable_gqa=True)
+        ts.nn.scaled_dot_product_attention(*tensors, dropout_p=0.1, backend="streaming",
+                                           enable_gqa=True)
+    dropped = ts.nn.scaled_dot_product_attention(*tensors, dropout_p=0.1, enable_gqa=True)
+    assert np.isfinite(dropped.numpy()).all()
     with pytest.raises(ValueError, match="Metal"):
         ts.nn.scaled_dot_product_attention(*tensors, backend="native", enable_gqa=True)
 

@@ -1,0 +1,173 @@
+"""Attention dropout on the MFMA kernels (needs an MI355X).
+
+The reference drops probabilities in its dense backend
+(src/tensorsmith/nn/attention.py:140-144, VJP :210-217) with uniforms from its
+global stream; the hip kernels regenerate a counter-based Philox4x64-10 mask
+(oracle/dropout.py states the element mapping and is pinned against
+numpy.random.Philox).  Checked here:
+
+* the keep mask the kernels draw (tsattn_dropout_keep) equals the oracle's
+  bit for bit -- ragged key lengths (rows padded to 16 words), GQA heads,
+  counters that carry past 2^64;
+* forward and backward with dropout against the oracle's dense dropout
+  attention under that same mask, at the bf16 / fp16 bounds of the parity
+  tests (relative L2 1e-2 / 2e-3 for O, 2e-2 / 5e-3 for gradients; max-abs
+  2e-2 / 5e-3 of max|ref|), with causal windows, offsets, GQA and a general
+  mask;
+* the generic kernels (fp32 / fp64 / other head dims) drop with the same
+  mask, at the reference's fp32 cross-backend bound (rtol 1e-4, atol 3e-5,
+  tests/test_transformer.py:92) and 1e-10 for fp64;
+* the same key and counter reproduce every output bit; another key changes
+  them; the mirror drops on backend "hip" / "dense" / "auto" and raises the
+  reference's ValueError on "streaming" (tests/test_transformer.py:164-171).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+if not torch.cuda.is_available():  # pragma: no cover
+    pytest.skip("no GPU", allow_module_level=True)
+
+import abi  # noqa: E402
+import tensorsmith_hip as ts  # noqa: E402
+from conftest import rel_l2  # noqa: E402
+from oracle import dropout as DR  # noqa: E402
+from oracle.inputs import attention_inputs  # noqa: E402
+from tensorsmith_hip import _lib, nn  # noqa: E402
+
+TOL = {"bfloat16": dict(o=1e-2, g=2e-2, mx=2e-2), "float16": dict(o=2e-3, g=5e-3, mx=5e-3)}
+
+
+def say(msg):
+    print(msg, flush=True)
+
+
+def check(got, ref, dtype, kind, name):
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = rel_l2(got, ref)
+    mx = np.abs(got - ref).max() / (np.abs(ref).max() or 1.0)
+    say(f"  {name}: rel_l2={err:.2e} max_abs/max|ref|={mx:.2e}")
+    assert np.isfinite(got).all(), name
+    assert err <= TOL[dtype][kind], f"{name}: rel_l2 {err:.3e}"
+    assert mx <= TOL[dtype]["mx"], f"{name}: max-abs {mx:.3e}"
+
+
+@pytest.mark.parametrize("shape,key,counter,p", [
+    ((2, 3, 37, 50), 12345, 0, 0.3),
+    ((1, 4, 128, 256), 2**127 + 99, 2**64 - 2, 0.1),
+    ((2, 2, 5, 16), 7, 3, 0.9),
+])
+def test_keep_mask_is_the_oracles(shape, key, counter, p):
+    b, h, sq, sk = shape
+    q = torch.zeros((b, h, sq, 64), dtype=torch.bfloat16, device="cuda")
+    kv = torch.zeros((b, 1, sk, 64), dtype=torch.bfloat16, device="cuda")
+    got = abi.dropout_keep(q, kv, kv, dropout=(p, key, counter)).cpu().numpy().astype(bool)
+    want = DR.keep_mask(key, counter, shape, p)
+    np.testing.assert_array_equal(got, want)
+
+
+CASES = [
+    # (dtype, B, Hq, Hkv, Sq, Sk, D, causal, offset, p, masked)
+    ("bfloat16", 2, 2, 2, 130, 130, 128, True, 0, 0.2, False),
+    ("float16", 1, 4, 2, 96, 200, 64, True, 104, 0.5, False),
+    ("bfloat16", 2, 2, 1, 77, 150, 128, False, 0, 0.1, True),
+    ("float16", 1, 2, 2, 256, 256, 128, False, 0, 0.3, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(map(str, c)))
+def test_dropout_attention_matches_oracle(case):
+    dtype, b, hq, hkv, sq, sk, d, causal, off, p, masked = case
+    say(f"dropout attention {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=31)
+    key, counter = 0x5EED_0000_0000_0000_1234_5678_9ABC_DEF0, 11
+    mask = np.random.default_rng(1).random((sq, sk)) > 0.25 if masked else None
+    out_c, ref_out, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, mask, causal, dtype=dtype, p=p,
+                                           rng_key=key, rng_counter=counter,
+                                           causal_offset=off, enable_gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    kw = dict(causal=causal, offset=off, dropout=(p, key, counter),
+              mask=None if mask is None else torch.from_numpy(mask).cuda())
+    out, lse, path = abi.forward(q, k, v, **kw)
+    assert path == _lib.PATH_MFMA
+    dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, **kw)
+    torch.cuda.synchronize()
+    check(abi.host(out), out_c, dtype, "o", "O")
+    for got, want, name in zip((dq, dk, dv), back(inp.do), ("dQ", "dK", "dV")):
+        check(abi.host(got), want, dtype, "g", name)
+    # the same stream again: every bit; another key: different outputs
+    out2, lse2, _ = abi.forward(q, k, v, **kw)
+    assert torch.equal(out, out2) and torch.equal(lse, lse2)
+    kw3 = dict(kw, dropout=(p, key + 1, counter))
+    out3, _, _ = abi.forward(q, k, v, **kw3)
+    assert not torch.equal(out, out3)
+
+
+GENERIC_CASES = [
+    # (dtype, B, Hq, Hkv, Sq, Sk, Dqk, Dv, causal, p): generic kernels
+    ("float32", 2, 2, 1, 33, 70, 32, 48, True, 0.25),
+    ("float64", 1, 2, 2, 20, 40, 16, 16, False, 0.5),
+    ("bfloat16", 1, 2, 2, 40, 40, 96, 96, True, 0.2),  # head dim 96: not an MFMA shape
+]
+
+
+@pytest.mark.parametrize("case", GENERIC_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_dropout_on_the_generic_kernels(case):
+    dtype, b, hq, hkv, sq, sk, d, dv_, causal, p = case
+    say(f"generic dropout {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, dim_v=dv_, seed=41)
+    key, counter = 2**100 + 17, 2**64 - 1
+    out_c, _, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, None, causal, dtype=dtype, p=p,
+                                     rng_key=key, rng_counter=counter, enable_gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    kw = dict(causal=causal, dropout=(p, key, counter))
+    out, lse, path = abi.forward(q, k, v, **kw)
+    assert path == _lib.PATH_GENERIC
+    grads = abi.backward(q, k, v, out, g, lse, **kw)[:3]
+    torch.cuda.synchronize()
+    if dtype in TOL:
+        check(abi.host(out), out_c, dtype, "o", "O")
+        for got, want, name in zip(grads, back(inp.do), ("dQ", "dK", "dV")):
+            check(abi.host(got), want, dtype, "g", name)
+    else:  # the reference's fp32 cross-backend bound / fp64
+        tol = dict(rtol=1e-4, atol=3e-5) if dtype == "float32" else dict(rtol=1e-10, atol=1e-12)
+        np.testing.assert_allclose(abi.host(out), out_c, **tol)
+        for got, want in zip(grads, back(inp.do)):
+            np.testing.assert_allclose(abi.host(got), want, **tol)
+
+
+def test_dropout_probability_is_validated():
+    q = torch.zeros((1, 1, 8, 32), dtype=torch.float32, device="cuda")
+    with pytest.raises(ValueError, match="dropout"):
+        abi.forward(q, q, q, dropout=(1.0, 1, 0))
+    with pytest.raises(ValueError, match="dropout"):
+        abi.forward(q, q, q, dropout=(-0.1, 1, 0))
+
+
+def test_mirror_dropout_backends_and_gradients():
+    ts.seed(8)
+    q, k, v = (ts.tensor(np.random.default_rng(i).standard_normal((2, 2, 64, 64)).astype(np.float32),
+                         device="hip", dtype="bfloat16", requires_grad=True) for i in range(3))
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    for backend in ("hip", "dense", "auto"):
+        out = nn.scaled_dot_product_attention(q, k, v, dropout_p=0.3, backend=backend)
+        out.sum().backward()
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert probes["fwd_mfma_dropout"][0] == 3 and probes["bwd_dkdv_mfma_dropout"][0] == 3
+    assert all(np.isfinite(t.grad.numpy()).all() for t in (q, k, v))
+    with pytest.raises(ValueError, match="dense backend"):
+        nn.scaled_dot_product_attention(q, k, v, dropout_p=0.1, backend="streaming")
+    # seeded: the same host seed gives the same draw
+    ts.seed(5)
+    a = nn.scaled_dot_product_attention(q, k, v, dropout_p=0.4, backend="hip").numpy()
+    ts.seed(5)
+    b_ = nn.scaled_dot_product_attention(q, k, v, dropout_p=0.4, backend="hip").numpy()
+    np.testing.assert_array_equal(a, b_)

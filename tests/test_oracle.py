@@ -255,3 +255,81 @@ def test_rope_rows_depend_only_on_absolute_position():
     whole = R.rope(x, offset=3)
     for t in range(8):
         np.testing.assert_array_equal(R.rope(x[..., t:t + 1, :], offset=3 + t), whole[..., t:t + 1, :])
+
+
+# ---------------------------------------------------------------------------
+# Dropout: Philox stream pinned against NumPy's own Philox bit generator; the
+# element mapping against an explicit loop; the attention math against the
+# dropout-free oracle (p = 0), finite differences (fixed mask) and the
+# reference's mask value formula.
+# ---------------------------------------------------------------------------
+
+from oracle import dropout as DR  # noqa: E402
+
+
+@pytest.mark.parametrize("key,counter", [(0, 0), (0x0123456789ABCDEF_FEDCBA9876543210, 5),
+                                         (2**128 - 1, 2**64 - 3), (987654321, 2**70 + 9)])
+def test_philox_stream_is_numpys_philox(key, counter):
+    want = np.random.Philox(key=key, counter=counter).random_raw(41)
+    np.testing.assert_array_equal(DR.raw_stream(key, counter, 41), want)
+
+
+def test_keep_mask_element_mapping():
+    key, counter, shape, p = 77, 3, (2, 3, 4, 5), 0.4
+    raw = np.random.Philox(key=key, counter=counter).random_raw(2 * 3 * 4 * 16 // 4)
+    got = DR.keep_mask(key, counter, shape, p)
+    thr = DR.threshold(p)
+    for b in range(2):
+        for h in range(3):
+            for i in range(4):
+                for j in range(5):
+                    word_index = ((b * 3 + h) * 4 + i) * 16 + j
+                    w = (int(raw[word_index // 4]) >> (16 * (word_index % 4))) & 0xFFFF
+                    assert got[b, h, i, j] == (w >= thr)
+
+
+def test_keep_fraction_and_scale():
+    p = 0.3
+    keep = DR.keep_mask(5, 0, (4, 8, 64, 200), p)
+    n = keep.size
+    assert abs(keep.mean() - (1 - p)) < 5 * math.sqrt(p * (1 - p) / n)
+    assert DR.threshold(0.0) == 0 and DR.keep_mask(1, 0, (1, 1, 3, 7), 0.0).all()
+    # the reference's mask value: keep.astype(float32) / (1 - p) with a Python float
+    ref = np.ones(3, np.float32) / (1 - p)
+    assert ref.dtype == np.float32 and (ref == DR.keep_scale(p)).all()
+
+
+def test_dropout_attention_without_dropout_is_the_dense_oracle():
+    inp = attention_inputs(2, 2, 9, 8, "float32", seed=3)
+    out, _, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, None, True, dtype="float32", p=0.0,
+                                   rng_key=9)
+    ref = A.sdpa(inp.q, inp.k, inp.v, None, True, dtype="float32", backend="dense")
+    np.testing.assert_array_equal(out, ref.out)
+    for got, want in zip(back(inp.do), ref.backward(inp.do)):
+        np.testing.assert_allclose(got, want, rtol=1e-6, atol=1e-7)
+
+
+def test_dropout_attention_vjp_matches_finite_differences():
+    rng = np.random.default_rng(4)
+    q, k, v = (rng.standard_normal((1, 2, 5, 4)) for _ in range(3))
+    g = rng.standard_normal((1, 2, 5, 4))
+    kw = dict(dtype="float64", p=0.35, rng_key=123, rng_counter=7)
+    mask = np.tril(np.ones((5, 5), bool))
+    _, _, back = DR.sdpa_dropout(q, k, v, mask, **kw)
+    grads = back(g)
+    f = lambda q_, k_, v_: float(np.sum(DR.sdpa_dropout(q_, k_, v_, mask, **kw)[0] * g))
+    eps = 1e-6
+    for which, grad in enumerate(grads):
+        args = [q, k, v]
+        x = args[which]
+        num = np.zeros_like(x)
+        for idx in np.ndindex(x.shape):
+            xp, xm = x.copy(), x.copy()
+            xp[idx] += eps
+            xm[idx] -= eps
+            num[idx] = (f(*[xp if i == which else a for i, a in enumerate(args)])
+                        - f(*[xm if i == which else a for i, a in enumerate(args)])) / (2 * eps)
+        np.testing.assert_allclose(grad, num, rtol=1e-6, atol=1e-8)
+    # the mask really drops something and keeps something
+    keep = DR.keep_mask(123, 7, (1, 2, 5, 5), 0.35)
+    assert 0 < keep.sum() < keep.size
