@@ -89,19 +89,24 @@ constexpr int KV_PD = 2;  // tiles in flight
 // Workgroups per CU: two, except the general-mask kernel at D = 128, whose
 // mask registers do not fit beside the two-workgroup register budget; alone
 // on its CU it has the accumulation registers as well.
-template <int D, int MK, bool DR>
-constexpr int dkdv_wg_per_cu() { return (MK != 0 || DR) && D > 64 ? 1 : 2; }
+template <int DK, int DV, int MK, bool DR>
+constexpr int dkdv_wg_per_cu() { return (MK != 0 || DR) && (DK > 64 || DV > 64) ? 1 : 2; }
 
-template <typename T, int D, int MK, bool DR>
-__global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel(BwdArgs a) {
-  constexpr int TILE_B = QT * D * 2;          // bytes of a Q (or dO) tile
-  constexpr int NBLK = TILE_B / 1024;
-  constexpr int STAGE_B = 2 * TILE_B + 256;   // Q | dO | nl (QT floats) | nd (QT floats)
-  constexpr int LPT = 2 * NBLK / NW;          // Q + dO DMA loads per wave per tile
-  constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
-  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
-  static_assert(SKS == 2 * PDT, "one dV and one dK MFMA per step");
-  static_assert(SKS == 2 * LPT, "one tile DMA part per two MFMA steps");
+// DK = head dim of q / k (and dK), DV = of v / dO (and dV); each 64 or 128.
+template <typename T, int DK, int DV, int MK, bool DR>
+__global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_kernel(BwdArgs a) {
+  constexpr int TILE_Q = QT * DK * 2, TILE_G = QT * DV * 2;  // bytes of a Q / dO tile
+  constexpr int STAGE_B = TILE_Q + TILE_G + 256;  // Q | dO | nl (QT floats) | nd (QT floats)
+  constexpr int QPARTS = TILE_Q / 1024 / NW, GPARTS = TILE_G / 1024 / NW;
+  constexpr int LPT = QPARTS + GPARTS;            // Q + dO DMA loads per wave per tile
+  constexpr int SKQ = DK / 16, SKV = DV / 16;     // k-steps of S (over DK) and dP (over DV)
+  constexpr int PDK = DK / 32, PDV = DV / 32;     // 32-row blocks of dK^T / dV^T
+  constexpr int STEPS = SKQ > SKV ? SKQ : SKV;    // MFMA steps of each block
+  constexpr int QGQ = DK / 32, QGG = DV / 32;     // 4-chunk groups per Q / dO row
+  constexpr int DMAX = DK > DV ? DK : DV;
+  static_assert(QPARTS >= 1 && GPARTS >= 1 && QPARTS * NW * 1024 == TILE_Q &&
+                GPARTS * NW * 1024 == TILE_G, "tile loads must split evenly over the waves");
+  static_assert(2 * LPT <= STEPS, "one tile DMA part per two MFMA steps");
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
   // Q / dO ring; with dropout each wave's 32 x 32 tile of dropout words after it
   __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B + (DR ? NW * 2048 : 0)];
@@ -113,7 +118,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, kb;  // early key blocks see the most queries: run them first
-  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<D, MK, DR>(), bh, kb);  // slots per XCD
+  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<DK, DV, MK, DR>(), bh, kb);  // slots per XCD
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
@@ -147,7 +152,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
   // Blocked layout: block n = (n / QG, n % QG); its lane l fetches row
   // 16 (n / QG) + l / 4, chunk 4 (n % QG) + ((l % 4) ^ ((l / 16) % 4)).  A
   // wave's blocks are w, w + 4, ..., all with n % QG = w % QG.
-  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
+  const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t lrow = lane >> 2;
   auto tile_of = [&](int itn, int &hq, int &q0) {
     const int r = itn / n_qt;
@@ -170,18 +175,17 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
     return t;
   };
   // Parts u < QPARTS are Q blocks, the rest dO blocks (a compile-time split).
-  constexpr int QPARTS = NBLK / NW;
-  static_assert(NBLK % NW == 0, "Q and dO blocks split evenly over the waves");
-  const uint32_t qvoff = lrow * qs_b + lane_chunk * 16, gvoff = lrow * gs_b + lane_chunk * 16;
+  const uint32_t qvoff = lrow * qs_b + (4 * (w % QGQ) + swz_chunk) * 16;
+  const uint32_t gvoff = lrow * gs_b + (4 * (w % QGG) + swz_chunk) * 16;
   // nl (wave 0) / nd (wave 1) rows of the group's first query head
   const float *rowv = a.delta + (static_cast<int64_t>(b) * p.Hq + hk * p.rep) * p.Sq + (w == 0 ? rows : 0);
   auto issue_part = [&](const TileDma &t, int u) {
     if (u < QPARTS) {
       const int n = w + NW * u;
-      dma16(t.qdesc, t.st + n * 1024, qvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QG)) * qs_b);
+      dma16(t.qdesc, t.st + n * 1024, qvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b);
     } else if (u < LPT) {
       const int n = w + NW * (u - QPARTS);
-      dma16(t.gdesc, t.st + TILE_B + n * 1024, gvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QG)) * gs_b);
+      dma16(t.gdesc, t.st + TILE_Q + n * 1024, gvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b);
     } else if (w < 2) {
       const u32x4 rdesc = make_desc(rowv + static_cast<int64_t>(t.hq - hk * p.rep) * p.Sq,
                                     static_cast<uint32_t>(p.Sq) * 4);
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
                    "v_lshlrev_b32 %0, 4, %0"
                    : "=v"(loff));
       if (lane < QT / 4)
-        dma16(rdesc, t.st + 2 * TILE_B + w * QT * 4, loff, static_cast<uint32_t>(t.q0) * 4);
+        dma16(rdesc, t.st + TILE_Q + TILE_G + w * QT * 4, loff, static_cast<uint32_t>(t.q0) * 4);
     }
   };
   auto issue = [&](int itn) {
@@ -212,17 +216,21 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
   // end read as zeros.
   const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
   const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
-  u32x4 kf[SKS], vf[SKS];
+  u32x4 kf[SKQ], vf[SKV];
 #pragma unroll
-  for (int i = 0; i < SKS; ++i) {
-    kf[i] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (16 * i + 8 * h) * 2);
-    vf[i] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (16 * i + 8 * h) * 2);
+  for (int i = 0; i < STEPS; ++i) {
+    if (i < SKQ) kf[i] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (16 * i + 8 * h) * 2);
+    if (i < SKV) vf[i] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (16 * i + 8 * h) * 2);
   }
 
-  const TileReader<T, D> rd(lane);
-  f32x16 dk_acc[PDT], dv_acc[PDT];
+  const TileReader<T, DK> rdq(lane);
+  const TileReader<T, DV> rdg(lane);
+  f32x16 dk_acc[PDK], dv_acc[PDV];
 #pragma unroll
-  for (int dt = 0; dt < PDT; ++dt) dk_acc[dt] = dv_acc[dt] = f32x16{};
+  for (int dt = 0; dt < (PDK > PDV ? PDK : PDV); ++dt) {
+    if (dt < PDK) dk_acc[dt] = f32x16{};
+    if (dt < PDV) dv_acc[dt] = f32x16{};
+  }
   const float sl = a.sl;
 
   // No zeroing: every LDS byte the loop reads is written by a DMA load first
@@ -233,7 +241,11 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
   // DMA loads) cannot land inside the loop.
   wait_vm(n_iter > 0 ? in_flight_after(0) : 0);
 #pragma unroll
-  for (int i = 0; i < SKS; ++i) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
+  for (int i = 0; i < STEPS; ++i) {
+    if (i < SKQ && i < SKV) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
+    else if (i < SKQ) asm volatile("" : "+v"(kf[i]));
+    else asm volatile("" : "+v"(vf[i]));
+  }
   __syncthreads();
 
   for (int itn = 0; itn < n_iter; ++itn) {
@@ -242,8 +254,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
     const bool prefetch = itn + KV_PD < n_iter;
     const TileDma nxt = tile_dma(prefetch ? itn + KV_PD : itn);
     const char *qt = ring + (itn % KV_NS) * STAGE_B;
-    const char *gt = qt + TILE_B;
-    const float *rv = reinterpret_cast<const float *>(qt + 2 * TILE_B);
+    const char *gt = qt + TILE_Q;
+    const float *rv = reinterpret_cast<const float *>(qt + TILE_Q + TILE_G);
     int hq, q0;
     tile_of(itn, hq, q0);
 
@@ -278,18 +290,18 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
     {
       u32x4 qa[FD + 1], ga[FD + 1];
       auto load = [&](int i) {
-        qa[i % (FD + 1)] = rd.rows(qt, 0, i);
-        ga[i % (FD + 1)] = rd.rows(gt, 0, i);
+        if (i < SKQ) qa[i % (FD + 1)] = rdq.rows(qt, 0, i);
+        if (i < SKV) ga[i % (FD + 1)] = rdg.rows(gt, 0, i);
       };
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < SKS; ++i) {
-        sacc = mfma32<T>(qa[i % (FD + 1)], kf[i], sacc);
-        dpacc = mfma32<T>(ga[i % (FD + 1)], vf[i], dpacc);
-        if (i + FD < SKS) load(i + FD);
-        if (prefetch && (i & 1)) issue_part(nxt, i >> 1);
+      for (int i = 0; i < STEPS; ++i) {
+        if (i < SKQ) sacc = mfma32<T>(qa[i % (FD + 1)], kf[i], sacc);
+        if (i < SKV) dpacc = mfma32<T>(ga[i % (FD + 1)], vf[i], dpacc);
+        if (i + FD < STEPS) load(i + FD);
+        if (prefetch && (i & 1) && (i >> 1) < LPT) issue_part(nxt, i >> 1);
         if (prefetch && i == 0) issue_part(nxt, LPT);
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -367,17 +379,17 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
     {
       u32x4 gc[FD + 1], qc[FD + 1];
       auto load = [&](int i) {
-        gc[i % (FD + 1)] = rd.cols(gt, i / PDT, i % PDT);
-        qc[i % (FD + 1)] = rd.cols(qt, i / PDT, i % PDT);
+        if (i < 2 * PDV) gc[i % (FD + 1)] = rdg.cols(gt, i / PDV, i % PDV);
+        if (i < 2 * PDK) qc[i % (FD + 1)] = rdq.cols(qt, i / PDK, i % PDK);
       };
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < SKS; ++i) {
-        dv_acc[i % PDT] = mfma32<T>(gc[i % (FD + 1)], pp[i / PDT], dv_acc[i % PDT]);
-        dk_acc[i % PDT] = mfma32<T>(qc[i % (FD + 1)], pd[i / PDT], dk_acc[i % PDT]);
-        if (i + FD < SKS) load(i + FD);
+      for (int i = 0; i < STEPS; ++i) {
+        if (i < 2 * PDV) dv_acc[i % PDV] = mfma32<T>(gc[i % (FD + 1)], pp[i / PDV], dv_acc[i % PDV]);
+        if (i < 2 * PDK) dk_acc[i % PDK] = mfma32<T>(qc[i % (FD + 1)], pd[i / PDK], dk_acc[i % PDK]);
+        if (i + FD < STEPS) load(i + FD);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -389,40 +401,36 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
 
   // Epilogue.  The loop ended on a barrier after every wave's last LDS read,
   // so the ring is free.  Each wave rounds its rows and stages them in its own
-  // slice of the ring -- key row r (0..31) at r * 2D bytes, 16-byte chunk q
+  // slice of the ring -- key row r (0..31) at r * 2DX bytes, 16-byte chunk q
   // at q ^ (r % CPR), the XOR keeping the row writes off one bank -- then
   // reads them back as whole 16-byte chunks of rows, so the global stores are
-  // coalesced.  dK first, then dV through the same slice.
-  constexpr int CPR = D / 8;  // 16-byte chunks per row
-  static_assert(NW * 32 * 2 * D <= KV_NS * STAGE_B, "epilogue slices fit in the ring");
-  static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
-  char *slice = ring + w * 32 * 2 * D;
-  const float sc = a.scale;
-#pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    const f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
-    const float f = pass == 0 ? sc : 1.f;
+  // coalesced.  dK (DX = DK) first, then dV (DX = DV) through the same slice.
+  static_assert(NW * 32 * 2 * DMAX <= KV_NS * STAGE_B, "epilogue slices fit in the ring");
+  char *slice = ring + w * 32 * 2 * DMAX;
+  auto store_rows = [&](auto dx, const auto &acc, const View &ov, float f, bool rope_back) {
+    constexpr int DX = decltype(dx)::value, PD = DX / 32;
+    constexpr int CPR = DX / 8;  // 16-byte chunks per row
+    static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
     // lane holds X^T[d = 32 dt + 8 g + 4 h + r][key row c]: 4 consecutive d
 #pragma unroll
-    for (int dt = 0; dt < PDT; ++dt)
+    for (int dt = 0; dt < PD; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+        const int off = c * 2 * DX + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
         *reinterpret_cast<u32x2 *>(slice + off) =
             u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
                   pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
       }
-    const View &ov = pass == 0 ? a.dk : a.dv;
     T *ob = mut<T>(ov) + b * ov.s0 + hk * ov.s1;
     u32x4 vr[32 * CPR / 64];
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-      vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+      vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DX + ((q ^ (r % CPR)) * 16));
     }
     // RoPE folded in: dK of the unrotated keys = the inverse rotation of the
     // rounded dK, key position kpos0 + kw + r, one 16-byte row chunk at a time.
-    if (pass == 0 && p.rope.R > 0) {
+    if (rope_back) {
 #pragma unroll
       for (int u = 0; u < 32 * CPR / 64; ++u) {
         const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
@@ -435,6 +443,50 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<D, MK, DR>())) void dkdv_kernel
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
       if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr[u];
     }
+  };
+  if constexpr (DK == DV) {
+    // one loop over the two passes (same dims: the register allocation of the
+    // tuned equal-dim kernels)
+    constexpr int CPR = DK / 8, PD = DK / 32;
+    const float sc = a.scale;
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+      const f32x16 *acc = pass == 0 ? dk_acc : dv_acc;
+      const float f = pass == 0 ? sc : 1.f;
+#pragma unroll
+      for (int dt = 0; dt < PD; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int off = c * 2 * DK + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+          *reinterpret_cast<u32x2 *>(slice + off) =
+              u32x2{pack2<T>(acc[dt][4 * g] * f, acc[dt][4 * g + 1] * f),
+                    pack2<T>(acc[dt][4 * g + 2] * f, acc[dt][4 * g + 3] * f)};
+        }
+      const View &ov = pass == 0 ? a.dk : a.dv;
+      T *ob = mut<T>(ov) + b * ov.s0 + hk * ov.s1;
+      u32x4 vr[32 * CPR / 64];
+#pragma unroll
+      for (int u = 0; u < 32 * CPR / 64; ++u) {
+        const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+        vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DK + ((q ^ (r % CPR)) * 16));
+      }
+      if (pass == 0 && p.rope.R > 0) {
+#pragma unroll
+        for (int u = 0; u < 32 * CPR / 64; ++u) {
+          const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+          const int key = kw + r < p.Sk ? kw + r : p.Sk - 1;  // rows past Sk: not stored
+          rotate_chunk<T>(vr[u], p.rope, p.rope.kpos0 + key, 4 * q, true);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 32 * CPR / 64; ++u) {
+        const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+        if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr[u];
+      }
+    }
+  } else {
+    store_rows(std::integral_constant<int, DK>{}, dk_acc, a.dk, a.scale, p.rope.R > 0);
+    store_rows(std::integral_constant<int, DV>{}, dv_acc, a.dv, 1.f, false);
   }
 }
 
@@ -453,15 +505,21 @@ constexpr int KT = 32;   // keys per tile
 constexpr int DQ_PD = 2;              // tiles issued ahead
 constexpr int DQ_NS = DQ_PD + 2;      // ring stages: tile j is read in iterations j and j + 1
 
-template <typename T, int D, int MK, bool DR>
+// DK = head dim of q / k (and dQ), DV = of v / dO; each 64 or 128.
+template <typename T, int DK, int DV, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
-  constexpr int TILE_B = KT * D * 2;   // bytes per K (or V) tile
-  constexpr int NBLK = TILE_B / 1024;  // 1 KiB blocks per tile
-  constexpr int LPT = 2 * NBLK / NW;   // DMA loads per wave per K+V tile
-  constexpr int SKS = D / 16, PDT = D / 32, QG = D / 32;
-  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
-  static_assert(SKS == 2 * PDT, "one dQ MFMA per step");
-  __shared__ __attribute__((aligned(1024))) char lds[DQ_NS * 2 * TILE_B];  // [stage][K | V]
+  constexpr int TILE_K = KT * DK * 2, TILE_V = KT * DV * 2;  // bytes per K / V tile
+  constexpr int STAGE = TILE_K + TILE_V;
+  constexpr int KPARTS = TILE_K / 1024 / NW, VPARTS = TILE_V / 1024 / NW;
+  constexpr int LPT = KPARTS + VPARTS;        // DMA loads per wave per K+V tile
+  constexpr int SKQ = DK / 16, SKV = DV / 16;  // k-steps of S (over DK), dP (over DV)
+  constexpr int PDQ = DK / 32;                 // 32-row blocks of dQ^T (2 key k-steps each)
+  constexpr int STEPS = SKQ > SKV ? SKQ : SKV;
+  constexpr int QGK = DK / 32, QGV = DV / 32;
+  static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
+                VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
+  static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
+  __shared__ __attribute__((aligned(1024))) char lds[DQ_NS * STAGE];  // [stage][K | V]
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -488,7 +546,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int n_tiles = lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0;
   const int w_tiles = wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0;
 
-  u32x4 qf[SKS], gf[SKS];
+  u32x4 qf[SKQ], gf[SKV];
   float lse2, delta;  // -safe(lse) in exp2 units, -delta
   {
     const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
@@ -496,23 +554,25 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
     const rsrc_t ors = make_rsrc(head_ptr<T>(a.o, b, hq), static_cast<uint32_t>(p.Sq) * os_b);
-    u32x4 of[SKS];
+    u32x4 of[SKV];
 #pragma unroll
-    for (int ks = 0; ks < SKS; ++ks) {
-      qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
-      gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
-      of[ks] = buf_load16(ors, static_cast<uint32_t>(qrow) * os_b + (ks * 16 + h * 8) * 2);
+    for (int ks = 0; ks < STEPS; ++ks) {
+      if (ks < SKQ) qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+      if (ks < SKV) {
+        gf[ks] = buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + (ks * 16 + h * 8) * 2);
+        of[ks] = buf_load16(ors, static_cast<uint32_t>(qrow) * os_b + (ks * 16 + h * 8) * 2);
+      }
     }
     // RoPE folded in: rotate the query fragments as the forward did, and
     // stage the rotated rows for the dK/dV kernel.
     if (p.rope.R > 0) {
       const int64_t row = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
 #pragma unroll
-      for (int ks = 0; ks < SKS; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
+      for (int ks = 0; ks < SKQ; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
       if (qrow < p.Sq) {
         T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
 #pragma unroll
-        for (int ks = 0; ks < SKS; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
+        for (int ks = 0; ks < SKQ; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
       }
     }
     const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
@@ -520,7 +580,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     // delta = sum_d dO O in fp32; lanes c and c + 32 hold the row's two halves
     float dsum = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < SKS; ++ks) {
+    for (int ks = 0; ks < SKV; ++ks) {
       const T *ge = reinterpret_cast<const T *>(&gf[ks]);
       const T *oe = reinterpret_cast<const T *>(&of[ks]);
 #pragma unroll
@@ -538,7 +598,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // Resolve these loads before the DMA loads start (the compiler's vmcnt
   // waits do not count those).
 #pragma unroll
-  for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
+  for (int ks = 0; ks < STEPS; ++ks) {
+    if (ks < SKQ && ks < SKV) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
+    else if (ks < SKQ) asm volatile("" : "+v"(qf[ks]));
+    else asm volatile("" : "+v"(gf[ks]));
+  }
   asm volatile("" : "+v"(delta), "+v"(lse2));
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
@@ -548,20 +612,18 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // Wave w loads blocks e = w, w + 4, ... of the tile (K blocks first, then V):
   // block n = (n / QG, n % QG), lane l fetches row 16 (n / QG) + l / 4, chunk
   // 4 (n % QG) + ((l % 4) ^ ((l / 16) % 4)); n % QG = w % QG for all of them.
-  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
-  const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
-  const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
+  const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
+  const uint32_t voff = (lane >> 2) * vs_b + (4 * (w % QGV) + swz_chunk) * 16;
   // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
-  constexpr int KPARTS = NBLK / NW;
-  static_assert(NBLK % NW == 0 && SKS == 2 * LPT, "one DMA part per two MFMA steps");
   auto issue_part = [&](int tile, int u) {
-    const uint32_t st = lds0 + (tile % DQ_NS) * 2 * TILE_B;
+    const uint32_t st = lds0 + (tile % DQ_NS) * STAGE;
     if (u < KPARTS) {
       const int n = w + NW * u;
-      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * KT + 16 * (n / QG)) * ks_b);
+      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * KT + 16 * (n / QGK)) * ks_b);
     } else {
       const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, st + TILE_B + n * 1024, voff, static_cast<uint32_t>(tile * KT + 16 * (n / QG)) * vs_b);
+      dma16(vdesc, st + TILE_K + n * 1024, voff, static_cast<uint32_t>(tile * KT + 16 * (n / QGV)) * vs_b);
     }
   };
   auto issue = [&](int tile) {
@@ -573,10 +635,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     return later > 0 ? later * LPT : 0;
   };
 
-  const TileReader<T, D> rd(lane);
-  f32x16 acc[PDT];
+  const TileReader<T, DK> rdk(lane);
+  const TileReader<T, DV> rdv(lane);
+  f32x16 acc[PDQ];
 #pragma unroll
-  for (int dt = 0; dt < PDT; ++dt) acc[dt] = f32x16{};
+  for (int dt = 0; dt < PDQ; ++dt) acc[dt] = f32x16{};
   f32x16 s = f32x16{}, dp = f32x16{};
   u32x4 pd[2];  // dS^T of the previous tile, packed: B operands of its 2 k-steps
   const float sl = a.sl;
@@ -607,7 +670,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
   // LDS byte is written by a DMA load before it is read (lanes past the
   // buffer range write zeros).
-  zero_lds<NT>(lds + (DQ_NS - 1) * 2 * TILE_B, TILE_B, tid);
+  zero_lds<NT>(lds + (DQ_NS - 1) * STAGE, TILE_K, tid);
   __syncthreads();
   for (int t = 0; t < DQ_PD && t < n_tiles; ++t) issue(t);
   wait_vm(in_flight_after(0));
@@ -622,15 +685,15 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
     if constexpr (MK != 0)
       if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * KT + 4 * h) * mstep, mstep);
-    const char *kt = lds + (j % DQ_NS) * 2 * TILE_B;
-    const char *vt = kt + TILE_B;
-    const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * 2 * TILE_B;
+    const char *kt = lds + (j % DQ_NS) * STAGE;
+    const char *vt = kt + TILE_K;
+    const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * STAGE;
     constexpr int FD = 2;
     u32x4 kr[FD + 1], vr[FD + 1], kc[FD + 1];
     auto load = [&](int i) {
-      kr[i % (FD + 1)] = rd.rows(kt, 0, i);
-      vr[i % (FD + 1)] = rd.rows(vt, 0, i);
-      kc[i % (FD + 1)] = rd.cols(kp, i / PDT, i % PDT);
+      if (i < SKQ) kr[i % (FD + 1)] = rdk.rows(kt, 0, i);
+      if (i < SKV) vr[i % (FD + 1)] = rdv.rows(vt, 0, i);
+      if (i < SKQ) kc[i % (FD + 1)] = rdk.cols(kp, i / PDQ, i % PDQ);
     };
     s = f32x16{};
     dp = f32x16{};
@@ -638,12 +701,12 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     for (int i = 0; i < FD; ++i) load(i);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < SKS; ++i) {
-      s = mfma32<T>(kr[i % (FD + 1)], qf[i], s);
-      dp = mfma32<T>(vr[i % (FD + 1)], gf[i], dp);
-      acc[i % PDT] = mfma32<T>(kc[i % (FD + 1)], pd[i / PDT], acc[i % PDT]);
-      if (i + FD < SKS) load(i + FD);
-      if (nt >= 0 && (i & 1)) issue_part(nt, i >> 1);
+    for (int i = 0; i < STEPS; ++i) {
+      if (i < SKQ) s = mfma32<T>(kr[i % (FD + 1)], qf[i], s);
+      if (i < SKV) dp = mfma32<T>(vr[i % (FD + 1)], gf[i], dp);
+      if (i < SKQ) acc[i % PDQ] = mfma32<T>(kc[i % (FD + 1)], pd[i / PDQ], acc[i % PDQ]);
+      if (i + FD < STEPS) load(i + FD);
+      if (nt >= 0 && (i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -721,16 +784,16 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // bytes, 16-byte chunk q at q ^ (r % CPR) -- then reads back whole 16-byte
   // chunks of rows for coalesced stores.  Lane holds dQ^T[d = 32 dt + 8 g +
   // 4 h + r][row c].
-  constexpr int CPR = D / 8;
-  static_assert(NW * 32 * 2 * D <= DQ_NS * 2 * TILE_B, "output slices fit in the ring");
+  constexpr int CPR = DK / 8;
+  static_assert(NW * 32 * 2 * DK <= DQ_NS * STAGE, "output slices fit in the ring");
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
-  char *slice = lds + w * 32 * 2 * D;
+  char *slice = lds + w * 32 * 2 * DK;
   const float sc = a.scale;
 #pragma unroll
-  for (int dt = 0; dt < PDT; ++dt) {
+  for (int dt = 0; dt < PDQ; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+      const int off = c * 2 * DK + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
       *reinterpret_cast<u32x2 *>(slice + off) =
           u32x2{pack2<T>(acc[dt][g * 4] * sc, acc[dt][g * 4 + 1] * sc),
                 pack2<T>(acc[dt][g * 4 + 2] * sc, acc[dt][g * 4 + 3] * sc)};
@@ -741,7 +804,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
     const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-    vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+    vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DK + ((q ^ (r % CPR)) * 16));
   }
   // RoPE folded in: dQ of the unrotated queries = the inverse rotation of the
   // rounded dQ (rotary_embedding's VJP), one 16-byte row chunk at a time.
@@ -760,35 +823,44 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
-template <typename T, int D, int MK, bool DR>
+template <typename T, int DK, int DV, int MK, bool DR>
 void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   {
     Probe pr_(DR ? "bwd_dq_mfma_dropout" : (MK ? "bwd_dq_mfma_masked" : "bwd_dq_mfma"), st);
-    dq_kernel<T, D, MK, DR><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+    dq_kernel<T, DK, DV, MK, DR><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
   }
   const int n_kb = (p.Sk + KB - 1) / KB;
   {
     Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
-    dkdv_kernel<T, D, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+    dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
   }
 }
 
-template <typename T, int D, bool DR>
+template <typename T, int DK, int DV, bool DR>
 void launch_dr(const BwdArgs &a, int mk, hipStream_t st) {
-  if (mk == 1) launch_mk<T, D, 1, DR>(a, st);
-  else if (mk == 2) launch_mk<T, D, 2, DR>(a, st);
-  else if (mk == 3) launch_mk<T, D, 3, DR>(a, st);
-  else launch_mk<T, D, 0, DR>(a, st);
+  if (mk == 1) launch_mk<T, DK, DV, 1, DR>(a, st);
+  else if (mk == 2) launch_mk<T, DK, DV, 2, DR>(a, st);
+  else if (mk == 3) launch_mk<T, DK, DV, 3, DR>(a, st);
+  else launch_mk<T, DK, DV, 0, DR>(a, st);
 }
 
-template <typename T, int D>
-hipError_t launch(const BwdArgs &a, hipStream_t st) {
+template <typename T, int DK, int DV>
+void launch_dims(const BwdArgs &a, hipStream_t st) {
   const int mk = mfma_mask_mode(a.p);
-  if (a.p.drop.on) launch_dr<T, D, true>(a, mk, st);
-  else launch_dr<T, D, false>(a, mk, st);
+  if (a.p.drop.on) launch_dr<T, DK, DV, true>(a, mk, st);
+  else launch_dr<T, DK, DV, false>(a, mk, st);
+}
+
+template <typename T>
+hipError_t launch(const BwdArgs &a, hipStream_t st) {
+  const Problem &p = a.p;
+  if (p.Dqk == 128 && p.Dv == 128) launch_dims<T, 128, 128>(a, st);
+  else if (p.Dqk == 64 && p.Dv == 64) launch_dims<T, 64, 64>(a, st);
+  else if (p.Dqk == 128) launch_dims<T, 128, 64>(a, st);
+  else launch_dims<T, 64, 128>(a, st);
   return hipGetLastError();
 }
 
@@ -811,8 +883,7 @@ hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, Vie
   }
   BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
             static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale)};
-  if (dtype == TSATTN_BF16) return p.Dqk == 128 ? launch<bf16, 128>(a, st) : launch<bf16, 64>(a, st);
-  return p.Dqk == 128 ? launch<f16, 128>(a, st) : launch<f16, 64>(a, st);
+  return dtype == TSATTN_BF16 ? launch<bf16>(a, st) : launch<f16>(a, st);
 }
 
 }  // namespace tsattn

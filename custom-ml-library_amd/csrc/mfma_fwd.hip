@@ -1,5 +1,7 @@
 // Flash-style attention forward for gfx950: MFMA 32x32x16 (f16/bf16 in,
-// fp32 accumulate), online softmax in the exp2 domain, row LSE saved.
+// fp32 accumulate), online softmax in the exp2 domain, row LSE saved.  Head
+// dims 64 or 128, q / k and v / o independently (Dqk != Dv, the reference's
+// value_dim).
 //
 // Algorithm: the reference's streaming forward (src/tensorsmith/nn/
 // attention.py:175-198) -- running max m, denominator l and accumulator per
@@ -69,17 +71,23 @@ __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
 }
 
-template <typename T, int D, int MK, bool DR>
+// DK = head dim of q / k, DV = of v / o (each 64 or 128).
+template <typename T, int DK, int DV, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
-  constexpr int TILE_B = BN * D * 2;        // bytes per K (or V) tile
-  constexpr int NBLK = TILE_B / 1024;       // 1 KiB blocks per tile
-  constexpr int LPT = 2 * NBLK / NW;        // DMA loads per wave per K+V tile
-  constexpr int SKS = D / 16;               // k-steps of S^T = K Q^T
-  constexpr int PDT = D / 32;               // 32-row blocks of O^T
-  constexpr int QG = D / 32;                // 4-chunk groups per row
-  static_assert(LPT >= 1 && LPT * NW == 2 * NBLK, "tile loads must split evenly over the waves");
-  static_assert(SKS == 2 * PDT, "one S and one PV MFMA per step");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * 2 * TILE_B];  // [stage][K | V]
+  constexpr int TILE_K = BN * DK * 2, TILE_V = BN * DV * 2;  // bytes per K / V tile
+  constexpr int STAGE = TILE_K + TILE_V;
+  constexpr int KPARTS = TILE_K / 1024 / NW;  // 1 KiB DMA blocks per wave per K tile
+  constexpr int VPARTS = TILE_V / 1024 / NW;  // ... per V tile
+  constexpr int LPT = KPARTS + VPARTS;        // DMA loads per wave per K+V tile
+  constexpr int SKS = DK / 16;                // k-steps of S^T = K Q^T
+  constexpr int PDT = DV / 32;                // 32-row blocks of O^T
+  constexpr int PVS = 2 * PDT;                // PV MFMAs per tile (two key k-steps each block)
+  constexpr int STEPS = SKS > PVS ? SKS : PVS;
+  constexpr int QGK = DK / 32, QGV = DV / 32;  // 4-chunk groups per K / V row
+  static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
+                VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
+  static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];  // [stage][K | V]
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -115,7 +123,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
 
   // Q fragments (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8h .. +7].
-  u32x4 qf[SKS];
+  u32x4 qf[SKS];  // (DK channels)
 #pragma unroll
   for (int ks = 0; ks < SKS; ++ks)
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
@@ -133,26 +141,24 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]));
 
   const uint32_t lds0 = lds_addr(lds);
-  // DMA of key tile `tile` into its ring stage.  The K and V blocks of a tile
-  // are numbered e = 0 .. 2 NBLK - 1 (K first); wave w loads e = w, w + 8, ...
+  // DMA of key tile `tile` into its ring stage.  The 1 KiB blocks of the K
+  // (then V) tile are numbered n = 0, 1, ...; wave w loads n = w, w + 4, ...
   // Block n = (rg, qg) = (n / QG, n % QG); its lane l fetches row 16 rg + l/4,
   // chunk 4 qg + ((l % 4) ^ ((l / 16) % 4)).  qg = w % QG for all of the
   // wave's blocks, so the per-lane part of the offset is loop-invariant and
   // the row part is wave-uniform.
-  const uint32_t lane_chunk = 4 * (w % QG) + ((lane & 3) ^ ((lane >> 4) & 3));
-  const uint32_t koff = (lane >> 2) * ks_b + lane_chunk * 16;
-  const uint32_t voff = (lane >> 2) * vs_b + lane_chunk * 16;
+  const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
+  const uint32_t voff = (lane >> 2) * vs_b + (4 * (w % QGV) + swz_chunk) * 16;
   // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
-  constexpr int KPARTS = NBLK / NW;
-  static_assert(NBLK % NW == 0 && SKS == 2 * LPT, "one DMA part per two MFMA steps");
   auto issue_part = [&](int tile, int u) {
-    const uint32_t st = lds0 + (tile % NS) * 2 * TILE_B;
+    const uint32_t st = lds0 + (tile % NS) * STAGE;
     if (u < KPARTS) {
       const int n = w + NW * u;
-      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * BN + 16 * (n / QG)) * ks_b);
+      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * BN + 16 * (n / QGK)) * ks_b);
     } else {
       const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, st + TILE_B + n * 1024, voff, static_cast<uint32_t>(tile * BN + 16 * (n / QG)) * vs_b);
+      dma16(vdesc, st + TILE_K + n * 1024, voff, static_cast<uint32_t>(tile * BN + 16 * (n / QGV)) * vs_b);
     }
   };
   auto issue = [&](int tile) {
@@ -166,7 +172,8 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     return later > 0 ? later * LPT : 0;
   };
 
-  const TileReader<T, D> rd(lane);
+  const TileReader<T, DK> rdk(lane);
+  const TileReader<T, DV> rdv(lane);
   f32x16 oacc[PDT];
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) oacc[dt] = f32x16{};
@@ -204,7 +211,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
   // Every other LDS byte is written by a DMA load before it is read (lanes
   // past the buffer range write zeros).
-  zero_lds<NT>(lds + (NS - 1) * 2 * TILE_B + TILE_B, TILE_B, tid);
+  zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
   __syncthreads();
   for (int t = 0; t < PD && t < n_tiles; ++t) issue(t);
   wait_vm(in_flight_after(0));
@@ -221,13 +228,13 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
     if constexpr (MK != 0)
       if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * BN + 4 * h) * mstep, mstep);
-    const char *kt = lds + (j % NS) * 2 * TILE_B;
-    const char *vt = lds + ((j + NS - 1) % NS) * 2 * TILE_B + TILE_B;
+    const char *kt = lds + (j % NS) * STAGE;
+    const char *vt = lds + ((j + NS - 1) % NS) * STAGE + TILE_K;
     constexpr int FD = 2;  // fragment prefetch distance, in steps
     u32x4 kf[FD + 1], vf[FD + 1];
     auto load = [&](int i) {
-      kf[i % (FD + 1)] = rd.rows(kt, 0, i);
-      vf[i % (FD + 1)] = rd.cols(vt, i / PDT, i % PDT);
+      if (i < SKS) kf[i % (FD + 1)] = rdk.rows(kt, 0, i);
+      if (i < PVS) vf[i % (FD + 1)] = rdv.cols(vt, i / PDT, i % PDT);
     };
     s = f32x16{};
 #pragma unroll
@@ -235,11 +242,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     // sched_barrier fences keep each step's reads FD steps ahead of its use.
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < SKS; ++i) {
-      s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
-      oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
-      if (i + FD < SKS) load(i + FD);
-      if (nt >= 0 && (i & 1)) issue_part(nt, i >> 1);
+    for (int i = 0; i < STEPS; ++i) {
+      if (i < SKS) s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
+      if (i < PVS) oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
+      if (i + FD < STEPS) load(i + FD);
+      if (nt >= 0 && (i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -339,15 +346,15 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // bytes, 16-byte chunk q at q ^ (r % CPR), the XOR keeping the row writes
   // off one bank -- then reads back whole 16-byte chunks of rows, so the
   // global stores are coalesced.  Lane holds O^T[d = 32 dt + 8 g + 4 h + r][row c].
-  constexpr int CPR = D / 8;
-  static_assert(NW * 32 * 2 * D <= NS * 2 * TILE_B, "output slices fit in the ring");
+  constexpr int CPR = DV / 8;
+  static_assert(NW * 32 * 2 * DV <= NS * STAGE, "output slices fit in the ring");
   static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
-  char *slice = lds + w * 32 * 2 * D;
+  char *slice = lds + w * 32 * 2 * DV;
 #pragma unroll
   for (int dt = 0; dt < PDT; ++dt) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      const int off = c * 2 * D + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+      const int off = c * 2 * DV + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
       *reinterpret_cast<u32x2 *>(slice + off) =
           u32x2{pack2<T>(oacc[dt][g * 4 + 0] * inv, oacc[dt][g * 4 + 1] * inv),
                 pack2<T>(oacc[dt][g * 4 + 2] * inv, oacc[dt][g * 4 + 3] * inv)};
@@ -357,7 +364,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
     const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * D + ((q ^ (r % CPR)) * 16));
+    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DV + ((q ^ (r % CPR)) * 16));
     if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.o.s2 + q * 8) = vr;
   }
   if (a.lse && h == 0 && qrow < p.Sq)
@@ -365,21 +372,30 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
         lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
 }
 
-template <typename T, int D, bool DR>
+template <typename T, int DK, int DV, bool DR>
 void launch_dr(const FwdArgs &a, int mk, hipStream_t st) {
-  if (mk == 1) fwd_kernel<T, D, 1, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 2) fwd_kernel<T, D, 2, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 3) fwd_kernel<T, D, 3, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else fwd_kernel<T, D, 0, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  if (mk == 1) fwd_kernel<T, DK, DV, 1, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 2) fwd_kernel<T, DK, DV, 2, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else if (mk == 3) fwd_kernel<T, DK, DV, 3, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  else fwd_kernel<T, DK, DV, 0, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
 }
 
-template <typename T, int D>
-hipError_t launch(const FwdArgs &a, hipStream_t st) {
+template <typename T, int DK, int DV>
+void launch_dims(const FwdArgs &a, hipStream_t st) {
   const int mk = mfma_mask_mode(a.p);
-  const bool dr = a.p.drop.on != 0;
-  Probe pr_(dr ? "fwd_mfma_dropout" : (mk ? "fwd_mfma_masked" : "fwd_mfma"), st);
-  if (dr) launch_dr<T, D, true>(a, mk, st);
-  else launch_dr<T, D, false>(a, mk, st);
+  if (a.p.drop.on) launch_dr<T, DK, DV, true>(a, mk, st);
+  else launch_dr<T, DK, DV, false>(a, mk, st);
+}
+
+template <typename T>
+hipError_t launch(const FwdArgs &a, hipStream_t st) {
+  const Problem &p = a.p;
+  const int mk = mfma_mask_mode(p);
+  Probe pr_(p.drop.on ? "fwd_mfma_dropout" : (mk ? "fwd_mfma_masked" : "fwd_mfma"), st);
+  if (p.Dqk == 128 && p.Dv == 128) launch_dims<T, 128, 128>(a, st);
+  else if (p.Dqk == 64 && p.Dv == 64) launch_dims<T, 64, 64>(a, st);
+  else if (p.Dqk == 128) launch_dims<T, 128, 64>(a, st);
+  else launch_dims<T, 64, 128>(a, st);
   return hipGetLastError();
 }
 
@@ -387,7 +403,7 @@ hipError_t launch(const FwdArgs &a, hipStream_t st) {
 
 bool mfma_supported(const Problem &p, int dtype) {
   if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
-  if (p.Dqk != p.Dv || (p.Dqk != 64 && p.Dqk != 128)) return false;
+  if ((p.Dqk != 64 && p.Dqk != 128) || (p.Dv != 64 && p.Dv != 128)) return false;
   if (!(p.scale > 0.0)) return false;
   if (p.mask.kind == TSATTN_MASK_ADDITIVE && p.mask.dtype != TSATTN_F32 &&
       p.mask.dtype != TSATTN_F16 && p.mask.dtype != TSATTN_BF16)
@@ -406,8 +422,7 @@ hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View
                                float *lse, hipStream_t st) {
   FwdArgs a{p, q, k, v, o, lse, static_cast<float>(p.scale) * kLog2e, (p.Sq + BM - 1) / BM, 0};
   a.total = a.n_qblocks * p.Hq * p.B;
-  if (dtype == TSATTN_BF16) return p.Dqk == 128 ? launch<bf16, 128>(a, st) : launch<bf16, 64>(a, st);
-  return p.Dqk == 128 ? launch<f16, 128>(a, st) : launch<f16, 64>(a, st);
+  return dtype == TSATTN_BF16 ? launch<bf16>(a, st) : launch<f16>(a, st);
 }
 
 }  // namespace tsattn

@@ -73,11 +73,12 @@ def test_keep_mask_is_the_oracles(shape, key, counter, p):
 
 
 CASES = [
-    # (dtype, B, Hq, Hkv, Sq, Sk, D, causal, offset, p, masked)
+    # (dtype, B, Hq, Hkv, Sq, Sk, D, causal, offset, p, masked); D may be (Dqk, Dv)
     ("bfloat16", 2, 2, 2, 130, 130, 128, True, 0, 0.2, False),
     ("float16", 1, 4, 2, 96, 200, 64, True, 104, 0.5, False),
     ("bfloat16", 2, 2, 1, 77, 150, 128, False, 0, 0.1, True),
     ("float16", 1, 2, 2, 256, 256, 128, False, 0, 0.3, False),
+    ("bfloat16", 1, 2, 2, 100, 140, (128, 64), True, 40, 0.25, False),
 ]
 
 
@@ -85,7 +86,9 @@ CASES = [
 def test_dropout_attention_matches_oracle(case):
     dtype, b, hq, hkv, sq, sk, d, causal, off, p, masked = case
     say(f"dropout attention {case}")
-    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=31)
+    d, dv = d if isinstance(d, tuple) else (d, d)
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, dim_v=dv, value_scale=0.5,
+                           seed=31)
     key, counter = 0x5EED_0000_0000_0000_1234_5678_9ABC_DEF0, 11
     mask = np.random.default_rng(1).random((sq, sk)) > 0.25 if masked else None
     out_c, ref_out, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, mask, causal, dtype=dtype, p=p,

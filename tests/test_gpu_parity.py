@@ -277,6 +277,57 @@ def test_mfma_key_mask_without_lengths_reads_the_mask():
         assert torch.equal(a_, b_)
 
 
+# Value head dim != query/key head dim on the MFMA kernels (the reference's
+# value_dim, tests/test_transformer.py:44-46): tiles and accumulators sized per
+# operand, with GQA, causal offsets and a general mask.
+VALUE_DIM_CASES = [
+    # (dtype, B, Hq, Hkv, Sq, Sk, Dqk, Dv, causal, offset, masked)
+    ("bfloat16", 2, 2, 2, 200, 333, 128, 64, True, 133, False),
+    ("float16", 1, 4, 2, 160, 160, 64, 128, True, 0, False),
+    ("bfloat16", 2, 2, 1, 77, 190, 128, 64, False, 0, True),
+    ("float16", 1, 2, 2, 129, 257, 64, 128, False, 0, True),
+]
+
+
+@pytest.mark.parametrize("case", VALUE_DIM_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_mfma_value_dim_differs(case):
+    dtype, b, hq, hkv, sq, sk, dqk, dv, causal, off, masked = case
+    say(f"mfma Dqk {dqk} Dv {dv} {case}")
+    inp = attention_inputs(b, hq, sq, dqk, dtype, heads_kv=hkv, seq_k=sk, dim_v=dv,
+                           value_scale=0.5, seed=17)
+    mask = np.random.default_rng(3).random((sq, sk)) > 0.2 if masked else None
+    ref = _oracle(inp, dtype, causal, off, mask=mask, gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    kw = dict(causal=causal, offset=off, mask=None if mask is None else torch.from_numpy(mask).cuda())
+    out, lse, path = abi.forward(q, k, v, **kw)
+    assert path == _lib.PATH_MFMA
+    dq, dk, dv_, bpath = abi.backward(q, k, v, out, g, lse, **kw)
+    assert bpath == _lib.PATH_MFMA
+    torch.cuda.synchronize()
+    check_half(abi.host(out), ref.out, dtype, "o", "O")
+    check_lse(abi.host(lse), ref.lse, "LSE")
+    rdq, rdk, rdv = ref.backward_compute(inp.do)
+    check_half(abi.host(dq), rdq, dtype, "g", "dQ")
+    check_half(abi.host(dk), rdk, dtype, "g", "dK")
+    check_half(abi.host(dv_), rdv, dtype, "g", "dV")
+
+
+def test_mfma_value_dim_differs_agrees_with_generic():
+    dtype = "bfloat16"
+    inp = attention_inputs(1, 2, 150, 64, dtype, seq_k=150, dim_v=128, value_scale=0.5, seed=2)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    out_m, lse_m, path = abi.forward(q, k, v, causal=True)
+    assert path == _lib.PATH_MFMA
+    grads_m = abi.backward(q, k, v, out_m, g, lse_m, causal=True)[:3]
+    with abi.generic_only():
+        out_g, lse_g, _ = abi.forward(q, k, v, causal=True)
+        grads_g = abi.backward(q, k, v, out_m, g, lse_m, causal=True)[:3]
+    torch.cuda.synchronize()
+    check_half(abi.host(out_m), abi.host(out_g), dtype, "o", "O mfma/generic")
+    for a_, b_, n in zip(grads_m, grads_g, ("dQ", "dK", "dV")):
+        check_half(abi.host(a_), abi.host(b_), dtype, "g", n + " mfma/generic")
+
+
 # ---------------------------------------------------------------------------
 # Decode kernel
 # ---------------------------------------------------------------------------

@@ -200,11 +200,12 @@ def test_fused_cached_decode_is_bitwise_the_two_step_path(quantized):
 
 
 FUSED_CASES = [
-    # (dtype, B, Hq, Hkv, Sq, Sk, D, R, causal, offset, q_pos0, k_pos0)
+    # (dtype, B, Hq, Hkv, Sq, Sk, D, R, causal, offset, q_pos0, k_pos0); D may be (Dqk, Dv)
     ("bfloat16", 2, 2, 2, 200, 200, 128, 128, True, 0, 0, 0),
     ("float16", 1, 4, 2, 130, 257, 64, 64, True, 127, 127, 0),
     ("bfloat16", 2, 2, 1, 77, 150, 128, 64, False, 0, 9, 3),
     ("float16", 1, 2, 2, 256, 256, 128, 96, True, 0, 5, 5),
+    ("bfloat16", 1, 2, 2, 90, 120, (128, 64), 128, True, 30, 30, 0),
 ]
 
 
@@ -212,9 +213,10 @@ FUSED_CASES = [
 def test_rope_folded_into_attention_is_bitwise_the_unfused_chain(case):
     dtype, b, hq, hkv, sq, sk, d, r, causal, off, qp, kp = case
     say(f"fused rope attention {case}")
+    d, dv = d if isinstance(d, tuple) else (d, d)
     rng = np.random.default_rng(sq + d)
     q, k, v, g = (abi.dev_tensor(rows(rng, shape, dtype, 0.7), dtype)
-                  for shape in ((b, hq, sq, d), (b, hkv, sk, d), (b, hkv, sk, d), (b, hq, sq, d)))
+                  for shape in ((b, hq, sq, d), (b, hkv, sk, d), (b, hkv, sk, dv), (b, hq, sq, dv)))
     cos, sin = tables(max(qp + sq, kp + sk) + 1, r, dtype)
     rot = lambda x, pos, inv=False: _rot(x, cos, sin, pos, r, inv)
     k_rot = rot(k, kp)
