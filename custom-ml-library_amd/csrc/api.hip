@@ -138,7 +138,7 @@ int check_rope(const tsattn_rope_desc *r, const tsattn::Problem &pr, tsattn::Rop
 
 int rope_unsupported() {
   return fail(TSATTN_ERR_UNSUPPORTED,
-              "RoPE folded into attention needs the MFMA kernels (f16/bf16, dim_qk == dim_v in "
+              "RoPE folded into attention needs the MFMA kernels (f16/bf16, dim_qk and dim_v in "
               "{64, 128}, 16-byte aligned views); rotate with tsattn_rope instead");
 }
 

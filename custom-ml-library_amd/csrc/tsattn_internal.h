@@ -151,7 +151,7 @@ hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, 
                                    View dout, const void *lse, View dq, View dk, View dv,
                                    void *delta, hipStream_t st);
 
-// MFMA kernels: f16 / bf16, dim_qk == dim_v in {64, 128}, scale > 0; any
+// MFMA kernels: f16 / bf16, dim_qk and dim_v each in {64, 128}, scale > 0; any
 // boolean mask, or an additive mask in f32 / f16 / bf16.
 bool mfma_supported(const Problem &p, int dtype);
 hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,

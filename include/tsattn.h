@@ -174,7 +174,7 @@ typedef struct tsattn_rope_desc {
  * the query rotation done in the kernel prologue: `q` holds the unrotated
  * queries, `k` the keys already rotated (tsattn_rope).  Bit-identical to
  * tsattn_rope on q followed by tsattn_sdpa_forward.  Only problems the MFMA
- * kernels take (f16/bf16, dim_qk == dim_v in {64, 128}, 16-byte aligned
+ * kernels take (f16/bf16, dim_qk and dim_v in {64, 128}, 16-byte aligned
  * views); others return TSATTN_ERR_UNSUPPORTED (rotate with tsattn_rope).
  */
 int tsattn_sdpa_forward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
