@@ -354,7 +354,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
             if (masked) pv[r] = ((kc >= lo) & (kc < hi)) ? pv[r] : 0.f;
           } else {
             // -inf where disallowed; additive-masked scores arrive scaled
-            pv[r] = fast_exp2(MK >= 2 ? xs[e] : xs[e] * sl);
+            pv[r] = fast_exp2(mask_kind(MK) >= 2 ? xs[e] : xs[e] * sl);
           }
           if constexpr (DR) {
             const bool keep = dtile[(8 * g + 4 * h + r) * 32 + c] >= p.drop.thr;
@@ -664,7 +664,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     if (qrow >= p.Sq) klim = 0;
   }
   MaskFetch mf;
-  const float slx = MK >= 2 ? 1.f : sl;  // additive-masked scores arrive scaled
+  const float slx = mask_kind(MK) >= 2 ? 1.f : sl;  // additive-masked scores arrive scaled
 
   // The first MFMA block multiplies the K half of stage DQ_NS - 1 (no DMA has
   // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
@@ -683,8 +683,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // wave's last tile S and dP are computed and ignored.
   // fetch: also load tile j's mask elements, before the DMA parts.
   auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
-    if constexpr (MK != 0)
+    if constexpr (mask_vec(MK)) {
+      if (fetch) mf.issue_vec<mes>(mdesc, mrow + static_cast<uint32_t>(j * KT + 16 * h) * mes);
+    } else if constexpr (MK != 0) {
       if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * KT + 4 * h) * mstep, mstep);
+    }
     const char *kt = lds + (j % DQ_NS) * STAGE;
     const char *vt = kt + TILE_K;
     const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * STAGE;
@@ -735,7 +738,12 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
         }
       } else {
         wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
-        mf.resolve();
+        if constexpr (mask_vec(MK)) {
+          mf.resolve_vec<mes>();
+          mf.unpack<mes>(h);
+        } else {
+          mf.resolve();
+        }
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim_l, sl);
       }
     }
@@ -823,14 +831,16 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
-template <typename T, int DK, int DV, int MK, bool DR>
+// MKQ: the dQ kernel's mask mode (0..6), MK the dK/dV kernel's (0..3: it
+// reads element by element, its loads already coalesced across keys).
+template <typename T, int DK, int DV, int MKQ, int MK, bool DR>
 void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   {
     Probe pr_(DR ? "bwd_dq_mfma_dropout" : (MK ? "bwd_dq_mfma_masked" : "bwd_dq_mfma"), st);
-    dq_kernel<T, DK, DV, MK, DR><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+    dq_kernel<T, DK, DV, MKQ, DR><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
   }
   const int n_kb = (p.Sk + KB - 1) / KB;
   {
@@ -840,18 +850,23 @@ void launch_mk(const BwdArgs &a, hipStream_t st) {
 }
 
 template <typename T, int DK, int DV, bool DR>
-void launch_dr(const BwdArgs &a, int mk, hipStream_t st) {
-  if (mk == 1) launch_mk<T, DK, DV, 1, DR>(a, st);
-  else if (mk == 2) launch_mk<T, DK, DV, 2, DR>(a, st);
-  else if (mk == 3) launch_mk<T, DK, DV, 3, DR>(a, st);
-  else launch_mk<T, DK, DV, 0, DR>(a, st);
+void launch_dr(const BwdArgs &a, int mkq, hipStream_t st) {
+  switch (mkq) {
+    case 1: launch_mk<T, DK, DV, 1, 1, DR>(a, st); break;
+    case 2: launch_mk<T, DK, DV, 2, 2, DR>(a, st); break;
+    case 3: launch_mk<T, DK, DV, 3, 3, DR>(a, st); break;
+    case 4: launch_mk<T, DK, DV, 4, 1, DR>(a, st); break;
+    case 5: launch_mk<T, DK, DV, 5, 2, DR>(a, st); break;
+    case 6: launch_mk<T, DK, DV, 6, 3, DR>(a, st); break;
+    default: launch_mk<T, DK, DV, 0, 0, DR>(a, st); break;
+  }
 }
 
 template <typename T, int DK, int DV>
 void launch_dims(const BwdArgs &a, hipStream_t st) {
-  const int mk = mfma_mask_mode(a.p);
-  if (a.p.drop.on) launch_dr<T, DK, DV, true>(a, mk, st);
-  else launch_dr<T, DK, DV, false>(a, mk, st);
+  const int mkq = mfma_mask_mode_vec(a.p);
+  if (a.p.drop.on) launch_dr<T, DK, DV, true>(a, mkq, st);
+  else launch_dr<T, DK, DV, false>(a, mkq, st);
 }
 
 template <typename T>

@@ -91,12 +91,79 @@ struct MaskFetch {
 #pragma unroll
     for (int i = 0; i < 16; ++i) asm volatile("" : "+v"(v[i]));
   }
+
+  // Key-contiguous masks with 16-byte aligned rows: lane half h loads keys
+  // 16 h .. 16 h + 15 of the lane's row within the 32-key tile (NQ 16-byte
+  // loads: bool 1, 16-bit 2, f32 4) into v[0 .. 4 NQ), resolve(), then
+  // unpack<ES>(h) trades quarters with the partner lane (keys 4 m .. 4 m + 3
+  // of a half, m = 0..3): the lane keeps quarters h and 2 + h of its own half
+  // and receives the same quarters of the other half, which gives exactly its
+  // keys 8 g + 4 h + r -- and spreads them to v[4 g + r] as the scalar fetch
+  // would.
+  // The raw pieces stay in vv, untouched until resolve_vec() has run after
+  // the wait (a copy before that would read registers still being loaded).
+  u32x4 vv[4];
+  template <int NQ>
+  __device__ __forceinline__ void issue_vec(u32x4 desc, uint32_t off) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(vv[q]) : "v"(off + 16u * q), "s"(desc) : "memory");
+  }
+  template <int NQ>
+  __device__ __forceinline__ void resolve_vec() {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) asm volatile("" : "+v"(vv[q]));
+  }
+  template <int ES>  // bytes per element: QD = ES dwords per quarter
+  __device__ __forceinline__ void unpack(int h);
 };
 
-// Bytes per mask element of mask mode MK (1 boolean, 2 additive f32,
-// 3 additive f16 / bf16).
+// The value x of the partner lane l ^ 32 (v_permlane32_swap exchanges the
+// upper half of one register with the lower half of another; with both
+// holding x, lanes 0..31 find the partner's value in the second, lanes
+// 32..63 in the first).  Assembly: the builtin returns the same register for
+// both halves when its operands are equal.
+__device__ __forceinline__ unsigned partner32(unsigned x, int h) {
+  unsigned a = x, b = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return h ? a : b;
+}
+
+template <int ES>
+__device__ __forceinline__ void MaskFetch::unpack(int h) {
+  constexpr int QD = ES;  // dwords per quarter (4 elements)
+  unsigned d[4 * QD];
+#pragma unroll
+  for (int i = 0; i < 4 * QD; ++i) d[i] = vv[i >> 2][i & 3];
+  unsigned g[4][QD];
+#pragma unroll
+  for (int t = 0; t < QD; ++t) {
+    const unsigned k0 = h ? d[QD + t] : d[t], k1 = h ? d[3 * QD + t] : d[2 * QD + t];
+    const unsigned s0 = h ? d[t] : d[QD + t], s1 = h ? d[2 * QD + t] : d[3 * QD + t];
+    const unsigned r0 = partner32(s0, h), r1 = partner32(s1, h);
+    g[0][t] = h ? r0 : k0;
+    g[1][t] = h ? r1 : k1;
+    g[2][t] = h ? k0 : r0;
+    g[3][t] = h ? k1 : r1;
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (ES == 1) v[4 * q + r] = (g[q][0] >> (8 * r)) & 0xFFu;
+      else if constexpr (ES == 2) v[4 * q + r] = (g[q][r >> 1] >> (16 * (r & 1))) & 0xFFFFu;
+      else v[4 * q + r] = g[q][r];
+    }
+}
+
+// Mask modes MK: 1 boolean, 2 additive f32, 3 additive f16 / bf16, read
+// element by element; 4, 5, 6 the same kinds read as 16-byte row pieces
+// (key-contiguous, 16-byte aligned rows; the forward and dQ kernels).
+constexpr int mask_kind(int MK) { return MK > 3 ? MK - 3 : MK; }
+constexpr bool mask_vec(int MK) { return MK > 3; }
+// Bytes per mask element.
 template <int MK>
-constexpr int mask_bytes() { return MK == 1 ? 1 : (MK == 2 ? 4 : 2); }
+constexpr int mask_bytes() { return mask_kind(MK) == 1 ? 1 : (mask_kind(MK) == 2 ? 4 : 2); }
 
 // Apply fetched mask elements: score i is allowed iff lo <= kc(i) < hi and
 // the mask allows it; disallowed scores become -inf.  With an additive mask
@@ -109,11 +176,11 @@ __device__ __forceinline__ void mask_scores(float (&x)[16], const MaskFetch &mf,
   for (int i = 0; i < 16; ++i) {
     const int kc = 8 * (i >> 2) + (i & 3);
     const bool in = (kc >= lo) & (kc < hi);
-    if constexpr (MK == 1) {
+    if constexpr (mask_kind(MK) == 1) {
       x[i] = in && mf.v[i] != 0u ? x[i] : -INFINITY;
     } else {
       float mv;
-      if constexpr (MK == 2) mv = __builtin_bit_cast(float, mf.v[i]);
+      if constexpr (mask_kind(MK) == 2) mv = __builtin_bit_cast(float, mf.v[i]);
       else if (mdtype == TSATTN_BF16) mv = __builtin_bit_cast(float, mf.v[i] << 16);
       else mv = static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(mf.v[i])));
       x[i] = in ? fmaf(x[i], sl, mv * kLog2e) : -INFINITY;
@@ -386,12 +453,6 @@ __device__ __forceinline__ float half_swap_max(float x) {
   return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
-// The value x of the partner lane l ^ 32 (v_permlane32_swap, as above).
-__device__ __forceinline__ unsigned partner32(unsigned x, int h) {
-  unsigned a = x, b = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
-  return h ? a : b;
-}
 __device__ __forceinline__ uint64_t partner64(uint64_t x, int h) {
   return static_cast<uint64_t>(partner32(static_cast<unsigned>(x), h)) |
          (static_cast<uint64_t>(partner32(static_cast<unsigned>(x >> 32), h)) << 32);

@@ -41,7 +41,8 @@
 // per tile; a general boolean or additive mask (MK = 1 / 2) is read per
 // (query row, key) from its broadcast strides on every tile, an additive one
 // entering as scores * scale + mask (attention.py:105-107) in log2 units
-// (MK = 2 for an f32 mask, 3 for f16 / bf16).
+// (MK = 2 for an f32 mask, 3 for f16 / bf16; 4..6 the same read as 16-byte
+// row pieces when the keys are contiguous and the rows aligned).
 #include "mfma_common.h"
 #include "philox.h"
 #include "rope_math.h"
@@ -205,7 +206,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   }
   MaskFetch mf;
   // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
-  const float slx = MK >= 2 ? 1.f : a.sl;
+  const float slx = mask_kind(MK) >= 2 ? 1.f : a.sl;
 
   // The first MFMA block runs PV with P = 0 against the V half of stage
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
@@ -226,8 +227,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // fetch: also load tile j's mask elements (before the DMA parts, so that
   // the softmax can wait for them and leave those parts in flight).
   auto mfma_block = [&](int j, int nt, bool fetch) {  // nt: tile whose DMA to issue, or -1
-    if constexpr (MK != 0)
+    if constexpr (mask_vec(MK)) {
+      if (fetch) mf.issue_vec<mes>(mdesc, mrow + static_cast<uint32_t>(j * BN + 16 * h) * mes);
+    } else if constexpr (MK != 0) {
       if (fetch) mf.issue<mes>(mdesc, mrow + static_cast<uint32_t>(j * BN + 4 * h) * mstep, mstep);
+    }
     const char *kt = lds + (j % NS) * STAGE;
     const char *vt = lds + ((j + NS - 1) % NS) * STAGE + TILE_K;
     constexpr int FD = 2;  // fragment prefetch distance, in steps
@@ -276,7 +280,12 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
         }
       } else {
         wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
-        mf.resolve();
+        if constexpr (mask_vec(MK)) {
+          mf.resolve_vec<mes>();
+          mf.unpack<mes>(h);
+        } else {
+          mf.resolve();
+        }
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim, sl);
       }
     }
@@ -374,15 +383,21 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 
 template <typename T, int DK, int DV, bool DR>
 void launch_dr(const FwdArgs &a, int mk, hipStream_t st) {
-  if (mk == 1) fwd_kernel<T, DK, DV, 1, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 2) fwd_kernel<T, DK, DV, 2, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else if (mk == 3) fwd_kernel<T, DK, DV, 3, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
-  else fwd_kernel<T, DK, DV, 0, DR><<<dim3(a.total), dim3(NT), 0, st>>>(a);
+  const dim3 g(a.total), blk(NT);
+  switch (mk) {
+    case 1: fwd_kernel<T, DK, DV, 1, DR><<<g, blk, 0, st>>>(a); break;
+    case 2: fwd_kernel<T, DK, DV, 2, DR><<<g, blk, 0, st>>>(a); break;
+    case 3: fwd_kernel<T, DK, DV, 3, DR><<<g, blk, 0, st>>>(a); break;
+    case 4: fwd_kernel<T, DK, DV, 4, DR><<<g, blk, 0, st>>>(a); break;
+    case 5: fwd_kernel<T, DK, DV, 5, DR><<<g, blk, 0, st>>>(a); break;
+    case 6: fwd_kernel<T, DK, DV, 6, DR><<<g, blk, 0, st>>>(a); break;
+    default: fwd_kernel<T, DK, DV, 0, DR><<<g, blk, 0, st>>>(a); break;
+  }
 }
 
 template <typename T, int DK, int DV>
 void launch_dims(const FwdArgs &a, hipStream_t st) {
-  const int mk = mfma_mask_mode(a.p);
+  const int mk = mfma_mask_mode_vec(a.p);
   if (a.p.drop.on) launch_dr<T, DK, DV, true>(a, mk, st);
   else launch_dr<T, DK, DV, false>(a, mk, st);
 }

@@ -109,6 +109,17 @@ inline int mfma_mask_mode(const Problem &p) {
   if (p.mask.kind != TSATTN_MASK_ADDITIVE) return 0;
   return p.mask.dtype == TSATTN_F32 ? 2 : 3;
 }
+// The same, read as 16-byte row pieces (modes 4..6) where the keys are
+// contiguous and every row starts 16-byte aligned.
+inline int mfma_mask_mode_vec(const Problem &p) {
+  const int mk = mfma_mask_mode(p);
+  if (mk == 0) return 0;
+  const int64_t es = mk == 1 ? 1 : (mk == 2 ? 4 : 2);
+  const MaskDesc &m = p.mask;
+  const bool ok = m.s3 == 1 && (m.s0 * es) % 16 == 0 && (m.s1 * es) % 16 == 0 &&
+                  (m.s2 * es) % 16 == 0 && reinterpret_cast<uintptr_t>(m.data) % 16 == 0;
+  return ok ? mk + 3 : mk;
+}
 
 // Valid keys for batch row b: [0, kv_end).
 __device__ __forceinline__ int kv_end_for(const Problem &p, int b) {

@@ -203,6 +203,9 @@ MASK_CASES = [
     ("add-f32-1hqk-causal", "float16", 1, 2, 2, 300, 300, 128, True, 0, (1, 2, 300, 300), "float32"),
     ("add-bf16-qk", "bfloat16", 2, 2, 1, 77, 150, 64, True, 73, (77, 150), "bfloat16"),
     ("add-f16-keybias", "float16", 3, 2, 2, 96, 200, 128, False, 0, (3, 1, 1, 200), "float16"),
+    # rows 16-byte aligned, keys contiguous: the 16-byte row-piece reads
+    ("bool-qk-rows", "bfloat16", 2, 2, 2, 160, 256, 128, True, 96, (160, 256), "bool"),
+    ("add-bf16-rows", "float16", 1, 4, 2, 128, 192, 64, False, 0, (128, 192), "bfloat16"),
 ]
 
 
