@@ -14,6 +14,8 @@ time.  The JSON line also carries
 * ``roofline`` -- the dominant kernel's achieved rate (algorithmic work per
   launch / its mean duration from HIP events recorded on its own stream
   during the timed steps) against the MI355X dense bf16 MFMA peak;
+* ``variants`` -- the headline step with a general [S, S] boolean mask,
+  with dropout p = 0.1, and with RoPE folded into the kernels;
 * ``decode`` -- KV-cache decode (B=64 H=32 D=128 fp16 cache, lengths
   U[512, 8192]): tokens/s and HBM GB/s with its own roofline;
 * ``prefill`` -- long-context causal prefill with a key-padding mask
@@ -51,9 +53,9 @@ B, H, S, D = 16, 16, 2048, 128
 DEC_B, DEC_H, DEC_D, DEC_CAP, DEC_LO, DEC_HI = 64, 32, 128, 8192, 512, 8192
 PF_B, PF_H, PF_S, PF_D, PF_LO = 2, 32, 32768, 128, 16384
 LM_LAYERS, LM_DIM, LM_HEADS, LM_FFN, LM_VOCAB, LM_B, LM_S = 6, 512, 8, 2048, 32000, 8, 1024
-ATTN_KERNELS = ("fwd_mfma", "bwd_row_prep", "bwd_dkdv_mfma", "bwd_dq_mfma", "generic_fwd",
+ATTN_KERNELS = ("fwd_mfma", "bwd_dkdv_mfma", "bwd_dq_mfma", "generic_fwd",
                 "generic_bwd_delta", "generic_bwd_dq", "generic_bwd_dkdv", "key_mask_lengths",
-                "decode_split", "decode_merge")
+                "decode_split", "decode_merge", "rope")
 
 
 def causal_fwd_flops(b, h, s, d):
@@ -146,6 +148,48 @@ def bench_fwd_bwd(ts, torch, steps, warmup):
     }
     host = {"q": q_raw, "k": k_raw, "v": v_raw, "g": g_raw}
     return result, host
+
+
+def bench_variants(ts, torch, steps, warmup, host):
+    """The headline shape again through the other MFMA kernel variants: a
+    general [S, S] boolean mask (with the causal flag), dropout p = 0.1 on the
+    hip backend, and RoPE folded into the kernels (unrotated q / k, as
+    MultiHeadAttention calls it).  Same FLOP count per step as the headline."""
+    q, k, v = (ts.Tensor(host[n], device="hip", requires_grad=True) for n in ("q", "k", "v"))
+    upstream = ts.Tensor(host["g"], device="hip")
+    tril = ts.Tensor(torch.ones((S, S), dtype=torch.bool, device="cuda").tril(), device="hip")
+    cases = {
+        "general_bool_mask": dict(attn_mask=tril, is_causal=True),
+        "dropout_p0.1": dict(is_causal=True, dropout_p=0.1, backend="hip"),
+        "rope_folded": dict(is_causal=True, _rope=(0, 0, 10000.0)),
+    }
+    from tensorsmith_hip import _lib
+
+    flops = causal_fwd_flops(B, H, S, D) * 3.5
+    out = {}
+    for name, kw in cases.items():
+        def step():
+            for t in (q, k, v):
+                t.zero_grad()
+            ts.nn.scaled_dot_product_attention(q, k, v, **kw).backward(upstream)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        step()
+        torch.cuda.synchronize()
+        _lib.profile_enable(False)
+        kernels = {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}
+        out[name] = {"ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                     "kernel_ms": kernels}
+    return out
 
 
 def bench_decode(ts, torch, steps, warmup):
@@ -532,6 +576,9 @@ def main():
                           "roofline": main_res["roofline"], "kernels": main_res["kernels"]}),
               flush=True)
         return
+    var_res = bench_variants(ts, torch, max(3, args.steps // 4), 2, host)
+    print("[bench] variants " + ", ".join(f"{n} {r['ms_per_step']:.3f} ms" for n, r in var_res.items()),
+          file=sys.stderr, flush=True)
     dec_res, dec_host = bench_decode(ts, torch, args.decode_steps, args.warmup)
     print(f"[bench] decode {dec_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
     q8_res = bench_decode_int8(ts, torch, args.decode_steps, args.warmup, dec_host)
@@ -564,6 +611,7 @@ def main():
                    "flop_per_step": causal_fwd_flops(B, H, S, D) * 3.5},
         "roofline": main_res["roofline"],
         "kernels": main_res["kernels"],
+        "variants": var_res,
         "cpu_baseline": cpu,
         "decode": dec_res,
         "decode_int8": q8_res,
