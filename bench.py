@@ -72,7 +72,8 @@ def parse():
                     help="batch rows (of 16 heads each) in the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload",
-                    choices=["all", "fwd_bwd", "decode", "decode_int8", "prefill", "lm", "copy"],
+                    choices=["all", "fwd_bwd", "variants", "decode", "decode_int8", "prefill", "lm",
+                             "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -574,6 +575,10 @@ def main():
     if args.workload == "fwd_bwd":
         print(json.dumps({"value": main_res["value"], "ms_per_step": main_res["ms_per_step"],
                           "roofline": main_res["roofline"], "kernels": main_res["kernels"]}),
+              flush=True)
+        return
+    if args.workload == "variants":
+        print(json.dumps({"variants": bench_variants(ts, torch, args.steps, args.warmup, host)}),
               flush=True)
         return
     var_res = bench_variants(ts, torch, max(3, args.steps // 4), 2, host)
