@@ -89,14 +89,27 @@ constexpr int KV_PD = 2;  // tiles in flight
 // Workgroups per CU: two, except the general-mask kernel at D = 128, whose
 // mask registers do not fit beside the two-workgroup register budget; alone
 // on its CU it has the accumulation registers as well.
+// Masks the dK/dV kernel stages through its LDS ring (modes 4 and 6: boolean
+// or 16-bit, key-contiguous with 16-byte aligned rows) hold no registers.
+constexpr bool mask_staged(int MK) { return MK == 4 || MK == 6; }
+
 template <int DK, int DV, int MK, bool DR>
-constexpr int dkdv_wg_per_cu() { return (MK != 0 || DR) && (DK > 64 || DV > 64) ? 1 : 2; }
+constexpr int dkdv_wg_per_cu() {
+  return ((MK != 0 && !mask_staged(MK)) || DR) && (DK > 64 || DV > 64) ? 1 : 2;
+}
 
 // DK = head dim of q / k (and dK), DV = of v / dO (and dV); each 64 or 128.
 template <typename T, int DK, int DV, int MK, bool DR>
 __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_kernel(BwdArgs a) {
   constexpr int TILE_Q = QT * DK * 2, TILE_G = QT * DV * 2;  // bytes of a Q / dO tile
-  constexpr int STAGE_B = TILE_Q + TILE_G + 256;  // Q | dO | nl (QT floats) | nd (QT floats)
+  // A staged mask: the tile's [QT rows][KB keys] elements, row-major.
+  constexpr bool MSTAGE = mask_staged(MK);
+  constexpr int MES = MSTAGE ? mask_bytes<MK>() : 0;
+  constexpr int MROW = KB * MES, MTILE = QT * MROW;  // bytes per mask row / tile
+  constexpr int MPARTS = MTILE / 1024 / NW;          // mask DMA loads per wave per tile
+  constexpr int MOFF = TILE_Q + TILE_G + 256;
+  // Q | dO | nl (QT floats) | nd (QT floats) | mask tile
+  constexpr int STAGE_B = TILE_Q + TILE_G + 256 + MTILE;
   constexpr int QPARTS = TILE_Q / 1024 / NW, GPARTS = TILE_G / 1024 / NW;
   constexpr int LPT = QPARTS + GPARTS;            // Q + dO DMA loads per wave per tile
   constexpr int SKQ = DK / 16, SKV = DV / 16;     // k-steps of S (over DK) and dP (over DV)
@@ -198,14 +211,39 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         dma16(rdesc, t.st + TILE_Q + TILE_G + w * QT * 4, loff, static_cast<uint32_t>(t.q0) * 4);
     }
   };
+  // Staged mask: 1 KiB block n = w + NW u of the tile holds rows
+  // n * 1024 / MROW ..; lane l fetches 16 bytes at byte 16 l of the block.
+  // The lane's offset is recomputed at each issue (no register held all loop:
+  // the two-workgroup budget is full).
+  auto issue_mask = [&](const TileDma &t) {
+    if constexpr (MSTAGE) {
+      const uint32_t ms2 = static_cast<uint32_t>(p.mask.s2 * MES);  // bytes between mask rows
+      uint32_t l16;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(l16));
+      const uint32_t mvoff = (l16 / MROW) * ms2 + l16 % MROW;
+      const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * MES;
+      const u32x4 mdesc = make_desc(
+          static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + t.hq * p.mask.s1) * MES,
+          static_cast<uint32_t>(extent));
+#pragma unroll
+      for (int u = 0; u < MPARTS; ++u) {
+        const int n = w + NW * u;
+        dma16(mdesc, t.st + MOFF + n * 1024, mvoff,
+              static_cast<uint32_t>(t.q0 + n * (1024 / MROW)) * ms2 + static_cast<uint32_t>(k0 * MES));
+      }
+    }
+  };
   auto issue = [&](int itn) {
     const TileDma t = tile_dma(itn);
 #pragma unroll
     for (int u = 0; u <= LPT; ++u) issue_part(t, u);
+    issue_mask(t);
   };
   // DMA loads this wave may leave in flight once tile itn has landed: those
   // of the later tiles already issued.
-  const int parts = LPT + (w < 2 ? 1 : 0);
+  const int parts = LPT + (w < 2 ? 1 : 0) + MPARTS;
   auto in_flight_after = [&](int itn) {
     const int later = min(KV_PD - 1, n_iter - 1 - itn);
     return later > 0 ? later * parts : 0;
@@ -265,7 +303,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     // under them) and before the next tile's DMA parts issued among those, so
     // that the wait for them leaves the parts in flight.
     MaskFetch mf;
-    if constexpr (MK != 0) {
+    if constexpr (MK != 0 && !MSTAGE) {
       constexpr int mes = mask_bytes<MK>();
       const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * mes;
       const u32x4 mdesc = make_desc(
@@ -302,7 +340,10 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         if (i < SKV) dpacc = mfma32<T>(ga[i % (FD + 1)], vf[i], dpacc);
         if (i + FD < STEPS) load(i + FD);
         if (prefetch && (i & 1) && (i >> 1) < LPT) issue_part(nxt, i >> 1);
-        if (prefetch && i == 0) issue_part(nxt, LPT);
+        if (prefetch && i == 0) {
+          issue_part(nxt, LPT);
+          issue_mask(nxt);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -330,10 +371,17 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int m = 0; m < 4; ++m) dst[m] = blk[m];
     }
+    // Staged mask: this lane's column (key 32 w + c) at row 4 h of the tile.
+    const char *mrow_base = nullptr;
+    if constexpr (MSTAGE) {
+      uint32_t l;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+      mrow_base = qt + MOFF + (l >> 5) * 4 * MROW + (32 * w + (l & 31)) * MES;
+    }
     // Interior tiles skip the per-element bounds (three VALU ops each).
     auto grad = [&](auto masked) {
       float xs[16];
-      if constexpr (MK != 0) {
+      if constexpr (MK != 0 && !MSTAGE) {
         // The mask loads; the next tile's Q / dO parts stay in flight (waves 0
         // and 1 also wait for their row-value part, the first one issued).
         if (prefetch) wait_vm_n<LPT>();
@@ -352,6 +400,19 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
           if constexpr (MK == 0) {
             pv[r] = fast_exp2(sacc[e] * sl);
             if (masked) pv[r] = ((kc >= lo) & (kc < hi)) ? pv[r] : 0.f;
+          } else if constexpr (MSTAGE) {
+            // element (row 8 g + 4 h + r, key 32 w + c) of the staged tile
+            const bool in = (kc >= lo) & (kc < hi);
+            const char *me = mrow_base + (8 * g + r) * MROW;
+            if constexpr (mask_kind(MK) == 1) {
+              pv[r] = in && *reinterpret_cast<const uint8_t *>(me) ? fast_exp2(sacc[e] * sl) : 0.f;
+            } else {
+              const uint32_t bits = *reinterpret_cast<const uint16_t *>(me);
+              const float mv = p.mask.dtype == TSATTN_BF16
+                                   ? __builtin_bit_cast(float, bits << 16)
+                                   : static_cast<float>(__builtin_bit_cast(f16, static_cast<uint16_t>(bits)));
+              pv[r] = in ? fast_exp2(fmaf(sacc[e], sl, mv * kLog2e)) : 0.f;
+            }
           } else {
             // -inf where disallowed; additive-masked scores arrive scaled
             pv[r] = fast_exp2(mask_kind(MK) >= 2 ? xs[e] : xs[e] * sl);
@@ -369,6 +430,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         pp[g >> 1][(g & 1) * 2 + 1] = pack2<T>(pv[2], pv[3]);
         pd[g >> 1][(g & 1) * 2] = pack2<T>(dsv[0], dsv[1]);
         pd[g >> 1][(g & 1) * 2 + 1] = pack2<T>(dsv[2], dsv[3]);
+        // staged masks: four LDS reads in flight at a time, not sixteen (the
+        // register budget of two workgroups per CU has no room for them)
+        if constexpr (MSTAGE) __builtin_amdgcn_sched_barrier(0);
       }
     };
     if (edge) grad(std::true_type{});
@@ -831,8 +895,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
-// MKQ: the dQ kernel's mask mode (0..6), MK the dK/dV kernel's (0..3: it
-// reads element by element, its loads already coalesced across keys).
+// MKQ: the dQ kernel's mask mode (0..6), MK the dK/dV kernel's: element reads
+// (1..3), or boolean / 16-bit row-piece masks staged through its LDS ring
+// (4, 6); f32 row-piece masks (5) read element by element there.
 template <typename T, int DK, int DV, int MKQ, int MK, bool DR>
 void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
@@ -855,9 +920,9 @@ void launch_dr(const BwdArgs &a, int mkq, hipStream_t st) {
     case 1: launch_mk<T, DK, DV, 1, 1, DR>(a, st); break;
     case 2: launch_mk<T, DK, DV, 2, 2, DR>(a, st); break;
     case 3: launch_mk<T, DK, DV, 3, 3, DR>(a, st); break;
-    case 4: launch_mk<T, DK, DV, 4, 1, DR>(a, st); break;
-    case 5: launch_mk<T, DK, DV, 5, 2, DR>(a, st); break;
-    case 6: launch_mk<T, DK, DV, 6, 3, DR>(a, st); break;
+    case 4: launch_mk<T, DK, DV, 4, 4, DR>(a, st); break;
+    case 5: launch_mk<T, DK, DV, 5, 2, DR>(a, st); break;  // f32 tiles: too much LDS to stage
+    case 6: launch_mk<T, DK, DV, 6, 6, DR>(a, st); break;
     default: launch_mk<T, DK, DV, 0, 0, DR>(a, st); break;
   }
 }
