@@ -221,6 +221,62 @@ int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const t
                     "generic backward launch");
 }
 
+// Decode over a 16-bit cache (k_scale == v_scale == NULL) or an int8 one,
+// with the query rotation folded in when `rope` is given.
+int decode_forward(const tsattn_problem *p, const tsattn_rope_desc *rope, const tsattn_view *q,
+                   const tsattn_view *k, const tsattn_view *v, const tsattn_view *k_scale,
+                   const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,
+                   void *workspace, size_t workspace_bytes, void *stream) {
+  const bool q8 = k_scale != nullptr;
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if (pr.drop.on)
+    return fail(TSATTN_ERR_UNSUPPORTED, "the decode kernel does not drop (inference only)");
+  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
+      (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
+    return rc;
+  if (q8 && ((rc = check_view(k_scale, "key scale")) || (rc = check_view(v_scale, "value scale"))))
+    return rc;
+  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
+  if (rope && (rc = check_rope(rope, pr, &pr.rope))) return rc;
+  const tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v);
+  if (q8) {
+    if (p->mask_kind != TSATTN_MASK_NONE && !p->kv_len)
+      return fail(TSATTN_ERR_UNSUPPORTED, "int8 decode takes key-padding lengths, not general masks");
+    // int8 rows are read as 8-byte chunks: 8-byte aligned bases and row strides
+    auto aligned8 = [](const tsattn::View &x) {
+      return reinterpret_cast<uintptr_t>(x.data) % 8 == 0 && x.s0 % 8 == 0 && x.s1 % 8 == 0 &&
+             x.s2 % 8 == 0;
+    };
+    if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(vq) || !aligned8(vk) ||
+        !aligned8(vv))
+      return fail(TSATTN_ERR_UNSUPPORTED,
+                  "int8 decode needs <= 8 query rows per KV head, f16/bf16 queries, equal head "
+                  "dims in {64,128,256} and 8-byte aligned cache rows");
+  } else if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(vq) ||
+             !tsattn::aligned16(vk) || !tsattn::aligned16(vv)) {
+    return fail(TSATTN_ERR_UNSUPPORTED,
+                "decode kernel needs <= 8 query rows per KV head, f16/bf16, equal head dims in "
+                "{64,128,256} and 16-byte aligned rows");
+  }
+  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(TSATTN_ERR_INVALID, "decode workspace too small: %zu < %zu bytes",
+                workspace_bytes, need);
+  g_last_path = 3;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (q8)
+    return hip_status(tsattn::launch_decode_int8(pr, p->dtype, vq, vk, vv,
+                                                 tsattn::make_view(k_scale),
+                                                 tsattn::make_view(v_scale),
+                                                 tsattn::make_view(out), split_len, workspace, st),
+                      "int8 decode launch");
+  return hip_status(tsattn::launch_decode(pr, p->dtype, vq, vk, vv, tsattn::make_view(out),
+                                          split_len, workspace, st),
+                    "decode launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -294,68 +350,29 @@ size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len) {
 int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                           const tsattn_view *v, const tsattn_view *out, int32_t split_len,
                           void *workspace, size_t workspace_bytes, void *stream) {
-  tsattn::Problem pr;
-  int rc = check_problem(p, &pr);
-  if (rc) return rc;
-  if (pr.drop.on)
-    return fail(TSATTN_ERR_UNSUPPORTED, "the decode kernel does not drop (inference only)");
-  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
-      (rc = check_view(v, "value")) || (rc = check_view(out, "output")))
-    return rc;
-  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
-  if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(tsattn::make_view(q)) ||
-      !tsattn::aligned16(tsattn::make_view(k)) || !tsattn::aligned16(tsattn::make_view(v)))
-    return fail(TSATTN_ERR_UNSUPPORTED,
-                "decode kernel needs <= 8 query rows per KV head, f16/bf16, equal head dims in "
-                "{64,128,256} and 16-byte aligned rows");
-  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(TSATTN_ERR_INVALID, "decode workspace too small: %zu < %zu bytes",
-                workspace_bytes, need);
-  g_last_path = 3;
-  return hip_status(tsattn::launch_decode(pr, p->dtype, tsattn::make_view(q), tsattn::make_view(k),
-                                          tsattn::make_view(v), tsattn::make_view(out), split_len,
-                                          workspace, static_cast<hipStream_t>(stream)),
-                    "decode launch");
+  return decode_forward(p, nullptr, q, k, v, nullptr, nullptr, out, split_len, workspace,
+                        workspace_bytes, stream);
 }
 
 int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                                const tsattn_view *v, const tsattn_view *k_scale,
                                const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,
                                void *workspace, size_t workspace_bytes, void *stream) {
-  tsattn::Problem pr;
-  int rc = check_problem(p, &pr);
-  if (rc) return rc;
-  if (pr.drop.on)
-    return fail(TSATTN_ERR_UNSUPPORTED, "the decode kernel does not drop (inference only)");
-  if ((rc = check_view(q, "query")) || (rc = check_view(k, "key")) ||
-      (rc = check_view(v, "value")) || (rc = check_view(k_scale, "key scale")) ||
-      (rc = check_view(v_scale, "value scale")) || (rc = check_view(out, "output")))
-    return rc;
-  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
-  if (p->mask_kind != TSATTN_MASK_NONE && !p->kv_len)
-    return fail(TSATTN_ERR_UNSUPPORTED, "int8 decode takes key-padding lengths, not general masks");
-  const tsattn::View vk = tsattn::make_view(k), vv = tsattn::make_view(v);
-  // int8 rows are read as 8-byte chunks: 8-byte aligned bases and row strides
-  auto aligned8 = [](const tsattn::View &x) {
-    return reinterpret_cast<uintptr_t>(x.data) % 8 == 0 && x.s0 % 8 == 0 && x.s1 % 8 == 0 &&
-           x.s2 % 8 == 0;
-  };
-  if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(tsattn::make_view(q)) ||
-      !aligned8(vk) || !aligned8(vv))
-    return fail(TSATTN_ERR_UNSUPPORTED,
-                "int8 decode needs <= 8 query rows per KV head, f16/bf16 queries, equal head dims "
-                "in {64,128,256} and 8-byte aligned cache rows");
-  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
-  if (need && (!workspace || workspace_bytes < need))
-    return fail(TSATTN_ERR_INVALID, "decode workspace too small: %zu < %zu bytes",
-                workspace_bytes, need);
-  g_last_path = 3;
-  return hip_status(tsattn::launch_decode_int8(pr, p->dtype, tsattn::make_view(q), vk, vv,
-                                               tsattn::make_view(k_scale), tsattn::make_view(v_scale),
-                                               tsattn::make_view(out), split_len, workspace,
-                                               static_cast<hipStream_t>(stream)),
-                    "int8 decode launch");
+  if (!k_scale || !v_scale) return fail(TSATTN_ERR_INVALID, "int8 decode needs both row-scale views");
+  return decode_forward(p, nullptr, q, k, v, k_scale, v_scale, out, split_len, workspace,
+                        workspace_bytes, stream);
+}
+
+int tsattn_decode_forward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                               const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                               const tsattn_view *k_scale, const tsattn_view *v_scale,
+                               const tsattn_view *out, int32_t split_len, void *workspace,
+                               size_t workspace_bytes, void *stream) {
+  if (!rope) return fail(TSATTN_ERR_INVALID, "RoPE descriptor is NULL");
+  if (!k_scale != !v_scale)
+    return fail(TSATTN_ERR_INVALID, "pass both row-scale views (int8 cache) or neither");
+  return decode_forward(p, rope, q, k, v, k_scale, v_scale, out, split_len, workspace,
+                        workspace_bytes, stream);
 }
 
 int tsattn_kv_append_int8(int32_t dtype, int32_t batch, int32_t heads, int32_t len, int32_t dim,

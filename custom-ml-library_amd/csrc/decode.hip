@@ -1,5 +1,6 @@
 // KV-cache decode attention for gfx950: a few query rows per KV head against
-// a long cached prefix; bound by HBM bandwidth, not by math.
+// a long cached prefix; bound by HBM bandwidth, not by math.  RoPE can be
+// folded into the query load (Problem::rope; the cache holds rotated keys).
 //
 // Math: the reference's online softmax (src/tensorsmith/nn/attention.py:
 // 185-193) applied twice.  Each workgroup reduces one split of the cache to a
@@ -24,6 +25,7 @@
 #include <type_traits>
 
 #include "mfma_common.h"
+#include "rope_math.h"
 
 namespace tsattn {
 namespace {
@@ -130,7 +132,9 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
                       !(p.kv_prefix && p.kv_prefix[b] && p.mask.s1 == 0 && p.mask.s2 == 0);
 
   // Query rows r = rr * Sq + i (query head hk*rep + rr, position i), pre-scaled
-  // so that s = q.k is already in log2 units.
+  // so that s = q.k is already in log2 units.  With RoPE folded in (the keys
+  // in the cache are stored rotated), row i is rotated to position q_pos0 + i
+  // here, rounded to T as the RoPE kernel rounds it.
   float qv[R][8];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -138,7 +142,9 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
       const int hq = hk * p.rep + r / p.Sq, i = r % p.Sq;
       const T *qp = static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1 +
                     static_cast<int64_t>(i) * a.q.s2 + dc * 8;
-      unpack8<T>(ld16(qp), qv[r]);
+      u32x4 raw = ld16(qp);
+      if (p.rope.R > 0) rotate_chunk<T>(raw, p.rope, p.rope.qpos0 + i, 4 * dc, false);
+      unpack8<T>(raw, qv[r]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) qv[r][e] *= a.sl;
     } else {

@@ -100,7 +100,9 @@ def scaled_dot_product_attention(
     keys are rotated once by the RoPE kernel; the query rotation and both
     inverse rotations of the gradients run inside the MFMA kernels
     (``tsattn_sdpa_forward_rope`` / ``_backward_rope``), with separate RoPE
-    kernels where those do not apply.
+    kernels where those do not apply.  ``k_pos0 = None``: the keys arrive
+    already rotated (a KV cache) and only the query is rotated -- inside the
+    decode kernel (``tsattn_decode_forward_rope``) when that runs.
     """
     # --- the reference's validation, same order and messages (:36-62) ---
     if any(t.ndim != 4 for t in (query, key, value)):
@@ -193,14 +195,17 @@ def scaled_dot_product_attention(
     rope = None  # (descriptor, tables) when the kernels fold the query rotation in
     if _rope is not None:
         q_pos0, k_pos0, base = _rope
-        if (dim % 2 or q_pos0 < 0 or k_pos0 < 0 or base <= 0 or not math.isfinite(base)
+        if (dim % 2 or q_pos0 < 0 or (k_pos0 is not None and k_pos0 < 0) or base <= 0
+                or not math.isfinite(base)
                 or q.dtype not in (torch.float32, torch.float16, torch.bfloat16)):
             raise ValueError("RoPE requires a positive even rotary dimension and valid positions/base")
-        k = _rope_rows(k, k_pos0, base, dim, False, query.device)
-        tables = rope_tables(base, dim, q.dtype, tdev, max(q_pos0 + qlen, k_pos0 + klen))
+        if k_pos0 is not None:
+            k = _rope_rows(k, k_pos0, base, dim, False, query.device)
+        tables = rope_tables(base, dim, q.dtype, tdev,
+                             max(q_pos0 + qlen, 0 if k_pos0 is None else k_pos0 + klen))
         desc = _lib.RopeDesc()
         desc.cos, desc.sin = tables[0].data_ptr(), tables[1].data_ptr()
-        desc.rotary_dim, desc.q_pos0, desc.k_pos0 = dim, q_pos0, k_pos0
+        desc.rotary_dim, desc.q_pos0, desc.k_pos0 = dim, q_pos0, k_pos0 or 0
         rope = (desc, tables)
     vq, vk, vv, vo = _view(q), _view(k), _view(v), _view(out)
 
@@ -215,18 +220,22 @@ def scaled_dot_product_attention(
         and all(_aligned16(t) for t in (q, k, v))
     )
     if use_decode:
-        if rope is not None:
-            q = _rope_rows(q, q_pos0, base, dim, False, query.device)
-            vq = _view(q)
         nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
         ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
-        _lib.check(
-            lib.tsattn_decode_forward(
-                ctypes.byref(prob), vq, vk, vv, vo, 0, ctypes.c_void_p(ws.data_ptr()), nbytes,
-                stream,
-            ),
-            "decode forward",
-        )
+        ws_ptr = ctypes.c_void_p(ws.data_ptr())
+        folded = False
+        if rope is not None:
+            try:  # the query rotation inside the decode kernel
+                _lib.check(lib.tsattn_decode_forward_rope(
+                    ctypes.byref(prob), ctypes.byref(rope[0]), vq, vk, vv, None, None, vo, 0,
+                    ws_ptr, nbytes, stream), "decode forward")
+                folded = True
+            except NotImplementedError:  # e.g. a rotary dim the kernel does not fold
+                q = _rope_rows(q, q_pos0, base, dim, False, query.device)
+                vq = _view(q)
+        if not folded:
+            _lib.check(lib.tsattn_decode_forward(ctypes.byref(prob), vq, vk, vv, vo, 0, ws_ptr,
+                                                 nbytes, stream), "decode forward")
         return Tensor._from_op(out, (query, key, value), None, "sdpa_hip")
 
     lse = None
@@ -235,7 +244,12 @@ def scaled_dot_product_attention(
         lse = torch.empty((b, hq, qlen), dtype=lse_dtype, device=tdev)
     lse_ptr = ctypes.c_void_p(None if lse is None else lse.data_ptr())
     fused = False
-    if rope is not None:
+    if rope is not None and k_pos0 is None:
+        # keys given rotated: their gradient takes no inverse rotation, which the
+        # folded backward would apply; rotate the queries on their own
+        q = _rope_rows(q, q_pos0, base, dim, False, query.device)
+        vq = _view(q)
+    elif rope is not None:
         try:
             _lib.check(lib.tsattn_sdpa_forward_rope(ctypes.byref(prob), ctypes.byref(rope[0]), vq, vk,
                                                     vv, vo, lse_ptr, stream), "attention forward")
@@ -267,24 +281,28 @@ def scaled_dot_product_attention(
                        "attention backward")
             return dq, dk, dv
         _lib.check(lib.tsattn_sdpa_backward(ctypes.byref(prob), *args), "attention backward")
-        if rope is not None:  # rotary_embedding's VJP on both
+        if rope is not None:  # rotary_embedding's VJP on the rotated operands
             dq = _rope_rows(dq, q_pos0, base, dim, True, query.device)
-            dk = _rope_rows(dk, k_pos0, base, dim, True, query.device)
+            if k_pos0 is not None:
+                dk = _rope_rows(dk, k_pos0, base, dim, True, query.device)
         return dq, dk, dv
 
     return Tensor._from_op(out, (query, key, value), backward, "sdpa_hip")
 
 
 def decode_int8_cache(query: Tensor, cache, *, is_causal: bool, causal_offset: int,
-                      scale: float | None = None) -> Tensor | None:
+                      scale: float | None = None, rope: tuple | None = None) -> Tensor | None:
     """Inference attention of ``query`` [B, Hq, Q, D] against an int8
     ``KVCache``'s active prefix, dequantised inside the decode kernel
     (``tsattn_decode_forward_int8``).  Same result as the reference's
     ``scaled_dot_product_attention(query, *cache.get(), ...)`` (the cache
     dequantised eagerly, ``src/tensorsmith/nn/cache.py:88-99``) up to the
-    rounding of the dequantised values to the cache dtype.  Returns None when
-    the shapes are outside the decode kernel (the caller then goes through
-    ``cache.get()``)."""
+    rounding of the dequantised values to the cache dtype.  ``rope = (q_pos0,
+    base)``: ``query`` is unrotated and the kernel rotates it
+    (``tsattn_decode_forward_rope``), bit for bit ``rotary_embedding(query,
+    q_pos0)``; the cached keys are rotated already.  Returns None when the
+    shapes are outside the decode kernel (the caller then goes through
+    ``cache.get()``, with ``query`` still unrotated)."""
     q = _operand(query._data)
     b, hq, qlen, dim = q.shape
     code = _dtype_code(q.dtype)
@@ -304,12 +322,23 @@ def decode_int8_cache(query: Tensor, cache, *, is_causal: bool, causal_offset: i
     lib = _lib.load()
     nbytes = lib.tsattn_decode_workspace(ctypes.byref(prob), 0)
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
-    _lib.check(
-        lib.tsattn_decode_forward_int8(
-            ctypes.byref(prob), _view(q), _view(keys), _view(values), _view(key_scales),
-            _view(value_scales), _view(out), 0, ctypes.c_void_p(ws.data_ptr()), nbytes,
-            ctypes.c_void_p(current_stream(query.device))),
-        "int8 decode forward")
+    stream = ctypes.c_void_p(current_stream(query.device))
+    args = (_view(keys), _view(values), _view(key_scales), _view(value_scales), _view(out), 0,
+            ctypes.c_void_p(ws.data_ptr()), nbytes, stream)
+    if rope is not None:
+        q_pos0, base = rope
+        tables = rope_tables(base, dim, q.dtype, q.device, q_pos0 + qlen)
+        desc = _lib.RopeDesc()
+        desc.cos, desc.sin = tables[0].data_ptr(), tables[1].data_ptr()
+        desc.rotary_dim, desc.q_pos0, desc.k_pos0 = dim, q_pos0, 0
+        try:
+            _lib.check(lib.tsattn_decode_forward_rope(ctypes.byref(prob), ctypes.byref(desc),
+                                                      _view(q), *args), "int8 decode forward")
+            return Tensor._from_op(out, (query,), None, "sdpa_hip")
+        except NotImplementedError:  # rotate the queries on their own
+            q = _rope_rows(q, q_pos0, base, dim, False, query.device)
+    _lib.check(lib.tsattn_decode_forward_int8(ctypes.byref(prob), _view(q), *args),
+               "int8 decode forward")
     return Tensor._from_op(out, (query,), None, "sdpa_hip")
 
 

@@ -102,8 +102,9 @@ class MultiHeadAttention(Module):
             # the attention kernels rotate the queries (and the gradients) themselves
             rope = (offset, offset if context is None else 0, 10000.0)
         elif self.rotary:
-            q = rotary_embedding(q, offset)
-            # rotate the new keys and write them (and the values) into the cache in one kernel
+            # the decode kernel rotates the queries; the new keys are rotated and
+            # written (with the values) into the cache in one kernel
+            rope = (offset, None, 10000.0)
             fused = cache._append_rotary(k, v)
             if not fused:
                 k = rotary_embedding(k, offset)
@@ -113,7 +114,8 @@ class MultiHeadAttention(Module):
                 cache._append(k, v)
             if cache.quantized and attn_mask is None:
                 # decode straight over the int8 storage (dequantised in the kernel)
-                attended = decode_int8_cache(q, cache, is_causal=is_causal, causal_offset=offset)
+                attended = decode_int8_cache(q, cache, is_causal=is_causal, causal_offset=offset,
+                                             rope=rope and (offset, 10000.0))
             if attended is None:
                 k, v = cache.get()
         if attended is None:

@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 5
+#define TSATTN_ABI_VERSION 6
 
 typedef enum {
   TSATTN_OK = 0,
@@ -239,6 +239,23 @@ int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, co
                                const tsattn_view *v, const tsattn_view *k_scale,
                                const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,
                                void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * KV-cache decode with RoPE folded into the query load: q is the unrotated
+ * query (row i at position rope->q_pos0 + i); the cache holds keys rotated
+ * when they were appended (tsattn_rope_append), so rope->k_pos0 is not used.
+ * Bit-identical to tsattn_rope on q followed by tsattn_decode_forward (or
+ * tsattn_decode_forward_int8 when k_scale / v_scale are given: pass both or
+ * neither).  Replaces the query half of MultiHeadAttention's rotary step on
+ * the cached path (src/tensorsmith/nn/transformer.py:139-141, rotary at
+ * src/tensorsmith/nn/attention.py:255-294) ahead of the decode attention.
+ * Same table and rotary-dim rules as tsattn_sdpa_forward_rope.
+ */
+int tsattn_decode_forward_rope(const tsattn_problem *p, const tsattn_rope_desc *rope,
+                               const tsattn_view *q, const tsattn_view *k, const tsattn_view *v,
+                               const tsattn_view *k_scale, const tsattn_view *v_scale,
+                               const tsattn_view *out, int32_t split_len, void *workspace,
+                               size_t workspace_bytes, void *stream);
 
 /*
  * KV-cache append into the int8 format (KVCache.append with quantized=True,

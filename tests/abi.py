@@ -109,6 +109,24 @@ def decode(q, k, v, split_len=0, **kw):
     return out
 
 
+def decode_rope(q, k, v, desc, ks=None, vs=None, split_len=0, **kw):
+    """tsattn_decode_forward_rope: q unrotated, the cache rows rotated; int8
+    caches pass their row scales ks / vs (len_kv in kw then)."""
+    len_kv = kw.pop("len_kv", None)
+    p = problem(q, k, v, **kw)
+    if len_kv is not None:
+        p.len_kv = len_kv
+    out = torch.empty(q.shape[:3] + (v.shape[3],), dtype=q.dtype, device=q.device)
+    lib = _lib.load()
+    nbytes = lib.tsattn_decode_workspace(ctypes.byref(p), split_len)
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=q.device)
+    _lib.check(lib.tsattn_decode_forward_rope(
+        ctypes.byref(p), ctypes.byref(desc), view(q), view(k), view(v),
+        None if ks is None else view(ks), None if vs is None else view(vs), view(out), split_len,
+        ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "decode rope")
+    return out
+
+
 def key_lengths(mask: torch.Tensor):
     """kv_len / kv_prefix of a bool key mask [B, K] via tsattn_key_mask_lengths."""
     b, kl = mask.shape

@@ -152,6 +152,8 @@ def test_lm_with_int8_cache_decodes_through_the_int8_kernel():
     assert probes["decode_split_int8"][0] == 4 * cfg.num_layers
     # one fused RoPE + quantising append (K and V) per layer and step
     assert probes["rope_append_int8"][0] == 4 * cfg.num_layers and "kv_append_int8" not in probes
+    # the decode kernel rotates the queries itself: no separate RoPE launch
+    assert "rope" not in probes and "rope" not in probes_ref
     assert "decode_split_int8" not in probes_ref and "decode_split" in probes_ref
     assert rel_l2(got, want) <= 5e-3
     assert np.abs(got - want).max() <= 5e-3 * np.abs(want).max()

@@ -236,6 +236,45 @@ def test_rope_folded_into_attention_is_bitwise_the_unfused_chain(case):
         assert torch.equal(a_, b_), name
 
 
+DECODE_CASES = [
+    # (dtype, B, Hq, Hkv, Sq, cached keys L, D, rotary dim, int8 cache)
+    ("float16", 4, 8, 2, 1, 700, 128, 128, False),
+    ("bfloat16", 2, 4, 4, 2, 300, 64, 32, False),   # two new rows, partial rotary dim
+    ("float16", 2, 4, 1, 1, 1000, 256, 128, False),  # D = 256, half of it rotated
+    ("bfloat16", 3, 8, 2, 1, 513, 128, 128, True),
+    ("float16", 2, 2, 2, 4, 260, 64, 64, True),
+]
+
+
+@pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: "-".join(map(str, c)))
+def test_decode_with_folded_rope_is_bitwise_the_two_step_path(case):
+    """tsattn_decode_forward_rope == tsattn_rope on q, then the decode kernel."""
+    dtype, b, hq, hkv, sq, klen, d, r, q8 = case
+    say(f"decode folded rope {case}")
+    rng = np.random.default_rng(klen + d)
+    q0 = klen - sq  # the new rows' positions: the last sq of the cache
+    q = abi.dev_tensor(rows(rng, (b, hq, sq, d), dtype, 0.7), dtype)
+    k, v = (abi.dev_tensor(rows(rng, (b, hkv, klen, d), dtype, 0.7), dtype) for _ in range(2))
+    cos, sin = tables(klen + 1, r, dtype)
+    desc = abi.rope_desc(cos, sin, r, q0, 0)
+    q_rot = _rot(q, cos, sin, q0, r, False)
+    kw = dict(causal=True, offset=q0)
+    if q8:
+        codes = [torch.zeros((b, hkv, klen, d), dtype=torch.int8, device="cuda") for _ in range(2)]
+        scales = [torch.ones((b, hkv, klen, 1), dtype=torch.float32, device="cuda") for _ in range(2)]
+        abi.kv_append_int8(k, codes[0], scales[0], 0)
+        abi.kv_append_int8(v, codes[1], scales[1], 0)
+        want, path = abi.decode_int8(q_rot, codes[0], codes[1], scales[0], scales[1], klen, **kw)
+        got = abi.decode_rope(q, codes[0], codes[1], desc, ks=scales[0], vs=scales[1],
+                              len_kv=klen, **kw)
+    else:
+        want = abi.decode(q_rot, k, v, **kw)
+        got = abi.decode_rope(q, k, v, desc, **kw)
+    torch.cuda.synchronize()
+    assert _lib.load().tsattn_last_kernel_path() == _lib.PATH_DECODE
+    assert torch.equal(got, want)
+
+
 def _rot(x, cos, sin, pos, r, inverse):
     out = torch.empty_like(x)
     abi.rope(x, out, cos, sin, pos, r, inverse)

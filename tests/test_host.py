@@ -104,6 +104,34 @@ def test_abi_rejects_null_views_and_small_workspace():
     assert lib.tsattn_key_mask_lengths(None, 1, 1, 1, 1, None, None, None) == _lib.ERR_INVALID
 
 
+def test_decode_rope_argument_checks_without_launching():
+    """tsattn_decode_forward_rope: descriptor and scale-pair rules, checked
+    before anything touches device memory."""
+    lib = _lib.load()
+    p = _problem(dtype=_lib.F16, len_q=1, len_kv=64, dim_qk=64, dim_v=64)
+    v = _lib.View()
+    v.data = 64  # never dereferenced: validation fails first
+    v.stride[3] = 1
+    ws = ctypes.c_void_p(64)
+    args = (v, v, v)
+    assert lib.tsattn_decode_forward_rope(ctypes.byref(p), None, *args, None, None, v, 0, ws,
+                                          1 << 20, None) == _lib.ERR_INVALID
+    assert "RoPE descriptor" in _lib.last_error()
+    d = _lib.RopeDesc()
+    d.cos = d.sin = 64
+    d.rotary_dim, d.q_pos0 = 64, 0
+    assert lib.tsattn_decode_forward_rope(ctypes.byref(p), ctypes.byref(d), *args, v, None, v, 0,
+                                          ws, 1 << 20, None) == _lib.ERR_INVALID
+    assert "both" in _lib.last_error()
+    d.rotary_dim = 36  # even, but not a whole number of 16-byte chunks
+    assert lib.tsattn_decode_forward_rope(ctypes.byref(p), ctypes.byref(d), *args, None, None, v,
+                                          0, ws, 1 << 20, None) == _lib.ERR_UNSUPPORTED
+    assert "divisible by 8" in _lib.last_error()
+    d.rotary_dim = 66  # past the head dim
+    assert lib.tsattn_decode_forward_rope(ctypes.byref(p), ctypes.byref(d), *args, None, None, v,
+                                          0, ws, 1 << 20, None) == _lib.ERR_INVALID
+
+
 def test_reference_argument_checks_before_device():
     """The reference's refusals (attention.py:36-62), same exception types."""
     q = ts.tensor(np.zeros((1, 2, 3, 4), np.float32))
