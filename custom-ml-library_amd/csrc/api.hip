@@ -103,6 +103,9 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
     q.drop.k1 = p->dropout_key[1];
     q.drop.c0 = p->dropout_counter + 1;
     q.drop.c1 = q.drop.c0 == 0 ? 1 : 0;
+    q.drop.bits = p->dropout_bits;
+    q.drop.nkt = (q.Sk + 31) / 32;
+    q.drop.sqp = (q.Sq + 3) / 4 * 4;
   }
   *out = q;
   return TSATTN_OK;
@@ -164,20 +167,43 @@ int sdpa_forward(const tsattn_problem *p, const tsattn_rope_desc *rope, const ts
   }
   if (rope) return rope_unsupported();
   g_last_path = 1;
-  return hip_status(tsattn::launch_generic_forward(pr, p->dtype, vq, vk, vv, vo, lse, st),
-                    "generic forward launch");
+  rc = hip_status(tsattn::launch_generic_forward(pr, p->dtype, vq, vk, vv, vo, lse, st),
+                  "generic forward launch");
+  // the generic kernels draw their keep bits on the fly: write them out too
+  if (!rc && pr.drop.on && pr.drop.bits)
+    rc = hip_status(tsattn::launch_dropout_bits(pr, pr.drop.bits, st), "dropout bits launch");
+  return rc;
 }
 
-size_t backward_workspace(const tsattn_problem *p) {
+size_t round256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Row deltas, then (MFMA path) the row LSE terms.
+size_t rows_workspace(const tsattn_problem *p) {
   if (!p || p->batch <= 0 || p->heads_q <= 0 || p->len_q <= 0) return 0;
-  // row deltas, then (MFMA path) the row LSE in log2 units
   return 2 * static_cast<size_t>(p->batch) * p->heads_q * p->len_q * acc_size(p->dtype);
 }
 
 // Row values (as above), then the rotated query rows the dK/dV kernel reads.
-size_t rope_backward_workspace(const tsattn::Problem &pr) {
+size_t rope_rows_workspace(const tsattn::Problem &pr) {
   return tsattn::mfma_rope_stage_offset(pr) +
          static_cast<size_t>(pr.B) * pr.Hq * pr.Sq * pr.Dqk * 2;
+}
+
+// When dropping, room after those for the keep bits the MFMA backward draws
+// when the problem brings none from its forward.
+size_t with_bits(size_t base, const tsattn::Problem &pr) {
+  return pr.drop.on ? round256(base) + tsattn::dropout_bits_bytes(pr) : base;
+}
+
+size_t backward_workspace(const tsattn_problem *p) {
+  const size_t base = rows_workspace(p);
+  tsattn::Problem pr;
+  if (!base || !(p->dropout_p > 0.0) || check_problem(p, &pr)) return base;
+  return with_bits(base, pr);
+}
+
+size_t rope_backward_workspace(const tsattn::Problem &pr) {
+  return with_bits(rope_rows_workspace(pr), pr);
 }
 
 int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const tsattn_view *q,
@@ -195,10 +221,10 @@ int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const t
     return rc;
   if (!lse) return fail(TSATTN_ERR_INVALID, "backward needs the saved LSE");
   if (rope && (rc = check_rope(rope, pr, &pr.rope))) return rc;
-  const size_t need = rope ? rope_backward_workspace(pr) : backward_workspace(p);
-  if (!workspace || workspace_bytes < need)
+  const size_t rows_need = rope ? rope_rows_workspace(pr) : rows_workspace(p);
+  if (!workspace || workspace_bytes < rows_need)
     return fail(TSATTN_ERR_INVALID, "backward workspace too small: %zu < %zu bytes",
-                workspace_bytes, need);
+                workspace_bytes, rows_need);
   hipStream_t st = static_cast<hipStream_t>(stream);
   tsattn::View vq = tsattn::make_view(q), vk = tsattn::make_view(k), vv = tsattn::make_view(v),
                vo = tsattn::make_view(out), vg = tsattn::make_view(dout),
@@ -208,6 +234,17 @@ int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const t
       mfma_view_ok(vk, pr.Sk) && mfma_view_ok(vv, pr.Sk) && mfma_view_ok(vo, pr.Sq) &&
       mfma_view_ok(vg, pr.Sq) && mfma_view_ok(vdq, pr.Sq) && mfma_view_ok(vdk, pr.Sk) &&
       mfma_view_ok(vdv, pr.Sk)) {
+    if (pr.drop.on && !pr.drop.bits) {
+      // no bits from the forward: draw them into the workspace, after the rows
+      const size_t need = with_bits(rows_need, pr);
+      if (workspace_bytes < need)
+        return fail(TSATTN_ERR_INVALID,
+                    "backward workspace too small for the dropout bits: %zu < %zu bytes",
+                    workspace_bytes, need);
+      pr.drop.bits = reinterpret_cast<uint32_t *>(static_cast<char *>(workspace) + round256(rows_need));
+      if ((rc = hip_status(tsattn::launch_dropout_bits(pr, pr.drop.bits, st), "dropout bits launch")))
+        return rc;
+    }
     g_last_path = 2;
     return hip_status(tsattn::launch_mfma_backward(pr, p->dtype, vq, vk, vv, vo, vg,
                                                    static_cast<const float *>(lse), vdq, vdk,
@@ -330,6 +367,12 @@ int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *r
   if (!rope) return fail(TSATTN_ERR_INVALID, "RoPE descriptor is NULL");
   return sdpa_backward(p, rope, q, k, v, out, dout, lse, dq, dk, dv, workspace, workspace_bytes,
                        stream);
+}
+
+size_t tsattn_dropout_bits_bytes(const tsattn_problem *p) {
+  tsattn::Problem pr;
+  if (check_problem(p, &pr)) return 0;
+  return tsattn::dropout_bits_bytes(pr);
 }
 
 int tsattn_dropout_keep(const tsattn_problem *p, uint8_t *out, void *stream) {

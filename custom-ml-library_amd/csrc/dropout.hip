@@ -1,7 +1,7 @@
-// The dropout keep mask of an attention problem, materialised: the mask the
-// MFMA kernels regenerate on the fly (philox.h), written out as bytes so it
-// can be inspected and checked against numpy.random.Philox on the host.
-// One thread per 16-word block of a query row.
+// The dropout keep mask of an attention problem, materialised: as bytes (one
+// thread per 16-word block of a query row), so it can be inspected and
+// checked against numpy.random.Philox on the host, and as the bits the MFMA
+// backward reads (philox.h draws the words).
 #include "philox.h"
 
 namespace tsattn {
@@ -26,7 +26,45 @@ __global__ __launch_bounds__(NT) void dropout_keep_kernel(Problem p, uint8_t *ou
   }
 }
 
+// The keep bits (DropDesc::bits layout), one thread per 32-bit word: the
+// word of row i and keys 32 t .. + 31 from two 16-word blocks.  Padding rows
+// (i >= Sq) and keys past Sk hold zeros.
+__global__ __launch_bounds__(NT) void dropout_bits_kernel(Problem p, uint32_t *out) {
+  const DropDesc &d = p.drop;
+  const int64_t words = static_cast<int64_t>(p.B) * p.Hq * d.nkt * d.sqp;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
+  if (idx >= words) return;
+  const int64_t line = idx / d.sqp;  // (b Hq + h) nkt + t
+  const int i = static_cast<int>(idx - line * d.sqp);
+  const int64_t bh = line / d.nkt;
+  const int t = static_cast<int>(line - bh * d.nkt);
+  uint32_t bits = 0;
+  if (i < p.Sq) {
+    const int64_t row = bh * p.Sq + i;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int j16 = 32 * t + 16 * half;
+      if (j16 >= p.Sk) break;
+      uint64_t w[4];
+      dropout_block(d, dropout_block_index(p, row, j16), w);
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const uint32_t word = static_cast<uint32_t>(w[m >> 2] >> (16 * (m & 3))) & 0xFFFFu;
+        if (j16 + m < p.Sk && word >= d.thr) bits |= 1u << (16 * half + m);
+      }
+    }
+  }
+  out[idx] = bits;
+}
+
 }  // namespace
+
+hipError_t launch_dropout_bits(const Problem &p, uint32_t *out, hipStream_t st) {
+  const int64_t words = static_cast<int64_t>(p.B) * p.Hq * p.drop.nkt * p.drop.sqp;
+  Probe pr_("dropout_bits", st);
+  dropout_bits_kernel<<<dim3(static_cast<unsigned>((words + NT - 1) / NT)), NT, 0, st>>>(p, out);
+  return hipGetLastError();
+}
 
 hipError_t launch_dropout_keep(const Problem &p, uint8_t *out, hipStream_t st) {
   const int64_t threads = static_cast<int64_t>(p.B) * p.Hq * p.Sq * ((p.Sk + 15) / 16);

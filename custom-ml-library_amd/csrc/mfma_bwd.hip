@@ -13,10 +13,13 @@
 // Tiles reach LDS by direct buffer loads into swizzled row-major layouts;
 // transposed operands (Q^T, dO^T, K^T) come from LDS transpose reads.
 //
-// Dropout (template DR): the mask is regenerated from the problem's Philox
-// stream (philox.h) in both kernels: dV = (P * mask)^T dO and
-// dS = P (dP * mask - delta) (attention.py:210-217; delta = rowsum(dO O)
-// already holds the mask through O).
+// Dropout (template DR): both kernels read the keep mask as bits (one 32-bit
+// word per query row and 32-key tile, DropDesc::bits) -- the forward's, or
+// drawn from the problem's Philox stream by dropout_bits_kernel first:
+// dV = (P * mask)^T dO and dS = P (dP * mask - delta) (attention.py:210-217;
+// delta = rowsum(dO O) already holds the mask through O).  The dQ kernel
+// fetches its row's word with each key tile, the dK/dV kernel stages the 32
+// words of its key tile through the LDS ring with the Q / dO tiles.
 //
 // RoPE (Problem::rope, R > 0): the dQ prologue rotates the query fragments
 // as the forward did; the dQ and dK epilogues apply the inverse rotation to
@@ -29,7 +32,6 @@
 #include <type_traits>
 
 #include "mfma_common.h"
-#include "philox.h"
 #include "rope_math.h"
 
 namespace tsattn {
@@ -108,8 +110,10 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   constexpr int MROW = KB * MES, MTILE = QT * MROW;  // bytes per mask row / tile
   constexpr int MPARTS = MTILE / 1024 / NW;          // mask DMA loads per wave per tile
   constexpr int MOFF = TILE_Q + TILE_G + 256;
-  // Q | dO | nl (QT floats) | nd (QT floats) | mask tile
-  constexpr int STAGE_B = TILE_Q + TILE_G + 256 + MTILE;
+  // Dropout: each wave's 32 keep-bit words (rows q0 .. q0 + 31 of its key tile)
+  constexpr int BOFF = MOFF + MTILE, BSZ = DR ? NW * 128 : 0;
+  // Q | dO | nl (QT floats) | nd (QT floats) | mask tile | keep bits
+  constexpr int STAGE_B = TILE_Q + TILE_G + 256 + MTILE + BSZ;
   constexpr int QPARTS = TILE_Q / 1024 / NW, GPARTS = TILE_G / 1024 / NW;
   constexpr int LPT = QPARTS + GPARTS;            // Q + dO DMA loads per wave per tile
   constexpr int SKQ = DK / 16, SKV = DV / 16;     // k-steps of S (over DK) and dP (over DV)
@@ -121,8 +125,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
                 GPARTS * NW * 1024 == TILE_G, "tile loads must split evenly over the waves");
   static_assert(2 * LPT <= STEPS, "one tile DMA part per two MFMA steps");
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
-  // Q / dO ring; with dropout each wave's 32 x 32 tile of dropout words after it
-  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B + (DR ? NW * 2048 : 0)];
+  // Q / dO ring
+  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -235,15 +239,32 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       }
     }
   };
+  // Dropout: this wave's 32 keep-bit words (key tile kb * 4 + w, rows q0 ..
+  // q0 + 31) as one 8-lane DMA part; past the slice they read as zero.
+  auto issue_bits = [&](const TileDma &t) {
+    if constexpr (DR) {
+      const DropDesc &d = p.drop;
+      const u32x4 bdesc = make_desc(d.bits + (static_cast<int64_t>(b) * p.Hq + t.hq) * d.nkt * d.sqp,
+                                    static_cast<uint32_t>(d.nkt * d.sqp * 4));
+      uint32_t loff;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(loff));
+      if (lane < 8)
+        dma16(bdesc, t.st + BOFF + w * 128, loff,
+              (static_cast<uint32_t>(kb * (KB / 32) + w) * d.sqp + t.q0) * 4);
+    }
+  };
   auto issue = [&](int itn) {
     const TileDma t = tile_dma(itn);
 #pragma unroll
     for (int u = 0; u <= LPT; ++u) issue_part(t, u);
     issue_mask(t);
+    issue_bits(t);
   };
   // DMA loads this wave may leave in flight once tile itn has landed: those
   // of the later tiles already issued.
-  const int parts = LPT + (w < 2 ? 1 : 0) + MPARTS;
+  const int parts = LPT + (w < 2 ? 1 : 0) + MPARTS + (DR ? 1 : 0);
   auto in_flight_after = [&](int itn) {
     const int later = min(KV_PD - 1, n_iter - 1 - itn);
     return later > 0 ? later * parts : 0;
@@ -343,6 +364,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         if (prefetch && i == 0) {
           issue_part(nxt, LPT);
           issue_mask(nxt);
+          issue_bits(nxt);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -357,20 +379,10 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       if (causal) lo = min(64, max(-64, kdiff - q0 - 4 * h));
     }
     u32x4 pp[2], pd[2];
-    // Dropout: lane (c, h) draws the 16 words of row q0 + c, keys kw + 16 h ..,
-    // into the wave's 32 x 32 word tile in LDS; lane (c, h) then reads its key
-    // c at rows 8 g + 4 h + r.  dV takes P * mask, dS = P (dP * mask - delta).
-    const uint16_t *dtile = reinterpret_cast<const uint16_t *>(ring + KV_NS * STAGE_B + w * 2048);
-    if constexpr (DR) {
-      uint64_t blk[4];
-      dropout_block(p.drop,
-                    dropout_block_index(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + q0 + c,
-                                        kw + 16 * h),
-                    blk);
-      uint64_t *dst = reinterpret_cast<uint64_t *>(ring + KV_NS * STAGE_B + w * 2048 + c * 64 + h * 32);
-#pragma unroll
-      for (int m = 0; m < 4; ++m) dst[m] = blk[m];
-    }
+    // Dropout: the staged keep bits; lane (c, h) reads rows 8 g + 4 h + r
+    // (four words per g) and takes bit c.  dV takes P * mask, dS = P (dP *
+    // mask - delta).
+    const char *btile = qt + BOFF + w * 128;
     // Staged mask: this lane's column (key 32 w + c) at row 4 h of the tile.
     const char *mrow_base = nullptr;
     if constexpr (MSTAGE) {
@@ -394,6 +406,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float pv[4], dsv[4];
+        u32x4 bw{};
+        if constexpr (DR) bw = *reinterpret_cast<const u32x4 *>(btile + (8 * g + 4 * h) * 4);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int e = 4 * g + r, kc = 8 * g + r;
@@ -418,7 +432,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
             pv[r] = fast_exp2(mask_kind(MK) >= 2 ? xs[e] : xs[e] * sl);
           }
           if constexpr (DR) {
-            const bool keep = dtile[(8 * g + 4 * h + r) * 32 + c] >= p.drop.thr;
+            const bool keep = (bw[r] >> c) & 1u;
             const float nd = rv[QT + 8 * g + 4 * h + r];
             dsv[r] = pv[r] * (keep ? fmaf(dpacc[e], p.drop.scale, nd) : nd);
             pv[r] = keep ? pv[r] * p.drop.scale : 0.f;
@@ -432,7 +446,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         pd[g >> 1][(g & 1) * 2 + 1] = pack2<T>(dsv[2], dsv[3]);
         // staged masks: four LDS reads in flight at a time, not sixteen (the
         // register budget of two workgroups per CU has no room for them)
-        if constexpr (MSTAGE) __builtin_amdgcn_sched_barrier(0);
+        if constexpr (MSTAGE || DR) __builtin_amdgcn_sched_barrier(0);
       }
     };
     if (edge) grad(std::true_type{});
@@ -573,9 +587,11 @@ constexpr int DQ_NS = DQ_PD + 2;      // ring stages: tile j is read in iteratio
 template <typename T, int DK, int DV, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   constexpr int TILE_K = KT * DK * 2, TILE_V = KT * DV * 2;  // bytes per K / V tile
-  constexpr int STAGE = TILE_K + TILE_V;
+  // K | V | with dropout each wave's 32 keep-bit words (its rows, this key tile)
+  constexpr int STAGE = TILE_K + TILE_V + (DR ? NW * 128 : 0);
   constexpr int KPARTS = TILE_K / 1024 / NW, VPARTS = TILE_V / 1024 / NW;
   constexpr int LPT = KPARTS + VPARTS;        // DMA loads per wave per K+V tile
+  constexpr int PPT = LPT + (DR ? 1 : 0);     // all DMA loads per wave per tile
   constexpr int SKQ = DK / 16, SKV = DV / 16;  // k-steps of S (over DK), dP (over DV)
   constexpr int PDQ = DK / 32;                 // 32-row blocks of dQ^T (2 key k-steps each)
   constexpr int STEPS = SKQ > SKV ? SKQ : SKV;
@@ -690,13 +706,30 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
       dma16(vdesc, st + TILE_K + n * 1024, voff, static_cast<uint32_t>(tile * KT + 16 * (n / QGV)) * vs_b);
     }
   };
+  // Dropout: the wave's 32 keep-bit words of the tile as one 8-lane part
+  // (rows past the (b, hq) slice read as zero; rows past Sq are unused).
+  auto issue_bits = [&](int tile) {
+    if constexpr (DR) {
+      const DropDesc &d = p.drop;
+      const u32x4 bdesc = make_desc(d.bits + (static_cast<int64_t>(b) * p.Hq + hq) * d.nkt * d.sqp,
+                                    static_cast<uint32_t>(d.nkt * d.sqp * 4));
+      uint32_t loff;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(loff));
+      if (lane < 8)
+        dma16(bdesc, lds0 + (tile % DQ_NS) * STAGE + TILE_K + TILE_V + w * 128, loff,
+              (static_cast<uint32_t>(tile) * d.sqp + qw) * 4);
+    }
+  };
   auto issue = [&](int tile) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) issue_part(tile, u);
+    issue_bits(tile);
   };
   auto in_flight_after = [&](int jn) {
     const int later = min(DQ_PD - 1, n_tiles - 1 - jn);
-    return later > 0 ? later * LPT : 0;
+    return later > 0 ? later * PPT : 0;
   };
 
   const TileReader<T, DK> rdk(lane);
@@ -764,6 +797,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     };
     s = f32x16{};
     dp = f32x16{};
+    if (nt >= 0) issue_bits(nt);
 #pragma unroll
     for (int i = 0; i < FD; ++i) load(i);
     __builtin_amdgcn_sched_barrier(0);
@@ -811,18 +845,20 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim_l, sl);
       }
     }
-    // Dropout: dS = P (dP * mask - delta) (attention.py:215-217).
-    uint64_t dw[4];
+    // Dropout: dS = P (dP * mask - delta) (attention.py:215-217), the mask
+    // from row qrow's keep-bit word of the tile, staged with it.
+    uint32_t kbits = 0;
     if constexpr (DR)
-      dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
+      kbits = *reinterpret_cast<const uint32_t *>(lds + (j % DQ_NS) * STAGE + TILE_K + TILE_V +
+                                                  w * 128 + c * 4);
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       const float p0 = fast_exp2(fmaf(x[i], slx, lse2));
       const float p1 = fast_exp2(fmaf(x[i + 1], slx, lse2));
       float d0 = dp[i], d1 = dp[i + 1];
       if constexpr (DR) {
-        d0 = dropout_keeps(p.drop, dw, i) ? d0 * p.drop.scale : 0.f;
-        d1 = dropout_keeps(p.drop, dw, i + 1) ? d1 * p.drop.scale : 0.f;
+        d0 = (kbits >> (8 * (i >> 2) + 4 * h + (i & 3))) & 1u ? d0 * p.drop.scale : 0.f;
+        d1 = (kbits >> (8 * (i >> 2) + 4 * h + (i & 3) + 1)) & 1u ? d1 * p.drop.scale : 0.f;
       }
       pd[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * (d0 + delta), p1 * (d1 + delta));
     }

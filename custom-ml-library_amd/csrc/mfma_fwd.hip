@@ -31,8 +31,10 @@
 // and most tiles skip the rescale.  O / l and the LSE are exact for any m.
 //
 // Dropout (template DR): the probabilities fed to PV are multiplied by the
-// keep mask the problem's Philox stream gives (philox.h) -- regenerated, not
-// stored -- while the softmax denominator sums the undropped ones.
+// keep mask the problem's Philox stream gives (philox.h), while the softmax
+// denominator sums the undropped ones; with DropDesc::bits set the kernel
+// also writes the mask as bits (one word per row and 32-key tile it
+// computes) for the backward.
 //
 // RoPE (Problem::rope, R > 0): the prologue rotates the query fragments it
 // loads (the keys come rotated), bit-identical to a separate tsattn_rope.
@@ -305,8 +307,20 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     // Dropout: the denominator sums the undropped probabilities (the
     // reference normalises first, attention.py:139-144); PV takes P * mask.
     uint64_t dw[4];
-    if constexpr (DR)
+    if constexpr (DR) {
       dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
+      // keep bits for the backward: lane half h holds keys 8 g + 4 h + r
+      if (p.drop.bits) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          bits |= (dropout_keeps(p.drop, dw, i) ? 1u : 0u) << (8 * (i >> 2) + 4 * h + (i & 3));
+        bits |= __shfl_xor(bits, 32, 64);
+        if (h == 0 && qrow < p.Sq)
+          p.drop.bits[((static_cast<int64_t>(b) * p.Hq + hq) * p.drop.nkt + kv0 / BN) * p.drop.sqp +
+                      qrow] = bits;
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
       float p0 = fast_exp2(fmaf(x[i], slx, -base));

@@ -85,6 +85,11 @@ struct DropDesc {
   float scale;
   double scale64;
   uint64_t k0, k1, c0, c1;
+  // keep bits (tsattn_problem.dropout_bits layout): word ((b Hq + h) nkt + t)
+  // sqp + i holds keys 32 t .. 32 t + 31 of row i; nkt = ceil(Sk / 32),
+  // sqp = Sq rounded up to 4
+  uint32_t *bits;
+  int nkt, sqp;
 };
 
 struct Problem {
@@ -200,6 +205,13 @@ hipError_t launch_rope_append(int dtype, int B, int H, int T, int D, int R, View
 
 // The dropout keep mask of problem p as a contiguous [B, Hq, Sq, Sk] uint8 array.
 hipError_t launch_dropout_keep(const Problem &p, uint8_t *out, hipStream_t st);
+// The keep bits of the problem's dropout stream into `out` (DropDesc::bits
+// layout, dropout_bits_bytes long).
+hipError_t launch_dropout_bits(const Problem &p, uint32_t *out, hipStream_t st);
+inline size_t dropout_bits_bytes(const Problem &p) {
+  return static_cast<size_t>(p.B) * p.Hq * ((p.Sk + 31) / 32) * ((p.Sq + 3) / 4 * 4) *
+         sizeof(uint32_t);
+}
 
 hipError_t launch_key_mask_lengths(const uint8_t *mask, int64_t sb, int64_t sk, int B, int K,
                                    int32_t *kv_len, int32_t *kv_prefix, hipStream_t st);

@@ -16,7 +16,7 @@ from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_native" / "libtsattn.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, F16, BF16, F64, BOOL, I8 = 0, 1, 2, 3, 4, 5
@@ -53,6 +53,7 @@ class Problem(ctypes.Structure):
         ("dropout_p", c_double),
         ("dropout_key", ctypes.c_uint64 * 2),
         ("dropout_counter", ctypes.c_uint64),
+        ("dropout_bits", ctypes.c_void_p),
     ]
 
 
@@ -87,6 +88,7 @@ SIGNATURES = {
     "tsattn_sdpa_forward_rope": (c_int, [_PP, _PR, _PV, _PV, _PV, _PV, c_void_p, c_void_p]),
     "tsattn_sdpa_backward_rope_workspace": (c_size_t, [_PP]),
     "tsattn_dropout_keep": (c_int, [_PP, c_void_p, c_void_p]),
+    "tsattn_dropout_bits_bytes": (c_size_t, [_PP]),
     "tsattn_sdpa_backward_rope": (
         c_int,
         [_PP, _PR, _PV, _PV, _PV, _PV, _PV, c_void_p, _PV, _PV, _PV, c_void_p, c_size_t,

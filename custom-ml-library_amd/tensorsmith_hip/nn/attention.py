@@ -242,6 +242,12 @@ def scaled_dot_product_attention(
     if recording:
         lse_dtype = torch.float64 if code == _lib.F64 else torch.float32
         lse = torch.empty((b, hq, qlen), dtype=lse_dtype, device=tdev)
+        if dropout_p:
+            # the forward writes its keep mask as bits; the backward reads them
+            bits = torch.empty(lib.tsattn_dropout_bits_bytes(ctypes.byref(prob)), dtype=torch.uint8,
+                               device=tdev)
+            prob.dropout_bits = bits.data_ptr()
+            keep.append(bits)
     lse_ptr = ctypes.c_void_p(None if lse is None else lse.data_ptr())
     fused = False
     if rope is not None and k_pos0 is None:

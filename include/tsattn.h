@@ -30,7 +30,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 6
+#define TSATTN_ABI_VERSION 7
 
 typedef enum {
   TSATTN_OK = 0,
@@ -87,11 +87,21 @@ typedef struct tsattn_problem {
    * numpy.random.Philox(key = key[0] + 2^64 key[1], counter = counter)
    * viewed as little-endian uint16, and is kept iff word >= round(65536 p);
    * kept probabilities scale by float32(1) / float32(1 - p).  The backward
-   * regenerates the same mask from the same key and counter.
+   * uses the same mask: from `dropout_bits`, or regenerated from the same key
+   * and counter.
    */
   double dropout_p;
   uint64_t dropout_key[2];
   uint64_t dropout_counter;
+  /*
+   * Optional device buffer (tsattn_dropout_bits_bytes) of the keep decisions
+   * as bits: word ((b Hq + h) ceil(Sk / 32) + t) round_up(Sq, 4) + i, bit j =
+   * element (b, h, i, 32 t + j).  A dropping forward fills it; the backward
+   * then reads it instead of drawing the stream again (pass the buffer its
+   * forward filled, or NULL: the backward then draws the bits into its
+   * workspace first).
+   */
+  uint32_t *dropout_bits;
 } tsattn_problem;
 
 /* ABI version of the loaded library (== TSATTN_ABI_VERSION). */
@@ -207,6 +217,11 @@ int tsattn_sdpa_backward_rope(const tsattn_problem *p, const tsattn_rope_desc *r
  * kernels regenerate, for inspection and tests.
  */
 int tsattn_dropout_keep(const tsattn_problem *p, uint8_t *out, void *stream);
+
+/* Bytes of tsattn_problem.dropout_bits for this problem (B Hq ceil(Sk / 32)
+ * round_up(Sq, 4) 32-bit words); no counterpart in the reference, whose
+ * dense backend keeps its mask as an array (attention.py:141-143). */
+size_t tsattn_dropout_bits_bytes(const tsattn_problem *p);
 
 /* Bytes of scratch tsattn_decode_forward needs for `split_len` keys per split. */
 size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);

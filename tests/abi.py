@@ -44,7 +44,7 @@ def stream():
 
 
 def problem(q, k, v, *, causal=False, offset=0, scale=None, mask=None, kv_len=None,
-            kv_prefix=None, dropout=None):
+            kv_prefix=None, dropout=None, dropout_bits=None):
     b, hq, sq, d = q.shape
     p = _lib.Problem()
     p.dtype = CODES[q.dtype]
@@ -61,6 +61,8 @@ def problem(q, k, v, *, causal=False, offset=0, scale=None, mask=None, kv_len=No
         p.dropout_key[0] = dropout[1] & (2**64 - 1)
         p.dropout_key[1] = dropout[1] >> 64
         p.dropout_counter = dropout[2]
+    if dropout_bits is not None:  # device buffer of tsattn_dropout_bits_bytes
+        p.dropout_bits = dropout_bits.data_ptr()
     if mask is not None:
         m = torch.broadcast_to(mask, (b, hq, sq, k.shape[2]))
         if m.dtype == torch.bool:
@@ -222,6 +224,17 @@ def backward_rope(q, k, v, out, g, lse, desc, **kw):
         ctypes.c_void_p(lse.data_ptr()), view(dq), view(dk), view(dv),
         ctypes.c_void_p(ws.data_ptr()), nbytes, stream()), "backward rope")
     return dq, dk, dv
+
+
+def dropout_bits_buffer(q, k, v, **kw):
+    """A device buffer of tsattn_dropout_bits_bytes for the problem, as int32
+    words [B, Hq, ceil(Sk / 32), round_up(Sq, 4)]."""
+    p = problem(q, k, v, **kw)
+    nbytes = _lib.load().tsattn_dropout_bits_bytes(ctypes.byref(p))
+    b, hq, sq = q.shape[:3]
+    nkt, sqp = -(-k.shape[2] // 32), -(-sq // 4) * 4
+    assert nbytes == b * hq * nkt * sqp * 4
+    return torch.full((b, hq, nkt, sqp), -1, dtype=torch.int32, device=q.device)
 
 
 def dropout_keep(q, k, v, **kw):

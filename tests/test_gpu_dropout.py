@@ -17,6 +17,10 @@ numpy.random.Philox).  Checked here:
 * the generic kernels (fp32 / fp64 / other head dims) drop with the same
   mask, at the reference's fp32 cross-backend bound (rtol 1e-4, atol 3e-5,
   tests/test_transformer.py:92) and 1e-10 for fp64;
+* the keep bits a dropping forward writes for its backward (the MFMA forward
+  for every tile it computes, the generic path for all) are that mask
+  packed; a backward that gets no bits draws the same ones into its
+  workspace, and both give the same gradients bit for bit;
 * the same key and counter reproduce every output bit; another key changes
   them; the mirror drops on backend "hip" / "dense" / "auto" and raises the
   reference's ValueError on "streaming" (tests/test_transformer.py:164-171).
@@ -72,6 +76,28 @@ def test_keep_mask_is_the_oracles(shape, key, counter, p):
     np.testing.assert_array_equal(got, want)
 
 
+def packed_bits(keep):
+    """The tsattn_problem.dropout_bits words of a [B, H, Sq, Sk] keep mask:
+    [B, H, ceil(Sk / 32), round_up(Sq, 4)] int32, bit j = key 32 t + j."""
+    b, h, sq, sk = keep.shape
+    nkt, sqp = -(-sk // 32), -(-sq // 4) * 4
+    padded = np.zeros((b, h, sqp, nkt * 32), dtype=np.uint64)
+    padded[:, :, :sq, :sk] = keep
+    tiles = padded.reshape(b, h, sqp, nkt, 32)
+    words = (tiles << np.arange(32, dtype=np.uint64)).sum(axis=-1)
+    return words.astype(np.uint32).view(np.int32).transpose(0, 1, 3, 2)
+
+
+def key_bits_valid(sk):
+    """Per key tile, the bits of keys below Sk."""
+    nkt = -(-sk // 32)
+    valid = np.zeros(nkt, dtype=np.uint64)
+    for t in range(nkt):
+        n = min(32, sk - 32 * t)
+        valid[t] = (1 << n) - 1
+    return valid.astype(np.uint32).view(np.int32)
+
+
 CASES = [
     # (dtype, B, Hq, Hkv, Sq, Sk, D, causal, offset, p, masked); D may be (Dqk, Dv)
     ("bfloat16", 2, 2, 2, 130, 130, 128, True, 0, 0.2, False),
@@ -97,13 +123,36 @@ def test_dropout_attention_matches_oracle(case):
     q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
     kw = dict(causal=causal, offset=off, dropout=(p, key, counter),
               mask=None if mask is None else torch.from_numpy(mask).cuda())
-    out, lse, path = abi.forward(q, k, v, **kw)
+    bits = abi.dropout_bits_buffer(q, k, v, **kw)
+    out, lse, path = abi.forward(q, k, v, dropout_bits=bits, **kw)
     assert path == _lib.PATH_MFMA
-    dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, **kw)
+    dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, dropout_bits=bits, **kw)
+    # without the forward's bits the backward draws them itself: same gradients
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    grads_drawn = abi.backward(q, k, v, out, g, lse, **kw)[:3]
     torch.cuda.synchronize()
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert probes["dropout_bits"][0] == 1
+    for a_, b_ in zip((dq, dk, dv), grads_drawn):
+        assert torch.equal(a_, b_)
     check(abi.host(out), out_c, dtype, "o", "O")
     for got, want, name in zip((dq, dk, dv), back(inp.do), ("dQ", "dK", "dV")):
         check(abi.host(got), want, dtype, "g", name)
+    # the bits the forward wrote: the keep mask packed, on every tile a wave of
+    # 32 rows computes (keys below Sk)
+    want_bits = packed_bits(abi.dropout_keep(q, k, v, **kw).cpu().numpy())
+    got_bits = bits.cpu().numpy()
+    valid = key_bits_valid(sk)
+    for qw in range(0, sq, 32):
+        last = min(qw + 32, sq) - 1
+        wlim = min(sk, last + off + 1) if causal else sk
+        tiles = -(-wlim // 32) if wlim > 0 else 0
+        for t in range(tiles):
+            rows = slice(qw, last + 1)
+            np.testing.assert_array_equal(got_bits[:, :, t, rows] & valid[t],
+                                          want_bits[:, :, t, rows] & valid[t])
     # the same stream again: every bit; another key: different outputs
     out2, lse2, _ = abi.forward(q, k, v, **kw)
     assert torch.equal(out, out2) and torch.equal(lse, lse2)
@@ -130,10 +179,14 @@ def test_dropout_on_the_generic_kernels(case):
                                      rng_key=key, rng_counter=counter, enable_gqa=hkv != hq)
     q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
     kw = dict(causal=causal, dropout=(p, key, counter))
-    out, lse, path = abi.forward(q, k, v, **kw)
+    bits = abi.dropout_bits_buffer(q, k, v, **kw)
+    out, lse, path = abi.forward(q, k, v, dropout_bits=bits, **kw)
     assert path == _lib.PATH_GENERIC
     grads = abi.backward(q, k, v, out, g, lse, **kw)[:3]
     torch.cuda.synchronize()
+    # the generic forward writes every word of the bits (padding rows zero)
+    np.testing.assert_array_equal(bits.cpu().numpy(),
+                                  packed_bits(abi.dropout_keep(q, k, v, **kw).cpu().numpy()))
     if dtype in TOL:
         check(abi.host(out), out_c, dtype, "o", "O")
         for got, want, name in zip(grads, back(inp.do), ("dQ", "dK", "dV")):
@@ -165,6 +218,7 @@ def test_mirror_dropout_backends_and_gradients():
     probes = _lib.profile_read()
     _lib.profile_enable(False)
     assert probes["fwd_mfma_dropout"][0] == 3 and probes["bwd_dkdv_mfma_dropout"][0] == 3
+    assert "dropout_bits" not in probes  # the backward reads the forward's bits
     assert all(np.isfinite(t.grad.numpy()).all() for t in (q, k, v))
     with pytest.raises(ValueError, match="dense backend"):
         nn.scaled_dot_product_attention(q, k, v, dropout_p=0.1, backend="streaming")
