@@ -434,6 +434,9 @@ bool mfma_supported(const Problem &p, int dtype) {
   if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
   if ((p.Dqk != 64 && p.Dqk != 128) || (p.Dv != 64 && p.Dv != 128)) return false;
   if (!(p.scale > 0.0)) return false;
+  // the backward reads each (b, h) slice of the dropout keep bits with 32-bit offsets
+  if (p.drop.on && static_cast<int64_t>((p.Sk + 31) / 32) * ((p.Sq + 3) / 4 * 4) * 4 >= (int64_t(1) << 31))
+    return false;
   if (p.mask.kind == TSATTN_MASK_ADDITIVE && p.mask.dtype != TSATTN_F32 &&
       p.mask.dtype != TSATTN_F16 && p.mask.dtype != TSATTN_BF16)
     return false;
