@@ -301,6 +301,36 @@ def test_rope_folded_with_a_general_mask():
     assert torch.equal(dv_f, grads_u[2])
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_rope_folded_with_dropout_is_bitwise_the_unfused_chain(dtype):
+    """RoPE folded in and dropout together: the same keep bits, the same
+    outputs and gradients as rotating first and dropping on the plain kernels."""
+    b, hq, hkv, s, d = 2, 4, 2, 160, 128
+    say(f"fused rope + dropout {dtype}")
+    rng = np.random.default_rng(99)
+    q, k, v, g = (abi.dev_tensor(rows(rng, shape, dtype, 0.7), dtype)
+                  for shape in ((b, hq, s, d), (b, hkv, s, d), (b, hkv, s, d), (b, hq, s, d)))
+    cos, sin = tables(s + 1, d, dtype)
+    k_rot = _rot(k, cos, sin, 0, d, False)
+    kw = dict(causal=True, dropout=(0.2, 0xABCDEF0123456789, 5))
+    bits_u = abi.dropout_bits_buffer(q, k, v, **kw)
+    q_rot = _rot(q, cos, sin, 0, d, False)
+    out_u, lse_u, _ = abi.forward(q_rot, k_rot, v, dropout_bits=bits_u, **kw)
+    dq_r, dk_r, dv_u, _ = abi.backward(q_rot, k_rot, v, out_u, g, lse_u, dropout_bits=bits_u, **kw)
+    desc = abi.rope_desc(cos, sin, d, 0, 0)
+    bits_f = abi.dropout_bits_buffer(q, k, v, **kw)
+    out_f, lse_f, path = abi.forward_rope(q, k_rot, v, desc, dropout_bits=bits_f, **kw)
+    assert path == _lib.PATH_MFMA
+    dq_f, dk_f, dv_f = abi.backward_rope(q, k_rot, v, out_f, g, lse_f, desc, dropout_bits=bits_f,
+                                         **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(bits_f, bits_u)
+    assert torch.equal(out_f, out_u) and torch.equal(lse_f, lse_u)
+    assert torch.equal(dq_f, _rot(dq_r, cos, sin, 0, d, True))
+    assert torch.equal(dk_f, _rot(dk_r, cos, sin, 0, d, True))
+    assert torch.equal(dv_f, dv_u)
+
+
 def test_rope_folded_refuses_problems_outside_the_mfma_kernels():
     q = torch.zeros((1, 1, 8, 32), dtype=torch.float32, device="cuda")
     cos, sin = tables(9, 32, "float32")
