@@ -161,6 +161,41 @@ def test_dropout_attention_matches_oracle(case):
     assert not torch.equal(out, out3)
 
 
+@pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
+def test_dropout_with_key_padding_lengths(dtype):
+    """Dropout with a [B,1,1,K] key-padding mask reduced to kv_len: the
+    kernels stop at each row's length (the forward writes bits only up to it)
+    and match the oracle under the same boolean mask."""
+    b, h, sq, sk, d, p = 3, 2, 96, 200, 128, 0.25
+    say(f"dropout + key padding {dtype}")
+    inp = attention_inputs(b, h, sq, d, dtype, seq_k=sk, value_scale=0.5, seed=53)
+    lens = np.array([200, 37, 129])
+    km = np.arange(sk)[None, :] < lens[:, None]  # [B, K] allowed keys
+    mask4 = km[:, None, None, :]
+    key, counter = 0x1234_5678_9ABC_DEF0, 2
+    out_c, _, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, mask4, True, dtype=dtype, p=p,
+                                     rng_key=key, rng_counter=counter, causal_offset=sk - sq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    tmask = torch.from_numpy(km).cuda()
+    kv_len, kv_prefix = abi.key_lengths(tmask)
+    kw = dict(causal=True, offset=sk - sq, dropout=(p, key, counter),
+              mask=tmask[:, None, None, :], kv_len=kv_len, kv_prefix=kv_prefix)
+    bits = abi.dropout_bits_buffer(q, k, v, **kw)
+    out, lse, path = abi.forward(q, k, v, dropout_bits=bits, **kw)
+    assert path == _lib.PATH_MFMA
+    grads = abi.backward(q, k, v, out, g, lse, dropout_bits=bits, **kw)[:3]
+    grads_drawn = abi.backward(q, k, v, out, g, lse, **kw)[:3]
+    torch.cuda.synchronize()
+    for a_, b_ in zip(grads, grads_drawn):
+        assert torch.equal(a_, b_)
+    check(abi.host(out), out_c, dtype, "o", "O")
+    for got, want, name in zip(grads, back(inp.do), ("dQ", "dK", "dV")):
+        check(abi.host(got), want, dtype, "g", name)
+    dk = abi.host(grads[1])
+    for bi, n in enumerate(lens):  # keys past a row's length get no gradient
+        assert (dk[bi, :, n:] == 0).all()
+
+
 GENERIC_CASES = [
     # (dtype, B, Hq, Hkv, Sq, Sk, Dqk, Dv, causal, p): generic kernels
     ("float32", 2, 2, 1, 33, 70, 32, 48, True, 0.25),

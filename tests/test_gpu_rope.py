@@ -243,6 +243,8 @@ DECODE_CASES = [
     ("float16", 2, 4, 1, 1, 1000, 256, 128, False),  # D = 256, half of it rotated
     ("bfloat16", 3, 8, 2, 1, 513, 128, 128, True),
     ("float16", 2, 2, 2, 4, 260, 64, 64, True),
+    ("bfloat16", 2, 8, 1, 1, 400, 128, 64, False),  # 8 query rows per KV head (the maximum)
+    ("float16", 1, 4, 2, 4, 333, 128, 128, True),   # 4 heads x 2 rows per KV head
 ]
 
 
