@@ -229,7 +229,9 @@ size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);
 /*
  * KV-cache decode: few query rows (len_q * heads_q / heads_kv <= 8 per KV
  * head) against a long cached prefix, split across the cache in chunks of
- * `split_len` keys (0 = choose), partial (max, sum, acc) merged as in the
+ * `split_len` keys (0 = choose: 640, halved while the grid is small; an
+ * explicit power of two makes concurrent splits share HBM channels and
+ * runs ~20% slower), partial (max, sum, acc) merged as in the
  * reference's online softmax (attention.py:185-193).  Replaces the dense
  * path the reference takes for cached decode (MultiHeadAttention.forward,
  * src/tensorsmith/nn/transformer.py:142-154 -> attention.py:132-145).
