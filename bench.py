@@ -475,6 +475,22 @@ def cpu_threads():
     return len(os.sched_getaffinity(0))
 
 
+def cpu_host_info():
+    """What the CPU leg ran on: the process's core affinity, the thread
+    environment and the BLAS NumPy was built with."""
+    import numpy as np
+
+    info = {"affinity_cores": len(os.sched_getaffinity(0)),
+            "OPENBLAS_NUM_THREADS": os.environ.get("OPENBLAS_NUM_THREADS"),
+            "OMP_NUM_THREADS": os.environ.get("OMP_NUM_THREADS")}
+    try:
+        blas = np.show_config(mode="dicts")["Build Dependencies"]["blas"]
+        info["blas"] = f"{blas.get('name')} {blas.get('version')}"
+    except Exception:  # noqa: BLE001 - reporting only
+        info["blas"] = None
+    return info
+
+
 def cpu_baseline(torch, host, dec_host, batches):
     """The NumPy oracle (reference algorithm) on a sample of the same inputs."""
     import numpy as np
@@ -518,12 +534,15 @@ def cpu_baseline(torch, host, dec_host, batches):
         dts.append(time.perf_counter() - t0)
     dmed = float(np.median(dts))
     cores = cpu_threads()
+    hinfo = cpu_host_info()
     return {
         "value": flops / med / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+        "host": hinfo,
         "sample": f"causal fwd+bwd of batch rows 0..{batches - 1} x {H} heads (S=2048 D=128, "
                   f"bf16 values in fp32), NumPy streaming block 64, median of 3: "
                   f"{med:.2f} s per sample",
         "decode": {"value": nseq / dmed, "unit": "tokens/s", "cores": cores, "kind": "port",
+                   "host": hinfo,
                    "sample": f"dense decode of all {nseq} sequences (fp16 values in fp32), "
                              f"median of 5 after 1 warmup: {dmed:.3f} s"},
     }
@@ -615,6 +634,10 @@ def main():
                    "seq_len": S, "head_dim": D, "causal": True,
                    "flop_per_step": causal_fwd_flops(B, H, S, D) * 3.5},
         "roofline": main_res["roofline"],
+        # the whole step (forward + backward, algorithmic FLOP / step time)
+        "step_roofline": {"bound": "mfma", "achieved": round(main_res["value"], 1),
+                          "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                          "frac": round(main_res["value"] / PEAK_BF16_TFLOPS, 4)},
         "kernels": main_res["kernels"],
         "variants": var_res,
         "cpu_baseline": cpu,

@@ -9,6 +9,7 @@ the HIP kernels of ``libtsattn.so``.
 
 from __future__ import annotations
 
+from contextvars import ContextVar
 from dataclasses import dataclass
 from functools import cache
 
@@ -109,12 +110,83 @@ def seed(value: int) -> None:
         pass
 
 
-def random_uniform(shape, value: DeviceLike = "hip"):
-    """Uniform [0, 1) float32 draws from the device generator (the reference's
-    ``device.random_uniform``, ``src/tensorsmith/device.py:276-297``)."""
+# Random draws made inside a checkpointed function are recorded on this tape
+# and replayed by its recomputation (the reference's ``_random_tape``,
+# ``src/tensorsmith/device.py:23,276-297``).  An entry is (kind, shape,
+# device, state): a uniform draw keeps the generator state it started from
+# (a few bytes, not the drawn array), an attention-dropout key keeps the key.
+_random_tape: ContextVar[dict | None] = ContextVar("tensorsmith_hip_random_tape", default=None)
+
+
+def _replay_entry(kind: str, shape, dev):
+    tape = _random_tape.get()
+    if tape is None or tape["mode"] != "replay":
+        return None
+    position = tape["position"]
+    if position >= len(tape["draws"]):
+        raise RuntimeError("checkpoint recomputation changed the number of random draws")
+    entry = tape["draws"][position]
+    if entry[0] != kind or entry[1] != shape or entry[2] != dev:
+        raise RuntimeError("checkpoint recomputation changed a random draw's shape/device")
+    tape["position"] += 1
+    return entry
+
+
+def _record(entry) -> None:
+    tape = _random_tape.get()
+    if tape is not None and tape["mode"] == "record":
+        tape["draws"].append(entry)
+
+
+def _generator_state(dev: Device):
     import torch
 
-    return torch.rand(tuple(shape), dtype=torch.float32, device=device(value).torch)
+    return torch.cuda.get_rng_state(dev.torch) if dev.type == "hip" else torch.get_rng_state()
+
+
+def _set_generator_state(dev: Device, state) -> None:
+    import torch
+
+    if dev.type == "hip":
+        torch.cuda.set_rng_state(state, dev.torch)
+    else:
+        torch.set_rng_state(state)
+
+
+def random_uniform(shape, value: DeviceLike = "hip"):
+    """Uniform [0, 1) float32 draws from the device generator (the reference's
+    ``device.random_uniform``, ``src/tensorsmith/device.py:276-297``).  Under a
+    checkpoint the recomputation redraws from the recorded generator state,
+    so it sees the same values, and the generator is left where it was."""
+    import torch
+
+    dev, shape = device(value), tuple(shape)
+
+    def draw():
+        return torch.rand(shape, dtype=torch.float32, device=dev.torch)
+
+    entry = _replay_entry("uniform", shape, dev)
+    if entry is not None:
+        current = _generator_state(dev)
+        _set_generator_state(dev, entry[3])
+        try:
+            return draw()
+        finally:
+            _set_generator_state(dev, current)
+    _record(("uniform", shape, dev, _generator_state(dev)))
+    return draw()
+
+
+def attention_dropout_key() -> int:
+    """A 128-bit Philox key for one attention-dropout call, drawn from NumPy's
+    global state (``ts.seed`` reproduces it).  A checkpoint's recomputation
+    gets the recorded key back, so the kernels regenerate the same keep mask."""
+    drawn = int.from_bytes(np.random.bytes(16), "little")
+    entry = _replay_entry("attention_key", None, None)
+    if entry is not None:
+        return entry[3]
+    _record(("attention_key", None, None, drawn))
+    return drawn
 
 
 def current_stream(dev: Device) -> int:

@@ -3,6 +3,7 @@
 from . import functional
 from .attention import rotary_embedding, scaled_dot_product_attention
 from .cache import KVCache
+from .checkpoint import checkpoint
 from .layers import GELU, Dropout, Embedding, LayerNorm, Linear
 from .module import Module, Parameter
 from .transformer import (
@@ -13,6 +14,6 @@ from .transformer import (
 __all__ = [
     "Dropout", "Embedding", "GELU", "KVCache", "LayerNorm", "Linear", "Module",
     "MultiHeadAttention", "Parameter", "RMSNorm", "SiLU", "SwiGLU", "TransformerConfig",
-    "TransformerDecoderBlock", "TransformerLM", "functional", "rotary_embedding",
+    "TransformerDecoderBlock", "TransformerLM", "checkpoint", "functional", "rotary_embedding",
     "sample_logits", "scaled_dot_product_attention",
 ]

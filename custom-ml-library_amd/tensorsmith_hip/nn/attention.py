@@ -5,7 +5,8 @@ Same signature, argument meaning and refusals as the reference
 backend allowlist and chosen by ``auto`` on a hip device (as ``native`` is on
 Metal, ``:78-80``).  ``dense`` and ``streaming`` name the same exact math;
 on hip both run the HIP kernels (online softmax, saved LSE, recomputing VJP).
-Dropout is refused like the reference's streaming backend (``:83-84``).
+Dropout runs in the kernels on ``hip`` / ``dense`` / ``auto`` and is refused on
+``streaming`` / ``native`` like the reference (``:83-84``).
 
 Kernel routing (all on the GPU, none on the CPU):
 
@@ -23,7 +24,7 @@ import math
 import numpy as np
 
 from .. import _lib
-from ..device import current_stream
+from ..device import attention_dropout_key, current_stream
 from ..tensor import Tensor, is_grad_enabled
 
 BACKENDS = {"auto", "dense", "streaming", "native", "hip"}
@@ -149,12 +150,13 @@ def scaled_dot_product_attention(
     tdev = q.device
     prob = _problem(b, hq, hkv, qlen, klen, dim, dim_v, code, multiplier, is_causal, causal_offset)
     if dropout_p:
-        # a fresh 128-bit Philox key per call from the host stream (ts.seed);
-        # the backward regenerates the same keep mask from it
-        key_bytes = np.random.bytes(16)
+        # a fresh 128-bit Philox key per call from the host stream (ts.seed),
+        # recorded / replayed under a checkpoint; the backward reads the keep
+        # mask the forward drew from it
+        drop_key = attention_dropout_key()
         prob.dropout_p = float(dropout_p)
-        prob.dropout_key[0] = int.from_bytes(key_bytes[:8], "little")
-        prob.dropout_key[1] = int.from_bytes(key_bytes[8:], "little")
+        prob.dropout_key[0] = drop_key & (2**64 - 1)
+        prob.dropout_key[1] = drop_key >> 64
         prob.dropout_counter = 0
     keep = []  # device buffers the launch reads, alive until the call returns
 
@@ -271,6 +273,10 @@ def scaled_dot_product_attention(
 
     def backward(upstream, _keep=keep):  # _keep: mask / length buffers the kernels read
         g = _operand(upstream)
+        if fused and (not _aligned16(g) or min(g.stride()[:3]) <= 0):
+            # the folded-RoPE backward runs on the MFMA kernels only, which need
+            # 16-byte aligned rows of a real (not expanded) gradient
+            g = g.contiguous()
         if g.dtype != out.dtype:
             g = g.to(out.dtype)
         dq = torch.empty(q.shape, dtype=q.dtype, device=tdev)

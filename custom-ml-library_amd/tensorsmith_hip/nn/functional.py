@@ -11,6 +11,7 @@ from __future__ import annotations
 import math
 
 from ..amp import _cast_inputs
+from ..device import random_uniform
 from ..tensor import Tensor, _sum_to_shape, is_torch
 from .attention import rotary_embedding, scaled_dot_product_attention
 
@@ -168,9 +169,7 @@ def dropout(input: Tensor, p: float = 0.5, training: bool = True) -> Tensor:
     if not training or p == 0:
         return input
     _require_hip(input, "dropout")
-    import torch
-
-    mask = (torch.rand(input.shape, device=input._data.device) >= p).to(input.dtype) / (1 - p)
+    mask = (random_uniform(input.shape, input.device) >= p).to(input.dtype) / (1 - p)
     return Tensor._from_op(input._data * mask, (input,), lambda g: (g * mask,), "dropout")
 
 

@@ -31,6 +31,7 @@ from ..tensor import Tensor, cat, is_grad_enabled, no_grad
 from . import functional as F
 from .attention import BACKENDS, decode_int8_cache, rotary_embedding, scaled_dot_product_attention
 from .cache import KVCache
+from .checkpoint import checkpoint
 from .layers import Dropout, Embedding, Linear
 from .module import Module, Parameter
 
@@ -98,7 +99,13 @@ class MultiHeadAttention(Module):
              .permute(0, 2, 1, 3))
         fused = False
         rope = None
-        if self.rotary and cache is None:
+        if self.rotary and str(q.dtype).split(".")[-1] not in ("float32", "float16", "bfloat16"):
+            # float64 (the generic kernels): rotate the operands first, as the
+            # reference does (transformer.py:139-141); the kernels fold RoPE
+            # for f32 / f16 / bf16 only
+            q = rotary_embedding(q, offset)
+            k = rotary_embedding(k, offset if context is None else 0)
+        elif self.rotary and cache is None:
             # the attention kernels rotate the queries (and the gradients) themselves
             rope = (offset, offset if context is None else 0, 10000.0)
         elif self.rotary:
@@ -207,8 +214,9 @@ class TransformerConfig:
 class TransformerLM(Module):
     """A decoder-only language model with [B,T,V] logits and cached generation.
 
-    ``activation_checkpointing`` is accepted for configuration compatibility;
-    blocks always keep their activations (same results, more memory).
+    With ``activation_checkpointing`` each block runs under ``nn.checkpoint``
+    while training (reference ``transformer.py:299-300``): its activations are
+    recomputed in backward, with the same dropout masks.
     """
 
     def __init__(self, config: TransformerConfig, device=None):
@@ -260,8 +268,12 @@ class TransformerLM(Module):
         hidden = self.embedding_dropout(self.token_embedding(tokens))
         try:
             for i, block in enumerate(self.blocks):
-                hidden = block(hidden, cache=None if caches is None else caches[i],
-                               attn_mask=attn_mask)
+                if self.config.activation_checkpointing and self.training and is_grad_enabled():
+                    # recompute the block in backward; its dropout draws replay
+                    hidden = checkpoint(block, hidden, attn_mask=attn_mask)
+                else:
+                    hidden = block(hidden, cache=None if caches is None else caches[i],
+                                   attn_mask=attn_mask)
             if logits_to_keep:
                 hidden = hidden[:, -logits_to_keep:, :]
             return F.linear(self.final_norm(hidden), self.output_weight)

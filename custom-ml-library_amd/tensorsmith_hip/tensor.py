@@ -474,13 +474,16 @@ def _run_backward(root: Tensor, seed, *, retain_graph=False, accumulate=False, r
 
 
 def grad(output: Tensor, inputs: Tensor | Sequence[Tensor], grad_outputs=None, *,
-         retain_graph=False) -> tuple[Tensor | None, ...]:
-    """Gradients of ``output`` w.r.t. ``inputs`` without touching ``.grad``."""
+         retain_graph=False, allow_unused=False) -> tuple[Tensor | None, ...]:
+    """Gradients of ``output`` w.r.t. ``inputs`` without touching ``.grad``
+    (reference ``tensor.py:727-760``)."""
     inputs = (inputs,) if isinstance(inputs, Tensor) else tuple(inputs)
     if not output.requires_grad or any(not x.requires_grad for x in inputs):
         raise RuntimeError("output and requested inputs must require gradients")
     seed = _ones_like(output._data) if grad_outputs is None else to_backend(grad_outputs, output.device)
     values = _run_backward(output, seed, retain_graph=retain_graph, requested=(id(x) for x in inputs))
+    if not allow_unused and any(id(x) not in values for x in inputs):
+        raise RuntimeError("a requested input is not used by the output")
     return tuple(Tensor(values[id(x)], device=x.device) if id(x) in values else None for x in inputs)
 
 
