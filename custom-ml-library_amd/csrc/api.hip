@@ -397,6 +397,25 @@ int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const t
                         workspace_bytes, stream);
 }
 
+int tsattn_decode_forward_noalloc(const tsattn_problem *p, const tsattn_view *q,
+                                  const tsattn_view *k, const tsattn_view *v,
+                                  const tsattn_view *out, int32_t split_len, void *stream) {
+  tsattn::Problem pr;
+  int rc = check_problem(p, &pr);
+  if (rc) return rc;
+  if (split_len < 0) return fail(TSATTN_ERR_INVALID, "split_len must be >= 0");
+  const size_t need = tsattn::decode_workspace_bytes(pr, split_len);
+  if (need > TSATTN_DECODE_SCRATCH_BYTES)
+    return fail(TSATTN_ERR_INVALID,
+                "decode needs %zu bytes of scratch; the allocation-free entry point holds %zu "
+                "(use tsattn_decode_forward with a workspace)",
+                need, static_cast<size_t>(TSATTN_DECODE_SCRATCH_BYTES));
+  void *ws = nullptr;
+  if ((rc = hip_status(tsattn::decode_scratch(&ws), "decode scratch address"))) return rc;
+  return decode_forward(p, nullptr, q, k, v, nullptr, nullptr, out, split_len, ws,
+                        TSATTN_DECODE_SCRATCH_BYTES, stream);
+}
+
 int tsattn_decode_forward_int8(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                                const tsattn_view *v, const tsattn_view *k_scale,
                                const tsattn_view *v_scale, const tsattn_view *out, int32_t split_len,

@@ -22,6 +22,7 @@
 // key instead of a pass over the cache.  The dequantised values enter the
 // math in fp32 (the reference rounds them to the cache dtype first: at most
 // half an ulp of that dtype per element).
+#include <mutex>
 #include <type_traits>
 
 #include "mfma_common.h"
@@ -422,6 +423,42 @@ size_t decode_workspace_bytes(const Problem &p, int split_len) {
   const int s = choose_split(p, split_len);
   const int64_t splits = (p.Sk + s - 1) / s;
   return static_cast<size_t>(p.B) * p.Hkv * splits * p.rep * p.Sq * (p.Dv + 2) * sizeof(float);
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned scratch for tsattn_decode_forward_noalloc: the split kernel's
+// partial (acc, m, l) states live in this array instead of a caller
+// workspace.  Each GPU the library runs on holds its own copy (zero-filled
+// .bss of the code object, kept until the process ends).  In host code
+// `scratch` names a host-side stand-in, never the device array: kernels get
+// the address hipGetSymbolAddress reports for the current device.  Every
+// call on one GPU shares that GPU's copy; the split kernel writes every slot
+// the merge reads before the merge runs, so nothing needs clearing, but
+// calls that overlap on one GPU (different streams) race.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[TSATTN_DECODE_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t decode_scratch(void **ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void *addr = nullptr;
+    e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!addr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = addr;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
 }
 
 hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,

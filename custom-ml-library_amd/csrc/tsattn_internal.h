@@ -182,6 +182,9 @@ size_t mfma_rope_stage_offset(const Problem &p);
 // Split-K decode.
 bool decode_supported(const Problem &p, int dtype);
 size_t decode_workspace_bytes(const Problem &p, int split_len);
+// Device address of this GPU's decode scratch array (TSATTN_DECODE_SCRATCH_BYTES),
+// looked up once per device with that device current.
+hipError_t decode_scratch(void **ptr);
 hipError_t launch_decode(const Problem &p, int dtype, View q, View k, View v, View o,
                          int split_len, void *workspace, hipStream_t st);
 // The same over an int8 cache with fp32 row scales ks / vs [B, Hkv, capacity, 1].

@@ -99,6 +99,7 @@ SIGNATURES = {
         c_int,
         [_PP, _PV, _PV, _PV, _PV, c_int32, c_void_p, c_size_t, c_void_p],
     ),
+    "tsattn_decode_forward_noalloc": (c_int, [_PP, _PV, _PV, _PV, _PV, c_int32, c_void_p]),
     "tsattn_decode_forward_int8": (
         c_int,
         [_PP, _PV, _PV, _PV, _PV, _PV, _PV, c_int32, c_void_p, c_size_t, c_void_p],

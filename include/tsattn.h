@@ -10,8 +10,9 @@
  *
  * Conventions
  *  - Every pointer is a device pointer owned by the caller; the library keeps
- *    no allocation.  Calls are asynchronous on `stream` (a hipStream_t, or
- *    NULL for the default stream).
+ *    no allocation (apart from the static scratch array of
+ *    tsattn_decode_forward_noalloc).  Calls are asynchronous on `stream` (a
+ *    hipStream_t, or NULL for the default stream).
  *  - Tensors are strided 4-D views [B, H, S, D] with strides in elements; the
  *    innermost (D) stride must be 1.  Broadcast masks use zero strides.
  *  - Every entry returns a tsattn_status; on failure tsattn_last_error()
@@ -240,6 +241,30 @@ size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);
 int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                           const tsattn_view *v, const tsattn_view *out, int32_t split_len,
                           void *workspace, size_t workspace_bytes, void *stream);
+
+/*
+ * Size of the library-owned scratch of tsattn_decode_forward_noalloc: one
+ * static device array per GPU, held from the first call on that GPU until the
+ * process ends.
+ */
+#define TSATTN_DECODE_SCRATCH_BYTES (32u << 20)
+
+/*
+ * tsattn_decode_forward without a workspace argument and without allocating:
+ * the split partials live in the library's static device array of
+ * TSATTN_DECODE_SCRATCH_BYTES (32 MiB) on the current GPU.  No counterpart in
+ * the reference; it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same inputs, outputs and results as tsattn_decode_forward
+ * (bit-identical); problems whose tsattn_decode_workspace exceeds the array
+ * return TSATTN_ERR_INVALID.  The first call on a GPU looks up the array's
+ * device address (hipGetSymbolAddress).  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU (e.g. on two streams) race --
+ * serialise them.
+ */
+int tsattn_decode_forward_noalloc(const tsattn_problem *p, const tsattn_view *q,
+                                  const tsattn_view *k, const tsattn_view *v,
+                                  const tsattn_view *out, int32_t split_len, void *stream);
 
 /*
  * KV-cache decode over an int8 cache: k / v are int8 views [B, Hkv, capacity,
