@@ -453,6 +453,21 @@ __device__ __forceinline__ float half_swap_max(float x) {
   return fmaxf(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b));
 }
 
+// max(a, b, c) in one v_max3_f32, without the NaN canonicalisation the
+// compiler adds around fmaxf (scores are never NaN unless an input is).
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// half_swap_max with the final max in one instruction (no canonicalisation).
+__device__ __forceinline__ float half_swap_max3(float x) {
+  unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  return max3f(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b), __builtin_bit_cast(float, b));
+}
+
 __device__ __forceinline__ uint64_t partner64(uint64_t x, int h) {
   return static_cast<uint64_t>(partner32(static_cast<unsigned>(x), h)) |
          (static_cast<uint64_t>(partner32(static_cast<unsigned>(x >> 32), h)) << 32);

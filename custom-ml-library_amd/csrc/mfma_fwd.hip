@@ -90,7 +90,9 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
                 VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
   static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
-  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];  // [stage][K | V]
+  // [stage][K | V], then one 1 KiB block that DMA parts past the last tile
+  // land in (nothing reads it)
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -115,8 +117,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     wlim = min(wlim, static_cast<int64_t>(last_qw) + p.offset + 1);
   }
   if (qw >= p.Sq) wlim = 0;
-  const int n_tiles = lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0;
-  const int w_tiles = wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0;
+  // wave-uniform by construction; readfirstlane keeps them in SGPRs
+  const int n_tiles =
+      __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0);
+  const int w_tiles =
+      __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0);
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2;
@@ -154,25 +159,29 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
   const uint32_t voff = (lane >> 2) * vs_b + (4 * (w % QGV) + swz_chunk) * 16;
   // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
+  // Every iteration issues its LPT parts: those of a tile past the last one
+  // read row 0 into the spare LDS block, so the count of loads in flight is
+  // the same on every iteration and no branch guards an issue.
+  const uint32_t spare = lds0 + NS * STAGE;
   auto issue_part = [&](int tile, int u) {
-    const uint32_t st = lds0 + (tile % NS) * STAGE;
+    // keep = all ones for a real tile, else 0: masks instead of selects, which
+    // the compiler would turn into branches between the MFMA steps
+    const uint32_t keep =
+        __builtin_amdgcn_readfirstlane(0u - static_cast<uint32_t>(tile < n_tiles));
+    const uint32_t st = lds0 + (tile % NS) * STAGE - spare;
     if (u < KPARTS) {
       const int n = w + NW * u;
-      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * BN + 16 * (n / QGK)) * ks_b);
+      dma16(kdesc, spare + ((st + n * 1024) & keep), koff,
+            (static_cast<uint32_t>(tile * BN + 16 * (n / QGK)) * ks_b) & keep);
     } else {
       const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, st + TILE_K + n * 1024, voff, static_cast<uint32_t>(tile * BN + 16 * (n / QGV)) * vs_b);
+      dma16(vdesc, spare + ((st + TILE_K + n * 1024) & keep), voff,
+            (static_cast<uint32_t>(tile * BN + 16 * (n / QGV)) * vs_b) & keep);
     }
   };
   auto issue = [&](int tile) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) issue_part(tile, u);
-  };
-  // Loads this wave may leave in flight once tile jn has landed: those of the
-  // (at most PD - 1) later tiles already issued.
-  auto in_flight_after = [&](int jn) {
-    const int later = min(PD - 1, n_tiles - 1 - jn);
-    return later > 0 ? later * LPT : 0;
   };
 
   const TileReader<T, DK> rdk(lane);
@@ -216,9 +225,19 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // past the buffer range write zeros).
   zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
   __syncthreads();
-  for (int t = 0; t < PD && t < n_tiles; ++t) issue(t);
-  wait_vm(in_flight_after(0));
+  for (int t = 0; t < PD; ++t) issue(t);
+  wait_vm_n<(PD - 1) * LPT>();
   __syncthreads();
+
+  // Tiles from j_edge on need masking (the causal diagonal, a ragged end, a
+  // key mask or a general mask); those before it are interior.
+  int j_edge = kv_end / BN;
+  if (MK != 0 || keymask) j_edge = 0;
+  if (p.causal) {
+    const int64_t d = static_cast<int64_t>(qw) + p.offset - (BN - 1);
+    const int jc = d < 0 ? 0 : static_cast<int>(min(d / BN + 1, static_cast<int64_t>(INT32_MAX)));
+    j_edge = min(j_edge, jc);
+  }
 
   // MFMA block of key tile j: O^T += V_{j-1}^T P_{j-1}^T and S_j^T = K_j Q^T.
   // Step i issues S k-step i and PV MFMA i (value block i % PDT, key k-step
@@ -252,7 +271,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       if (i < SKS) s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
       if (i < PVS) oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
       if (i + FD < STEPS) load(i + FD);
-      if (nt >= 0 && (i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
+      if ((i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -262,9 +281,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     float x[16];  // scores of this lane's query row; element i is key kv0 + crow(i, h)
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = s[i];
-    const bool edge = MK != 0 || (kv0 + BN > kv_end) || keymask ||
-                      (p.causal && static_cast<int64_t>(kv0 + BN - 1) > qw + p.offset);
-    if (edge) {
+    if (j >= j_edge) {
       // Key kv0 + 4h + kc(i), kc a compile-time constant.
       const int lim = klim - kv0 - 4 * h;
       if constexpr (MK == 0) {
@@ -281,7 +298,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
           x[i] = ok ? x[i] : -INFINITY;
         }
       } else {
-        wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
+        wait_vm_n<LPT>();  // the mask loads; tile nt's parts stay in flight
         if constexpr (mask_vec(MK)) {
           mf.resolve_vec<mes>();
           mf.unpack<mes>(h);
@@ -291,10 +308,12 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim, sl);
       }
     }
-    float mx = -INFINITY;
+    // row max: a v_max3 chain (fmaxf would add NaN canonicalisations)
+    float mx = max3f(x[0], x[1], x[2]);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
-    const float mt = half_swap_max(mx) * slx;
+    for (int i = 3; i < 15; i += 2) mx = max3f(mx, x[i], x[i + 1]);
+    mx = max3f(mx, x[15], x[15]);
+    const float mt = half_swap_max3(mx) * slx;
     if (__ballot(mt > m + kTau) != 0ull) {
       const float m_new = fmaxf(m, mt);
       const float corr = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
@@ -339,9 +358,9 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // (j + PD) % NS last held tile j - 2, read up to iteration j - 1).  Each
   // wave's work is one straight loop, so the accumulators stay in place;
   // iterations past the wave's last tile only keep the barrier count.
-  auto next_dma = [&](int j) { return j + PD < n_tiles ? j + PD : -1; };
-  auto it_end = [&](int j) {
-    wait_vm(in_flight_after(j + 1));
+  auto next_dma = [&](int j) { return j + PD; };
+  auto it_end = [&](int) {
+    wait_vm_n<(PD - 1) * LPT>();  // tile j + 1 has landed
     wait_lgkm0();
     phase_barrier();
   };
@@ -358,9 +377,10 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     ++j;
   }
   for (; j <= n_tiles; ++j) {
-    if (next_dma(j) >= 0) issue(next_dma(j));
+    issue(next_dma(j));
     it_end(j);
   }
+  wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
 
   const float lt = xor32_sum(l);  // lanes c and c+32 share a query row
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
