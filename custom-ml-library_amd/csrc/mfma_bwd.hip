@@ -125,8 +125,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
                 GPARTS * NW * 1024 == TILE_G, "tile loads must split evenly over the waves");
   static_assert(2 * LPT <= STEPS, "one tile DMA part per two MFMA steps");
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
-  // Q / dO ring
-  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B];
+  // Q / dO ring, then a 1 KiB block that DMA parts of tiles past the last
+  // one land in (nothing reads it)
+  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -160,8 +161,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     q_start = s0 <= 0 ? 0 : static_cast<int>(s0 < p.Sq ? s0 : p.Sq);
     q_start = (q_start / QT) * QT;
   }
-  const int n_qt = k0 < kv_end ? (p.Sq - q_start + QT - 1) / QT : 0;
-  const int n_iter = n_qt * p.rep;
+  // wave-uniform by construction; readfirstlane keeps them in SGPRs
+  const int n_qt = __builtin_amdgcn_readfirstlane(k0 < kv_end ? (p.Sq - q_start + QT - 1) / QT : 0);
+  const int n_iter = __builtin_amdgcn_readfirstlane(n_qt * p.rep);
 
   const uint32_t qs_b = static_cast<uint32_t>(a.qk.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
@@ -171,22 +173,40 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // wave's blocks are w, w + 4, ..., all with n % QG = w % QG.
   const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t lrow = lane >> 2;
-  auto tile_of = [&](int itn, int &hq, int &q0) {
-    const int r = itn / n_qt;
-    hq = hk * p.rep + r;
-    q0 = q_start + (itn - r * n_qt) * QT;
+  // Tile itn is query tile qi = itn % n_qt of query head hk rep + itn / n_qt;
+  // TileIdx walks that order without a division per tile.
+  struct TileIdx {
+    int itn, r, qi;
   };
-  // DMA of tile itn into its ring stage, in LPT + 1 parts: part u < LPT is
-  // this wave's u-th Q / dO block, part LPT the nl / nd rows (waves 0, 1).
+  auto tile_next = [&](TileIdx t) {
+    ++t.itn;
+    const bool wrap = ++t.qi == n_qt;
+    t.qi = wrap ? 0 : t.qi;
+    t.r += wrap ? 1 : 0;
+    return t;
+  };
+  // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
+  // this wave's u-th Q / dO block, part LPT the nl / nd rows (waves 0, 1;
+  // waves 2, 3 load past the range into the spare block, so every wave
+  // issues the same count).  Tiles past the last one (itn >= n_iter) read
+  // at offsets >= 2^31 -- past every range: zeros, no memory access -- into
+  // the spare block: every iteration issues the same loads, so the waits are
+  // constants and no branch guards an issue.  keep = all ones for a real
+  // tile, else 0 (masks, not selects, which the compiler turns into
+  // branches between the MFMA steps).
+  const uint32_t spare = ring0 + KV_NS * STAGE_B;
   struct TileDma {
-    uint32_t st;
+    uint32_t st, keep, far;
     int q0, hq;
     u32x4 qdesc, gdesc;
   };
-  auto tile_dma = [&](int itn) {
+  auto tile_dma = [&](TileIdx x) {
     TileDma t;
-    tile_of(itn, t.hq, t.q0);
-    t.st = ring0 + (itn % KV_NS) * STAGE_B;
+    t.hq = hk * p.rep + x.r;
+    t.q0 = q_start + x.qi * QT;
+    t.keep = ~static_cast<uint32_t>((n_iter - 1 - x.itn) >> 31);  // sign fill
+    t.far = ~t.keep & 0x80000000u;
+    t.st = (ring0 + (x.itn % KV_NS) * STAGE_B - spare) & t.keep;
     t.qdesc = make_desc(head_ptr<T>(a.qk, b, t.hq), static_cast<uint32_t>(p.Sq) * qs_b);
     t.gdesc = make_desc(head_ptr<T>(a.dout, b, t.hq), static_cast<uint32_t>(p.Sq) * gs_b);
     return t;
@@ -199,11 +219,13 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   auto issue_part = [&](const TileDma &t, int u) {
     if (u < QPARTS) {
       const int n = w + NW * u;
-      dma16(t.qdesc, t.st + n * 1024, qvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b);
+      dma16(t.qdesc, spare + t.st + ((n * 1024) & t.keep), qvoff,
+            (static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b) | t.far);
     } else if (u < LPT) {
       const int n = w + NW * (u - QPARTS);
-      dma16(t.gdesc, t.st + TILE_Q + n * 1024, gvoff, static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b);
-    } else if (w < 2) {
+      dma16(t.gdesc, spare + t.st + ((TILE_Q + n * 1024) & t.keep), gvoff,
+            (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
+    } else {
       const u32x4 rdesc = make_desc(rowv + static_cast<int64_t>(t.hq - hk * p.rep) * p.Sq,
                                     static_cast<uint32_t>(p.Sq) * 4);
       // lane * 16, recomputed here rather than held in a register all loop
@@ -211,8 +233,10 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
                    "v_lshlrev_b32 %0, 4, %0"
                    : "=v"(loff));
+      const uint32_t mine = w < 2 ? t.keep : 0u;  // waves 2, 3: the spare block
       if (lane < QT / 4)
-        dma16(rdesc, t.st + TILE_Q + TILE_G + w * QT * 4, loff, static_cast<uint32_t>(t.q0) * 4);
+        dma16(rdesc, spare + (t.st & mine) + ((TILE_Q + TILE_G + w * QT * 4) & mine), loff,
+              (static_cast<uint32_t>(t.q0) * 4) | (~mine & 0x80000000u));
     }
   };
   // Staged mask: 1 KiB block n = w + NW u of the tile holds rows
@@ -234,8 +258,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int u = 0; u < MPARTS; ++u) {
         const int n = w + NW * u;
-        dma16(mdesc, t.st + MOFF + n * 1024, mvoff,
-              static_cast<uint32_t>(t.q0 + n * (1024 / MROW)) * ms2 + static_cast<uint32_t>(k0 * MES));
+        dma16(mdesc, spare + t.st + ((MOFF + n * 1024) & t.keep), mvoff,
+              (static_cast<uint32_t>(t.q0 + n * (1024 / MROW)) * ms2 +
+               static_cast<uint32_t>(k0 * MES)) | t.far);
       }
     }
   };
@@ -251,24 +276,20 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
                    "v_lshlrev_b32 %0, 4, %0"
                    : "=v"(loff));
       if (lane < 8)
-        dma16(bdesc, t.st + BOFF + w * 128, loff,
-              (static_cast<uint32_t>(kb * (KB / 32) + w) * d.sqp + t.q0) * 4);
+        dma16(bdesc, spare + t.st + ((BOFF + w * 128) & t.keep), loff,
+              ((static_cast<uint32_t>(kb * (KB / 32) + w) * d.sqp + t.q0) * 4) | t.far);
     }
   };
-  auto issue = [&](int itn) {
-    const TileDma t = tile_dma(itn);
+  auto issue = [&](TileIdx x) {
+    const TileDma t = tile_dma(x);
 #pragma unroll
     for (int u = 0; u <= LPT; ++u) issue_part(t, u);
     issue_mask(t);
     issue_bits(t);
   };
-  // DMA loads this wave may leave in flight once tile itn has landed: those
-  // of the later tiles already issued.
-  const int parts = LPT + (w < 2 ? 1 : 0) + MPARTS + (DR ? 1 : 0);
-  auto in_flight_after = [&](int itn) {
-    const int later = min(KV_PD - 1, n_iter - 1 - itn);
-    return later > 0 ? later * parts : 0;
-  };
+  // DMA loads per wave per tile; a wave leaves those of the (KV_PD - 1) later
+  // tiles already issued in flight once a tile has landed.
+  constexpr int PARTS = LPT + 1 + MPARTS + (DR ? 1 : 0);
 
   // This wave's K / V row fragments (B operands of S = Q K^T, dP = dO V^T):
   // lane (c, h) holds row key, columns 16 i + 8 h .. +7.  Keys past the cache
@@ -294,11 +315,15 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 
   // No zeroing: every LDS byte the loop reads is written by a DMA load first
   // (lanes past a buffer's range write zeros).
-  for (int t = 0; t < KV_PD && t < n_iter; ++t) issue(t);
+  TileIdx nxt_idx{0, 0, 0};
+  for (int t = 0; t < KV_PD; ++t) {
+    issue(nxt_idx);
+    nxt_idx = tile_next(nxt_idx);
+  }
   // The K / V loads were issued first, so this also waits for them; resolve
   // them here, where the compiler's own vmcnt waits (which do not count the
   // DMA loads) cannot land inside the loop.
-  wait_vm(n_iter > 0 ? in_flight_after(0) : 0);
+  wait_vm_n<(KV_PD - 1) * PARTS>();
 #pragma unroll
   for (int i = 0; i < STEPS; ++i) {
     if (i < SKQ && i < SKV) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
@@ -307,16 +332,17 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   }
   __syncthreads();
 
+  TileIdx cur_idx{0, 0, 0};
   for (int itn = 0; itn < n_iter; ++itn) {
     // Tile itn + 2 is issued between the S / dP MFMA steps below, so a wave
     // never stalls on the address unit before its first MFMA.
-    const bool prefetch = itn + KV_PD < n_iter;
-    const TileDma nxt = tile_dma(prefetch ? itn + KV_PD : itn);
+    const TileDma nxt = tile_dma(nxt_idx);
+    nxt_idx = tile_next(nxt_idx);
     const char *qt = ring + (itn % KV_NS) * STAGE_B;
     const char *gt = qt + TILE_Q;
     const float *rv = reinterpret_cast<const float *>(qt + TILE_Q + TILE_G);
-    int hq, q0;
-    tile_of(itn, hq, q0);
+    const int hq = hk * p.rep + cur_idx.r, q0 = q_start + cur_idx.qi * QT;
+    cur_idx = tile_next(cur_idx);
 
     constexpr int FD = DKDV_FD;
     // A general mask: this tile's elements (b, hq, q0 + 4h + kc, key), kc
@@ -360,8 +386,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         if (i < SKQ) sacc = mfma32<T>(qa[i % (FD + 1)], kf[i], sacc);
         if (i < SKV) dpacc = mfma32<T>(ga[i % (FD + 1)], vf[i], dpacc);
         if (i + FD < STEPS) load(i + FD);
-        if (prefetch && (i & 1) && (i >> 1) < LPT) issue_part(nxt, i >> 1);
-        if (prefetch && i == 0) {
+        if ((i & 1) && (i >> 1) < LPT) issue_part(nxt, i >> 1);
+        if (i == 0) {
           issue_part(nxt, LPT);
           issue_mask(nxt);
           issue_bits(nxt);
@@ -396,8 +422,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       if constexpr (MK != 0 && !MSTAGE) {
         // The mask loads; the next tile's Q / dO parts stay in flight (waves 0
         // and 1 also wait for their row-value part, the first one issued).
-        if (prefetch) wait_vm_n<LPT>();
-        else wait_vm_n<0>();
+        wait_vm_n<LPT>();
         mf.resolve();
 #pragma unroll
         for (int e = 0; e < 16; ++e) xs[e] = sacc[e];
@@ -472,10 +497,11 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       }
     }
 
-    wait_vm(in_flight_after(itn + 1));  // tile itn + 1 has landed
+    wait_vm_n<(KV_PD - 1) * PARTS>();  // tile itn + 1 has landed
     wait_lgkm0();
     phase_barrier();
   }
+  wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
 
   // Epilogue.  The loop ended on a barrier after every wave's last LDS read,
   // so the ring is free.  Each wave rounds its rows and stages them in its own
@@ -599,7 +625,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
                 VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
   static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
-  __shared__ __attribute__((aligned(1024))) char lds[DQ_NS * STAGE];  // [stage][K | V]
+  // [stage][K | V (| bits)], then a 1 KiB block that DMA parts past the last
+  // tile land in (nothing reads it)
+  __shared__ __attribute__((aligned(1024))) char lds[DQ_NS * STAGE + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -623,8 +651,11 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
   }
   if (qw >= p.Sq) wlim = 0;
-  const int n_tiles = lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0;
-  const int w_tiles = wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0;
+  // wave-uniform by construction; readfirstlane keeps them in SGPRs
+  const int n_tiles =
+      __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0);
+  const int w_tiles =
+      __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0);
 
   u32x4 qf[SKQ], gf[SKV];
   float lse2, delta;  // -safe(lse) in exp2 units, -delta
@@ -695,20 +726,43 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
   const uint32_t voff = (lane >> 2) * vs_b + (4 * (w % QGV) + swz_chunk) * 16;
+  // Every iteration issues its parts: those of a tile past the last one read
+  // past the buffer range (zeros, no memory access) into the spare LDS
+  // block, so the count of loads in flight is the same on every iteration
+  // and no branch guards an issue.  Per tile, computed once: its first row's
+  // byte offset in K and V and its stage offset from the spare block, masked
+  // by keep (all ones for a real tile, else 0 -- masks, not selects, which
+  // the compiler would turn into branches between the MFMA steps).
+  const uint32_t spare = lds0 + DQ_NS * STAGE;
+  struct DmaTile {
+    uint32_t krow, vrow, st, keep, far;
+    int tile;
+  };
+  auto dma_tile = [&](int tile) {
+    DmaTile d;
+    d.tile = tile;
+    d.keep = ~static_cast<uint32_t>((n_tiles - 1 - tile) >> 31);  // sign fill
+    d.far = ~d.keep & 0x80000000u;  // offsets >= 2^31 are past every range
+    d.krow = (static_cast<uint32_t>(tile * KT) * ks_b) | d.far;
+    d.vrow = (static_cast<uint32_t>(tile * KT) * vs_b) | d.far;
+    d.st = (lds0 + (tile % DQ_NS) * STAGE - spare) & d.keep;
+    return d;
+  };
   // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
-  auto issue_part = [&](int tile, int u) {
-    const uint32_t st = lds0 + (tile % DQ_NS) * STAGE;
+  auto issue_part = [&](const DmaTile &d, int u) {
     if (u < KPARTS) {
       const int n = w + NW * u;
-      dma16(kdesc, st + n * 1024, koff, static_cast<uint32_t>(tile * KT + 16 * (n / QGK)) * ks_b);
+      dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
+            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
     } else {
       const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, st + TILE_K + n * 1024, voff, static_cast<uint32_t>(tile * KT + 16 * (n / QGV)) * vs_b);
+      dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
+            d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
     }
   };
   // Dropout: the wave's 32 keep-bit words of the tile as one 8-lane part
   // (rows past the (b, hq) slice read as zero; rows past Sq are unused).
-  auto issue_bits = [&](int tile) {
+  auto issue_bits = [&](const DmaTile &t) {
     if constexpr (DR) {
       const DropDesc &d = p.drop;
       const u32x4 bdesc = make_desc(d.bits + (static_cast<int64_t>(b) * p.Hq + hq) * d.nkt * d.sqp,
@@ -718,18 +772,15 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
                    "v_lshlrev_b32 %0, 4, %0"
                    : "=v"(loff));
       if (lane < 8)
-        dma16(bdesc, lds0 + (tile % DQ_NS) * STAGE + TILE_K + TILE_V + w * 128, loff,
-              (static_cast<uint32_t>(tile) * d.sqp + qw) * 4);
+        dma16(bdesc, spare + t.st + ((TILE_K + TILE_V + w * 128) & t.keep), loff,
+              ((static_cast<uint32_t>(t.tile) * d.sqp + qw) * 4) | t.far);
     }
   };
   auto issue = [&](int tile) {
+    const DmaTile d = dma_tile(tile);
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) issue_part(tile, u);
-    issue_bits(tile);
-  };
-  auto in_flight_after = [&](int jn) {
-    const int later = min(DQ_PD - 1, n_tiles - 1 - jn);
-    return later > 0 ? later * PPT : 0;
+    for (int u = 0; u < LPT; ++u) issue_part(d, u);
+    issue_bits(d);
   };
 
   const TileReader<T, DK> rdk(lane);
@@ -769,9 +820,19 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // buffer range write zeros).
   zero_lds<NT>(lds + (DQ_NS - 1) * STAGE, TILE_K, tid);
   __syncthreads();
-  for (int t = 0; t < DQ_PD && t < n_tiles; ++t) issue(t);
-  wait_vm(in_flight_after(0));
+  for (int t = 0; t < DQ_PD; ++t) issue(t);
+  wait_vm_n<(DQ_PD - 1) * PPT>();
   __syncthreads();
+
+  // Tiles from j_edge on need masking (the causal diagonal, a ragged end, a
+  // key mask or a general mask); those before it are interior.
+  int j_edge = kv_end / KT;
+  if (MK != 0 || keymask) j_edge = 0;
+  if (causal) {
+    const int64_t d = static_cast<int64_t>(qw) + p.offset - (KT - 1);
+    const int jc = d < 0 ? 0 : static_cast<int>(min(d / KT + 1, static_cast<int64_t>(INT32_MAX)));
+    j_edge = min(j_edge, jc);
+  }
 
   // MFMA block of tile j: S_j^T, dP_j^T (k-step i each) and dQ MFMA i of the
   // previous tile (value block i % PDT, key k-step i / PDT); fragments two
@@ -788,6 +849,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     const char *kt = lds + (j % DQ_NS) * STAGE;
     const char *vt = kt + TILE_K;
     const char *kp = lds + ((j + DQ_NS - 1) % DQ_NS) * STAGE;
+    const DmaTile dt_next = dma_tile(nt);
     constexpr int FD = 2;
     u32x4 kr[FD + 1], vr[FD + 1], kc[FD + 1];
     auto load = [&](int i) {
@@ -797,7 +859,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     };
     s = f32x16{};
     dp = f32x16{};
-    if (nt >= 0) issue_bits(nt);
+    issue_bits(dt_next);
 #pragma unroll
     for (int i = 0; i < FD; ++i) load(i);
     __builtin_amdgcn_sched_barrier(0);
@@ -807,19 +869,17 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
       if (i < SKV) dp = mfma32<T>(vr[i % (FD + 1)], gf[i], dp);
       if (i < SKQ) acc[i % PDQ] = mfma32<T>(kc[i % (FD + 1)], pd[i / PDQ], acc[i % PDQ]);
       if (i + FD < STEPS) load(i + FD);
-      if (nt >= 0 && (i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
+      if ((i & 1) && (i >> 1) < LPT) issue_part(dt_next, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  auto grad = [&](int j, int nt) {
+  auto grad = [&](int j, int) {
     const int kv0 = j * KT;
     float x[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) x[i] = s[i];
-    const bool edge = MK != 0 || (kv0 + KT > kv_end) || keymask ||
-                      (causal && static_cast<int64_t>(kv0 + KT - 1) > qw + p.offset);
-    if (edge) {
+    if (j >= j_edge) {
       const int lim_l = klim - kv0 - 4 * h;
       if constexpr (MK == 0) {
         unsigned kbits = ~0u;
@@ -835,7 +895,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
           x[i] = ok ? x[i] : -INFINITY;
         }
       } else {
-        wait_vm(nt >= 0 ? LPT : 0);  // the mask loads; tile nt's parts stay in flight
+        wait_vm_n<LPT>();  // the mask loads; the next tile's parts stay in flight
         if constexpr (mask_vec(MK)) {
           mf.resolve_vec<mes>();
           mf.unpack<mes>(h);
@@ -864,9 +924,9 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     }
   };
 
-  auto next_dma = [&](int j) { return j + DQ_PD < n_tiles ? j + DQ_PD : -1; };
-  auto it_end = [&](int j) {
-    wait_vm(in_flight_after(j + 1));
+  auto next_dma = [&](int j) { return j + DQ_PD; };
+  auto it_end = [&](int) {
+    wait_vm_n<(DQ_PD - 1) * PPT>();  // tile j + 1 has landed
     wait_lgkm0();
     phase_barrier();
   };
@@ -883,9 +943,10 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     ++j;
   }
   for (; j <= n_tiles; ++j) {
-    if (next_dma(j) >= 0) issue(next_dma(j));
+    issue(next_dma(j));
     it_end(j);
   }
+  wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
 
   // dQ rows leave through LDS (free after the last barrier, all loads waited
   // for): each wave rounds its 32 rows into its own slice -- row r at r * 2D

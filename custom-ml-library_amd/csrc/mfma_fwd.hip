@@ -163,25 +163,41 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // read row 0 into the spare LDS block, so the count of loads in flight is
   // the same on every iteration and no branch guards an issue.
   const uint32_t spare = lds0 + NS * STAGE;
-  auto issue_part = [&](int tile, int u) {
-    // keep = all ones for a real tile, else 0: masks instead of selects, which
-    // the compiler would turn into branches between the MFMA steps
-    const uint32_t keep =
-        __builtin_amdgcn_readfirstlane(0u - static_cast<uint32_t>(tile < n_tiles));
-    const uint32_t st = lds0 + (tile % NS) * STAGE - spare;
+  // Per-tile DMA state, computed once per tile: the byte offset of its first
+  // row in K and V, and its stage offset from the spare block masked by keep
+  // (all ones for a real tile, else 0 -- masks instead of selects, which the
+  // compiler turns into branches between the MFMA steps).  A tile past the
+  // last one reads past the buffer range (zeros, no memory access) into the
+  // spare block.
+  struct DmaTile {
+    uint32_t krow, vrow, st, keep;
+  };
+  auto dma_tile = [&](int tile) {
+    DmaTile d;
+    // all ones iff n_tiles - 1 - tile >= 0 (sign fill of the difference)
+    d.keep = ~static_cast<uint32_t>((n_tiles - 1 - tile) >> 31);
+    // a tile past the last one reads at offsets >= 2^31, past the range
+    const uint32_t far = ~d.keep & 0x80000000u;
+    d.krow = (static_cast<uint32_t>(tile * BN) * ks_b) | far;
+    d.vrow = (static_cast<uint32_t>(tile * BN) * vs_b) | far;
+    d.st = (lds0 + (tile % NS) * STAGE - spare) & d.keep;
+    return d;
+  };
+  auto issue_part = [&](const DmaTile &d, int u) {
     if (u < KPARTS) {
       const int n = w + NW * u;
-      dma16(kdesc, spare + ((st + n * 1024) & keep), koff,
-            (static_cast<uint32_t>(tile * BN + 16 * (n / QGK)) * ks_b) & keep);
+      dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
+            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
     } else {
       const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, spare + ((st + TILE_K + n * 1024) & keep), voff,
-            (static_cast<uint32_t>(tile * BN + 16 * (n / QGV)) * vs_b) & keep);
+      dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
+            d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
     }
   };
   auto issue = [&](int tile) {
+    const DmaTile d = dma_tile(tile);
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) issue_part(tile, u);
+    for (int u = 0; u < LPT; ++u) issue_part(d, u);
   };
 
   const TileReader<T, DK> rdk(lane);
@@ -193,6 +209,10 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   u32x4 pb[2];  // P^T of the previous tile, packed: B operands of its 2 PV k-steps
   float m = -INFINITY, l = 0.f;
   const float sl = a.sl;
+  // Kept with m, recomputed only when it moves: raw row maxima above thr =
+  // (m + kTau) / scale trigger a rescale, and nbase = -m (0 while m = -inf)
+  // is the exponent offset.
+  float thr = -INFINITY, nbase = 0.f;
   // This lane's allowed keys are [0, klim) (cache end and causal window),
   // further thinned by the key mask row kmask_b when there is one.
   int klim = kv_end;
@@ -218,6 +238,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   MaskFetch mf;
   // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
   const float slx = mask_kind(MK) >= 2 ? 1.f : a.sl;
+  const float inv_slx = 1.f / slx;
 
   // The first MFMA block runs PV with P = 0 against the V half of stage
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
@@ -255,6 +276,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     }
     const char *kt = lds + (j % NS) * STAGE;
     const char *vt = lds + ((j + NS - 1) % NS) * STAGE + TILE_K;
+    const DmaTile dt_next = dma_tile(nt);
     constexpr int FD = 2;  // fragment prefetch distance, in steps
     u32x4 kf[FD + 1], vf[FD + 1];
     auto load = [&](int i) {
@@ -271,7 +293,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       if (i < SKS) s = mfma32<T>(kf[i % (FD + 1)], qf[i], s);
       if (i < PVS) oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
       if (i + FD < STEPS) load(i + FD);
-      if ((i & 1) && (i >> 1) < LPT) issue_part(nt, i >> 1);
+      if ((i & 1) && (i >> 1) < LPT) issue_part(dt_next, i >> 1);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -308,21 +330,22 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
         mask_scores<MK>(x, mf, p.mask.dtype, -64, lim, sl);
       }
     }
-    // row max: a v_max3 chain (fmaxf would add NaN canonicalisations)
-    float mx = max3f(x[0], x[1], x[2]);
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 3; i < 15; i += 2) mx = max3f(mx, x[i], x[i + 1]);
-    mx = max3f(mx, x[15], x[15]);
-    const float mt = half_swap_max3(mx) * slx;
-    if (__ballot(mt > m + kTau) != 0ull) {
-      const float m_new = fmaxf(m, mt);
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
+    // the partner's max joins in one v_max3 (fmaxf would canonicalise both
+    // values the permlane returns)
+    const float mxr = half_swap_max3(mx);
+    if (__ballot(mxr > thr) != 0ull) {
+      const float m_new = fmaxf(m, mxr * slx);
       const float corr = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
       m = m_new;
+      thr = (m + kTau) * inv_slx;
+      nbase = m == -INFINITY ? 0.f : -m;
       l *= corr;
 #pragma unroll
       for (int dt = 0; dt < PDT; ++dt) oacc[dt] *= corr;
     }
-    const float base = m == -INFINITY ? 0.f : m;
     // Dropout: the denominator sums the undropped probabilities (the
     // reference normalises first, attention.py:139-144); PV takes P * mask.
     uint64_t dw[4];
@@ -342,8 +365,8 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < 16; i += 2) {
-      float p0 = fast_exp2(fmaf(x[i], slx, -base));
-      float p1 = fast_exp2(fmaf(x[i + 1], slx, -base));
+      float p0 = fast_exp2(fmaf(x[i], slx, nbase));
+      float p1 = fast_exp2(fmaf(x[i + 1], slx, nbase));
       l += p0 + p1;  // fp32 sum of the unrounded probabilities, as the reference
       if constexpr (DR) {
         p0 = dropout_keeps(p.drop, dw, i) ? p0 * p.drop.scale : 0.f;
