@@ -175,14 +175,23 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   const uint32_t lrow = lane >> 2;
   // Tile itn is query tile qi = itn % n_qt of query head hk rep + itn / n_qt;
   // TileIdx walks that order without a division per tile.
+  // It also carries the byte addresses of the tile's Q, dO and row-value
+  // slices, advanced by one head when the walk wraps (no 64-bit products per
+  // tile).
+  const uint64_t qstep = static_cast<uint64_t>(a.qk.s1) * 2, gstep = static_cast<uint64_t>(a.dout.s1) * 2;
+  const uint64_t rstep = static_cast<uint64_t>(p.Sq) * 4;
   struct TileIdx {
     int itn, r, qi;
+    uint64_t qa, ga, ra;
   };
   auto tile_next = [&](TileIdx t) {
     ++t.itn;
     const bool wrap = ++t.qi == n_qt;
     t.qi = wrap ? 0 : t.qi;
     t.r += wrap ? 1 : 0;
+    t.qa += wrap ? qstep : 0;
+    t.ga += wrap ? gstep : 0;
+    t.ra += wrap ? rstep : 0;
     return t;
   };
   // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
@@ -199,6 +208,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     uint32_t st, keep, far;
     int q0, hq;
     u32x4 qdesc, gdesc;
+    uint64_t ra;
   };
   auto tile_dma = [&](TileIdx x) {
     TileDma t;
@@ -207,8 +217,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     t.keep = ~static_cast<uint32_t>((n_iter - 1 - x.itn) >> 31);  // sign fill
     t.far = ~t.keep & 0x80000000u;
     t.st = (ring0 + (x.itn % KV_NS) * STAGE_B - spare) & t.keep;
-    t.qdesc = make_desc(head_ptr<T>(a.qk, b, t.hq), static_cast<uint32_t>(p.Sq) * qs_b);
-    t.gdesc = make_desc(head_ptr<T>(a.dout, b, t.hq), static_cast<uint32_t>(p.Sq) * gs_b);
+    t.qdesc = make_desc(reinterpret_cast<const void *>(x.qa), static_cast<uint32_t>(p.Sq) * qs_b);
+    t.gdesc = make_desc(reinterpret_cast<const void *>(x.ga), static_cast<uint32_t>(p.Sq) * gs_b);
+    t.ra = x.ra;
     return t;
   };
   // Parts u < QPARTS are Q blocks, the rest dO blocks (a compile-time split).
@@ -226,7 +237,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       dma16(t.gdesc, spare + t.st + ((TILE_Q + n * 1024) & t.keep), gvoff,
             (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
     } else {
-      const u32x4 rdesc = make_desc(rowv + static_cast<int64_t>(t.hq - hk * p.rep) * p.Sq,
+      const u32x4 rdesc = make_desc(reinterpret_cast<const void *>(t.ra),
                                     static_cast<uint32_t>(p.Sq) * 4);
       // lane * 16, recomputed here rather than held in a register all loop
       uint32_t loff;
@@ -315,7 +326,10 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 
   // No zeroing: every LDS byte the loop reads is written by a DMA load first
   // (lanes past a buffer's range write zeros).
-  TileIdx nxt_idx{0, 0, 0};
+  const TileIdx first{0, 0, 0, reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep)),
+                      reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep)),
+                      reinterpret_cast<uint64_t>(rowv)};
+  TileIdx nxt_idx = first;
   for (int t = 0; t < KV_PD; ++t) {
     issue(nxt_idx);
     nxt_idx = tile_next(nxt_idx);
@@ -332,7 +346,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   }
   __syncthreads();
 
-  TileIdx cur_idx{0, 0, 0};
+  TileIdx cur_idx = first;
   for (int itn = 0; itn < n_iter; ++itn) {
     // Tile itn + 2 is issued between the S / dP MFMA steps below, so a wave
     // never stalls on the address unit before its first MFMA.
