@@ -271,10 +271,25 @@ def bench_decode_int8(ts, torch, steps, warmup, dec_inputs):
     shape = (DEC_B, DEC_H, DEC_CAP, DEC_D)
     k8, v8 = (torch.empty(shape, dtype=torch.int8, device="cuda") for _ in range(2))
     ks, vs = (torch.empty(shape[:3] + (1,), dtype=torch.float32, device="cuda") for _ in range(2))
-    for src, codes, scales in ((k_raw, k8, ks), (v_raw, v8, vs)):
+    def append(src, codes, scales):
         _lib.check(lib.tsattn_kv_append_int8(_lib.F16, DEC_B, DEC_H, DEC_CAP, DEC_D,
                                              ctypes.byref(_view(src)), ctypes.byref(_view(codes)),
                                              ctypes.byref(_view(scales)), 0, stream), "append")
+
+    for src, codes, scales in ((k_raw, k8, ks), (v_raw, v8, vs)):
+        append(src, codes, scales)
+    # the quantising append itself (whole cache, one tensor per launch), timed
+    # with the library's HIP-event probes on its stream
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    for _ in range(3):
+        append(k_raw, k8, ks)
+    torch.cuda.synchronize()
+    _lib.profile_enable(False)
+    n_app, t_app = _lib.profile_read()["kv_append_int8"]
+    app_ms = t_app / n_app
+    app_bytes = float(DEC_B * DEC_H * DEC_CAP) * (DEC_D * 2 + DEC_D + 4)  # fp16 in, int8 + scale out
     kv_len = torch.as_tensor(lens.astype(np.int32), device="cuda")
     prob = _problem(DEC_B, DEC_H, DEC_H, 1, DEC_CAP, DEC_D, DEC_D, _lib.F16, 1 / math.sqrt(DEC_D),
                     False, 0)
@@ -318,6 +333,12 @@ def bench_decode_int8(ts, torch, steps, warmup, dec_inputs):
         "roofline": {
             "kernel": "decode_split_int8", "bound": "hbm", "achieved": round(achieved, 1),
             "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBPS, 4),
+        },
+        "append": {
+            "kernel": "kv_append_int8", "mean_ms": round(app_ms, 4), "bytes_per_launch": app_bytes,
+            "roofline": {"bound": "hbm", "achieved": round(app_bytes / (app_ms * 1e-3) / 1e9, 1),
+                         "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                         "frac": round(app_bytes / (app_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)},
         },
         "config": {"workload": "decode_int8cache_f16q_b64h32d128_len512_8192", "batch": DEC_B,
                    "heads": DEC_H, "head_dim": DEC_D, "cache_capacity": DEC_CAP},

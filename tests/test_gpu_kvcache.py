@@ -68,6 +68,63 @@ def test_append_is_bit_exact_with_the_reference_quantiser(dtype, dim):
     assert (codes[1, :, pos + 2] == torch.as_tensor(want_q[1, :, 2], device="cuda")).all()
 
 
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+@pytest.mark.parametrize("d,t", [(64, 509), (128, 512), (256, 501)])
+def test_append_many_rows_bit_exact_near_rounding_ties(dtype, d, t):
+    """Thousands of rows through the vectorised append, with row counts per
+    head that do and do not fill the kernel's row chunks: random rows (whose
+    quotients come within 5e-5 of a half-integer many times: the kernel
+    multiplies by 1 / scale and divides only there), rows whose quotients are
+    exact half-integers (scale exactly 1), and rows of tiny values (scale at
+    the 1e-8 floor); codes and scales bit-identical to the reference
+    quantiser."""
+    say(f"append int8 many rows {dtype} D{d} T{t}")
+    rng = np.random.default_rng(11)
+    b, h, pos = 2, 8, 3
+    cap = pos + t + 5
+    x = rng.standard_normal((b, h, t, d)).astype(np.float32) * 4
+    # rows with max 127 (scale exactly 1): quotients k + 0.5 and their neighbours
+    ties = (rng.integers(-120, 120, (b, h, 64, d)) + 0.5).astype(np.float32)
+    ties[..., 0] = 127.0
+    x[:, :, :64] = ties
+    x[:, :, 64:96] *= np.float32(1e-9)  # scales at the 1e-8 floor
+    x = round_to(x, dtype)
+    src = abi.dev_tensor(x, dtype)
+    codes = torch.zeros((b, h, cap, d), dtype=torch.int8, device="cuda")
+    scales = torch.zeros((b, h, cap, 1), dtype=torch.float32, device="cuda")
+    abi.kv_append_int8(src, codes, scales, pos)
+    want_q, want_s = A.quantize_int8(x)
+    np.testing.assert_array_equal(codes[:, :, pos:pos + t].cpu().numpy(), want_q)
+    np.testing.assert_array_equal(scales[:, :, pos:pos + t].cpu().numpy(), want_s)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def test_append_scale_is_exact_for_every_16bit_row_maximum(dtype):
+    """One row per finite non-negative fp16 / bf16 value m, holding m and
+    smaller values of both signs: the kernel's division-free row scale
+    max(m / 127, 1e-8) and every code equal the reference quantiser's, over
+    the whole range of the format."""
+    say(f"append int8 every row maximum {dtype}")
+    if dtype == "float16":
+        m = np.arange(0, 0x7C00, dtype=np.uint16).view(np.float16).astype(np.float32)
+    else:
+        m = (np.arange(0, 0x7F80, dtype=np.uint32) << 16).view(np.float32)
+    d = 64
+    rng = np.random.default_rng(5)
+    x = m[:, None] * rng.uniform(-1.0, 1.0, (m.size, d)).astype(np.float32)
+    x[:, 0] = m
+    x = round_to(x, dtype)
+    rows = m.size
+    x = x.reshape(1, 1, rows, d)
+    src = abi.dev_tensor(x, dtype)
+    codes = torch.zeros((1, 1, rows, d), dtype=torch.int8, device="cuda")
+    scales = torch.zeros((1, 1, rows, 1), dtype=torch.float32, device="cuda")
+    abi.kv_append_int8(src, codes, scales, 0)
+    want_q, want_s = A.quantize_int8(x)
+    np.testing.assert_array_equal(scales.cpu().numpy(), want_s)
+    np.testing.assert_array_equal(codes.cpu().numpy(), want_q)
+
+
 def _int8_cache(rng, b, hkv, cap, d, dtype):
     k = round_to(rng.standard_normal((b, hkv, cap, d)).astype(np.float32), dtype)
     v = round_to(rng.standard_normal((b, hkv, cap, d)).astype(np.float32), dtype)
