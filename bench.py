@@ -53,7 +53,7 @@ B, H, S, D = 16, 16, 2048, 128
 DEC_B, DEC_H, DEC_D, DEC_CAP, DEC_LO, DEC_HI = 64, 32, 128, 8192, 512, 8192
 PF_B, PF_H, PF_S, PF_D, PF_LO = 2, 32, 32768, 128, 16384
 LM_LAYERS, LM_DIM, LM_HEADS, LM_FFN, LM_VOCAB, LM_B, LM_S = 6, 512, 8, 2048, 32000, 8, 1024
-ATTN_KERNELS = ("fwd_mfma", "bwd_dkdv_mfma", "bwd_dq_mfma", "generic_fwd",
+ATTN_KERNELS = ("fwd_mfma", "bwd_dkdv_mfma", "bwd_dq_ds", "bwd_dq_mfma", "bwd_rows", "generic_fwd",
                 "generic_bwd_delta", "generic_bwd_dq", "generic_bwd_dkdv", "key_mask_lengths",
                 "decode_split", "decode_merge", "rope")
 
@@ -128,8 +128,10 @@ def bench_fwd_bwd(ts, torch, steps, warmup):
     ms = elapsed / steps * 1e3
     # algorithmic FLOP per launch: forward kernel = QK^T + PV (2 GEMMs);
     # dK/dV kernel = S recompute, dP, dV, dK (4 of the backward's 5 GEMMs);
-    # dQ kernel = dQ (1 GEMM; its S/dP recompute is overhead, not counted)
-    work = {"fwd_mfma": fwd, "bwd_dkdv_mfma": 2.0 * fwd, "bwd_dq_mfma": 0.5 * fwd}
+    # dQ kernel = dQ (1 GEMM: from the stored dS, or with an S / dP recompute
+    # that is overhead, not counted)
+    work = {"fwd_mfma": fwd, "bwd_dkdv_mfma": 2.0 * fwd, "bwd_dq_ds": 0.5 * fwd,
+            "bwd_dq_mfma": 0.5 * fwd}
     per_kernel = {n: {"launches": c, "mean_ms": t / max(c, 1)} for n, (c, t) in kernels.items()}
     dom = max((n for n in per_kernel if n in work), key=lambda n: per_kernel[n]["mean_ms"])
     achieved = work[dom] / (per_kernel[dom]["mean_ms"] * 1e-3) / 1e12

@@ -195,15 +195,24 @@ size_t with_bits(size_t base, const tsattn::Problem &pr) {
   return pr.drop.on ? round256(base) + tsattn::dropout_bits_bytes(pr) : base;
 }
 
+// Then (MFMA kernels) room for stored dS, with which the dK/dV kernel runs
+// first and dQ takes one GEMM instead of recomputing S and dP; a smaller
+// workspace runs the recomputing dQ kernel.
+size_t with_ds(size_t base, const tsattn::Problem &pr, int dtype) {
+  if (!tsattn::mfma_supported(pr, dtype)) return base;
+  const size_t ds = tsattn::mfma_ds_bytes(pr);
+  return ds ? round256(base) + ds : base;
+}
+
 size_t backward_workspace(const tsattn_problem *p) {
   const size_t base = rows_workspace(p);
   tsattn::Problem pr;
-  if (!base || !(p->dropout_p > 0.0) || check_problem(p, &pr)) return base;
-  return with_bits(base, pr);
+  if (!base || check_problem(p, &pr)) return base;
+  return with_ds(with_bits(base, pr), pr, p->dtype);
 }
 
-size_t rope_backward_workspace(const tsattn::Problem &pr) {
-  return with_bits(rope_rows_workspace(pr), pr);
+size_t rope_backward_workspace(const tsattn::Problem &pr, int dtype) {
+  return with_ds(with_bits(rope_rows_workspace(pr), pr), pr, dtype);
 }
 
 int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const tsattn_view *q,
@@ -245,10 +254,15 @@ int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const t
       if ((rc = hip_status(tsattn::launch_dropout_bits(pr, pr.drop.bits, st), "dropout bits launch")))
         return rc;
     }
+    // stored dS when the workspace has room for it (as sized by the query)
+    void *ds = nullptr;
+    const size_t ds_bytes = tsattn::mfma_ds_bytes(pr);
+    const size_t ds_off = round256(with_bits(rows_need, pr));
+    if (ds_bytes && workspace_bytes >= ds_off + ds_bytes) ds = static_cast<char *>(workspace) + ds_off;
     g_last_path = 2;
     return hip_status(tsattn::launch_mfma_backward(pr, p->dtype, vq, vk, vv, vo, vg,
                                                    static_cast<const float *>(lse), vdq, vdk,
-                                                   vdv, static_cast<float *>(workspace), st),
+                                                   vdv, static_cast<float *>(workspace), ds, st),
                       "mfma backward launch");
   }
   if (rope) return rope_unsupported();
@@ -347,7 +361,7 @@ size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p) { return backward
 size_t tsattn_sdpa_backward_rope_workspace(const tsattn_problem *p) {
   tsattn::Problem pr;
   if (check_problem(p, &pr)) return 0;
-  return rope_backward_workspace(pr);
+  return rope_backward_workspace(pr, p->dtype);
 }
 
 int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,

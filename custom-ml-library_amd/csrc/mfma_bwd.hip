@@ -55,7 +55,16 @@ struct BwdArgs {
   float *delta;
   float sl;      // scale * log2(e)
   float scale;   // final gradient scale
+  // Stored dS (NULL: the dQ kernel recomputes S and dP itself).  Per (b, q
+  // head) ds_nqt x ds_nkt tiles of 32 query rows x 32 keys; tile (qt, kt) at
+  // byte ((bh ds_nqt + qt) ds_nkt + kt) * 2 KiB, as the dK/dV kernel's lanes
+  // hold it: dS[q][k] (q, k within the tile, q = 4 m + r) at
+  // (m / 4) KiB + (m % 2) 512 + 16 k + ((m / 2) % 2) 8 + 2 r.
+  char *ds;
+  int ds_nqt, ds_nkt;
 };
+
+constexpr int DS_TILE = 2048;  // bytes of one stored dS tile
 
 template <typename T>
 __device__ __forceinline__ T *mut(View v) {
@@ -180,9 +189,13 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // tile).
   const uint64_t qstep = static_cast<uint64_t>(a.qk.s1) * 2, gstep = static_cast<uint64_t>(a.dout.s1) * 2;
   const uint64_t rstep = static_cast<uint64_t>(p.Sq) * 4;
+  // With stored dS, da is the byte offset of the tile's dS (query tile
+  // q0 / 32, this wave's key tile): one query tile on, or on to the next head.
+  const uint64_t dstep = static_cast<uint64_t>(a.ds_nkt) * DS_TILE;
+  const uint64_t dwrap = (static_cast<uint64_t>(a.ds_nqt) - n_qt + 1) * dstep;
   struct TileIdx {
     int itn, r, qi;
-    uint64_t qa, ga, ra;
+    uint64_t qa, ga, ra, da;
   };
   auto tile_next = [&](TileIdx t) {
     ++t.itn;
@@ -192,6 +205,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     t.qa += wrap ? qstep : 0;
     t.ga += wrap ? gstep : 0;
     t.ra += wrap ? rstep : 0;
+    t.da += wrap ? dwrap : dstep;
     return t;
   };
   // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
@@ -328,7 +342,9 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // (lanes past a buffer's range write zeros).
   const TileIdx first{0, 0, 0, reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep)),
                       reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep)),
-                      reinterpret_cast<uint64_t>(rowv)};
+                      reinterpret_cast<uint64_t>(rowv),
+                      ((static_cast<uint64_t>(b) * p.Hq + hk * p.rep) * a.ds_nqt + q_start / QT) * dstep +
+                          static_cast<uint64_t>(kw / 32) * DS_TILE};
   TileIdx nxt_idx = first;
   for (int t = 0; t < KV_PD; ++t) {
     issue(nxt_idx);
@@ -344,6 +360,13 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     else if (i < SKQ) asm volatile("" : "+v"(kf[i]));
     else asm volatile("" : "+v"(vf[i]));
   }
+  if (a.ds) {
+    // two loads past the range (zeros into the spare block, no memory
+    // access) in place of a previous tile's two dS stores: the loop's waits
+    // then count the same on every tile
+    dma16(make_desc(a.ds, 0), spare, qvoff, 0x80000000u);
+    dma16(make_desc(a.ds, 0), spare, qvoff, 0x80000000u);
+  }
   __syncthreads();
 
   TileIdx cur_idx = first;
@@ -356,6 +379,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     const char *gt = qt + TILE_Q;
     const float *rv = reinterpret_cast<const float *>(qt + TILE_Q + TILE_G);
     const int hq = hk * p.rep + cur_idx.r, q0 = q_start + cur_idx.qi * QT;
+    const uint64_t ds_at = cur_idx.da;
     cur_idx = tile_next(cur_idx);
 
     constexpr int FD = DKDV_FD;
@@ -511,7 +535,26 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       }
     }
 
-    wait_vm_n<(KV_PD - 1) * PARTS>();  // tile itn + 1 has landed
+    // Stored dS (dQ as one GEMM after this kernel): the wave's packed dS
+    // registers as they are, pd[0] then pd[1], 1 KiB per wave store (the dQ
+    // kernel transposes them with LDS transpose reads).  Stores count in
+    // vmcnt: the tile wait leaves these two in flight too.
+    if (a.ds) {
+      // lane * 16, recomputed here rather than held in a register all loop
+      uint32_t l16;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(l16));
+      char *dst = a.ds + ds_at + l16;
+      *reinterpret_cast<u32x4 *>(dst) = pd[0];
+      *reinterpret_cast<u32x4 *>(dst + 1024) = pd[1];
+      // tile itn + 1 has landed; the previous tile's stores may still be in
+      // flight (they were issued after its loads; before the first tile two
+      // empty loads stand in for them)
+      wait_vm_n<(KV_PD - 1) * PARTS + 4>();
+    } else {
+      wait_vm_n<(KV_PD - 1) * PARTS>();  // tile itn + 1 has landed
+    }
     wait_lgkm0();
     phase_barrier();
   }
@@ -1006,12 +1049,297 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Row values when the dK/dV kernel runs first (stored dS): nd = -delta, the
+// fp32 sum over the row of dO O, and nl = -safe(lse) / scale, the values the
+// dQ kernel's prologue writes otherwise; with RoPE folded in, also the
+// rotated query rows the dK/dV kernel reads.  A row is G = DV / 8 lanes, one
+// 16-byte piece each, 64 / G rows per wave.
+// ---------------------------------------------------------------------------
+template <typename T, int DK, int DV>
+__global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a) {
+  constexpr int G = DV / 8, RPW = 64 / G;
+  const Problem &p = a.p;
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  const int lane = threadIdx.x & 63, g = lane % G;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * (NT / 64) + (threadIdx.x >> 6)) * RPW + lane / G;
+  if (row >= rows) return;  // a row's G lanes leave together
+  const int qrow = static_cast<int>(row % p.Sq);
+  const int bh = static_cast<int>(row / p.Sq), b = bh / p.Hq, hq = bh - b * p.Hq;
+  const T *go = head_ptr<T>(a.dout, b, hq) + static_cast<int64_t>(qrow) * a.dout.s2 + 8 * g;
+  const T *oo = head_ptr<T>(a.o, b, hq) + static_cast<int64_t>(qrow) * a.o.s2 + 8 * g;
+  const u32x4 gv = ld16(go), ov = ld16(oo);
+  const T *ge = reinterpret_cast<const T *>(&gv);
+  const T *oe = reinterpret_cast<const T *>(&ov);
+  float dsum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
+  if (g == 0) {
+    const float l = a.lse[row];
+    a.delta[row] = -dsum;
+    a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
+  }
+  if (p.rope.R > 0) {
+    const T *qi = head_ptr<T>(a.q, b, hq) + static_cast<int64_t>(qrow) * a.q.s2;
+    T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+#pragma unroll
+    for (int ch = g; ch < DK / 8; ch += G) {
+      u32x4 v = ld16(qi + 8 * ch);
+      rotate_chunk<T>(v, p.rope, p.rope.qpos0 + qrow, 4 * ch, false);
+      *reinterpret_cast<u32x4 *>(qk + 8 * ch) = v;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ from stored dS: dQ^T = scale K^T dS^T over the key tiles of each row
+// (one GEMM; the dK/dV kernel left dS in the workspace).  One workgroup = 256
+// query rows of one (b, q head), 4 waves x 64 rows (two 32-row subtiles
+// sharing every K^T fragment), two workgroups per CU.  Per 32-key tile, K
+// (shared) and each wave's two dS tiles stream global -> LDS by DMA loads
+// into 3-stage rings, issued two tiles ahead; K^T and dS^T fragments come
+// from LDS transpose reads; one fence-free barrier per tile.  dS tiles past a
+// subtile's causal end, or past the rows, read as zeros (offsets past the
+// buffer range).
+// ---------------------------------------------------------------------------
+constexpr int QB2 = 256;          // query rows per workgroup
+constexpr int DS_PD = 2;          // tiles issued ahead
+constexpr int DS_NS = DS_PD + 1;  // ring stages: tile j is read in iteration j only
+
+template <typename T, int DK>
+__global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
+  constexpr int TILE_K = KT * DK * 2;
+  constexpr int KPARTS = TILE_K / 1024 / NW;  // K DMA loads per wave per tile
+  constexpr int LPT = KPARTS + 4;             // all DMA loads per wave per tile
+  constexpr int PDQ = DK / 32;                // 32-row blocks of dQ^T
+  constexpr int QGK = DK / 32;
+  constexpr int STEPS = 2 * PDQ;              // K^T fragments per tile (2 key k-steps)
+  constexpr int KRING = DS_NS * TILE_K;
+  constexpr int SRING = DS_NS * 2 * DS_TILE;  // per wave: two dS tiles per stage
+  constexpr int RINGS = KRING + NW * SRING;
+  constexpr int EPI = NW * 32 * 2 * DK;       // epilogue: 32 rows per wave at a time
+  static_assert(EPI <= RINGS, "epilogue slices fit in the rings");
+  static_assert(KPARTS >= 1 && KPARTS * NW * 1024 == TILE_K, "tile loads split evenly over the waves");
+  // K ring, the waves' dS rings, then a 1 KiB block that DMA parts past the
+  // last tile land in
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS + 1024];
+
+  const Problem &p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_qb = (p.Sq + QB2 - 1) / QB2;
+  const int total = n_qb * p.Hq * p.B;
+  const int logical = xcd_remap(blockIdx.x, total);
+  int bh, rank;
+  heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);  // 2 WG per CU
+  const int qb = n_qb - 1 - rank;  // long causal rows first
+  const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
+  const int q0 = qb * QB2, qw = q0 + 64 * w;
+  const int kv_end = kv_end_for(p, b);
+  // key tiles up to query row `last` (its cache end and causal window)
+  auto tiles_to = [&](int last) {
+    int64_t lim = kv_end;
+    if (p.causal) lim = min(lim, static_cast<int64_t>(last) + p.offset + 1);
+    return lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0;
+  };
+  const int n_tiles = __builtin_amdgcn_readfirstlane(tiles_to(min(q0 + QB2, p.Sq) - 1));
+  const int w_tiles = __builtin_amdgcn_readfirstlane(qw < p.Sq ? tiles_to(min(qw + 64, p.Sq) - 1) : 0);
+  const int s_tiles = __builtin_amdgcn_readfirstlane(qw < p.Sq ? tiles_to(min(qw + 32, p.Sq) - 1) : 0);
+
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2;
+  const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  // dS of this (b, q head); subtile s of this wave is query tile qw / 32 + s
+  const int64_t slice = static_cast<int64_t>(a.ds_nqt) * a.ds_nkt * DS_TILE;
+  const u32x4 sdesc = make_desc(a.ds + (static_cast<int64_t>(b) * p.Hq + hq) * slice,
+                                static_cast<uint32_t>(slice));
+  const uint32_t ds_row = static_cast<uint32_t>(a.ds_nkt * DS_TILE);
+  const uint32_t ds0 = static_cast<uint32_t>(qw / 32) * ds_row;
+  const uint32_t lds0 = lds_addr(lds);
+  const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
+  const uint32_t loff = lane * 16;
+  const uint32_t spare = lds0 + RINGS;
+  const uint32_t sring = lds0 + KRING + w * SRING;
+  // Per tile, as in the forward: every iteration issues the same loads; those
+  // of a tile past the last one read past the range into the spare block.
+  // Part u < KPARTS: this wave's u-th K block; then its dS tiles in four
+  // 1 KiB parts (subtile u / 2, half u % 2), past the range (zeros) beyond the
+  // subtile's causal end.
+  struct DmaTile {
+    uint32_t krow, kst, sst, keep, far0, far1, srow;
+  };
+  auto dma_tile = [&](int tile) {
+    DmaTile d;
+    d.keep = ~static_cast<uint32_t>((n_tiles - 1 - tile) >> 31);  // sign fill
+    const uint32_t far = ~d.keep & 0x80000000u;
+    d.krow = (static_cast<uint32_t>(tile * KT) * ks_b) | far;
+    d.kst = (lds0 + (tile % DS_NS) * TILE_K - spare) & d.keep;
+    d.sst = (sring + (tile % DS_NS) * 2 * DS_TILE - spare) & d.keep;
+    d.far0 = tile < s_tiles ? 0u : 0x80000000u;
+    d.far1 = tile < w_tiles ? 0u : 0x80000000u;
+    d.srow = ds0 + static_cast<uint32_t>(tile) * DS_TILE;
+    return d;
+  };
+  auto issue_part = [&](const DmaTile &d, int u) {
+    if (u < KPARTS) {
+      const int n = w + NW * u;
+      dma16(kdesc, spare + d.kst + ((n * 1024) & d.keep), koff,
+            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+    } else {
+      const int s = (u - KPARTS) >> 1, half = (u - KPARTS) & 1;
+      dma16_nt(sdesc, spare + d.sst + ((s * DS_TILE + half * 1024) & d.keep), loff,
+               (d.srow + s * ds_row + half * 1024) | (s ? d.far1 : d.far0));
+    }
+  };
+  // dS^T operand (16 keys of k-step ks x 32 queries) of one stored tile by
+  // transpose reads: the 16 lanes of a read group each name 4 queries of one
+  // key row (dS[4 m .. 4 m + 3][k] is 8 contiguous bytes of the tile), and
+  // lane (c, h) receives query c at keys 16 ks + 4 h .. + 3 (then + 8 ..),
+  // the key order of TileReader::cols.
+  const int i16 = lane & 15;
+  const uint32_t s_lo = ((lane >> 4) & 1) * 1024 + (i16 & 1) * 512 + ((i16 >> 1) & 1) * 8 +
+                        ((i16 >> 2) + 4 * h) * 16;
+  auto ds_frag = [&](const char *tile, int ks) {
+    const char *base = tile + s_lo + ks * 256;
+    const u32x2 lo = ds_read_tr<T>(reinterpret_cast<const T *>(base));
+    const u32x2 hi = ds_read_tr<T>(reinterpret_cast<const T *>(base + 128));
+    return u32x4{lo[0], lo[1], hi[0], hi[1]};
+  };
+
+  const TileReader<T, DK> rdk(lane);
+  f32x16 acc[PDQ][2];
+#pragma unroll
+  for (int dt = 0; dt < PDQ; ++dt) acc[dt][0] = acc[dt][1] = f32x16{};
+
+  for (int t = 0; t < DS_PD; ++t) {
+    const DmaTile d = dma_tile(t);
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) issue_part(d, u);
+  }
+  wait_vm_n<(DS_PD - 1) * LPT>();  // tile 0
+  __syncthreads();
+
+  // Iteration j: issue tile j + 2 among the MFMA steps, dQ^T += K_j^T dS_j^T
+  // for both subtiles, then wait for tile j + 1 and barrier.
+  auto iteration = [&](int j) {
+    const DmaTile dn = dma_tile(j + DS_PD);
+    const char *kt = lds + (j % DS_NS) * TILE_K;
+    const char *st = lds + KRING + w * SRING + (j % DS_NS) * 2 * DS_TILE;
+    u32x4 sf[2][2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) sf[s][ks] = ds_frag(st + s * DS_TILE, ks);
+    constexpr int FD = 2;
+    u32x4 kf[FD + 1];
+    auto load = [&](int i) { kf[i % (FD + 1)] = rdk.cols(kt, i / PDQ, i % PDQ); };
+#pragma unroll
+    for (int i = 0; i < FD; ++i) load(i);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      const int ks = i / PDQ, dt = i % PDQ;
+      acc[dt][0] = mfma32<T>(kf[i % (FD + 1)], sf[0][ks], acc[dt][0]);
+      acc[dt][1] = mfma32<T>(kf[i % (FD + 1)], sf[1][ks], acc[dt][1]);
+      if (i + FD < STEPS) load(i + FD);
+      if (i < LPT) issue_part(dn, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int u = STEPS; u < LPT; ++u) issue_part(dn, u);  // D = 64: one MFMA step short
+    wait_vm_n<(DS_PD - 1) * LPT>();  // tile j + 1 has landed
+    wait_lgkm0();
+    phase_barrier();
+  };
+  // Iterations past the wave's last tile only keep the DMA and barrier count.
+  auto idle = [&](int j) {
+    const DmaTile dn = dma_tile(j + DS_PD);
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) issue_part(dn, u);
+    wait_vm_n<(DS_PD - 1) * LPT>();
+    wait_lgkm0();
+    phase_barrier();
+  };
+  int j = 0;
+  for (; j < w_tiles; ++j) iteration(j);
+  for (; j < n_tiles; ++j) idle(j);
+  wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the rings
+
+  // dQ rows leave through LDS, 32 rows (one subtile) per wave at a time:
+  // each wave rounds them into its own slice -- row r at r * 2D bytes,
+  // 16-byte chunk q at q ^ (r % CPR) -- then reads back whole 16-byte chunks
+  // of rows for coalesced stores.  Lane holds dQ^T[d = 32 dt + 8 g + 4 h +
+  // r][row c] of each subtile.
+  constexpr int CPR = DK / 8;
+  static_assert(32 * CPR % 64 == 0, "store chunks split evenly over the lanes");
+  char *wslice = lds + w * 32 * 2 * DK;
+  const float sc = a.scale;
+  T *ob = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1;
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const int qs = qw + 32 * s;
+#pragma unroll
+    for (int dt = 0; dt < PDQ; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int off = c * 2 * DK + (((4 * dt + g) ^ (c % CPR)) * 16) + 8 * h;
+        *reinterpret_cast<u32x2 *>(wslice + off) =
+            u32x2{pack2<T>(acc[dt][s][g * 4] * sc, acc[dt][s][g * 4 + 1] * sc),
+                  pack2<T>(acc[dt][s][g * 4 + 2] * sc, acc[dt][s][g * 4 + 3] * sc)};
+      }
+    }
+    u32x4 vr[32 * CPR / 64];
+#pragma unroll
+    for (int u = 0; u < 32 * CPR / 64; ++u) {
+      const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+      vr[u] = *reinterpret_cast<const u32x4 *>(wslice + r * 2 * DK + ((q ^ (r % CPR)) * 16));
+    }
+    // RoPE folded in: the inverse rotation of the rounded dQ.
+    if (p.rope.R > 0) {
+#pragma unroll
+      for (int u = 0; u < 32 * CPR / 64; ++u) {
+        const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+        const int row = qs + r < p.Sq ? qs + r : p.Sq - 1;  // rows past Sq: not stored
+        rotate_chunk<T>(vr[u], p.rope, p.rope.qpos0 + row, 4 * q, true);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 32 * CPR / 64; ++u) {
+      const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+      if (qs + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qs + r) * a.dq.s2 + q * 8) = vr[u];
+    }
+  }
+}
+
 // MKQ: the dQ kernel's mask mode (0..6), MK the dK/dV kernel's: element reads
 // (1..3), or boolean / 16-bit row-piece masks staged through its LDS ring
 // (4, 6); f32 row-piece masks (5) read element by element there.
 template <typename T, int DK, int DV, int MKQ, int MK, bool DR>
 void launch_mk(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
+  if (a.ds) {
+    // Stored dS: row values, then dK/dV (storing dS), then dQ as one GEMM.
+    {
+      Probe pr_("bwd_rows", st);
+      const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+      const int per_block = (NT / 64) * (64 / (DV / 8));
+      bwd_rows_kernel<T, DK, DV><<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)),
+                                  dim3(NT), 0, st>>>(a);
+    }
+    const int n_kb = (p.Sk + KB - 1) / KB;
+    {
+      Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
+      dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+    }
+    const int n_qb = (p.Sq + QB2 - 1) / QB2;
+    {
+      Probe pr_(DR ? "bwd_dq_ds_dropout" : (MK ? "bwd_dq_ds_masked" : "bwd_dq_ds"), st);
+      dq_ds_kernel<T, DK><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+    }
+    return;
+  }
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   {
@@ -1062,9 +1390,22 @@ size_t mfma_rope_stage_offset(const Problem &p) {
   return (2 * rows * sizeof(float) + 255) / 256 * 256;
 }
 
+// Key tiles of stored dS per query tile: every 32-key tile of the dK/dV
+// kernel's 128-key blocks, including those past the keys (zeros, never read).
+static int ds_key_tiles(const Problem &p) { return (p.Sk + KB - 1) / KB * (KB / 32); }
+
+size_t mfma_ds_bytes(const Problem &p) {
+  // Stored dS stays within 8 GiB, and each (b, q head) slice within 2^31
+  // bytes (32-bit buffer offsets, bit 31 marking a zero read).
+  constexpr int64_t kCap = int64_t(8) << 30;
+  const int64_t slice = static_cast<int64_t>((p.Sq + 31) / 32) * ds_key_tiles(p) * DS_TILE;
+  const int64_t total = slice * p.B * p.Hq;
+  return slice <= (int64_t(1) << 31) && total <= kCap ? static_cast<size_t>(total) : 0;
+}
+
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
                                 View dout, const float *lse, View dq, View dk, View dv,
-                                float *delta, hipStream_t st) {
+                                float *delta, void *ds, hipStream_t st) {
   View qk = q;
   if (p.rope.R > 0) {
     // rotated query rows staged after the row values, 256-byte aligned
@@ -1073,7 +1414,8 @@ hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, Vie
               static_cast<int64_t>(p.Hq) * p.Sq * D, static_cast<int64_t>(p.Sq) * D, D};
   }
   BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
-            static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale)};
+            static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale),
+            static_cast<char *>(ds), (p.Sq + 31) / 32, ds_key_tiles(p)};
   return dtype == TSATTN_BF16 ? launch<bf16>(a, st) : launch<f16>(a, st);
 }
 

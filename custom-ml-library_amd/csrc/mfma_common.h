@@ -443,6 +443,15 @@ __device__ __forceinline__ void dma16(u32x4 desc, uint32_t lds_addr, uint32_t vo
                : "memory", "m0");
 }
 
+// The same for data read once (streaming: nontemporal cache policy).
+__device__ __forceinline__ void dma16_nt(u32x4 desc, uint32_t lds_addr, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory", "m0");
+}
+
 // max(x, x of lane l ^ 32) without an LDS round trip: v_permlane32_swap
 // exchanges the upper half of `a` with the lower half of `b`, so afterwards
 // {a, b} holds {own, partner} in every lane.  (Assembly: the compiler builtin

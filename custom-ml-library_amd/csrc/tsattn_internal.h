@@ -172,9 +172,14 @@ hipError_t launch_generic_backward(const Problem &p, int dtype, View q, View k, 
 bool mfma_supported(const Problem &p, int dtype);
 hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View v, View o,
                                float *lse, hipStream_t st);
+// ds: NULL, or mfma_ds_bytes(p) bytes in which the dK/dV kernel stores dS
+// for the dQ product (then it runs first and dQ takes one GEMM).
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
                                 View dout, const float *lse, View dq, View dk, View dv,
-                                float *delta, hipStream_t st);
+                                float *delta, void *ds, hipStream_t st);
+// Bytes of stored dS (bf16 / f16 32 x 32 tiles of every (b, q head)), or 0
+// when they would exceed the cap the backward keeps on its workspace.
+size_t mfma_ds_bytes(const Problem &p);
 // With RoPE folded in (p.rope.R > 0) the backward workspace also holds the
 // rotated query rows [B, Hq, Sq, Dqk] (16-bit) from this byte offset on.
 size_t mfma_rope_stage_offset(const Problem &p);

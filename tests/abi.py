@@ -86,11 +86,12 @@ def forward(q, k, v, **kw):
     return out, lse, lib.tsattn_last_kernel_path()
 
 
-def backward(q, k, v, out, g, lse, **kw):
+def backward(q, k, v, out, g, lse, ws_bytes=None, **kw):
+    """tsattn_sdpa_backward with the queried workspace, or ws_bytes of it."""
     p = problem(q, k, v, **kw)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     lib = _lib.load()
-    nbytes = lib.tsattn_sdpa_backward_workspace(ctypes.byref(p))
+    nbytes = lib.tsattn_sdpa_backward_workspace(ctypes.byref(p)) if ws_bytes is None else ws_bytes
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     _lib.check(lib.tsattn_sdpa_backward(
         ctypes.byref(p), view(q), view(k), view(v), view(out), view(g),

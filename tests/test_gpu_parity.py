@@ -141,6 +141,33 @@ def test_mfma_forward_backward(dtype, case):
     check_half(abi.host(dv), rdv, dtype, "g", "dV")
 
 
+@pytest.mark.parametrize("case", MFMA_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_mfma_backward_both_dq_paths(case):
+    """The queried workspace holds dS for the one-GEMM dQ (row values, dK/dV
+    storing dS, then dQ = scale dS K); a workspace of the row values alone
+    runs the dQ kernel that recomputes S and dP.  Both meet the bounds."""
+    b, hq, hkv, sq, sk, d, causal, off = case
+    dtype = "bfloat16"
+    say(f"mfma backward dQ paths {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=13)
+    ref = _oracle(inp, dtype, causal, off, gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    out, lse, _ = abi.forward(q, k, v, causal=causal, offset=off)
+    rdq, rdk, rdv = ref.backward_compute(inp.do)
+    rows_bytes = 2 * b * hq * sq * 4
+    for ws, dq_probe in ((None, "bwd_dq_ds"), (rows_bytes, "bwd_dq_mfma")):
+        _lib.profile_enable(True)
+        _lib.profile_reset()
+        dq, dk, dv, bpath = abi.backward(q, k, v, out, g, lse, ws_bytes=ws, causal=causal, offset=off)
+        torch.cuda.synchronize()
+        probes = _lib.profile_read()
+        _lib.profile_enable(False)
+        assert bpath == _lib.PATH_MFMA
+        assert dq_probe in probes and (ws is None) == ("bwd_rows" in probes), sorted(probes)
+        for got, want, n in ((dq, rdq, "dQ"), (dk, rdk, "dK"), (dv, rdv, "dV")):
+            check_half(abi.host(got), want, dtype, "g", f"{n} ({dq_probe})")
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_mfma_agrees_with_generic_on_same_inputs(dtype):
     inp = attention_inputs(2, 2, 190, 128, dtype, value_scale=0.5, seed=5)
@@ -242,7 +269,7 @@ def test_mfma_general_masks(case):
     torch.cuda.synchronize()
     probes = _lib.profile_read()
     _lib.profile_enable(False)
-    assert {"fwd_mfma_masked", "bwd_dq_mfma_masked", "bwd_dkdv_mfma_masked"} <= set(probes)
+    assert {"fwd_mfma_masked", "bwd_dq_ds_masked", "bwd_dkdv_mfma_masked"} <= set(probes)
     check_half(abi.host(out), ref.out, dtype, "o", "O")
     check_lse(abi.host(lse), ref.lse, "LSE")
     rdq, rdk, rdv = ref.backward_compute(inp.do)
