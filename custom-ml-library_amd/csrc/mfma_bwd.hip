@@ -56,15 +56,29 @@ struct BwdArgs {
   float sl;      // scale * log2(e)
   float scale;   // final gradient scale
   // Stored dS (NULL: the dQ kernel recomputes S and dP itself).  Per (b, q
-  // head) ds_nqt x ds_nkt tiles of 32 query rows x 32 keys; tile (qt, kt) at
-  // byte ((bh ds_nqt + qt) ds_nkt + kt) * 2 KiB, as the dK/dV kernel's lanes
-  // hold it: dS[q][k] (q, k within the tile, q = 4 m + r) at
-  // (m / 4) KiB + (m % 2) 512 + 16 k + ((m / 2) % 2) 8 + 2 r.
+  // head) a slice of ds_slice tiles of 32 query rows x 32 keys, query tile qt
+  // owning the ds_row_len(qt) tiles from ds_row_start(qt) on (key tiles 0 ..,
+  // those of every 128-key block the dK/dV kernel visits for it); tile (qt,
+  // kt) at byte (bh ds_slice + ds_row_start(qt) + kt) * 2 KiB, as the dK/dV
+  // kernel's lanes hold it: dS[q][k] (q, k within the tile, q = 4 m + r) at
+  // (m / 4) KiB + (m % 2) 512 + 16 (k ^ 4 (m % 2) ^ 8 (m / 4)) + ((m / 2) % 2) 8
+  // + 2 r.  ds_tri: causal with Sq = Sk and no offset, rows packed (row qt
+  // holds 4 (qt / 4 + 1) tiles), so the reads sweep the slice densely; else
+  // rows of ds_nkt tiles.
   char *ds;
-  int ds_nqt, ds_nkt;
+  int ds_nkt, ds_tri;
+  int64_t ds_slice;
 };
 
+// Start of query tile qt's dS row within its slice, in tiles.
+__host__ __device__ __forceinline__ int64_t ds_row_start(int tri, int nkt, int qt) {
+  if (!tri) return static_cast<int64_t>(qt) * nkt;
+  const int64_t g = qt >> 2, r = qt & 3;  // rows 4 g .. 4 g + 3 hold 4 (g + 1) tiles each
+  return (g + 1) * (8 * g + 4 * r);
+}
+
 constexpr int DS_TILE = 2048;  // bytes of one stored dS tile
+constexpr int kStreamStore = 18;  // buffer store cache policy: sc1 (16) | nt (2)
 
 template <typename T>
 __device__ __forceinline__ T *mut(View v) {
@@ -189,10 +203,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // tile).
   const uint64_t qstep = static_cast<uint64_t>(a.qk.s1) * 2, gstep = static_cast<uint64_t>(a.dout.s1) * 2;
   const uint64_t rstep = static_cast<uint64_t>(p.Sq) * 4;
-  // With stored dS, da is the byte offset of the tile's dS (query tile
-  // q0 / 32, this wave's key tile): one query tile on, or on to the next head.
-  const uint64_t dstep = static_cast<uint64_t>(a.ds_nkt) * DS_TILE;
-  const uint64_t dwrap = (static_cast<uint64_t>(a.ds_nqt) - n_qt + 1) * dstep;
+  // With stored dS, da is the byte offset of the tile's head slice.
+  const uint64_t dwrap = static_cast<uint64_t>(a.ds_slice) * DS_TILE;
   struct TileIdx {
     int itn, r, qi;
     uint64_t qa, ga, ra, da;
@@ -205,7 +217,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     t.qa += wrap ? qstep : 0;
     t.ga += wrap ? gstep : 0;
     t.ra += wrap ? rstep : 0;
-    t.da += wrap ? dwrap : dstep;
+    t.da += wrap ? dwrap : 0;
     return t;
   };
   // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
@@ -343,8 +355,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   const TileIdx first{0, 0, 0, reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep)),
                       reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep)),
                       reinterpret_cast<uint64_t>(rowv),
-                      ((static_cast<uint64_t>(b) * p.Hq + hk * p.rep) * a.ds_nqt + q_start / QT) * dstep +
-                          static_cast<uint64_t>(kw / 32) * DS_TILE};
+                      (static_cast<uint64_t>(b) * p.Hq + hk * p.rep) * dwrap};
   TileIdx nxt_idx = first;
   for (int t = 0; t < KV_PD; ++t) {
     issue(nxt_idx);
@@ -379,7 +390,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     const char *gt = qt + TILE_Q;
     const float *rv = reinterpret_cast<const float *>(qt + TILE_Q + TILE_G);
     const int hq = hk * p.rep + cur_idx.r, q0 = q_start + cur_idx.qi * QT;
-    const uint64_t ds_at = cur_idx.da;
+    const uint64_t cur_idx_da = cur_idx.da;
+    const int64_t ds_tile = (ds_row_start(a.ds_tri, a.ds_nkt, q0 / QT) + kw / 32) * DS_TILE;
     cur_idx = tile_next(cur_idx);
 
     constexpr int FD = DKDV_FD;
@@ -536,18 +548,26 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     }
 
     // Stored dS (dQ as one GEMM after this kernel): the wave's packed dS
-    // registers as they are, pd[0] then pd[1], 1 KiB per wave store (the dQ
-    // kernel transposes them with LDS transpose reads).  Stores count in
-    // vmcnt: the tile wait leaves these two in flight too.
+    // registers as they are, pd[0] then pd[1], 1 KiB per wave store, lane
+    // (c, h) of pd[gg] at 16 (c ^ 4 h ^ 8 gg) + 512 h (the dQ kernel's
+    // transpose reads of them are then free of bank conflicts).  Stores
+    // count in vmcnt: the tile wait leaves these two in flight too.
     if (a.ds) {
-      // lane * 16, recomputed here rather than held in a register all loop
+      // lane * 16 ^ (h * 64), recomputed here rather than held in a
+      // register all loop
       uint32_t l16;
       asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
                    "v_lshlrev_b32 %0, 4, %0"
                    : "=v"(l16));
-      char *dst = a.ds + ds_at + l16;
-      *reinterpret_cast<u32x4 *>(dst) = pd[0];
-      *reinterpret_cast<u32x4 *>(dst + 1024) = pd[1];
+      l16 ^= (l16 >> 9) << 6;
+      // streaming stores (cache policy sc1 nt): written once, read once by
+      // the dQ kernel, kept from evicting the Q / dO rows other key blocks
+      // reuse.  Offsets within the head slice (below 2^31 bytes).
+      const rsrc_t dsr = make_rsrc(a.ds + cur_idx_da, static_cast<uint32_t>(a.ds_slice * DS_TILE));
+      const uint32_t o = static_cast<uint32_t>(ds_tile);
+      __builtin_amdgcn_raw_buffer_store_b128(pd[0], dsr, static_cast<int>(o + l16), 0, kStreamStore);
+      __builtin_amdgcn_raw_buffer_store_b128(pd[1], dsr, static_cast<int>(o + 1024 + (l16 ^ 128)), 0,
+                                             kStreamStore);
       // tile itn + 1 has landed; the previous tile's stores may still be in
       // flight (they were issued after its loads; before the first tile two
       // empty loads stand in for them)
@@ -1096,7 +1116,7 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // dQ from stored dS: dQ^T = scale K^T dS^T over the key tiles of each row
 // (one GEMM; the dK/dV kernel left dS in the workspace).  One workgroup = 256
-// query rows of one (b, q head), 4 waves x 64 rows (two 32-row subtiles
+// query rows of one (b, q head), 4 waves x two 32-row subtiles (w and 7 - w,
 // sharing every K^T fragment), two workgroups per CU.  Per 32-key tile, K
 // (shared) and each wave's two dS tiles stream global -> LDS by DMA loads
 // into 3-stage rings, issued two tiles ahead; K^T and dS^T fragments come
@@ -1136,7 +1156,10 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
   heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);  // 2 WG per CU
   const int qb = n_qb - 1 - rank;  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
-  const int q0 = qb * QB2, qw = q0 + 64 * w;
+  // Wave w takes the block's 32-row subtiles w and 7 - w, so that the
+  // causal work of the four waves is alike (the subtiles share every K^T
+  // fragment; the shorter one's operands past its end read as zeros).
+  const int q0 = qb * QB2, qa = q0 + 32 * w, qz = q0 + 32 * (7 - w);
   const int kv_end = kv_end_for(p, b);
   // key tiles up to query row `last` (its cache end and causal window)
   auto tiles_to = [&](int last) {
@@ -1145,17 +1168,19 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
     return lim > 0 ? static_cast<int>((lim + KT - 1) / KT) : 0;
   };
   const int n_tiles = __builtin_amdgcn_readfirstlane(tiles_to(min(q0 + QB2, p.Sq) - 1));
-  const int w_tiles = __builtin_amdgcn_readfirstlane(qw < p.Sq ? tiles_to(min(qw + 64, p.Sq) - 1) : 0);
-  const int s_tiles = __builtin_amdgcn_readfirstlane(qw < p.Sq ? tiles_to(min(qw + 32, p.Sq) - 1) : 0);
+  const int s_tiles = __builtin_amdgcn_readfirstlane(qa < p.Sq ? tiles_to(min(qa + 32, p.Sq) - 1) : 0);
+  const int z_tiles = __builtin_amdgcn_readfirstlane(qz < p.Sq ? tiles_to(min(qz + 32, p.Sq) - 1) : 0);
+  const int w_tiles = max(s_tiles, z_tiles);
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2;
   const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-  // dS of this (b, q head); subtile s of this wave is query tile qw / 32 + s
-  const int64_t slice = static_cast<int64_t>(a.ds_nqt) * a.ds_nkt * DS_TILE;
+  // dS of this (b, q head); the wave's subtiles are query tiles qa / 32, qz / 32
+  const int64_t slice = a.ds_slice * DS_TILE;
   const u32x4 sdesc = make_desc(a.ds + (static_cast<int64_t>(b) * p.Hq + hq) * slice,
                                 static_cast<uint32_t>(slice));
-  const uint32_t ds_row = static_cast<uint32_t>(a.ds_nkt * DS_TILE);
-  const uint32_t ds0 = static_cast<uint32_t>(qw / 32) * ds_row;
+  // (rows past Sq: past the slice, or masked off below)
+  const uint32_t dsa = static_cast<uint32_t>(ds_row_start(a.ds_tri, a.ds_nkt, qa / 32) * DS_TILE);
+  const uint32_t dsz = static_cast<uint32_t>(ds_row_start(a.ds_tri, a.ds_nkt, qz / 32) * DS_TILE);
   const uint32_t lds0 = lds_addr(lds);
   const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t koff = (lane >> 2) * ks_b + (4 * (w % QGK) + swz_chunk) * 16;
@@ -1168,7 +1193,7 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
   // 1 KiB parts (subtile u / 2, half u % 2), past the range (zeros) beyond the
   // subtile's causal end.
   struct DmaTile {
-    uint32_t krow, kst, sst, keep, far0, far1, srow;
+    uint32_t krow, kst, sst, keep, far0, far1, srow0, srow1;
   };
   auto dma_tile = [&](int tile) {
     DmaTile d;
@@ -1178,8 +1203,9 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
     d.kst = (lds0 + (tile % DS_NS) * TILE_K - spare) & d.keep;
     d.sst = (sring + (tile % DS_NS) * 2 * DS_TILE - spare) & d.keep;
     d.far0 = tile < s_tiles ? 0u : 0x80000000u;
-    d.far1 = tile < w_tiles ? 0u : 0x80000000u;
-    d.srow = ds0 + static_cast<uint32_t>(tile) * DS_TILE;
+    d.far1 = tile < z_tiles ? 0u : 0x80000000u;
+    d.srow0 = (dsa + static_cast<uint32_t>(tile) * DS_TILE) | d.far0;
+    d.srow1 = (dsz + static_cast<uint32_t>(tile) * DS_TILE) | d.far1;
     return d;
   };
   auto issue_part = [&](const DmaTile &d, int u) {
@@ -1190,21 +1216,24 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
     } else {
       const int s = (u - KPARTS) >> 1, half = (u - KPARTS) & 1;
       dma16_nt(sdesc, spare + d.sst + ((s * DS_TILE + half * 1024) & d.keep), loff,
-               (d.srow + s * ds_row + half * 1024) | (s ? d.far1 : d.far0));
+               (s ? d.srow1 : d.srow0) + half * 1024);
     }
   };
   // dS^T operand (16 keys of k-step ks x 32 queries) of one stored tile by
   // transpose reads: the 16 lanes of a read group each name 4 queries of one
   // key row (dS[4 m .. 4 m + 3][k] is 8 contiguous bytes of the tile), and
   // lane (c, h) receives query c at keys 16 ks + 4 h .. + 3 (then + 8 ..),
-  // the key order of TileReader::cols.
-  const int i16 = lane & 15;
-  const uint32_t s_lo = ((lane >> 4) & 1) * 1024 + (i16 & 1) * 512 + ((i16 >> 1) & 1) * 8 +
-                        ((i16 >> 2) + 4 * h) * 16;
+  // the key order of TileReader::cols.  Lane (i, g) of the read (i = lane %
+  // 16, g = lane / 16) names m = 4 (g % 2) + i % 4 and key row kb + i / 4,
+  // kb = 16 ks + 4 h (+ 8): the stored layout's key swizzle turns into
+  // per-lane bases for the two halves.
+  const int i16 = lane & 15, gg = (lane >> 4) & 1, hp = i16 & 1;
+  const uint32_t s_base = gg * 1024 + hp * 512 + ((i16 >> 1) & 1) * 8 + (i16 >> 2) * 16 +
+                          ((h ^ hp) * 4) * 16;
+  const uint32_t s_lo = s_base + (gg * 8) * 16, s_hi = s_base + ((gg ^ 1) * 8) * 16;
   auto ds_frag = [&](const char *tile, int ks) {
-    const char *base = tile + s_lo + ks * 256;
-    const u32x2 lo = ds_read_tr<T>(reinterpret_cast<const T *>(base));
-    const u32x2 hi = ds_read_tr<T>(reinterpret_cast<const T *>(base + 128));
+    const u32x2 lo = ds_read_tr<T>(reinterpret_cast<const T *>(tile + s_lo + ks * 256));
+    const u32x2 hi = ds_read_tr<T>(reinterpret_cast<const T *>(tile + s_hi + ks * 256));
     return u32x4{lo[0], lo[1], hi[0], hi[1]};
   };
 
@@ -1279,7 +1308,7 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
   T *ob = mut<T>(a.dq) + b * a.dq.s0 + hq * a.dq.s1;
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
-    const int qs = qw + 32 * s;
+    const int qs = s ? qz : qa;
 #pragma unroll
     for (int dt = 0; dt < PDQ; ++dt) {
 #pragma unroll
@@ -1394,11 +1423,17 @@ size_t mfma_rope_stage_offset(const Problem &p) {
 // kernel's 128-key blocks, including those past the keys (zeros, never read).
 static int ds_key_tiles(const Problem &p) { return (p.Sk + KB - 1) / KB * (KB / 32); }
 
+static int ds_packed(const Problem &p) { return p.causal && p.offset == 0 && p.Sq == p.Sk; }
+
+static int64_t ds_slice_tiles(const Problem &p) {
+  return ds_row_start(ds_packed(p), ds_key_tiles(p), (p.Sq + 31) / 32);
+}
+
 size_t mfma_ds_bytes(const Problem &p) {
   // Stored dS stays within 8 GiB, and each (b, q head) slice within 2^31
   // bytes (32-bit buffer offsets, bit 31 marking a zero read).
   constexpr int64_t kCap = int64_t(8) << 30;
-  const int64_t slice = static_cast<int64_t>((p.Sq + 31) / 32) * ds_key_tiles(p) * DS_TILE;
+  const int64_t slice = ds_slice_tiles(p) * DS_TILE;
   const int64_t total = slice * p.B * p.Hq;
   return slice <= (int64_t(1) << 31) && total <= kCap ? static_cast<size_t>(total) : 0;
 }
@@ -1415,7 +1450,7 @@ hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, Vie
   }
   BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
             static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale),
-            static_cast<char *>(ds), (p.Sq + 31) / 32, ds_key_tiles(p)};
+            static_cast<char *>(ds), ds_key_tiles(p), ds_packed(p), ds_slice_tiles(p)};
   return dtype == TSATTN_BF16 ? launch<bf16>(a, st) : launch<f16>(a, st);
 }
 
