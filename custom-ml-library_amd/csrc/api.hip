@@ -519,6 +519,63 @@ int tsattn_rope_append(int32_t dtype, int32_t batch, int32_t heads, int32_t len,
                     "RoPE append launch");
 }
 
+int tsattn_qkv_rope_append(int32_t dtype, int32_t batch, int32_t len, int32_t embed, int32_t heads_q,
+                           int32_t heads_kv, int32_t dim, const tsattn_view *x, const void *wq,
+                           const void *wk, const void *wv, const void *bq, const void *bk,
+                           const void *bv, const tsattn_view *q_out, const tsattn_view *k_cache,
+                           const tsattn_view *v_cache, const tsattn_view *k_scale,
+                           const tsattn_view *v_scale, const void *cos, const void *sin, int64_t pos,
+                           void *stream) {
+  int rc;
+  if ((rc = check_view(x, "input rows")) || (rc = check_view(q_out, "query output")) ||
+      (rc = check_view(k_cache, "key cache")) ||
+      (rc = check_view(v_cache, "value cache")))
+    return rc;
+  if (!k_scale != !v_scale)
+    return fail(TSATTN_ERR_INVALID, "an int8 cache needs both key and value scales");
+  if ((k_scale && (rc = check_view(k_scale, "key scales"))) ||
+      (v_scale && (rc = check_view(v_scale, "value scales"))))
+    return rc;
+  if (dtype != TSATTN_F16 && dtype != TSATTN_BF16)
+    return fail(TSATTN_ERR_INVALID, "the fused projection takes f16 or bf16 rows (got dtype %d)", dtype);
+  if (batch <= 0 || len <= 0 || embed <= 0 || heads_q <= 0 || heads_kv <= 0 || pos < 0)
+    return fail(TSATTN_ERR_INVALID, "projection needs positive sizes and a nonnegative position");
+  if (heads_q % heads_kv)
+    return fail(TSATTN_ERR_INVALID, "query heads must divide into KV groups");
+  if (dim != 64 && dim != 128)
+    return fail(TSATTN_ERR_UNSUPPORTED, "the fused projection supports head dims 64 and 128");
+  if (embed % 16) return fail(TSATTN_ERR_UNSUPPORTED, "the fused projection needs embed % 16 == 0");
+  if (!wq || !wk || !wv) return fail(TSATTN_ERR_INVALID, "the weights must be non-NULL");
+  if (!cos != !sin) return fail(TSATTN_ERR_INVALID, "RoPE needs both cos and sin tables");
+  const tsattn::View vx = tsattn::make_view(x);
+  const uintptr_t al = reinterpret_cast<uintptr_t>(vx.data) | reinterpret_cast<uintptr_t>(wq) |
+                       reinterpret_cast<uintptr_t>(wk) | reinterpret_cast<uintptr_t>(wv);
+  if (al % 16 || vx.s0 % 8 || vx.s2 % 8 || vx.s0 < 0 || vx.s2 < 0)
+    return fail(TSATTN_ERR_INVALID, "x rows and the weights must be 16-byte aligned");
+  const int64_t xext = (static_cast<int64_t>(batch) - 1) * vx.s0 + (static_cast<int64_t>(len) - 1) * vx.s2 + embed;
+  if (xext * 2 >= (int64_t(1) << 31) ||
+      static_cast<int64_t>(heads_q > heads_kv ? heads_q : heads_kv) * dim * embed * 2 >= (int64_t(1) << 31))
+    return fail(TSATTN_ERR_UNSUPPORTED, "x or a weight matrix exceeds 2^31 bytes");
+  const tsattn::View vq = tsattn::make_view(q_out), vk = tsattn::make_view(k_cache),
+                     vv = tsattn::make_view(v_cache);
+  // 4-element row pieces: 8-byte stores (16-bit) / 4-byte (int8)
+  auto al4 = [](const tsattn::View &v, size_t es) {
+    return reinterpret_cast<uintptr_t>(v.data) % (4 * es) == 0 && v.s0 % 4 == 0 && v.s1 % 4 == 0 &&
+           v.s2 % 4 == 0;
+  };
+  const size_t ce = k_scale ? 1 : 2;
+  if (!al4(vq, 2) || !al4(vk, ce) || !al4(vv, ce))
+    return fail(TSATTN_ERR_INVALID, "query output and cache rows need 4-element aligned strides");
+  tsattn::View ks, vs;
+  if (k_scale) ks = tsattn::make_view(k_scale), vs = tsattn::make_view(v_scale);
+  const void *w[3] = {wq, wk, wv}, *bias[3] = {bq, bk, bv};
+  return hip_status(tsattn::launch_qkv_rope_append(dtype, batch, len, embed, heads_q, heads_kv, dim, vx, w,
+                                                   bias, vq, vk, vv, k_scale ? &ks : nullptr,
+                                                   v_scale ? &vs : nullptr, cos, sin, pos,
+                                                   static_cast<hipStream_t>(stream)),
+                    "fused projection launch");
+}
+
 int tsattn_key_mask_lengths(const uint8_t *mask, int64_t stride_b, int64_t stride_k,
                             int32_t batch, int32_t len_kv, int32_t *kv_len, int32_t *kv_prefix,
                             void *stream) {

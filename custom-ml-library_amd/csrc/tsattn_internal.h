@@ -211,6 +211,15 @@ hipError_t launch_rope_append(int dtype, int B, int H, int T, int D, int R, View
                               View vc, const View *ks, const View *vs, const void *cos,
                               const void *sin, int64_t pos, hipStream_t st);
 
+// The q / k / v projections of the `batch x len` rows of x (embed wide; a
+// [batch, 1, len, embed] view) with
+// RoPE of q and k at rows pos .. (cos == nullptr: none) and the k / v cache
+// append at pos; ks / vs non-null for int8 caches.  dim is 64 or 128.
+hipError_t launch_qkv_rope_append(int dtype, int batch, int len, int embed, int heads_q, int heads_kv,
+                                  int dim, View x, const void *const w[3], const void *const bias[3],
+                                  View q, View kc, View vc, const View *ks, const View *vs, const void *cos,
+                                  const void *sin, int64_t pos, hipStream_t st);
+
 // The dropout keep mask of problem p as a contiguous [B, Hq, Sq, Sk] uint8 array.
 hipError_t launch_dropout_keep(const Problem &p, uint8_t *out, hipStream_t st);
 // The keep bits of the problem's dropout stream into `out` (DropDesc::bits

@@ -122,6 +122,12 @@ SIGNATURES = {
         [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _PV, _PV, _PV, _PV, _PV, _PV,
          c_void_p, c_void_p, c_int64, c_void_p],
     ),
+    "tsattn_qkv_rope_append": (
+        c_int,
+        [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, _PV, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, _PV, _PV, _PV, _PV, _PV, c_void_p,
+         c_void_p, c_int64, c_void_p],
+    ),
     "tsattn_key_mask_lengths": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int32, c_int32, c_void_p, c_void_p, c_void_p],

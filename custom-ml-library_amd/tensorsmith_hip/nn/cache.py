@@ -116,6 +116,56 @@ class KVCache:
         self.length = stop
         return True
 
+    def _project_append(self, input: Tensor, projections, num_heads: int, rotary: bool,
+                        base: float = 10000.0):
+        """The cached attention step's q / k / v projections (``projections``:
+        the q, k, v ``Linear`` layers), RoPE of q and k at positions
+        ``length ..`` and the k / v append, in one kernel
+        (``tsattn_qkv_rope_append``).  Returns the rotated queries [B, H, T, D]
+        (a device tensor) and advances ``length``; or None, writing nothing,
+        when the operands are outside the kernel (16-bit input in the cache
+        dtype and the layers' dtype, head dim 64 / 128 equal to the value dim,
+        embed a multiple of 16): the caller then projects and appends in steps.
+        """
+        import torch
+
+        x = input._data
+        lin = [(layer.weight._data, None if layer.bias is None else layer.bias._data)
+               for layer in projections]
+        tensors = [t for pair in lin for t in pair if t is not None]
+        if (x.dtype != self.dtype or self.dtype not in (torch.float16, torch.bfloat16)
+                or self.head_dim not in (64, 128) or self.value_dim != self.head_dim
+                or x.ndim != 3 or x.shape[0] != self.batch_size or x.shape[-1] % 16
+                or x.stride(-1) != 1 or x.data_ptr() % 16 or x.stride(0) % 8 or x.stride(1) % 8
+                or any(t.dtype != x.dtype or not t.is_contiguous() or t.data_ptr() % 16
+                       for t in tensors)
+                or lin[0][0].shape[0] != num_heads * self.head_dim
+                or any(w.shape[0] != self.num_heads * self.head_dim for w, _ in lin[1:])):
+            return None
+        b, t, e = x.shape
+        stop = self.length + t
+        if t == 0 or stop > self.max_seq_len:
+            raise ValueError(f"cache capacity {self.max_seq_len} exceeded or empty append")
+        q = torch.empty((b, num_heads, t, self.head_dim), dtype=x.dtype, device=x.device)
+        cos = sin = None
+        if rotary:
+            from .attention import rope_tables
+
+            cos, sin = rope_tables(base, self.head_dim, self.dtype, self._keys.device, stop)
+        ptr = lambda z: None if z is None else ctypes.c_void_p(z.data_ptr())
+        scales = ((ctypes.byref(_view(self._key_scales)), ctypes.byref(_view(self._value_scales)))
+                  if self.quantized else (None, None))
+        code = _CODES[str(x.dtype)]
+        _lib.check(
+            _lib.load().tsattn_qkv_rope_append(
+                code, b, t, e, num_heads, self.num_heads, self.head_dim, ctypes.byref(_view(x.unsqueeze(1))),
+                *(ptr(w) for w, _ in lin), *(ptr(bias) for _, bias in lin), ctypes.byref(_view(q)),
+                ctypes.byref(_view(self._keys)), ctypes.byref(_view(self._values)), *scales,
+                ptr(cos), ptr(sin), self.length, ctypes.c_void_p(current_stream(self.device))),
+            "fused projection, RoPE and cache append")
+        self.length = stop
+        return q
+
     def _check(self, key: Tensor, value: Tensor) -> int:
         """Validate an append (reference order, cache.py:54-70); return the new length."""
         if key.device != self.device or value.device != self.device:

@@ -7,9 +7,11 @@ reshaped to ``[B,S,H,D]`` and permuted to ``[B,H,S,D]`` *views* (the HIP
 kernels take the strides, so no copy is made), optional interleaved RoPE
 (without a cache the attention kernels rotate the queries in their prologue
 and rotate the query / key gradients back in their epilogues, the keys taking
-one RoPE kernel; with a cache, one RoPE kernel for the queries and one kernel
-for the key rotation and the K / V append), KV-cache append with
-``causal_offset = cache.length``, then
+one RoPE kernel; with a cache, one kernel for the three projections, the
+rotation of q and k and the K / V append -- ``tsattn_qkv_rope_append`` --
+where the operands allow, else the projections, one kernel for the key
+rotation and the append, and the decode kernel rotating the queries), KV-cache
+append with ``causal_offset = cache.length``, then
 ``scaled_dot_product_attention`` with ``backend`` (``"hip"`` added to the
 allowlist; ``"auto"`` picks it).
 
@@ -92,6 +94,23 @@ class MultiHeadAttention(Module):
                     raise TypeError("attention masks must be boolean or floating point")
             except ValueError as error:
                 raise ValueError("attention mask is not broadcastable to [B,H,Q,K]") from error
+        # cached self-attention: projections, RoPE and the append in one kernel
+        # where the operands allow (the queries come back rotated)
+        q_fused = None
+        if cache is not None and context is None:
+            q_fused = cache._project_append(input, (self.q_proj, self.k_proj, self.v_proj),
+                                            self.num_heads, self.rotary)
+        if q_fused is not None:
+            q = Tensor._from_op(q_fused, (input,), None, "qkv_rope_append")
+            attended = None
+            if cache.quantized and attn_mask is None:
+                attended = decode_int8_cache(q, cache, is_causal=is_causal, causal_offset=offset)
+            if attended is None:
+                k, v = cache.get()
+                attended = scaled_dot_product_attention(
+                    q, k, v, attn_mask, 0.0, is_causal, causal_offset=offset, backend=self.backend,
+                    enable_gqa=self.num_kv_heads != self.num_heads)
+            return self.out_proj(attended.permute(0, 2, 1, 3).reshape(batch, steps, self.embed_dim))
         q = self.q_proj(input).reshape(batch, steps, self.num_heads, self.head_dim).permute(0, 2, 1, 3)
         k = (self.k_proj(source).reshape(batch, source.shape[1], self.num_kv_heads, self.head_dim)
              .permute(0, 2, 1, 3))

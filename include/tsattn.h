@@ -342,6 +342,34 @@ int tsattn_rope_append(int32_t dtype, int32_t batch, int32_t heads, int32_t len,
                        const void *sin, int64_t pos, void *stream);
 
 /*
+ * The cached MultiHeadAttention step before the attention in one kernel:
+ * the three input projections (MultiHeadAttention.forward, src/tensorsmith/
+ * nn/transformer.py:124-138: q = x Wq^T (+ bq), k = x Wk^T (+ bk),
+ * v = x Wv^T (+ bv)), RoPE of q and k at positions pos .. pos + len - 1
+ * (:139-141, as tsattn_rope with rotary_dim = dim; cos == NULL skips it) and
+ * the append of k and v at position pos of the caches (:142, KVCache.append,
+ * cache.py:54-86; k_scale / v_scale non-NULL: int8 caches with fp32 row
+ * scales, quantised as tsattn_kv_append_int8).  x: the [batch, len, embed]
+ * input as a [batch, 1, len, embed] view (stride[1] unused), rows and row
+ * strides 16-byte aligned; wq: [heads_q * dim, embed], wk / wv:
+ * [heads_kv * dim, embed], row-major (Linear.weight), 16-byte aligned;
+ * bq / bk / bv: NULL or [rows of the matching weight]; q_out: [batch,
+ * heads_q, len, dim] (the rotated queries); caches [batch, heads_kv,
+ * capacity >= pos + len, dim]; cos / sin as tsattn_rope's tables.  dtype f16
+ * or bf16, dim 64 or 128, embed a multiple of 16.  The projections
+ * accumulate in fp32 and round once to the dtype, as the reference's Linear
+ * output; the rotation and the int8 rounding are then bit-identical to the
+ * reference's on those rows.
+ */
+int tsattn_qkv_rope_append(int32_t dtype, int32_t batch, int32_t len, int32_t embed, int32_t heads_q,
+                           int32_t heads_kv, int32_t dim, const tsattn_view *x, const void *wq,
+                           const void *wk, const void *wv, const void *bq, const void *bk,
+                           const void *bv, const tsattn_view *q_out, const tsattn_view *k_cache,
+                           const tsattn_view *v_cache, const tsattn_view *k_scale,
+                           const tsattn_view *v_scale, const void *cos, const void *sin, int64_t pos,
+                           void *stream);
+
+/*
  * Boolean key mask [B, K] (strides in bytes-as-elements) -> kv_len[b] = 1 +
  * last allowed key (0 if none) and kv_prefix[b] = 1 iff the allowed keys are
  * exactly [0, kv_len[b]).  Serves the reference's key-padding masks

@@ -245,3 +245,17 @@ def dropout_keep(q, k, v, **kw):
     _lib.check(_lib.load().tsattn_dropout_keep(ctypes.byref(p), ctypes.c_void_p(out.data_ptr()),
                                                stream()), "dropout keep")
     return out
+
+
+def qkv_rope_append(x, wq, wk, wv, bias, q_out, kc, vc, scales, cos, sin, pos, heads_q, heads_kv):
+    """tsattn_qkv_rope_append: x [B, T, E]; bias = (bq, bk, bv) or None;
+    scales = (ks, vs) for int8 caches or None; cos = None skips RoPE."""
+    b, t, e = x.shape
+    d = q_out.shape[-1]
+    bq, bk, bv = bias if bias is not None else (None, None, None)
+    ptr = lambda z: ctypes.c_void_p(z.data_ptr()) if z is not None else None
+    sc = (view(scales[0]), view(scales[1])) if scales is not None else (None, None)
+    _lib.check(_lib.load().tsattn_qkv_rope_append(
+        CODES[x.dtype], b, t, e, heads_q, heads_kv, d, view(x.unsqueeze(1)), ptr(wq), ptr(wk), ptr(wv),
+        ptr(bq), ptr(bk), ptr(bv), view(q_out), view(kc), view(vc), *sc, ptr(cos), ptr(sin), pos,
+        stream()), "fused projection")

@@ -11,9 +11,9 @@ kernel that dequantises inside (needs an MI355X).
   (relative L2 <= 2e-3 / 1e-2, max-abs <= 5e-3 / 2e-2 of max|ref|), for
   uniform and ragged (kv_len) lengths; and against the reference's order
   (dequantise, round to the cache dtype, then attend) within the same bound.
-* Model level: an fp16 TransformerLM with a quantised cache appends through
-  the fused RoPE + quantise kernel and decodes through the int8 kernel (their
-  timing probes fire) and agrees with the same steps
+* Model level: an fp16 TransformerLM with a quantised cache projects, rotates
+  and appends through the fused projection kernel and decodes through the
+  int8 kernel (their timing probes fire) and agrees with the same steps
   taken in the reference's order (dequantised fp16 views, fp decode kernel)
   at the fp16 bound; both stay within relative L2 3e-2 of the unquantised
   model.  (The reference's rtol 0.08 / atol 0.006 int8 check,
@@ -207,9 +207,10 @@ def test_lm_with_int8_cache_decodes_through_the_int8_kernel():
         got, probes = run(False)
         want, probes_ref = run(True)
     assert probes["decode_split_int8"][0] == 4 * cfg.num_layers
-    # one fused RoPE + quantising append (K and V) per layer and step
-    assert probes["rope_append_int8"][0] == 4 * cfg.num_layers and "kv_append_int8" not in probes
-    # the decode kernel rotates the queries itself: no separate RoPE launch
+    # one fused projection + RoPE + quantising append (q, K and V) per layer and step
+    assert probes["qkv_rope_append_int8"][0] == 4 * cfg.num_layers
+    assert "kv_append_int8" not in probes and "rope_append_int8" not in probes
+    # the queries come out of it rotated: no separate RoPE launch
     assert "rope" not in probes and "rope" not in probes_ref
     assert "decode_split_int8" not in probes_ref and "decode_split" in probes_ref
     assert rel_l2(got, want) <= 5e-3

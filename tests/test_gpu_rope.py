@@ -186,7 +186,9 @@ def test_fused_cached_decode_is_bitwise_the_two_step_path(quantized):
             parts.append(model(tokens[:, t:t + 1], caches=caches).numpy())
         return np.concatenate(parts, axis=1), [c.storage for c in caches]
 
-    with ts.no_grad():
+    # the fused projection kernel (one launch for projections, RoPE and the
+    # append) switched off: this is the path for what it does not take
+    with ts.no_grad(), patch.object(KVCache, "_project_append", lambda *a, **k: None):
         with patch.object(KVCache, "_append_rotary", counting):
             got, got_store = run()
         with patch.object(KVCache, "_append_rotary", lambda self, *a, **k: False):
