@@ -39,6 +39,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -153,15 +154,19 @@ def bench_fwd_bwd(ts, torch, steps, warmup):
     return result, host
 
 
-def bench_variants(ts, torch, steps, warmup, host):
+def bench_variants(ts, torch, steps, warmup, host, rounds=3):
     """The headline shape again through the other MFMA kernel variants: a
     general [S, S] boolean mask (with the causal flag), dropout p = 0.1 on the
     hip backend, and RoPE folded into the kernels (unrotated q / k, as
-    MultiHeadAttention calls it).  Same FLOP count per step as the headline."""
+    MultiHeadAttention calls it).  Same FLOP count per step as the headline.
+    The plain causal step runs in the same leg and the cases take turns over
+    `rounds` rounds of `steps` steps (medians reported), so each ratio to the
+    plain step compares runs at the same clocks."""
     q, k, v = (ts.Tensor(host[n], device="hip", requires_grad=True) for n in ("q", "k", "v"))
     upstream = ts.Tensor(host["g"], device="hip")
     tril = ts.Tensor(torch.ones((S, S), dtype=torch.bool, device="cuda").tril(), device="hip")
     cases = {
+        "plain": dict(is_causal=True),
         "general_bool_mask": dict(attn_mask=tril, is_causal=True),
         "dropout_p0.1": dict(is_causal=True, dropout_p=0.1, backend="hip"),
         "rope_folded": dict(is_causal=True, _rope=(0, 0, 10000.0)),
@@ -169,29 +174,37 @@ def bench_variants(ts, torch, steps, warmup, host):
     from tensorsmith_hip import _lib
 
     flops = causal_fwd_flops(B, H, S, D) * 3.5
+
+    def step(kw):
+        for t in (q, k, v):
+            t.zero_grad()
+        ts.nn.scaled_dot_product_attention(q, k, v, **kw).backward(upstream)
+
+    times = {name: [] for name in cases}
+    for r in range(rounds):
+        for name, kw in cases.items():
+            for _ in range(warmup if r == 0 else 1):
+                step(kw)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step(kw)
+            torch.cuda.synchronize()
+            times[name].append((time.perf_counter() - t0) / steps * 1e3)
     out = {}
     for name, kw in cases.items():
-        def step():
-            for t in (q, k, v):
-                t.zero_grad()
-            ts.nn.scaled_dot_product_attention(q, k, v, **kw).backward(upstream)
-
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        ms = (time.perf_counter() - t0) / steps * 1e3
         _lib.profile_reset()
         _lib.profile_enable(True)
-        step()
+        for _ in range(2):
+            step(kw)
         torch.cuda.synchronize()
         _lib.profile_enable(False)
         kernels = {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}
+        ms = statistics.median(times[name])
         out[name] = {"ms_per_step": round(ms, 4), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
                      "kernel_ms": kernels}
+    for name in cases:
+        out[name]["vs_plain"] = round(out[name]["ms_per_step"] / out["plain"]["ms_per_step"], 3)
     return out
 
 

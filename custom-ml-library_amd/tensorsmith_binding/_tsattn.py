@@ -7,7 +7,7 @@ to the MI355X kernels, next to the device allowlist entry
 (``src/tensorsmith/device.py:34-38``) and the backend allowlist entry
 (``nn/attention.py:55-56``, ``:78-80``).  It depends only on ctypes, NumPy
 and torch-ROCm (the array library of a ``hip`` device) and declares the C ABI
-of ``include/tsattn.h`` version 7 in full; ``load()`` refuses any other
+of ``include/tsattn.h`` version 8; ``load()`` refuses any other
 version.
 
 The reference calls ``sdpa_hip`` from its dispatch and wraps the result the
@@ -31,7 +31,7 @@ from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_
 import numpy as np
 import torch
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 MASK_NONE, MASK_BOOL, MASK_ADDITIVE = 0, 1, 2
 BOOL_CODE = 4
@@ -85,6 +85,9 @@ _SIGNATURES = {
                                         c_void_p, c_void_p]),
     "tsattn_kv_append_int8": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, _V, _V, _V,
                                       c_int64, c_void_p]),
+    "tsattn_qkv_rope_append": (c_int, [c_int32, c_int32, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                       _V, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       _V, _V, _V, _V, _V, c_void_p, c_void_p, c_int64, c_void_p]),
 }
 
 _lib = None
@@ -266,3 +269,26 @@ def append_int8(rows, codes, scales, pos: int) -> None:
     b, h, t, d = rows.shape
     check(load().tsattn_kv_append_int8(DTYPES[rows.dtype], b, h, t, d, view(rows), view(codes),
                                        view(scales), int(pos), _stream(rows)))
+
+
+def project_rope_append(x, weights, biases, q_out, k_cache, v_cache, scales, cos, sin, pos: int,
+                        heads_q: int, heads_kv: int) -> None:
+    """The cached ``MultiHeadAttention`` step before its attention call
+    (``nn/transformer.py:124-142``) in one kernel: q / k / v projections of
+    ``x`` [B, T, E] (``weights`` / ``biases``: the three ``Linear`` layers'
+    arrays, biases may be None), RoPE of q and k at positions pos .. (cos /
+    sin: the device tables of ``rotary_embedding``, or None) and the append
+    of k and v at ``pos`` (``scales``: (key, value) fp32 scale arrays of an
+    int8 cache, or None).  q_out [B, Hq, T, D] receives the rotated queries.
+    Raises NotImplementedError outside the kernel's shapes (f16 / bf16, head
+    dim 64 / 128, E % 16 == 0): project and append in steps then."""
+    b, t, e = x.shape
+    xv = View(x.data_ptr())
+    xv.stride[0], xv.stride[1], xv.stride[2], xv.stride[3] = x.stride(0), 0, x.stride(1), 1
+    ptr = lambda a: None if a is None else a.data_ptr()
+    bq, bk, bv = biases if biases is not None else (None, None, None)
+    ks, vs = (None, None) if scales is None else (ctypes.byref(view(scales[0])), ctypes.byref(view(scales[1])))
+    check(load().tsattn_qkv_rope_append(
+        DTYPES[x.dtype], b, t, e, heads_q, heads_kv, q_out.shape[-1], ctypes.byref(xv),
+        *(w.data_ptr() for w in weights), ptr(bq), ptr(bk), ptr(bv), view(q_out), view(k_cache),
+        view(v_cache), ks, vs, ptr(cos), ptr(sin), int(pos), _stream(x)))

@@ -16,7 +16,7 @@ from ctypes import POINTER, c_char_p, c_double, c_int, c_int32, c_int64, c_size_
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_native" / "libtsattn.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK, ERR_INVALID, ERR_UNSUPPORTED, ERR_HIP = 0, 1, 2, 3
 F32, F16, BF16, F64, BOOL, I8 = 0, 1, 2, 3, 4, 5

@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define TSATTN_ABI_VERSION 7
+#define TSATTN_ABI_VERSION 8
 
 typedef enum {
   TSATTN_OK = 0,
@@ -147,7 +147,10 @@ int tsattn_profile_read(int index, char *name, size_t name_len, long long *launc
 int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                         const tsattn_view *v, const tsattn_view *out, void *lse, void *stream);
 
-/* Bytes of scratch tsattn_sdpa_backward needs (row deltas and row LSEs). */
+/* Bytes of scratch tsattn_sdpa_backward needs: row deltas and row LSEs (fp32,
+ * 2 per query row), the keep bits when dropping without
+ * p->dropout_bits, and on the MFMA kernels room for dS stored once (2 KiB per
+ * 32 x 32 tile the causal structure visits). */
 size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
 
 /*
@@ -155,6 +158,9 @@ size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
  * blockwise, with delta = rowsum(dout * out).  Replaces
  * src/tensorsmith/nn/attention.py:200-248 (incl. the GQA group sums at
  * :245-247).  Deterministic: no atomics, every element is written once.
+ * With the queried workspace the MFMA path stores dS from the dK/dV kernel
+ * and forms dQ as one GEMM over it; a smaller workspace that still holds the
+ * row values (and keep bits) makes the dQ kernel recompute S and dP instead.
  */
 int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                          const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,

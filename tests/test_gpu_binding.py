@@ -39,9 +39,9 @@ def host(t):
     return t.detach().float().cpu().numpy()
 
 
-def test_binding_loads_abi7():
+def test_binding_loads_abi():
     lib = B.load()
-    assert lib.tsattn_abi_version() == 7
+    assert lib.tsattn_abi_version() == B.ABI_VERSION == 8
     assert B.Problem.dropout_bits.offset == 152
 
 
@@ -116,3 +116,34 @@ def test_binding_decode_and_int8_append():
     want_codes, want_scales = A.quantize_int8(host(kc[:, :, :length]))
     np.testing.assert_array_equal(codes[:, :, 16:16 + length].cpu().numpy(), want_codes)
     np.testing.assert_array_equal(scales[:, :, 16:16 + length].cpu().numpy(), want_scales)
+
+
+@pytest.mark.parametrize("quantized", [False, True])
+def test_binding_project_rope_append(quantized):
+    """The cached step before the attention through the binding gives the
+    same bits as the C-ABI driver of the parity suite (test_gpu_qkv.py checks
+    that driver against the oracle)."""
+    say(f"binding: fused projection + RoPE + append, int8 cache={quantized}")
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    b, t, e, hq, hkv, d, cap, pos = 2, 3, 256, 4, 2, 128, 16, 5
+    x = torch.randn((b, t, e), generator=gen, device="cuda").half()
+    ws = [(torch.randn((h * d, e), generator=gen, device="cuda") / 16).half() for h in (hq, hkv, hkv)]
+    bs = [(torch.randn(h * d, generator=gen, device="cuda") / 10).half() for h in (hq, hkv, hkv)]
+    ang = torch.arange(pos + t, device="cuda", dtype=torch.float32)[:, None] * torch.exp(
+        -torch.arange(0, d, 2, device="cuda", dtype=torch.float32) / d * np.log(10000.0))
+    cos, sin = ang.cos().half(), ang.sin().half()
+    outs = []
+    for drive in ("abi", "binding"):
+        q = torch.zeros((b, hq, t, d), dtype=torch.float16, device="cuda")
+        cdt = torch.int8 if quantized else torch.float16
+        kc, vc = (torch.zeros((b, hkv, cap, d), dtype=cdt, device="cuda") for _ in range(2))
+        sc = tuple(torch.ones((b, hkv, cap, 1), device="cuda") for _ in range(2)) if quantized else None
+        if drive == "abi":
+            abi.qkv_rope_append(x, *ws, bs, q, kc, vc, sc, cos, sin, pos, hq, hkv)
+        else:
+            B.project_rope_append(x, ws, bs, q, kc, vc, sc, cos, sin, pos, hq, hkv)
+        torch.cuda.synchronize()
+        outs.append([q, kc, vc] + list(sc or ()))
+    for got, want in zip(outs[1], outs[0]):
+        assert torch.equal(got, want)
+    assert outs[0][1][:, :, pos:pos + t].abs().sum() > 0
