@@ -135,7 +135,9 @@ int check_rope(const tsattn_rope_desc *r, const tsattn::Problem &pr, tsattn::Rop
                 "with tsattn_rope instead", r->rotary_dim);
   if (reinterpret_cast<uintptr_t>(r->cos) % 8 || reinterpret_cast<uintptr_t>(r->sin) % 8)
     return fail(TSATTN_ERR_UNSUPPORTED, "RoPE tables must be 8-byte aligned; rotate with tsattn_rope instead");
-  *out = tsattn::RopeDesc{r->cos, r->sin, r->rotary_dim, r->q_pos0, r->k_pos0};
+  if (reinterpret_cast<uintptr_t>(r->q_rotated) % 16)
+    return fail(TSATTN_ERR_INVALID, "the rotated-query buffer must be 16-byte aligned");
+  *out = tsattn::RopeDesc{r->cos, r->sin, r->rotary_dim, r->q_pos0, r->k_pos0, r->q_rotated};
   return TSATTN_OK;
 }
 

@@ -612,12 +612,15 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     // RoPE folded in: dK of the unrotated keys = the inverse rotation of the
     // rounded dK, key position kpos0 + kw + r, one 16-byte row chunk at a time.
     if (rope_back) {
+      int64_t rows[32 * CPR / 64];
+      int p0[32 * CPR / 64];
 #pragma unroll
       for (int u = 0; u < 32 * CPR / 64; ++u) {
         const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-        const int key = kw + r < p.Sk ? kw + r : p.Sk - 1;  // rows past Sk: not stored
-        rotate_chunk<T>(vr[u], p.rope, p.rope.kpos0 + key, 4 * q, true);
+        rows[u] = p.rope.kpos0 + (kw + r < p.Sk ? kw + r : p.Sk - 1);  // rows past Sk: not stored
+        p0[u] = 4 * q;
       }
+      rotate_chunks<T, 32 * CPR / 64>(vr, p.rope, rows, p0, true);
     }
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
@@ -652,12 +655,15 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DK + ((q ^ (r % CPR)) * 16));
       }
       if (pass == 0 && p.rope.R > 0) {
+        int64_t rows[32 * CPR / 64];
+        int p0[32 * CPR / 64];
 #pragma unroll
         for (int u = 0; u < 32 * CPR / 64; ++u) {
           const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-          const int key = kw + r < p.Sk ? kw + r : p.Sk - 1;  // rows past Sk: not stored
-          rotate_chunk<T>(vr[u], p.rope, p.rope.kpos0 + key, 4 * q, true);
+          rows[u] = p.rope.kpos0 + (kw + r < p.Sk ? kw + r : p.Sk - 1);  // rows past Sk: not stored
+          p0[u] = 4 * q;
         }
+        rotate_chunks<T, 32 * CPR / 64>(vr, p.rope, rows, p0, true);
       }
 #pragma unroll
       for (int u = 0; u < 32 * CPR / 64; ++u) {
@@ -754,10 +760,15 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     // RoPE folded in: rotate the query fragments as the forward did, and
     // stage the rotated rows for the dK/dV kernel.
     if (p.rope.R > 0) {
-      const int64_t row = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
+      int64_t rows[SKQ];
+      int p0[SKQ];
 #pragma unroll
-      for (int ks = 0; ks < SKQ; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
-      if (qrow < p.Sq) {
+      for (int ks = 0; ks < SKQ; ++ks) {
+        rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
+        p0[ks] = 8 * ks + 4 * h;
+      }
+      rotate_chunks<T, SKQ>(qf, p.rope, rows, p0, false);
+      if (qrow < p.Sq && !p.rope.qrot) {  // (qrot: the forward stored them)
         T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
 #pragma unroll
         for (int ks = 0; ks < SKQ; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
@@ -1055,12 +1066,15 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // RoPE folded in: dQ of the unrotated queries = the inverse rotation of the
   // rounded dQ (rotary_embedding's VJP), one 16-byte row chunk at a time.
   if (p.rope.R > 0) {
+    int64_t rows[32 * CPR / 64];
+    int p0[32 * CPR / 64];
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-      const int row = qw + r < p.Sq ? qw + r : p.Sq - 1;  // rows past Sq: not stored
-      rotate_chunk<T>(vr[u], p.rope, p.rope.qpos0 + row, 4 * q, true);
+      rows[u] = p.rope.qpos0 + (qw + r < p.Sq ? qw + r : p.Sq - 1);  // rows past Sq: not stored
+      p0[u] = 4 * q;
     }
+    rotate_chunks<T, 32 * CPR / 64>(vr, p.rope, rows, p0, true);
   }
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
@@ -1101,7 +1115,7 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a) {
     a.delta[row] = -dsum;
     a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
   }
-  if (p.rope.R > 0) {
+  if (p.rope.R > 0 && !p.rope.qrot) {  // (qrot: the forward stored them)
     const T *qi = head_ptr<T>(a.q, b, hq) + static_cast<int64_t>(qrow) * a.q.s2;
     T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
 #pragma unroll
@@ -1327,12 +1341,15 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
     }
     // RoPE folded in: the inverse rotation of the rounded dQ.
     if (p.rope.R > 0) {
+      int64_t rows[32 * CPR / 64];
+      int p0[32 * CPR / 64];
 #pragma unroll
       for (int u = 0; u < 32 * CPR / 64; ++u) {
         const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-        const int row = qs + r < p.Sq ? qs + r : p.Sq - 1;  // rows past Sq: not stored
-        rotate_chunk<T>(vr[u], p.rope, p.rope.qpos0 + row, 4 * q, true);
+        rows[u] = p.rope.qpos0 + (qs + r < p.Sq ? qs + r : p.Sq - 1);  // rows past Sq: not stored
+        p0[u] = 4 * q;
       }
+      rotate_chunks<T, 32 * CPR / 64>(vr, p.rope, rows, p0, true);
     }
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
@@ -1443,10 +1460,11 @@ hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, Vie
                                 float *delta, void *ds, hipStream_t st) {
   View qk = q;
   if (p.rope.R > 0) {
-    // rotated query rows staged after the row values, 256-byte aligned
+    // rotated query rows: the forward's (rope.qrot), or staged after the row
+    // values, 256-byte aligned
     const int64_t D = p.Dqk;
-    qk = View{reinterpret_cast<char *>(delta) + mfma_rope_stage_offset(p),
-              static_cast<int64_t>(p.Hq) * p.Sq * D, static_cast<int64_t>(p.Sq) * D, D};
+    void *rows = p.rope.qrot ? p.rope.qrot : reinterpret_cast<char *>(delta) + mfma_rope_stage_offset(p);
+    qk = View{rows, static_cast<int64_t>(p.Hq) * p.Sq * D, static_cast<int64_t>(p.Sq) * D, D};
   }
   BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
             static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale),

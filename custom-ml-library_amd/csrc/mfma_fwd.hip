@@ -37,7 +37,8 @@
 // computes) for the backward.
 //
 // RoPE (Problem::rope, R > 0): the prologue rotates the query fragments it
-// loads (the keys come rotated), bit-identical to a separate tsattn_rope.
+// loads (the keys come rotated), bit-identical to a separate tsattn_rope;
+// with rope.qrot set the epilogue also stores them there for the backward.
 //
 // Masks (template MK): a key mask reduced to per-row lengths costs one ballot
 // per tile; a general boolean or additive mask (MK = 1 / 2) is read per
@@ -135,12 +136,20 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 #pragma unroll
   for (int ks = 0; ks < SKS; ++ks)
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
-  // RoPE folded in: rotate the lane's channels 16 ks + 8 h .. + 7 (pairs
-  // 8 ks + 4 h ..) by position qpos0 + qrow, exactly as tsattn_rope would.
-  if (p.rope.R > 0) {
-    const int64_t row = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
+  // RoPE folded in: the lane's channels 16 ks + 8 h .. + 7 (pairs 8 ks +
+  // 4 h ..) rotate by position qpos0 + qrow, exactly as tsattn_rope would.
+  // The table loads go out with the Q loads; the rotation itself runs after
+  // the first tiles' DMA issue, under their latency.
+  const bool rope = p.rope.R > 0;
+  int rp0[SKS];
+  u32x2 rcw[SKS], rsw[SKS];
 #pragma unroll
-    for (int ks = 0; ks < SKS; ++ks) rotate_chunk<T>(qf[ks], p.rope, row, 8 * ks + 4 * h, false);
+  for (int ks = 0; ks < SKS; ++ks) rp0[ks] = 8 * ks + 4 * h;
+  if (rope) {
+    int64_t rows[SKS];
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks) rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // past Sq: unused
+    rope_load_tables<T, SKS>(p.rope, rows, rp0, rcw, rsw);
   }
   // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
   // DMA loads below, so a first use of qf inside the main loop would make it
@@ -247,6 +256,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
   __syncthreads();
   for (int t = 0; t < PD; ++t) issue(t);
+  if (rope) rope_rotate_loaded<T, SKS>(qf, rcw, rsw, rp0, p.rope.R / 2, false);
   wait_vm_n<(PD - 1) * LPT>();
   __syncthreads();
 
@@ -404,6 +414,14 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     it_end(j);
   }
   wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
+
+  // RoPE with a rotated-query buffer: the rotated rows, for the backward's
+  // dK/dV kernel (which reads Q tiles by DMA and cannot rotate them).
+  if (p.rope.qrot && qrow < p.Sq) {
+    T *qr = static_cast<T *>(p.rope.qrot) + ((static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow) * DK + 8 * h;
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks) *reinterpret_cast<u32x4 *>(qr + 16 * ks) = qf[ks];
+  }
 
   const float lt = xor32_sum(l);  // lanes c and c+32 share a query row
   const float inv = lt > 0.f ? 1.f / lt : 0.f;

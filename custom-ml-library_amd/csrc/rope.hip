@@ -45,54 +45,68 @@ __global__ __launch_bounds__(NT) void rope_kernel(RopeArgs a) {
   }
 }
 
-// The same with one thread per 16-byte chunk of a row (8 16-bit or 4 f32
-// values, NP = 4 or 2 pairs): one 16-byte load and store per thread and one
-// 8-byte load from each table.  Needs 16-byte aligned rows, D * size(T) a
-// multiple of 16, R a multiple of 2 NP (a chunk is wholly inside or outside
-// the rotated channels) and 8-byte aligned tables.
+// The same with 16-byte chunks of rows (8 16-bit or 4 f32 values, NP = 4 or
+// 2 pairs): a workgroup takes NT * RU consecutive chunks of one (b, h) --
+// block `blk` of the nblk blocks of that head, so the head's coordinates come
+// from the workgroup index alone -- and a thread RU of them, NT apart (each
+// load instruction of a wave covers 1 KiB of consecutive chunks), all its
+// loads issued before any rotation; one 8-byte load from each table per
+// chunk.  Needs 16-byte aligned rows, D * size(T) a multiple of 16, R a
+// multiple of 2 NP (a chunk is wholly inside or outside the rotated
+// channels), 8-byte aligned tables and T * D * size(T) / 16 < 2^31.
+constexpr int RU = 4;
+
 template <typename T>
-__global__ __launch_bounds__(NT) void rope_vec_kernel(RopeArgs a) {
+__global__ __launch_bounds__(NT) void rope_vec_kernel(RopeArgs a, int nblk) {
   constexpr int CH = 16 / static_cast<int>(sizeof(T)), NP = CH / 2;
   const int cpr = a.D / CH;
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * NT + threadIdx.x;
-  const int64_t rows = static_cast<int64_t>(a.B) * a.H * a.T;
-  if (idx >= rows * cpr) return;
-  const int64_t row = idx / cpr;
-  const int q = static_cast<int>(idx - row * cpr);
-  const int t = static_cast<int>(row % a.T);
-  const int64_t bh = row / a.T;
-  const int h = static_cast<int>(bh % a.H), b = static_cast<int>(bh / a.H);
-  const T *x = static_cast<const T *>(a.x.data) + b * a.x.s0 + h * a.x.s1 + static_cast<int64_t>(t) * a.x.s2;
-  T *y = static_cast<T *>(const_cast<void *>(a.out.data)) + b * a.out.s0 + h * a.out.s1 +
-         static_cast<int64_t>(t) * a.out.s2;
-  u32x4 v = *reinterpret_cast<const u32x4 *>(x + q * CH);
-  const int p0 = q * NP;
-  if (2 * p0 < a.R) {
-    const int64_t at = (a.pos0 + t) * (a.R / 2) + p0;
-    const u32x2 cw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(a.cos) + at);
-    const u32x2 sw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(a.sin) + at);
-    if constexpr (sizeof(T) == 4) {
+  const int bh = blockIdx.x / nblk, blk = blockIdx.x - bh * nblk;
+  const int h = bh % a.H, b = bh / a.H;
+  const int n = a.T * cpr;  // chunks of this head
+  const T *xb = static_cast<const T *>(a.x.data) + b * a.x.s0 + h * a.x.s1;
+  T *yb = static_cast<T *>(const_cast<void *>(a.out.data)) + b * a.out.s0 + h * a.out.s1;
+  u32x4 v[RU];
+  int tq[RU][2];
 #pragma unroll
-      for (int m = 0; m < NP; ++m) {
-        // vector elements go through scalars: a bit cast of `v[i]` itself
-        // reads element 0
-        const unsigned w0 = v[2 * m], w1 = v[2 * m + 1], cb = cw[m], sb = sw[m];
-        T x0 = __builtin_bit_cast(T, w0), x1 = __builtin_bit_cast(T, w1);
-        rotate_pair(x0, x1, __builtin_bit_cast(T, cb), __builtin_bit_cast(T, sb), a.inverse != 0);
-        v[2 * m] = __builtin_bit_cast(unsigned, x0);
-        v[2 * m + 1] = __builtin_bit_cast(unsigned, x1);
-      }
-    } else {
+  for (int u = 0; u < RU; ++u) {
+    int idx = (blk * RU + u) * NT + static_cast<int>(threadIdx.x);
+    idx = idx < n ? idx : n - 1;  // past the head: reload its last chunk, store nothing
+    const int t = idx / cpr;
+    tq[u][0] = t;
+    tq[u][1] = idx - t * cpr;
+    v[u] = *reinterpret_cast<const u32x4 *>(xb + static_cast<int64_t>(t) * a.x.s2 + tq[u][1] * CH);
+  }
 #pragma unroll
-      for (int m = 0; m < NP; ++m) {
-        const int sh = (m & 1) * 16;
-        const T c = __builtin_bit_cast(T, static_cast<uint16_t>(cw[m >> 1] >> sh));
-        const T sn = __builtin_bit_cast(T, static_cast<uint16_t>(sw[m >> 1] >> sh));
-        v[m] = rotate_word<T>(v[m], c, sn, a.inverse != 0);
+  for (int u = 0; u < RU; ++u) {
+    const int t = tq[u][0], q = tq[u][1], p0 = q * NP;
+    if (2 * p0 < a.R) {
+      const int64_t at = (a.pos0 + t) * (a.R / 2) + p0;
+      const u32x2 cw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(a.cos) + at);
+      const u32x2 sw = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(a.sin) + at);
+      if constexpr (sizeof(T) == 4) {
+#pragma unroll
+        for (int m = 0; m < NP; ++m) {
+          // vector elements go through scalars: a bit cast of `v[u][i]`
+          // itself reads element 0
+          const unsigned w0 = v[u][2 * m], w1 = v[u][2 * m + 1], cb = cw[m], sb = sw[m];
+          T x0 = __builtin_bit_cast(T, w0), x1 = __builtin_bit_cast(T, w1);
+          rotate_pair(x0, x1, __builtin_bit_cast(T, cb), __builtin_bit_cast(T, sb), a.inverse != 0);
+          v[u][2 * m] = __builtin_bit_cast(unsigned, x0);
+          v[u][2 * m + 1] = __builtin_bit_cast(unsigned, x1);
+        }
+      } else {
+#pragma unroll
+        for (int m = 0; m < NP; ++m) {
+          const int sh = (m & 1) * 16;
+          const T c = __builtin_bit_cast(T, static_cast<uint16_t>(cw[m >> 1] >> sh));
+          const T sn = __builtin_bit_cast(T, static_cast<uint16_t>(sw[m >> 1] >> sh));
+          v[u][m] = rotate_word<T>(v[u][m], c, sn, a.inverse != 0);
+        }
       }
     }
+    if ((blk * RU + u) * NT + static_cast<int>(threadIdx.x) < n)
+      *reinterpret_cast<u32x4 *>(yb + static_cast<int64_t>(t) * a.out.s2 + q * CH) = v[u];
   }
-  *reinterpret_cast<u32x4 *>(y + q * CH) = v;
 }
 
 bool rope_vec_ok(const RopeArgs &a, int esize) {
@@ -100,7 +114,8 @@ bool rope_vec_ok(const RopeArgs &a, int esize) {
   auto al = [](const void *p, int n) { return reinterpret_cast<uintptr_t>(p) % n == 0; };
   auto st = [&](const View &v) { return (v.s0 * esize) % 16 == 0 && (v.s1 * esize) % 16 == 0 && (v.s2 * esize) % 16 == 0; };
   return (a.D * esize) % 16 == 0 && a.R % ch == 0 && al(a.x.data, 16) && al(a.out.data, 16) &&
-         st(a.x) && st(a.out) && al(a.cos, 8) && al(a.sin, 8);
+         st(a.x) && st(a.out) && al(a.cos, 8) && al(a.sin, 8) &&
+         static_cast<int64_t>(a.T) * (a.D * esize / 16) + NT * RU < (int64_t(1) << 31);
 }
 
 struct AppendArgs {
@@ -198,11 +213,14 @@ hipError_t launch_rope(int dtype, int B, int H, int T, int D, int R, View x, Vie
   Probe pr_("rope", st);
   const int esize = dtype == TSATTN_F32 ? 4 : 2;
   if (rope_vec_ok(a, esize)) {
-    const int64_t chunks = static_cast<int64_t>(B) * H * T * (D * esize / 16);
-    const dim3 g(static_cast<unsigned>((chunks + NT - 1) / NT));
-    if (dtype == TSATTN_F32) rope_vec_kernel<float><<<g, NT, 0, st>>>(a);
-    else if (dtype == TSATTN_F16) rope_vec_kernel<f16><<<g, NT, 0, st>>>(a);
-    else rope_vec_kernel<bf16><<<g, NT, 0, st>>>(a);
+    const int64_t chunks = static_cast<int64_t>(T) * (D * esize / 16);  // per head
+    const int nblk = static_cast<int>((chunks + NT * RU - 1) / (NT * RU));
+    const int64_t blocks = static_cast<int64_t>(B) * H * nblk;
+    if (blocks >= (int64_t(1) << 31)) return hipErrorInvalidConfiguration;
+    const dim3 g(static_cast<unsigned>(blocks));
+    if (dtype == TSATTN_F32) rope_vec_kernel<float><<<g, NT, 0, st>>>(a, nblk);
+    else if (dtype == TSATTN_F16) rope_vec_kernel<f16><<<g, NT, 0, st>>>(a, nblk);
+    else rope_vec_kernel<bf16><<<g, NT, 0, st>>>(a, nblk);
   } else if (dtype == TSATTN_F32) {
     rope_kernel<float><<<row_grid(B, H, T), NT, 0, st>>>(a);
   } else if (dtype == TSATTN_F16) {

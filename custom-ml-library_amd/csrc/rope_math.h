@@ -76,4 +76,51 @@ __device__ __forceinline__ void rotate_chunk(u32x4 &x, const RopeDesc &r, int64_
   if (p0 < half) x = y;
 }
 
+// rotate_chunk over N chunks at once, in two steps, so that a caller can
+// put other work (DMA issue) between the table loads and the rotation:
+// rope_load_tables issues all 2 N table loads -- x[i] will hold pairs p0[i]
+// .. p0[i] + 3 of table row row[i] -- and resolves them (the empty asm
+// statements use every loaded value unconditionally: the compiler cannot
+// sink a load into the conditional use below it, which would serialise one
+// memory latency per chunk); rope_rotate_loaded then rotates from registers.
+template <typename T, int N>
+__device__ __forceinline__ void rope_load_tables(const RopeDesc &r, const int64_t (&row)[N],
+                                                 const int (&p0)[N], u32x2 (&cw)[N], u32x2 (&sw)[N]) {
+  const int half = r.R / 2;
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const int pc = p0[i] < half ? p0[i] : half - 4;
+    const int64_t at = row[i] * half + pc;
+    cw[i] = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(r.cos) + at);
+    sw[i] = *reinterpret_cast<const u32x2 *>(static_cast<const T *>(r.sin) + at);
+  }
+#pragma unroll
+  for (int i = 0; i < N; ++i) asm volatile("" : "+v"(cw[i]), "+v"(sw[i]));
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void rope_rotate_loaded(u32x4 (&x)[N], const u32x2 (&cw)[N], const u32x2 (&sw)[N],
+                                                   const int (&p0)[N], int half, bool inverse) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    u32x4 y;
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int sh = (m & 1) * 16;
+      const T c = __builtin_bit_cast(T, static_cast<uint16_t>(cw[i][m >> 1] >> sh));
+      const T s = __builtin_bit_cast(T, static_cast<uint16_t>(sw[i][m >> 1] >> sh));
+      y[m] = rotate_word<T>(x[i][m], c, s, inverse);
+    }
+    if (p0[i] < half) x[i] = y;
+  }
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void rotate_chunks(u32x4 (&x)[N], const RopeDesc &r, const int64_t (&row)[N],
+                                              const int (&p0)[N], bool inverse) {
+  u32x2 cw[N], sw[N];
+  rope_load_tables<T, N>(r, row, p0, cw, sw);
+  rope_rotate_loaded<T, N>(x, cw, sw, p0, r.R / 2, inverse);
+}
+
 }  // namespace tsattn

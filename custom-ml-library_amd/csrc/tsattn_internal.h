@@ -73,6 +73,7 @@ struct RopeDesc {
   const void *cos, *sin;
   int R;
   int64_t qpos0, kpos0;
+  void *qrot;  // rotated query rows [B, Hq, Sq, Dqk]: written by the forward, read by the backward
 };
 
 // Attention dropout (on = 0: none): keep a 16-bit word w iff w >= thr, kept

@@ -58,7 +58,8 @@ class Problem(ctypes.Structure):
 
 
 class RopeDesc(ctypes.Structure):
-    """``tsattn_rope_desc``: cos / sin tables, rotary dim, query / key positions."""
+    """``tsattn_rope_desc``: cos / sin tables, rotary dim, query / key positions,
+    optional rotated-query buffer."""
 
     _fields_ = [
         ("cos", c_void_p),
@@ -66,6 +67,7 @@ class RopeDesc(ctypes.Structure):
         ("rotary_dim", c_int32),
         ("q_pos0", c_int64),
         ("k_pos0", c_int64),
+        ("q_rotated", c_void_p),
     ]
 
 

@@ -258,6 +258,12 @@ def scaled_dot_product_attention(
         q = _rope_rows(q, q_pos0, base, dim, False, query.device)
         vq = _view(q)
     elif rope is not None:
+        if recording:
+            # the forward also stores the rotated queries, which the backward's
+            # dK/dV kernel reads (instead of rotating and staging them again)
+            q_rot = torch.empty((b, hq, qlen, dim), dtype=q.dtype, device=tdev)
+            rope[0].q_rotated = q_rot.data_ptr()
+            keep.append(q_rot)
         try:
             _lib.check(lib.tsattn_sdpa_forward_rope(ctypes.byref(prob), ctypes.byref(rope[0]), vq, vk,
                                                     vv, vo, lse_ptr, stream), "attention forward")

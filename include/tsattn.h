@@ -183,6 +183,12 @@ typedef struct tsattn_rope_desc {
   int32_t rotary_dim; /* even, 0 < rotary_dim <= dim_qk; later channels pass through */
   int64_t q_pos0;
   int64_t k_pos0;
+  /* Optional (NULL: unused), 16-byte aligned [B, Hq, Sq, dim_qk] contiguous
+   * rows.  tsattn_sdpa_forward_rope writes the rotated queries there (bits
+   * of tsattn_rope on q); tsattn_sdpa_backward_rope given the same buffer
+   * reads them instead of rotating and staging the queries itself.  The
+   * decode entry points ignore it. */
+  void *q_rotated;
 } tsattn_rope_desc;
 
 /*

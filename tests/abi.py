@@ -213,12 +213,13 @@ def forward_rope(q, k, v, desc, **kw):
     return out, lse, lib.tsattn_last_kernel_path()
 
 
-def backward_rope(q, k, v, out, g, lse, desc, **kw):
-    """tsattn_sdpa_backward_rope: gradients of the unrotated q and k."""
+def backward_rope(q, k, v, out, g, lse, desc, ws_bytes=None, **kw):
+    """tsattn_sdpa_backward_rope: gradients of the unrotated q and k (with the
+    queried workspace, or ws_bytes of it)."""
     p = problem(q, k, v, **kw)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     lib = _lib.load()
-    nbytes = lib.tsattn_sdpa_backward_rope_workspace(ctypes.byref(p))
+    nbytes = lib.tsattn_sdpa_backward_rope_workspace(ctypes.byref(p)) if ws_bytes is None else ws_bytes
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     _lib.check(lib.tsattn_sdpa_backward_rope(
         ctypes.byref(p), ctypes.byref(desc), view(q), view(k), view(v), view(out), view(g),

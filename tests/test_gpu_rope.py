@@ -236,6 +236,24 @@ def test_rope_folded_into_attention_is_bitwise_the_unfused_chain(case):
     for name, a_, b_ in (("O", out_f, out_u), ("LSE", lse_f, lse_u), ("dQ", dq_f, dq_u),
                          ("dK", dk_f, dk_u), ("dV", dv_f, dv_u)):
         assert torch.equal(a_, b_), name
+    # with a rotated-query buffer: the forward stores tsattn_rope(q) there and
+    # the backward reads it -- the same bits as without, in the stored-dS
+    # pipeline (the queried workspace) and in the recomputing one (a
+    # workspace holding only the row values and the staged queries)
+    rows_bytes = (2 * b * hq * sq * 4 + 255) // 256 * 256 + b * hq * sq * d * 2
+    want = {None: (dq_f, dk_f, dv_f),
+            rows_bytes: abi.backward_rope(q, k_rot, v, out_f, g, lse_f, desc, ws_bytes=rows_bytes, **kw)}
+    q_rot = torch.full((b, hq, sq, d), 7.0, dtype=q.dtype, device=q.device)
+    desc.q_rotated = q_rot.data_ptr()
+    out_r, lse_r, _ = abi.forward_rope(q, k_rot, v, desc, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(q_rot, rot(q, qp)), "rotated queries"
+    assert torch.equal(out_r, out_u) and torch.equal(lse_r, lse_u)
+    for ws, grads in want.items():
+        got = abi.backward_rope(q, k_rot, v, out_r, g, lse_r, desc, ws_bytes=ws, **kw)
+        torch.cuda.synchronize()
+        for name, a_, b_ in zip(("dQ", "dK", "dV"), got, grads):
+            assert torch.equal(a_, b_), f"{name} with the rotated-query buffer, workspace {ws}"
 
 
 DECODE_CASES = [

@@ -43,7 +43,7 @@ _STRUCT_FIELDS = {
                        "dim_v", "scale", "is_causal", "causal_offset", "kv_len", "kv_prefix",
                        "mask_kind", "mask_dtype", "mask", "dropout_p", "dropout_key",
                        "dropout_counter", "dropout_bits"],
-    "tsattn_rope_desc": ["cos", "sin", "rotary_dim", "q_pos0", "k_pos0"],
+    "tsattn_rope_desc": ["cos", "sin", "rotary_dim", "q_pos0", "k_pos0", "q_rotated"],
 }
 
 
