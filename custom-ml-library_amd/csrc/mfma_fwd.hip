@@ -138,19 +138,9 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
   // RoPE folded in: the lane's channels 16 ks + 8 h .. + 7 (pairs 8 ks +
   // 4 h ..) rotate by position qpos0 + qrow, exactly as tsattn_rope would.
-  // The table loads go out with the Q loads; the rotation itself runs after
-  // the first tiles' DMA issue, under their latency.
+  // The table loads and the rotation run after the first tiles' DMA issue,
+  // under their latency.
   const bool rope = p.rope.R > 0;
-  int rp0[SKS];
-  u32x2 rcw[SKS], rsw[SKS];
-#pragma unroll
-  for (int ks = 0; ks < SKS; ++ks) rp0[ks] = 8 * ks + 4 * h;
-  if (rope) {
-    int64_t rows[SKS];
-#pragma unroll
-    for (int ks = 0; ks < SKS; ++ks) rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // past Sq: unused
-    rope_load_tables<T, SKS>(p.rope, rows, rp0, rcw, rsw);
-  }
   // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
   // DMA loads below, so a first use of qf inside the main loop would make it
   // wait there for tiles still in flight.
@@ -256,7 +246,18 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
   __syncthreads();
   for (int t = 0; t < PD; ++t) issue(t);
-  if (rope) rope_rotate_loaded<T, SKS>(qf, rcw, rsw, rp0, p.rope.R / 2, false);
+  if (rope) {
+    // (the compiler's wait for the tables also covers the DMA parts issued
+    // before them, which the wait below needs anyway)
+    int64_t rows[SKS];
+    int rp0[SKS];
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks) {
+      rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
+      rp0[ks] = 8 * ks + 4 * h;
+    }
+    rotate_chunks<T, SKS>(qf, p.rope, rows, rp0, false);
+  }
   wait_vm_n<(PD - 1) * LPT>();
   __syncthreads();
 

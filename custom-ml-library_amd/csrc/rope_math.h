@@ -40,14 +40,24 @@ __device__ __forceinline__ void rotate_pair(T &x0, T &x1, T c, T s, bool inverse
 }
 
 // 16-bit T: one channel pair packed in a 32-bit word (low half = even
-// channel), rotated in place.
+// channel), rotated in place.  The same operations as rotate_pair, paired up so that each rounding step
+// rounds two values with one packed conversion: (x0 c, x1 c), (x1 s, x0 s),
+// then (y0, y1) -- the products of two 16-bit values are exact in fp32, and
+// rnd(-x1 s) = -rnd(x1 s), so the results are rotate_pair's bit for bit.
 template <typename T>
 __device__ __forceinline__ unsigned rotate_word(unsigned w, T c, T s, bool inverse) {
-  T x0 = __builtin_bit_cast(T, static_cast<uint16_t>(w & 0xFFFFu));
-  T x1 = __builtin_bit_cast(T, static_cast<uint16_t>(w >> 16));
-  rotate_pair(x0, x1, c, s, inverse);
-  return static_cast<unsigned>(__builtin_bit_cast(uint16_t, x0)) |
-         (static_cast<unsigned>(__builtin_bit_cast(uint16_t, x1)) << 16);
+#pragma clang fp contract(off)
+  typedef float f2v __attribute__((ext_vector_type(2)));
+  typedef T t2v __attribute__((ext_vector_type(2)));
+  const float fc = static_cast<float>(c);
+  const float fs = inverse ? -static_cast<float>(s) : static_cast<float>(s);
+  const t2v xv = __builtin_bit_cast(t2v, w);
+  const float x0 = static_cast<float>(xv[0]), x1 = static_cast<float>(xv[1]);
+  const t2v pc = __builtin_convertvector(f2v{x0 * fc, x1 * fc}, t2v);
+  const t2v ps = __builtin_convertvector(f2v{x1 * fs, x0 * fs}, t2v);
+  const f2v y{static_cast<float>(pc[0]) - static_cast<float>(ps[0]),
+              static_cast<float>(pc[1]) + static_cast<float>(ps[1])};
+  return __builtin_bit_cast(unsigned, __builtin_convertvector(y, t2v));
 }
 
 // Rotate one 16-byte chunk of a row -- 4 pairs packed in x, pairs p0 .. p0 + 3
