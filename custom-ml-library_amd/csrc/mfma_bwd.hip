@@ -431,6 +431,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
         if (i < SKQ) sacc = mfma32<T>(qa[i % (FD + 1)], kf[i], sacc);
@@ -444,6 +445,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         }
         __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
 
     // P = exp2(sacc sl), dS = P dpacc; rows crow(e, h) = 8 g + 4 h + e % 4.
@@ -538,6 +540,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int i = 0; i < FD; ++i) load(i);
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int i = 0; i < STEPS; ++i) {
         if (i < 2 * PDV) dv_acc[i % PDV] = mfma32<T>(gc[i % (FD + 1)], pp[i / PDV], dv_acc[i % PDV]);
@@ -545,6 +548,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         if (i + FD < STEPS) load(i + FD);
         __builtin_amdgcn_sched_barrier(0);
       }
+      __builtin_amdgcn_s_setprio(0);
     }
 
     // Stored dS (dQ as one GEMM after this kernel): the wave's packed dS
