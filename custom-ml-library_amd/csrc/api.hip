@@ -101,8 +101,8 @@ int check_problem(const tsattn_problem *p, tsattn::Problem *out) {
     q.drop.scale64 = 1.0 / (1.0 - p->dropout_p);
     q.drop.k0 = p->dropout_key[0];
     q.drop.k1 = p->dropout_key[1];
-    q.drop.c0 = p->dropout_counter + 1;
-    q.drop.c1 = q.drop.c0 == 0 ? 1 : 0;
+    q.drop.c0 = p->dropout_counter;
+    q.drop.c1 = 0;
     q.drop.bits = p->dropout_bits;
     q.drop.nkt = (q.Sk + 31) / 32;
     q.drop.sqp = (q.Sq + 3) / 4 * 4;

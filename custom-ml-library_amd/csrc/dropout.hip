@@ -1,7 +1,7 @@
 // The dropout keep mask of an attention problem, materialised: as bytes (one
-// thread per 16-word block of a query row), so it can be inspected and
-// checked against numpy.random.Philox on the host, and as the bits the MFMA
-// backward reads (philox.h draws the words).
+// thread per 16-word group of a query row), so it can be inspected and
+// checked against the host's restatement of the stream, and as the bits the
+// MFMA backward reads (philox.h draws the words).
 #include "philox.h"
 
 namespace tsattn {

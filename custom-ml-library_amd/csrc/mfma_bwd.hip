@@ -113,14 +113,17 @@ constexpr int KV_PD = 2;  // tiles in flight
 
 // Workgroups per CU: two, except the general-mask kernel at D = 128, whose
 // mask registers do not fit beside the two-workgroup register budget; alone
-// on its CU it has the accumulation registers as well.
+// on its CU it has the accumulation registers as well.  (The dropout kernel
+// at D = 128 spills 13 VGPRs at two per CU -- fragment reloads each tile --
+// and is still faster than alone on its CU: 0.88 against 1.07 ms at B16 H16
+// S2048 D128.)
 // Masks the dK/dV kernel stages through its LDS ring (modes 4 and 6: boolean
 // or 16-bit, key-contiguous with 16-byte aligned rows) hold no registers.
 constexpr bool mask_staged(int MK) { return MK == 4 || MK == 6; }
 
 template <int DK, int DV, int MK, bool DR>
 constexpr int dkdv_wg_per_cu() {
-  return ((MK != 0 && !mask_staged(MK)) || DR) && (DK > 64 || DV > 64) ? 1 : 2;
+  return (MK != 0 && !mask_staged(MK)) && (DK > 64 || DV > 64) ? 1 : 2;
 }
 
 // DK = head dim of q / k (and dK), DV = of v / dO (and dV); each 64 or 128.
@@ -483,8 +486,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float pv[4], dsv[4];
-        u32x4 bw{};
-        if constexpr (DR) bw = *reinterpret_cast<const u32x4 *>(btile + (8 * g + 4 * h) * 4);
+        // (read word by word where used: four words held at once spill)
+        const uint32_t *bw = reinterpret_cast<const uint32_t *>(btile + (8 * g + 4 * h) * 4);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int e = 4 * g + r, kc = 8 * g + r;

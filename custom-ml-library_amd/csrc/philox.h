@@ -1,43 +1,49 @@
-// Counter-based random numbers for attention dropout: Philox4x64-10 (Salmon,
-// Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC'11),
-// the generator behind numpy.random.Philox, so that a mask can be checked bit
-// for bit on the host.  Block n of a stream with key k and counter c is
-// Philox4x64-10 of the 256-bit counter c + 1 + n (NumPy increments before
-// each block); its four 64-bit outputs are 16 dropout words of 16 bits,
-// little-endian.
+// Counter-based random numbers for attention dropout: Philox4x32-10 (Salmon,
+// Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC'11;
+// the round constants and known-answer vectors of its Random123 release).
+// Word group n (16 dropout words of 16 bits) of a stream with key (K0, K1)
+// and counter c is the two blocks Philox4x32-10(t, key K0) and
+// Philox4x32-10(t + 1, key K0), t = 2 (c + n) mod 2^64, each of the 128-bit
+// counter (lo32 t, hi32 t, lo32 K1, hi32 K1): the four 32-bit outputs of each
+// block give 8 words, little-endian.  A round takes two 32 x 32 -> 64-bit
+// products (one instruction each on CDNA), where Philox4x64 needs eight
+// 32-bit multiplies for its two 64 x 64 -> 128-bit products.
 #pragma once
 
 #include "mfma_common.h"
 
 namespace tsattn {
 
-__device__ __forceinline__ void philox4x64(uint64_t (&c)[4], uint64_t k0, uint64_t k1) {
-  constexpr uint64_t M0 = 0xD2E7470EE14C6C93ull, M1 = 0xCA5A826395121157ull;
-  constexpr uint64_t W0 = 0x9E3779B97F4A7C15ull, W1 = 0xBB67AE8584CAA73Bull;
+__device__ __forceinline__ void philox4x32(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
 #pragma unroll
   for (int r = 0; r < 10; ++r) {
     if (r) {
       k0 += W0;
       k1 += W1;
     }
-    const uint64_t hi0 = __umul64hi(M0, c[0]), lo0 = M0 * c[0];
-    const uint64_t hi1 = __umul64hi(M1, c[2]), lo1 = M1 * c[2];
-    const uint64_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    const uint64_t p0 = static_cast<uint64_t>(M0) * c[0], p1 = static_cast<uint64_t>(M1) * c[2];
+    const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c[1] ^ k0;
+    const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c[3] ^ k1;
     c[0] = n0;
-    c[1] = lo1;
+    c[1] = static_cast<uint32_t>(p1);
     c[2] = n2;
-    c[3] = lo0;
+    c[3] = static_cast<uint32_t>(p0);
   }
 }
 
-// The 16 words of block n of the problem's dropout stream.
+// The 16 words of group n of the problem's dropout stream.
 __device__ __forceinline__ void dropout_block(const DropDesc &d, uint64_t n, uint64_t (&out)[4]) {
-  const uint64_t c0 = d.c0 + n;
-  out[0] = c0;
-  out[1] = d.c1 + (c0 < n ? 1u : 0u);  // carry past 2^64
-  out[2] = 0;
-  out[3] = 0;
-  philox4x64(out, d.k0, d.k1);
+  const uint64_t t = 2 * (d.c0 + n);
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    uint32_t c[4] = {static_cast<uint32_t>(t) | static_cast<uint32_t>(half), static_cast<uint32_t>(t >> 32),
+                     static_cast<uint32_t>(d.k1), static_cast<uint32_t>(d.k1 >> 32)};
+    philox4x32(c, static_cast<uint32_t>(d.k0), static_cast<uint32_t>(d.k0 >> 32));
+    out[2 * half] = c[0] | (static_cast<uint64_t>(c[1]) << 32);
+    out[2 * half + 1] = c[2] | (static_cast<uint64_t>(c[3]) << 32);
+  }
 }
 
 // Block index of the 16 words starting at key j16 (a multiple of 16) of

@@ -78,8 +78,9 @@ struct RopeDesc {
 
 // Attention dropout (on = 0: none): keep a 16-bit word w iff w >= thr, kept
 // probabilities times `scale` (f32 compute) / `scale64` (f64 compute), the
-// reference's keep.astype(compute dtype) / (1 - p); Philox key (k0, k1) and
-// first block counter (c0, c1) = the stream counter + 1 (128 bits).
+// reference's keep.astype(compute dtype) / (1 - p); Philox4x32 key k0 (two
+// 32-bit words), stream words k1 (the high half of every block counter) and
+// stream counter c0 (philox.h); c1 unused.
 struct DropDesc {
   int on;
   uint32_t thr;

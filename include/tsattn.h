@@ -84,9 +84,11 @@ typedef struct tsattn_problem {
    * Attention dropout (src/tensorsmith/nn/attention.py:140-144): probability
    * p in [0, 1) (0 = none) and the counter-based stream it draws from.
    * Element (b, h, i, j) takes 16-bit word L = ((b Hq + h) Sq + i) Sk16 + j
-   * (Sk16 = len_kv rounded up to 16) of the raw Philox4x64-10 stream of
-   * numpy.random.Philox(key = key[0] + 2^64 key[1], counter = counter)
-   * viewed as little-endian uint16, and is kept iff word >= round(65536 p);
+   * (Sk16 = len_kv rounded up to 16) of a Philox4x32-10 stream: words
+   * 16 n .. 16 n + 15 are the outputs of the blocks with 128-bit counters
+   * (lo32 t, hi32 t, lo32 key[1], hi32 key[1]) for t = 2 (counter + n) and
+   * t + 1 (mod 2^64) under the 64-bit key key[0], four 32-bit outputs per
+   * block as little-endian uint16 pairs; it is kept iff word >= round(65536 p);
    * kept probabilities scale by float32(1) / float32(1 - p).  The backward
    * uses the same mask: from `dropout_bits`, or regenerated from the same key
    * and counter.

@@ -11,10 +11,14 @@ kernel can reproduce; the hip kernels draw them from a counter-based
 generator instead, so that the backward (and any recompute) regenerates the
 same mask from (key, counter):
 
-* Philox4x64-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
-  easy as 1, 2, 3", SC'11) -- the generator behind ``numpy.random.Philox``;
-  ``raw_stream`` reproduces that bit generator's raw output for the same key
-  and counter (pinned in tests against NumPy itself);
+* Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+  easy as 1, 2, 3", SC'11), pinned in tests against the known-answer vectors
+  of its Random123 release; word group n (16 words) of the stream with a
+  128-bit key K = K0 + 2^64 K1 and counter c is the two blocks
+  Philox4x32-10(t, key K0) and Philox4x32-10(t + 1, key K0), t = 2 (c + n)
+  mod 2^64, of the 128-bit counter (lo32 t, hi32 t, lo32 K1, hi32 K1); each
+  block's four 32-bit outputs are 8 words, little-endian (``raw_stream``
+  packs them as uint64 outputs 4 n .. 4 n + 3);
 * element (b, h, i, j) of a [B, H, Sq, Sk] problem takes 16-bit word
   L = ((b H + h) Sq + i) Sk16 + j of the stream viewed as little-endian uint16
   (Sk16 = Sk rounded up to 16): bits 16 (L % 4) .. 16 (L % 4) + 15 of raw
@@ -35,51 +39,43 @@ import numpy as np
 from .attention import Problem, _as_compute, expand_gqa, reduce_gqa, _finite_or_zero
 from .halfprec import round_to
 
-M0, M1 = 0xD2E7470EE14C6C93, 0xCA5A826395121157  # round multipliers
-W0, W1 = 0x9E3779B97F4A7C15, 0xBB67AE8584CAA73B  # key bumps (golden ratio, sqrt(3) - 1)
+M0, M1 = 0xD2511F53, 0xCD9E8D57  # round multipliers
+W0, W1 = 0x9E3779B9, 0xBB67AE85  # key bumps (golden ratio, sqrt(3) - 1)
 _M32 = np.uint64(0xFFFFFFFF)
 _S32 = np.uint64(32)
 
 
-def _mulhilo(a, m: int):
-    """(high, low) 64-bit halves of the 128-bit products a * m (uint64 a)."""
-    al, ah = a & _M32, a >> _S32
-    ml, mh = np.uint64(m & 0xFFFFFFFF), np.uint64(m >> 32)
-    ll, lh, hl, hh = al * ml, al * mh, ah * ml, ah * mh
-    mid = (ll >> _S32) + (lh & _M32) + (hl & _M32)
-    lo = (ll & _M32) | ((mid & _M32) << _S32)
-    hi = hh + (lh >> _S32) + (hl >> _S32) + (mid >> _S32)
-    return hi, lo
-
-
-def philox4x64(c0, c1, c2, c3, key: int):
-    """Philox4x64-10 of counters (c0..c3 uint64 arrays) under a 128-bit key."""
-    k0 = np.uint64(key & 0xFFFFFFFFFFFFFFFF)
-    k1 = np.uint64((key >> 64) & 0xFFFFFFFFFFFFFFFF)
-    with np.errstate(over="ignore"):
-        for r in range(10):
-            if r:
-                k0 = k0 + np.uint64(W0)
-                k1 = k1 + np.uint64(W1)
-            hi0, lo0 = _mulhilo(c0, M0)
-            hi1, lo1 = _mulhilo(c2, M1)
-            c0, c1, c2, c3 = hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0
+def philox4x32(c0, c1, c2, c3, k0: int, k1: int):
+    """Philox4x32-10 of 128-bit counters (c0..c3: uint32 values held in
+    uint64 arrays) under the 64-bit key (k0, k1)."""
+    ka, kb = np.uint64(k0 & 0xFFFFFFFF), np.uint64(k1 & 0xFFFFFFFF)
+    for r in range(10):
+        if r:
+            ka = (ka + np.uint64(W0)) & _M32
+            kb = (kb + np.uint64(W1)) & _M32
+        p0 = np.uint64(M0) * c0  # < 2^64: exact
+        p1 = np.uint64(M1) * c2
+        c0, c1, c2, c3 = (p1 >> _S32) ^ c1 ^ ka, p1 & _M32, (p0 >> _S32) ^ c3 ^ kb, p0 & _M32
     return c0, c1, c2, c3
 
 
 def raw_stream(key: int, counter: int, n: int) -> np.ndarray:
-    """First n raw uint64 outputs of a Philox(key, counter) bit generator:
-    block b (outputs 4b .. 4b + 3) is Philox4x64-10 of counter + 1 + b."""
-    blocks = (n + 3) // 4
-    idx = np.arange(blocks, dtype=np.uint64)
-    base = counter + 1
+    """First n raw uint64 outputs of the dropout stream: outputs 4 g .. 4 g + 3
+    are word group g (block t = 2 (counter + g), then block t + 1; each block
+    as (out0 | out1 << 32, out2 | out3 << 32))."""
+    groups = (n + 3) // 4
+    g = np.arange(groups, dtype=np.uint64)
+    k_lo, k_hi = key & 0xFFFFFFFFFFFFFFFF, (key >> 64) & 0xFFFFFFFFFFFFFFFF
     with np.errstate(over="ignore"):
-        c0 = np.uint64(base & 0xFFFFFFFFFFFFFFFF) + idx
-    carry = (c0 < idx).astype(np.uint64)  # wrap past 2^64
-    c1 = np.uint64((base >> 64) & 0xFFFFFFFFFFFFFFFF) + carry
-    zero = np.zeros(blocks, dtype=np.uint64)
-    out = philox4x64(c0, c1, zero, zero, key)
-    return np.stack(out, axis=1).reshape(-1)[:n]
+        t = (np.uint64(counter & 0xFFFFFFFFFFFFFFFF) + g) * np.uint64(2)
+    outs = []
+    for half in (0, 1):
+        tt = t | np.uint64(half)
+        c = (tt & _M32, tt >> _S32, np.full(groups, k_hi & 0xFFFFFFFF, np.uint64),
+             np.full(groups, k_hi >> 32, np.uint64))
+        x0, x1, x2, x3 = philox4x32(*c, k_lo & 0xFFFFFFFF, k_lo >> 32)
+        outs += [x0 | (x1 << _S32), x2 | (x3 << _S32)]
+    return np.stack(outs, axis=1).reshape(-1)[:n]
 
 
 def threshold(p: float) -> int:

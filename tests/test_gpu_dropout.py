@@ -2,9 +2,9 @@
 
 The reference drops probabilities in its dense backend
 (src/tensorsmith/nn/attention.py:140-144, VJP :210-217) with uniforms from its
-global stream; the hip kernels regenerate a counter-based Philox4x64-10 mask
-(oracle/dropout.py states the element mapping and is pinned against
-numpy.random.Philox).  Checked here:
+global stream; the hip kernels regenerate a counter-based Philox4x32-10 mask
+(oracle/dropout.py states the element mapping and is pinned against the
+generator's published known-answer vectors).  Checked here:
 
 * the keep mask the kernels draw (tsattn_dropout_keep) equals the oracle's
   bit for bit -- ragged key lengths (rows padded to 16 words), GQA heads,

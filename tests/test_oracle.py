@@ -258,7 +258,8 @@ def test_rope_rows_depend_only_on_absolute_position():
 
 
 # ---------------------------------------------------------------------------
-# Dropout: Philox stream pinned against NumPy's own Philox bit generator; the
+# Dropout: Philox4x32-10 pinned against the known-answer vectors of its
+# Random123 release; the stream layout against those blocks one by one; the
 # element mapping against an explicit loop; the attention math against the
 # dropout-free oracle (p = 0), finite differences (fixed mask) and the
 # reference's mask value formula.
@@ -266,17 +267,43 @@ def test_rope_rows_depend_only_on_absolute_position():
 
 from oracle import dropout as DR  # noqa: E402
 
+# (counter words, key words) -> output words, Random123's kat_vectors for
+# philox4x32 with 10 rounds
+PHILOX4X32_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX4X32_KAT)
+def test_philox4x32_known_answers(ctr, key, want):
+    got = DR.philox4x32(*(np.array([c], np.uint64) for c in ctr), *key)
+    assert tuple(int(x[0]) for x in got) == want
+
 
 @pytest.mark.parametrize("key,counter", [(0, 0), (0x0123456789ABCDEF_FEDCBA9876543210, 5),
-                                         (2**128 - 1, 2**64 - 3), (987654321, 2**70 + 9)])
-def test_philox_stream_is_numpys_philox(key, counter):
-    want = np.random.Philox(key=key, counter=counter).random_raw(41)
-    np.testing.assert_array_equal(DR.raw_stream(key, counter, 41), want)
+                                         (2**128 - 1, 2**64 - 3), (987654321, 2**63 + 9)])
+def test_stream_is_the_philox_blocks_in_order(key, counter):
+    """Group g = blocks t = 2 (counter + g) and t + 1 (mod 2^64), counter
+    words (lo t, hi t, lo K1, hi K1), key K0; outputs packed little-endian."""
+    raw = DR.raw_stream(key, counter, 41)
+    k0, k1 = key & (2**64 - 1), key >> 64
+    words = []
+    for g in range(11):
+        for half in (0, 1):
+            t = (2 * (counter + g) + half) % 2**64
+            ctr = (t & 0xFFFFFFFF, t >> 32, k1 & 0xFFFFFFFF, k1 >> 32)
+            out = DR.philox4x32(*(np.array([c], np.uint64) for c in ctr), k0 & 0xFFFFFFFF, k0 >> 32)
+            x = [int(v[0]) for v in out]
+            words += [x[0] | x[1] << 32, x[2] | x[3] << 32]
+    assert [int(v) for v in raw] == words[:41]
 
 
 def test_keep_mask_element_mapping():
     key, counter, shape, p = 77, 3, (2, 3, 4, 5), 0.4
-    raw = np.random.Philox(key=key, counter=counter).random_raw(2 * 3 * 4 * 16 // 4)
+    raw = DR.raw_stream(key, counter, 2 * 3 * 4 * 16 // 4)
     got = DR.keep_mask(key, counter, shape, p)
     thr = DR.threshold(p)
     for b in range(2):
