@@ -1136,33 +1136,40 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a) {
 
 // ---------------------------------------------------------------------------
 // dQ from stored dS: dQ^T = scale K^T dS^T over the key tiles of each row
-// (one GEMM; the dK/dV kernel left dS in the workspace).  One workgroup = 256
-// query rows of one (b, q head), 4 waves x two 32-row subtiles (w and 7 - w,
-// sharing every K^T fragment), two workgroups per CU.  Per 32-key tile, K
+// (one GEMM; the dK/dV kernel left dS in the workspace).  One workgroup = 512
+// query rows of one (b, q head), 8 waves x two 32-row subtiles (w and 15 - w,
+// sharing every K^T fragment), one workgroup per CU: each K tile fetched
+// serves 512 rows (two 4-wave workgroups of 256 rows fetched it twice, 5%
+// slower at B16 H16 S2048 D128).  Per 32-key tile, K
 // (shared) and each wave's two dS tiles stream global -> LDS by DMA loads
 // into 3-stage rings, issued two tiles ahead; K^T and dS^T fragments come
 // from LDS transpose reads; one fence-free barrier per tile.  dS tiles past a
 // subtile's causal end, or past the rows, read as zeros (offsets past the
 // buffer range).
 // ---------------------------------------------------------------------------
-constexpr int QB2 = 256;          // query rows per workgroup
+constexpr int DQ_NT = 512, DQ_NW = DQ_NT / 64;  // one 8-wave workgroup per CU
+constexpr int QB2 = 64 * DQ_NW;   // query rows per workgroup
 constexpr int DS_PD = 2;          // tiles issued ahead
 constexpr int DS_NS = DS_PD + 1;  // ring stages: tile j is read in iteration j only
 
 template <typename T, int DK>
-__global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
+__global__ __launch_bounds__(DQ_NT, 1) void dq_ds_kernel(BwdArgs a) {
   constexpr int TILE_K = KT * DK * 2;
-  constexpr int KPARTS = TILE_K / 1024 / NW;  // K DMA loads per wave per tile
+  // K DMA loads per wave per tile (D = 64: one, the waves past the tile's
+  // four blocks loading nothing into the spare block, so that every wave
+  // issues the same count)
+  constexpr int KPARTS = TILE_K / 1024 > DQ_NW ? TILE_K / 1024 / DQ_NW : 1;
   constexpr int LPT = KPARTS + 4;             // all DMA loads per wave per tile
   constexpr int PDQ = DK / 32;                // 32-row blocks of dQ^T
   constexpr int QGK = DK / 32;
   constexpr int STEPS = 2 * PDQ;              // K^T fragments per tile (2 key k-steps)
   constexpr int KRING = DS_NS * TILE_K;
   constexpr int SRING = DS_NS * 2 * DS_TILE;  // per wave: two dS tiles per stage
-  constexpr int RINGS = KRING + NW * SRING;
-  constexpr int EPI = NW * 32 * 2 * DK;       // epilogue: 32 rows per wave at a time
+  constexpr int RINGS = KRING + DQ_NW * SRING;
+  constexpr int EPI = DQ_NW * 32 * 2 * DK;       // epilogue: 32 rows per wave at a time
   static_assert(EPI <= RINGS, "epilogue slices fit in the rings");
-  static_assert(KPARTS >= 1 && KPARTS * NW * 1024 == TILE_K, "tile loads split evenly over the waves");
+  static_assert(KPARTS * DQ_NW * 1024 == TILE_K || (KPARTS == 1 && TILE_K <= DQ_NW * 1024),
+                "tile loads split evenly over the waves");
   // K ring, the waves' dS rings, then a 1 KiB block that DMA parts past the
   // last tile land in
   __shared__ __attribute__((aligned(1024))) char lds[RINGS + 1024];
@@ -1174,13 +1181,13 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
   const int total = n_qb * p.Hq * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, rank;
-  heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);  // 2 WG per CU
+  heavy_first(logical, n_qb, p.Hq * p.B, 32, bh, rank);  // 1 WG per CU
   const int qb = n_qb - 1 - rank;  // long causal rows first
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
-  // Wave w takes the block's 32-row subtiles w and 7 - w, so that the
+  // Wave w takes the block's 32-row subtiles w and 15 - w, so that the
   // causal work of the four waves is alike (the subtiles share every K^T
   // fragment; the shorter one's operands past its end read as zeros).
-  const int q0 = qb * QB2, qa = q0 + 32 * w, qz = q0 + 32 * (7 - w);
+  const int q0 = qb * QB2, qa = q0 + 32 * w, qz = q0 + 32 * (2 * DQ_NW - 1 - w);
   const int kv_end = kv_end_for(p, b);
   // key tiles up to query row `last` (its cache end and causal window)
   auto tiles_to = [&](int last) {
@@ -1231,9 +1238,12 @@ __global__ __launch_bounds__(NT, 2) void dq_ds_kernel(BwdArgs a) {
   };
   auto issue_part = [&](const DmaTile &d, int u) {
     if (u < KPARTS) {
-      const int n = w + NW * u;
-      dma16(kdesc, spare + d.kst + ((n * 1024) & d.keep), koff,
-            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+      const int n = w + DQ_NW * u;  // wave-uniform
+      if (n * 1024 < TILE_K)
+        dma16(kdesc, spare + d.kst + ((n * 1024) & d.keep), koff,
+              d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+      else
+        dma16(kdesc, spare, koff, 0x80000000u);  // past the range: zeros into the spare block
     } else {
       const int s = (u - KPARTS) >> 1, half = (u - KPARTS) & 1;
       dma16_nt(sdesc, spare + d.sst + ((s * DS_TILE + half * 1024) & d.keep), loff,
@@ -1389,7 +1399,7 @@ void launch_mk(const BwdArgs &a, hipStream_t st) {
     const int n_qb = (p.Sq + QB2 - 1) / QB2;
     {
       Probe pr_(DR ? "bwd_dq_ds_dropout" : (MK ? "bwd_dq_ds_masked" : "bwd_dq_ds"), st);
-      dq_ds_kernel<T, DK><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+      dq_ds_kernel<T, DK><<<dim3(n_qb * p.Hq * p.B), dim3(DQ_NT), 0, st>>>(a);
     }
     return;
   }
