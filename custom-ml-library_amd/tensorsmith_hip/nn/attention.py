@@ -103,8 +103,17 @@ def scaled_dot_product_attention(
     (``tsattn_sdpa_forward_rope`` / ``_backward_rope``), with separate RoPE
     kernels where those do not apply.  ``k_pos0 = None``: the keys arrive
     already rotated (a KV cache) and only the query is rotated -- inside the
-    decode kernel (``tsattn_decode_forward_rope``) when that runs.
+    decode kernel (``tsattn_decode_forward_rope``) when that runs.  Other
+    dtypes than f32 / f16 / bf16 (float64) are rotated by ``rotary_embedding``
+    first and then attended as usual.
     """
+    if (_rope is not None and getattr(query, "device", None) is not None
+            and query.device.type == "hip" and query._data.dtype not in _ROPE_KERNEL_DTYPES()):
+        q_pos0, k_pos0, base = _rope
+        query = rotary_embedding(query, q_pos0, base)
+        if k_pos0 is not None:
+            key = rotary_embedding(key, k_pos0, base)
+        _rope = None
     # --- the reference's validation, same order and messages (:36-62) ---
     if any(t.ndim != 4 for t in (query, key, value)):
         raise ValueError("attention expects [batch, heads, sequence, channels]")
@@ -361,6 +370,13 @@ def decode_int8_cache(query: Tensor, cache, *, is_causal: bool, causal_offset: i
 
 
 _ROPE_TABLES: dict = {}
+
+
+def _ROPE_KERNEL_DTYPES():
+    """Dtypes the RoPE kernels and the folded attention kernels take."""
+    import torch
+
+    return (torch.float32, torch.float16, torch.bfloat16)
 
 
 def rope_tables(base: float, dim: int, dtype, dev, length: int):

@@ -33,8 +33,10 @@ def tables(length: int, rotary_dim: int, base: float = 10000.0, offset: int = 0)
 def rope(x, offset: int = 0, base: float = 10000.0, rotary_dim: int | None = None,
          dtype: str = "float32", inverse: bool = False):
     """RoPE of x [..., S, D] (values already in ``dtype``), rounded per
-    operation in ``dtype``; ``inverse`` gives the VJP's rotation."""
-    x = np.asarray(x, np.float32)
+    operation in ``dtype``; ``inverse`` gives the VJP's rotation.  float64
+    inputs stay float64 (the float32 tables cast up, as the reference casts
+    them to the input dtype)."""
+    x = np.asarray(x, np.float64 if dtype == "float64" else np.float32)
     seq, d = x.shape[-2], x.shape[-1]
     dim = d if rotary_dim is None else rotary_dim
     if dim <= 0 or dim % 2 or dim > d or offset < 0 or base <= 0:

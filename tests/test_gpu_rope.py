@@ -409,3 +409,23 @@ def test_attention_module_fused_rope_is_bitwise_the_two_step_path(dtype):
     np.testing.assert_array_equal(y_f, y_u)
     for a_, b_ in zip(g_f, g_u):
         np.testing.assert_array_equal(a_, b_)
+
+
+def test_rope_attention_in_float64_rotates_then_attends():
+    """float64 has no RoPE kernel: the mirror rotates with rotary_embedding
+    and runs the generic kernels -- against the oracle's float64 RoPE and
+    dense attention, forward and VJP (1e-10)."""
+    from tensorsmith_hip.nn import attention as attn_mod
+
+    rng = np.random.default_rng(8)
+    q, k, v, g = (rng.standard_normal((1, 2, 40, 16)) for _ in range(4))
+    tq, tk, tv = (ts.tensor(a, device="hip", dtype="float64", requires_grad=True) for a in (q, k, v))
+    out = attn_mod.scaled_dot_product_attention(tq, tk, tv, is_causal=True, _rope=(3, 3, 10000.0))
+    out.backward(ts.tensor(g, device="hip", dtype="float64"))
+    qr, kr = R.rope(q, 3, dtype="float64"), R.rope(k, 3, dtype="float64")
+    ref = A.sdpa(qr, kr, v, None, True, dtype="float64", backend="dense")
+    dq_r, dk_r, dv = ref.backward(g)
+    want = (ref.out, R.rope(dq_r, 3, dtype="float64", inverse=True),
+            R.rope(dk_r, 3, dtype="float64", inverse=True), dv)
+    for got, w in zip((out.numpy(), tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy()), want):
+        np.testing.assert_allclose(got, w, rtol=1e-10, atol=1e-10)

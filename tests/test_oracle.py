@@ -237,6 +237,19 @@ def test_rope_f32_is_complex_multiplication():
     np.testing.assert_allclose(y[..., 1::2], z.imag, rtol=0, atol=4e-7 * np.abs(x).max())
 
 
+def test_rope_f64_is_complex_multiplication():
+    """float64 inputs: the float32 cos / sin cast to float64, products and
+    sums in float64."""
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((3, 9, 16))
+    y = R.rope(x, offset=5, dtype="float64")
+    assert y.dtype == np.float64
+    c, s = R.tables(9, 16, 10000.0, 5)
+    z = (x[..., 0::2] + 1j * x[..., 1::2]) * (c.astype(np.float64) + 1j * s.astype(np.float64))
+    np.testing.assert_allclose(y[..., 0::2], z.real, rtol=0, atol=1e-15 * np.abs(x).max())
+    np.testing.assert_allclose(y[..., 1::2], z.imag, rtol=0, atol=1e-15 * np.abs(x).max())
+
+
 @pytest.mark.parametrize("dtype,tol", [("float32", 1e-6), ("float16", 2e-3), ("bfloat16", 1.6e-2)])
 def test_rope_inverse_undoes_rotation_and_keeps_pair_norms(dtype, tol):
     from oracle.halfprec import round_to
