@@ -402,9 +402,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   if (w_tiles > 0) {
     pb[0] = pb[1] = u32x4{0, 0, 0, 0};
     for (; j < w_tiles; ++j) {
-      __builtin_amdgcn_s_setprio(1);
       mfma_block(j, next_dma(j), true);
-      __builtin_amdgcn_s_setprio(0);
       softmax(j, next_dma(j));
       it_end(j);
     }
