@@ -1097,39 +1097,59 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
 // rotated query rows the dK/dV kernel reads.  A row is G = DV / 8 lanes, one
 // 16-byte piece each, 64 / G rows per wave.
 // ---------------------------------------------------------------------------
+constexpr int ROWS_U = 4;  // row groups per wave in the row-value kernel
+
 template <typename T, int DK, int DV>
-__global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a) {
-  constexpr int G = DV / 8, RPW = 64 / G;
+__global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a, int nqb) {
+  // Workgroup = block qb of the query rows of head bh (blockIdx = bh nqb +
+  // qb: 32-bit index arithmetic only); a wave takes ROWS_U groups of RPW
+  // rows, a row G = DV / 8 lanes, and issues all its loads before any math.
+  constexpr int G = DV / 8, RPW = 64 / G, RPB = (NT / 64) * RPW * ROWS_U;
   const Problem &p = a.p;
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-  const int lane = threadIdx.x & 63, g = lane % G;
-  const int64_t row = (static_cast<int64_t>(blockIdx.x) * (NT / 64) + (threadIdx.x >> 6)) * RPW + lane / G;
-  if (row >= rows) return;  // a row's G lanes leave together
-  const int qrow = static_cast<int>(row % p.Sq);
-  const int bh = static_cast<int>(row / p.Sq), b = bh / p.Hq, hq = bh - b * p.Hq;
-  const T *go = head_ptr<T>(a.dout, b, hq) + static_cast<int64_t>(qrow) * a.dout.s2 + 8 * g;
-  const T *oo = head_ptr<T>(a.o, b, hq) + static_cast<int64_t>(qrow) * a.o.s2 + 8 * g;
-  const u32x4 gv = ld16(go), ov = ld16(oo);
-  const T *ge = reinterpret_cast<const T *>(&gv);
-  const T *oe = reinterpret_cast<const T *>(&ov);
-  float dsum = 0.f;
+  const int lane = threadIdx.x & 63, g = lane % G, w = threadIdx.x >> 6;
+  const int bh = blockIdx.x / nqb, qb = blockIdx.x - bh * nqb;
+  const int b = bh / p.Hq, hq = bh - b * p.Hq;
+  const T *gh = head_ptr<T>(a.dout, b, hq) + 8 * g;
+  const T *oh = head_ptr<T>(a.o, b, hq) + 8 * g;
+  int qr[ROWS_U];
+  u32x4 gv[ROWS_U], ov[ROWS_U];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
+  for (int u = 0; u < ROWS_U; ++u) {
+    qr[u] = qb * RPB + (u * (NT / 64) + w) * RPW + lane / G;
+    const int r = qr[u] < p.Sq ? qr[u] : p.Sq - 1;  // past the head: reload its last row, store nothing
+    gv[u] = ld16(gh + static_cast<int64_t>(r) * a.dout.s2);
+    ov[u] = ld16(oh + static_cast<int64_t>(r) * a.o.s2);
+  }
 #pragma unroll
-  for (int o = 1; o < G; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
-  if (g == 0) {
-    const float l = a.lse[row];
-    a.delta[row] = -dsum;
-    a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
+  for (int u = 0; u < ROWS_U; ++u) {
+    const T *ge = reinterpret_cast<const T *>(&gv[u]);
+    const T *oe = reinterpret_cast<const T *>(&ov[u]);
+    float dsum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
+#pragma unroll
+    for (int o = 1; o < G; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
+    if (g == 0 && qr[u] < p.Sq) {
+      const int64_t row = static_cast<int64_t>(bh) * p.Sq + qr[u];
+      const float l = a.lse[row];
+      a.delta[row] = -dsum;
+      a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
+    }
   }
   if (p.rope.R > 0 && !p.rope.qrot) {  // (qrot: the forward stored them)
-    const T *qi = head_ptr<T>(a.q, b, hq) + static_cast<int64_t>(qrow) * a.q.s2;
-    T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
 #pragma unroll
-    for (int ch = g; ch < DK / 8; ch += G) {
-      u32x4 v = ld16(qi + 8 * ch);
-      rotate_chunk<T>(v, p.rope, p.rope.qpos0 + qrow, 4 * ch, false);
-      *reinterpret_cast<u32x4 *>(qk + 8 * ch) = v;
+    for (int u = 0; u < ROWS_U; ++u) {
+      if (qr[u] >= p.Sq) continue;
+      const int qrow = qr[u];
+      const T *qi = head_ptr<T>(a.q, b, hq) + static_cast<int64_t>(qrow) * a.q.s2;
+      T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+#pragma unroll
+      for (int ch = g; ch < DK / 8; ch += G) {
+        u32x4 v = ld16(qi + 8 * ch);
+        rotate_chunk<T>(v, p.rope, p.rope.qpos0 + qrow, 4 * ch, false);
+        *reinterpret_cast<u32x4 *>(qk + 8 * ch) = v;
+      }
     }
   }
 }
@@ -1386,10 +1406,10 @@ void launch_mk(const BwdArgs &a, hipStream_t st) {
     // Stored dS: row values, then dK/dV (storing dS), then dQ as one GEMM.
     {
       Probe pr_("bwd_rows", st);
-      const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-      const int per_block = (NT / 64) * (64 / (DV / 8));
-      bwd_rows_kernel<T, DK, DV><<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)),
-                                  dim3(NT), 0, st>>>(a);
+      const int per_block = (NT / 64) * (64 / (DV / 8)) * ROWS_U;
+      const int nqb = (p.Sq + per_block - 1) / per_block;
+      bwd_rows_kernel<T, DK, DV><<<dim3(static_cast<unsigned>(static_cast<int64_t>(nqb) * p.B * p.Hq)),
+                                  dim3(NT), 0, st>>>(a, nqb);
     }
     const int n_kb = (p.Sk + KB - 1) / KB;
     {
