@@ -26,6 +26,10 @@ time.  The JSON line also carries
   pre-LayerNorm, learned positions, vocab 32000), fp16 autocast, forward +
   backward of next-token cross-entropy at batch 8 x 1024 tokens: step time,
   tokens/s and the share of the step spent in the attention kernels;
+* ``cached_step`` -- one cached MultiHeadAttention decode step (E 4096,
+  32 / 8 heads of 128, fp16, batch 64, 1024 cached positions) with the
+  projections, RoPE and K/V append in one kernel, against the same module
+  with that kernel switched off, and the fused kernel's HBM rate;
 * ``cpu_baseline`` -- the NumPy oracle (a restatement of the reference's
   streaming algorithm) on a bounded sample of the same inputs, on this
   host's cores.
@@ -74,7 +78,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload",
                     choices=["all", "fwd_bwd", "variants", "decode", "decode_int8", "prefill", "lm",
-                             "copy"],
+                             "cached_step", "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -413,6 +417,71 @@ def bench_prefill(ts, torch, steps, warmup):
     }
 
 
+def bench_cached_step(ts, torch, steps, warmup):
+    """One cached MultiHeadAttention decode step (E 4096, 32 query heads, 8 KV
+    heads of 128, fp16, batch 64, 1024 cached positions): the q/k/v
+    projections, RoPE and the K/V append in one kernel
+    (tsattn_qkv_rope_append), then the decode kernel and the output
+    projection -- against the same module with the fused kernel switched off
+    (torch projections, then the RoPE-append kernel).  Random-init weights,
+    synthetic activations."""
+    from unittest.mock import patch
+
+    import numpy as np
+
+    from tensorsmith_hip import _lib, nn
+    from tensorsmith_hip.nn.cache import KVCache
+
+    bsz, embed, hq, hkv, cached = 64, 4096, 32, 8, 1024
+    ts.seed(0)
+    mha = nn.MultiHeadAttention(embed, hq, num_kv_heads=hkv, device="hip")
+    mha.to(dtype="float16")
+    mha.eval()
+    cache = mha.new_cache(bsz, cached + 16, dtype="float16")
+    rng = np.random.default_rng(0)
+    x0 = ts.tensor((rng.standard_normal((bsz, cached, embed)) * 0.1).astype(np.float32), device="hip",
+                   dtype="float16")
+    x1 = ts.tensor((rng.standard_normal((bsz, 1, embed)) * 0.1).astype(np.float32), device="hip",
+                   dtype="float16")
+    with ts.no_grad():
+        mha(x0, cache=cache)
+
+    def step():
+        with ts.no_grad():
+            cache.truncate(cached)
+            return mha(x1, cache=cache)
+
+    out = {}
+    for name, fn in (("fused", KVCache._project_append), ("unfused", lambda *a, **k: None)):
+        with patch.object(KVCache, "_project_append", fn):
+            for _ in range(warmup):
+                step()
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                step()
+            torch.cuda.synchronize()
+            ms = (time.perf_counter() - t0) / steps * 1e3
+            _lib.profile_reset()
+            _lib.profile_enable(True)
+            for _ in range(10):
+                step()
+            torch.cuda.synchronize()
+            _lib.profile_enable(False)
+            out[name] = {"ms_per_step": round(ms, 4),
+                         "kernel_ms": {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}}
+    qkv_ms = out["fused"]["kernel_ms"]["qkv_rope_append"]
+    # weights once per 32-row block (two blocks at batch 64), x, q, K/V rows
+    qkv_bytes = float((hq + 2 * hkv) * 128 * embed * 2 * 2 + bsz * embed * 2 + bsz * (hq + 2 * hkv) * 128 * 2)
+    out["qkv_rope_append"] = {
+        "bytes_per_launch": qkv_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(qkv_bytes / (qkv_ms * 1e-3) / 1e9, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(qkv_bytes / (qkv_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}}
+    out["config"] = {"workload": "mha_cached_step_f16_b64_e4096_h32kv8d128_len1024"}
+    return out
+
+
 def bench_lm(ts, torch, steps, warmup):
     """6-layer decoder LM, fp16 autocast, forward + backward, random init."""
     from tensorsmith_hip import _lib
@@ -623,6 +692,9 @@ def main():
     if args.workload == "lm":
         print(json.dumps({"lm_step": bench_lm(ts, torch, 5, 2)}), flush=True)
         return
+    if args.workload == "cached_step":
+        print(json.dumps({"cached_step": bench_cached_step(ts, torch, 50, 5)}), flush=True)
+        return
     print(f"[bench] fwd+bwd B{B} H{H} S{S} D{D} bf16: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
     main_res, host = bench_fwd_bwd(ts, torch, args.steps, args.warmup)
@@ -648,6 +720,9 @@ def main():
     print(f"[bench] prefill {pf_res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
     lm_res = bench_lm(ts, torch, 5, 2)
     print(f"[bench] lm step {lm_res['ms_per_step']:.2f} ms", file=sys.stderr, flush=True)
+    cs_res = bench_cached_step(ts, torch, 50, 5)
+    print(f"[bench] cached MHA step {cs_res['fused']['ms_per_step']:.3f} ms "
+          f"(unfused {cs_res['unfused']['ms_per_step']:.3f} ms)", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (NumPy oracle sample)", file=sys.stderr, flush=True)
@@ -681,6 +756,7 @@ def main():
         "decode_int8": q8_res,
         "prefill": pf_res,
         "lm_step": lm_res,
+        "cached_step": cs_res,
     }
     print(json.dumps(line), flush=True)
 

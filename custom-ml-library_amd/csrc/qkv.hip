@@ -6,11 +6,14 @@
 // cache (:142 -> KVCache.append, cache.py:54-86, int8 rows with fp32 row
 // scales when the cache is quantised).
 //
-// One workgroup = one head of q, k or v for 32 rows (b, t) of x; its four
+// One workgroup = one head of q, k or v for 32 rows (b, t) of x; its eight
 // waves split the embedding (k-steps of 16 in turn) and run
 // out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16 -- W rows and x rows are
-// both row fragments, read straight from memory -- then sum their partial
-// tiles through LDS.  Wave 0 finishes: bias, rounding to the dtype (as the
+// both row fragments, read straight from memory, two k-steps of loads in
+// flight ahead of the MFMAs -- then sum their partial tiles through LDS.
+// (For decode the weights dominate: (Hq + 2 Hkv) D E 2 bytes streamed by a
+// few hundred waves, so the loads have to be deep.)  Wave 0 finishes: bias,
+// rounding to the dtype (as the
 // reference's Linear output), the rotation (lane (c, h) holds channels
 // 8 g + 4 h .. + 3 of row c, so every channel pair is lane-local), then the
 // row stores: q to its output, k and v into the cache (quantised per row
@@ -21,8 +24,9 @@
 namespace tsattn {
 namespace {
 
-constexpr int NT = 256;
+constexpr int NT = 512;
 constexpr int NW = NT / 64;
+constexpr int KU = 2;  // k-steps per wave and load batch
 
 struct QkvArgs {
   int rows, len, E, Hq, Hkv, rope;
@@ -34,8 +38,18 @@ struct QkvArgs {
   int64_t pos;
 };
 
+// The same pointer in scalar registers (the compiler cannot prove a value
+// selected by a block-uniform index uniform, and a buffer resource in vector
+// registers turns every load into a loop over the lanes' values).
+__device__ __forceinline__ const void *uniform_ptr(const void *p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(NT) void qkv_rope_append_kernel(QkvArgs a) {
+__global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
   constexpr int TILES = D / 32;
   __shared__ float part[NW][TILES][16][64];
 
@@ -45,7 +59,8 @@ __global__ __launch_bounds__(NT) void qkv_rope_append_kernel(QkvArgs a) {
   const int slot = blockIdx.x % nslot, rb = blockIdx.x / nslot;
   const int kind = slot < a.Hq ? 0 : (slot < a.Hq + a.Hkv ? 1 : 2);
   const int head = kind == 0 ? slot : (kind == 1 ? slot - a.Hq : slot - a.Hq - a.Hkv);
-  const T *W = static_cast<const T *>(a.w[kind]) + static_cast<int64_t>(head) * D * a.E;
+  const void *wk = kind == 0 ? a.w[0] : (kind == 1 ? a.w[1] : a.w[2]);
+  const T *W = static_cast<const T *>(uniform_ptr(static_cast<const T *>(wk) + static_cast<int64_t>(head) * D * a.E));
   const int r0 = rb * 32;
 
   // row r = r0 + c of x is (b, t) = (r / len, r % len); rows past the last
@@ -56,7 +71,7 @@ __global__ __launch_bounds__(NT) void qkv_rope_append_kernel(QkvArgs a) {
   const int b = rr / a.len, tt = rr - b * a.len;
   const int64_t xext = (static_cast<int64_t>(a.rows / a.len) - 1) * a.xs_b +
                        (static_cast<int64_t>(a.len) - 1) * a.xs_t + a.E;
-  const rsrc_t xr = make_rsrc(a.x, static_cast<uint32_t>(xext * 2));
+  const rsrc_t xr = make_rsrc(uniform_ptr(a.x), static_cast<uint32_t>(xext * 2));
   const rsrc_t wr = make_rsrc(W, static_cast<uint32_t>(D) * a.E * 2);
   const uint32_t xo = (static_cast<uint32_t>(b * a.xs_b + tt * a.xs_t + 8 * h) * 2) |
                       (live ? 0u : 0x80000000u);
@@ -65,13 +80,36 @@ __global__ __launch_bounds__(NT) void qkv_rope_append_kernel(QkvArgs a) {
   f32x16 acc[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) acc[t] = f32x16{};
+  // k-steps w, w + NW, ...: batches of KU k-steps in two register sets, a
+  // batch's loads issued a batch ahead of its MFMAs; k-steps past the
+  // embedding read zeros (offsets past the buffer ranges), so every wave runs
+  // the same even number of batches without branches
   const int nks = a.E / 16;
-#pragma unroll 4
-  for (int ks = w; ks < nks; ks += NW) {
-    const uint32_t ko = static_cast<uint32_t>(ks) * 32;
-    const u32x4 xb = buf_load16(xr, xo + ko);
+  const int nb = (nks + 2 * NW * KU - 1) / (2 * NW * KU) * 2;
+  u32x4 xb[2][KU], wb[2][KU][TILES];
+  auto load = [&](int bi, int buf) {
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) acc[t] = mfma32<T>(buf_load16(wr, wo + t * wt + ko), xb, acc[t]);
+    for (int u = 0; u < KU; ++u) {
+      const int ks = (bi * KU + u) * NW + w;
+      const bool in = ks < nks;
+      const uint32_t ko = static_cast<uint32_t>(ks) * 32;
+      xb[buf][u] = buf_load16(xr, in ? xo + ko : 0x80000000u);
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) wb[buf][u][t] = buf_load16(wr, in ? wo + t * wt + ko : 0x80000000u);
+    }
+  };
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < KU; ++u)
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) acc[t] = mfma32<T>(wb[buf][u][t], xb[buf][u], acc[t]);
+  };
+  load(0, 0);
+  for (int bi = 0; bi < nb; bi += 2) {
+    load(bi + 1, 1);
+    compute(0);
+    load(bi + 2, 0);  // (past the last batch: zeros, never used)
+    compute(1);
   }
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
@@ -88,7 +126,9 @@ __global__ __launch_bounds__(NT) void qkv_rope_append_kernel(QkvArgs a) {
   for (int t = 0; t < TILES; ++t)
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      float s = part[0][t][e][lane] + part[1][t][e][lane] + part[2][t][e][lane] + part[3][t][e][lane];
+      float s = 0.f;
+#pragma unroll
+      for (int v = 0; v < NW; ++v) s += part[v][t][e][lane];
       if (bias) s += static_cast<float>(bias[head * D + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]);
       y[t][e] = static_cast<T>(s);
     }
