@@ -48,19 +48,26 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
   return reinterpret_cast<const void *>((static_cast<uint64_t>(hi) << 32) | lo);
 }
 
-template <typename T, int D>
+// CT: 32-channel tiles of the head per workgroup -- D / 32 (the whole head,
+// which the int8 quantiser's row maximum needs), or fewer for 16-bit caches,
+// so that more workgroups share the weight stream.
+template <typename T, int D, int CT>
 __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
-  constexpr int TILES = D / 32;
+  constexpr int TILES = CT, NCB = D / 32 / CT;
+  static_assert(NCB * CT * 32 == D, "column blocks split the head");
   __shared__ float part[NW][TILES][16][64];
 
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int nslot = a.Hq + 2 * a.Hkv;
-  const int slot = blockIdx.x % nslot, rb = blockIdx.x / nslot;
+  const int slot = blockIdx.x % nslot, rest = blockIdx.x / nslot;
+  const int cb = rest % NCB, rb = rest / NCB;
+  const int c0 = 32 * CT * cb;  // first channel of this workgroup's columns
   const int kind = slot < a.Hq ? 0 : (slot < a.Hq + a.Hkv ? 1 : 2);
   const int head = kind == 0 ? slot : (kind == 1 ? slot - a.Hq : slot - a.Hq - a.Hkv);
   const void *wk = kind == 0 ? a.w[0] : (kind == 1 ? a.w[1] : a.w[2]);
-  const T *W = static_cast<const T *>(uniform_ptr(static_cast<const T *>(wk) + static_cast<int64_t>(head) * D * a.E));
+  const T *W = static_cast<const T *>(
+      uniform_ptr(static_cast<const T *>(wk) + (static_cast<int64_t>(head) * D + c0) * a.E));
   const int r0 = rb * 32;
 
   // row r = r0 + c of x is (b, t) = (r / len, r % len); rows past the last
@@ -72,7 +79,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
   const int64_t xext = (static_cast<int64_t>(a.rows / a.len) - 1) * a.xs_b +
                        (static_cast<int64_t>(a.len) - 1) * a.xs_t + a.E;
   const rsrc_t xr = make_rsrc(uniform_ptr(a.x), static_cast<uint32_t>(xext * 2));
-  const rsrc_t wr = make_rsrc(W, static_cast<uint32_t>(D) * a.E * 2);
+  const rsrc_t wr = make_rsrc(W, static_cast<uint32_t>(32 * CT) * a.E * 2);
   const uint32_t xo = (static_cast<uint32_t>(b * a.xs_b + tt * a.xs_t + 8 * h) * 2) |
                       (live ? 0u : 0x80000000u);
   const uint32_t wo = (static_cast<uint32_t>(c) * a.E + 8 * h) * 2;
@@ -120,7 +127,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
 
   const int64_t prow = a.pos + tt;
   const T *bias = static_cast<const T *>(a.bias[kind]);
-  // y[t][e]: channel n = 32 t + 8 (e / 4) + 4 h + e % 4 of the head
+  // y[t][e]: channel n = c0 + 32 t + 8 (e / 4) + 4 h + e % 4 of the head
   T y[TILES][16];
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
@@ -129,7 +136,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < NW; ++v) s += part[v][t][e][lane];
-      if (bias) s += static_cast<float>(bias[head * D + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]);
+      if (bias) s += static_cast<float>(bias[head * D + c0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]);
       y[t][e] = static_cast<T>(s);
     }
   if (kind < 2 && a.rope) {
@@ -139,7 +146,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     for (int t = 0; t < TILES; ++t)
 #pragma unroll
       for (int e = 0; e < 16; e += 2) {
-        const int pair = (32 * t + 8 * (e >> 2) + 4 * h + (e & 3)) / 2;
+        const int pair = (c0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)) / 2;
         rotate_pair(y[t][e], y[t][e + 1], cs[pair], sn[pair], false);
       }
   }
@@ -151,7 +158,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
   };
   if (kind == 0) {
     T *q = static_cast<T *>(const_cast<void *>(a.q.data)) + b * a.q.s0 + head * a.q.s1 +
-           static_cast<int64_t>(tt) * a.q.s2;
+           static_cast<int64_t>(tt) * a.q.s2 + c0;
     if (live)
 #pragma unroll
       for (int t = 0; t < TILES; ++t)
@@ -160,8 +167,8 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     return;
   }
   const View &cv = kind == 1 ? a.kc : a.vc;
-  const int64_t crow = b * cv.s0 + head * cv.s1 + prow * cv.s2;
-  if (!a.ks.data) {
+  const int64_t crow = b * cv.s0 + head * cv.s1 + prow * cv.s2 + c0;
+  if (NCB > 1 || !a.ks.data) {  // 16-bit caches (the host splits only those)
     T *dst = static_cast<T *>(const_cast<void *>(cv.data)) + crow;
     if (live)
 #pragma unroll
@@ -170,6 +177,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
         for (int g = 0; g < 4; ++g) *reinterpret_cast<u32x2 *>(dst + 32 * t + 8 * g + 4 * h) = pack4(t, g);
     return;
   }
+  if constexpr (NCB == 1) {
   // int8 cache (cache.py:73-77): s = max(max |x| / 127, 1e-8), q = rint(x / s),
   // fp32 arithmetic on the row in the cache dtype; lanes c and c + 32 hold
   // the two halves of row c.
@@ -197,6 +205,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     if (h == 0)
       static_cast<float *>(const_cast<void *>(sv.data))[b * sv.s0 + head * sv.s1 + prow * sv.s2] = sc;
   }
+  }
 }
 
 }  // namespace
@@ -209,14 +218,27 @@ hipError_t launch_qkv_rope_append(int dtype, int batch, int len, int embed, int 
             {w[0], w[1], w[2]}, {bias[0], bias[1], bias[2]}, q, kc, vc,
             ks ? *ks : View{nullptr, 0, 0, 0}, vs ? *vs : View{nullptr, 0, 0, 0}, cos, sin, pos};
   const int rblocks = (a.rows + 31) / 32;
-  const dim3 grid(static_cast<unsigned>((heads_q + 2 * heads_kv) * rblocks)), block(NT);
+  // 16-bit caches: one 32-channel tile of a head per workgroup; int8 caches:
+  // the whole head (its row maximum)
+  const int ncb = ks ? 1 : dim / 32;
+  const dim3 grid(static_cast<unsigned>((heads_q + 2 * heads_kv) * ncb * rblocks)), block(NT);
   Probe pr_(ks ? "qkv_rope_append_int8" : "qkv_rope_append", st);
   if (dtype == TSATTN_BF16) {
-    if (dim == 128) qkv_rope_append_kernel<bf16, 128><<<grid, block, 0, st>>>(a);
-    else qkv_rope_append_kernel<bf16, 64><<<grid, block, 0, st>>>(a);
+    if (dim == 128) {
+      if (ks) qkv_rope_append_kernel<bf16, 128, 4><<<grid, block, 0, st>>>(a);
+      else qkv_rope_append_kernel<bf16, 128, 1><<<grid, block, 0, st>>>(a);
+    } else {
+      if (ks) qkv_rope_append_kernel<bf16, 64, 2><<<grid, block, 0, st>>>(a);
+      else qkv_rope_append_kernel<bf16, 64, 1><<<grid, block, 0, st>>>(a);
+    }
   } else {
-    if (dim == 128) qkv_rope_append_kernel<f16, 128><<<grid, block, 0, st>>>(a);
-    else qkv_rope_append_kernel<f16, 64><<<grid, block, 0, st>>>(a);
+    if (dim == 128) {
+      if (ks) qkv_rope_append_kernel<f16, 128, 4><<<grid, block, 0, st>>>(a);
+      else qkv_rope_append_kernel<f16, 128, 1><<<grid, block, 0, st>>>(a);
+    } else {
+      if (ks) qkv_rope_append_kernel<f16, 64, 2><<<grid, block, 0, st>>>(a);
+      else qkv_rope_append_kernel<f16, 64, 1><<<grid, block, 0, st>>>(a);
+    }
   }
   return hipGetLastError();
 }
