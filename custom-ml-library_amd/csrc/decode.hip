@@ -326,33 +326,43 @@ __global__ __launch_bounds__(64) void decode_merge_kernel(DecArgs a) {
   constexpr int PER = (D + 63) / 64;
   float acc[PER] = {};
   float M = -INFINITY, L = 0.f;
-  for (int s0 = 0; s0 < n; s0 += 64) {  // one pass for up to 64 splits
+  // passes of up to SB splits; each issues every load of its splits (the
+  // partial rows and their (m, l), indices clamped to the last split, which
+  // then weighs 0) before any use, so a pass costs one memory latency
+  constexpr int SB = 16;
+  for (int s0 = 0; s0 < n; s0 += SB) {
+    float pv[SB][PER];
+#pragma unroll
+    for (int u = 0; u < SB; ++u) {
+      const float *part = base + min(s0 + u, n - 1) * stride;
+#pragma unroll
+      for (int t = 0; t < PER; ++t) {
+        const int d = lane + 64 * t;
+        pv[u][t] = part[d < D ? d : D - 1];
+      }
+    }
     const int s = s0 + lane;
-    const float ms = s < n ? base[s * stride + D] : -INFINITY;
-    const float ls = s < n ? base[s * stride + D + 1] : 0.f;
+    const bool live = lane < SB && s < n;
+    const float ms = live ? base[s * stride + D] : -INFINITY;
+    const float ls = live ? base[s * stride + D + 1] : 0.f;
     float mx = ms;
 #pragma unroll
     for (int x = 32; x >= 1; x >>= 1) mx = fmaxf(mx, __shfl_xor(mx, x, 64));
     const float M2 = fmaxf(M, mx);
     const float mb = M2 == -INFINITY ? 0.f : M2;
     const float cold = fast_exp2(M - mb);  // rescale what earlier passes summed
-    const float cs = s < n ? fast_exp2(ms - mb) : 0.f;
+    const float cs = live ? fast_exp2(ms - mb) : 0.f;
     float lsum = ls * cs;
 #pragma unroll
     for (int x = 32; x >= 1; x >>= 1) lsum += __shfl_xor(lsum, x, 64);
     L = L * cold + lsum;
 #pragma unroll
     for (int t = 0; t < PER; ++t) acc[t] *= cold;
-    const int cnt = min(64, n - s0);
-#pragma unroll 4
-    for (int u = 0; u < cnt; ++u) {
-      const float c = __shfl(cs, u, 64);
-      const float *part = base + (s0 + u) * stride;
 #pragma unroll
-      for (int t = 0; t < PER; ++t) {
-        const int d = lane + 64 * t;
-        if (d < D) acc[t] = fmaf(part[d], c, acc[t]);
-      }
+    for (int u = 0; u < SB; ++u) {
+      const float c = __shfl(cs, u, 64);  // 0 past the last split
+#pragma unroll
+      for (int t = 0; t < PER; ++t) acc[t] = fmaf(pv[u][t], c, acc[t]);
     }
     M = M2;
   }
