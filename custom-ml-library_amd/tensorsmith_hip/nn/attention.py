@@ -288,9 +288,10 @@ def scaled_dot_product_attention(
 
     def backward(upstream, _keep=keep):  # _keep: mask / length buffers the kernels read
         g = _operand(upstream)
-        if fused and (not _aligned16(g) or min(g.stride()[:3]) <= 0):
-            # the folded-RoPE backward runs on the MFMA kernels only, which need
-            # 16-byte aligned rows of a real (not expanded) gradient
+        if (fused or code in (_lib.F16, _lib.BF16)) and (not _aligned16(g) or min(g.stride()[:3]) <= 0):
+            # the MFMA kernels (the only ones the folded-RoPE backward has) need
+            # 16-byte aligned rows of a real gradient: an expanded one (a sum's
+            # VJP) would send the plain backward to the generic kernels
             g = g.contiguous()
         if g.dtype != out.dtype:
             g = g.to(out.dtype)

@@ -429,3 +429,30 @@ def test_rope_attention_in_float64_rotates_then_attends():
             R.rope(dk_r, 3, dtype="float64", inverse=True), dv)
     for got, w in zip((out.numpy(), tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy()), want):
         np.testing.assert_allclose(got, w, rtol=1e-10, atol=1e-10)
+
+
+def test_rope_folded_backward_takes_an_expanded_upstream_gradient():
+    """An upstream gradient with stride 0 (an expand, as a sum's VJP gives)
+    cannot be read by the MFMA kernels as it is: the mirror makes it
+    contiguous and the folded backward runs -- same bits as the two-step
+    path (rotary_embedding, plain attention)."""
+    from tensorsmith_hip.nn import attention as attn_mod
+
+    rng = np.random.default_rng(12)
+    b, h, s, d = 1, 2, 96, 64
+    q, k, v = (rng.standard_normal((b, h, s, d)).astype(np.float32) for _ in range(3))
+    g_row = torch.from_numpy(rng.standard_normal((1, 1, 1, d)).astype(np.float32))
+
+    def run(fused):
+        tq, tk, tv = (ts.tensor(a, device="hip", dtype="bfloat16", requires_grad=True) for a in (q, k, v))
+        up = ts.Tensor(g_row.to("cuda", torch.bfloat16).expand(b, h, s, d), device="hip")
+        if fused:
+            out = attn_mod.scaled_dot_product_attention(tq, tk, tv, is_causal=True, _rope=(0, 0, 10000.0))
+        else:
+            out = attn_mod.scaled_dot_product_attention(attn_mod.rotary_embedding(tq, 0),
+                                                        attn_mod.rotary_embedding(tk, 0), tv, is_causal=True)
+        out.backward(up)
+        return [out.numpy()] + [t.grad.numpy() for t in (tq, tk, tv)]
+
+    for a_, b_ in zip(run(True), run(False)):
+        np.testing.assert_array_equal(a_, b_)
