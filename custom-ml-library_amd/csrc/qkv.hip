@@ -6,14 +6,15 @@
 // cache (:142 -> KVCache.append, cache.py:54-86, int8 rows with fp32 row
 // scales when the cache is quantised).
 //
-// One workgroup = one head of q, k or v for 32 rows (b, t) of x; its eight
-// waves split the embedding (k-steps of 16 in turn) and run
-// out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16 -- W rows and x rows are
-// both row fragments, read straight from memory, two k-steps of loads in
-// flight ahead of the MFMAs -- then sum their partial tiles through LDS.
-// (For decode the weights dominate: (Hq + 2 Hkv) D E 2 bytes streamed by a
-// few hundred waves, so the loads have to be deep.)  Wave 0 finishes: bias,
-// rounding to the dtype (as the
+// One workgroup = one 32-channel tile of a head of q, k or v (16-bit
+// caches; the whole head for int8 caches, whose quantiser needs the row
+// maximum) for 32 rows (b, t) of x.  Its eight waves split the embedding in
+// 64-column chunks and run out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16
+// with W rows and x rows as row fragments -- staged through per-wave LDS
+// rings by DMA (whole cache lines per load instruction) for one-tile
+// workgroups, loaded directly for whole heads -- then sum their partial
+// tiles through LDS.  (For decode the weights dominate: (Hq + 2 Hkv) D E 2
+// bytes.)  Wave 0 finishes: bias, rounding to the dtype (as the
 // reference's Linear output), the rotation (lane (c, h) holds channels
 // 8 g + 4 h .. + 3 of row c, so every channel pair is lane-local), then the
 // row stores: q to its output, k and v into the cache (quantised per row
@@ -26,7 +27,6 @@ namespace {
 
 constexpr int NT = 512;
 constexpr int NW = NT / 64;
-constexpr int KU = 2;  // k-steps per wave and load batch
 
 struct QkvArgs {
   int rows, len, E, Hq, Hkv, rope;
@@ -55,7 +55,12 @@ template <typename T, int D, int CT>
 __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
   constexpr int TILES = CT, NCB = D / 32 / CT;
   static_assert(NCB * CT * 32 == D, "column blocks split the head");
-  __shared__ float part[NW][TILES][16][64];
+  // CT == 1: per-wave staging rings (two 8 KiB stages: 32 W rows and 32 x
+  // rows of 64 columns) during the loop, the partial tiles after it
+  constexpr int RING = 2 * 8192;
+  constexpr int PART = NW * TILES * 16 * 64 * 4;
+  __shared__ __attribute__((aligned(1024))) char smem[(CT == 1 ? (NW * RING > PART ? NW * RING : PART) : PART) + 1024];
+  auto part = reinterpret_cast<float (*)[TILES][16][64]>(smem);
 
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -87,36 +92,98 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
   f32x16 acc[TILES];
 #pragma unroll
   for (int t = 0; t < TILES; ++t) acc[t] = f32x16{};
-  // k-steps w, w + NW, ...: batches of KU k-steps in two register sets, a
-  // batch's loads issued a batch ahead of its MFMAs; k-steps past the
-  // embedding read zeros (offsets past the buffer ranges), so every wave runs
-  // the same even number of batches without branches
-  const int nks = a.E / 16;
-  const int nb = (nks + 2 * NW * KU - 1) / (2 * NW * KU) * 2;
-  u32x4 xb[2][KU], wb[2][KU][TILES];
-  auto load = [&](int bi, int buf) {
+  if constexpr (CT == 1) {
+    // Staged through LDS: a wave takes the 64-column chunks w, w + NW, ...
+    // of the embedding and DMAs each chunk's 32 W rows and 32 x rows into
+    // its own two-stage ring, eight rows of 128 bytes (whole cache lines)
+    // per load instruction -- direct fragment loads touch 32 lines each, and
+    // the address unit, not HBM, bounded them.  In the ring, 16-byte unit u
+    // of row r holds unit u ^ (r % 8) of the chunk (conflict-free fragment
+    // reads); columns past the embedding, and rows past the last, read zeros.
+    // The loop needs no barrier: no wave reads another's ring.
+    const uint32_t sbase = lds_addr(smem) + w * RING, spare = lds_addr(smem) + NW * RING;
+    const int nch = (a.E + 63) / 64;
+    const int mine = nch > w ? (nch - 1 - w) / NW + 1 : 0;  // this wave's chunks
+    const int lr = lane >> 3, gu = (lane & 7) ^ lr;  // row within 8, global unit
+    const u32x4 wdesc = make_desc(W, static_cast<uint32_t>(32) * a.E * 2);
+    const u32x4 xdesc = make_desc(uniform_ptr(a.x), static_cast<uint32_t>(xext * 2));
+    uint32_t wv[4], xv[4];
 #pragma unroll
-    for (int u = 0; u < KU; ++u) {
-      const int ks = (bi * KU + u) * NW + w;
-      const bool in = ks < nks;
-      const uint32_t ko = static_cast<uint32_t>(ks) * 32;
-      xb[buf][u] = buf_load16(xr, in ? xo + ko : 0x80000000u);
-#pragma unroll
-      for (int t = 0; t < TILES; ++t) wb[buf][u][t] = buf_load16(wr, in ? wo + t * wt + ko : 0x80000000u);
+    for (int i = 0; i < 4; ++i) {
+      const int row = 8 * i + lr;  // W row (channel) and x row of this lane's DMA piece
+      wv[i] = (static_cast<uint32_t>(row) * a.E + 8 * gu) * 2;
+      const int xr_ = r0 + row;
+      const int xrr = xr_ < a.rows ? xr_ : a.rows - 1;
+      const int xb_ = xrr / a.len, xt_ = xrr - xb_ * a.len;
+      xv[i] = (static_cast<uint32_t>(xb_ * a.xs_b + xt_ * a.xs_t + 8 * gu) * 2) |
+              (xr_ < a.rows ? 0u : 0x80000000u);
     }
-  };
-  auto compute = [&](int buf) {
+    // chunk k of this wave (k-th of `mine`; past them: zeros into the spare)
+    auto issue = [&](int k) {
+      const int ch = w + NW * k;
+      const bool real = k < mine;
+      const uint32_t st = real ? sbase + (k & 1) * 8192 : spare;
+      const uint32_t col = static_cast<uint32_t>(ch) * 64 + 8 * gu;  // first column of the lane's unit
+      const uint32_t far = (real && col < static_cast<uint32_t>(a.E)) ? 0u : 0x80000000u;
+      const uint32_t soff = real ? static_cast<uint32_t>(ch) * 128 : 0u;
 #pragma unroll
-    for (int u = 0; u < KU; ++u)
+      for (int i = 0; i < 4; ++i) dma16(wdesc, real ? st + i * 1024 : spare, wv[i] | far, soff);
 #pragma unroll
-      for (int t = 0; t < TILES; ++t) acc[t] = mfma32<T>(wb[buf][u][t], xb[buf][u], acc[t]);
-  };
-  load(0, 0);
-  for (int bi = 0; bi < nb; bi += 2) {
-    load(bi + 1, 1);
-    compute(0);
-    load(bi + 2, 0);  // (past the last batch: zeros, never used)
-    compute(1);
+      for (int i = 0; i < 4; ++i) dma16(xdesc, real ? st + 4096 + i * 1024 : spare, xv[i] | far, soff);
+    };
+    // fragment of k-step s (0..3) of a staged 32 x 64 tile: row c, unit 2 s + h
+    const uint32_t fo = static_cast<uint32_t>(c) * 128;
+    issue(0);
+    for (int k = 0; k < mine; ++k) {
+      issue(k + 1);
+      wait_vm_n<8>();  // chunk k has landed; chunk k + 1's eight loads stay in flight
+      const char *stg = smem + w * RING + (k & 1) * 8192;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint32_t u = static_cast<uint32_t>((2 * s + h) ^ (c & 7)) * 16;
+        const u32x4 wf = *reinterpret_cast<const u32x4 *>(stg + fo + u);
+        const u32x4 xf = *reinterpret_cast<const u32x4 *>(stg + 4096 + fo + u);
+        acc[0] = mfma32<T>(wf, xf, acc[0]);
+      }
+      wait_lgkm0();  // reads of this stage done before chunk k + 2 overwrites it
+    }
+    wait_vm_n<0>();
+    __syncthreads();  // every ring read before the partial tiles reuse the LDS
+  } else {
+    // Direct fragment loads (whole-head workgroups, whose fragments would not
+    // fit the rings): the same chunks per wave and the same MFMA order as the
+    // staged path, so the projections are bit-identical across cache types;
+    // chunk loads double-buffered, columns past the embedding read zeros.
+    const int nks = a.E / 16;
+    const int nch = (a.E + 63) / 64;
+    const int mine = nch > w ? (nch - 1 - w) / NW + 1 : 0;
+    u32x4 xb[2][4], wb[2][4][TILES];
+    auto load = [&](int k, int buf) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int ks = 4 * (w + NW * k) + s4;
+        const bool in = k < mine && ks < nks;
+        const uint32_t ko = static_cast<uint32_t>(ks) * 32;
+        xb[buf][s4] = buf_load16(xr, in ? xo + ko : 0x80000000u);
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) wb[buf][s4][t] = buf_load16(wr, in ? wo + t * wt + ko : 0x80000000u);
+      }
+    };
+    auto compute = [&](int buf) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) acc[t] = mfma32<T>(wb[buf][s4][t], xb[buf][s4], acc[t]);
+    };
+    load(0, 0);
+    for (int k = 0; k < mine; k += 2) {
+      load(k + 1, 1);  // (past this wave's chunks: zeros, not used)
+      compute(0);
+      if (k + 1 < mine) {
+        load(k + 2, 0);
+        compute(1);
+      }
+    }
   }
 #pragma unroll
   for (int t = 0; t < TILES; ++t)
