@@ -51,7 +51,8 @@ struct BwdArgs {
   // then [rows] nl = -safe(lse) / scale, safe(lse) = isfinite(lse) ? lse : 0
   // (the reference's safe_lse, attention.py:231).  Stored negated so the
   // dK/dV kernel starts its S and dP accumulators from them:
-  // S + nl = (S scale - lse) / scale and dP + nd = dP - delta.
+  // S + nl = (S scale - lse) / scale and dP + nd = dP - delta (with dropout
+  // both absorb the mask value, store_row_values).
   float *delta;
   float sl;      // scale * log2(e)
   float scale;   // final gradient scale
@@ -87,6 +88,24 @@ __device__ __forceinline__ T *mut(View v) {
 template <typename T>
 __device__ __forceinline__ const T *head_ptr(View v, int b, int h) {
   return static_cast<const T *>(v.data) + b * v.s0 + h * v.s1;
+}
+
+// The dK/dV kernel's row values of query row `row`: nd = -delta at [row], nl =
+// -lse / scale at [rows + row] (0 for a row that sees no key), so that the
+// kernel's S accumulator started from nl gives P = exp2(acc sl).  With
+// dropout (mask value m = 1 / (1 - p) where kept) they absorb m: nl + ln(m) /
+// scale gives P m, and nd / m gives dS = P m (dP + nd / m) = P (m dP - delta)
+// for a kept element and P m (nd / m) = -P delta for a dropped one.
+__device__ __forceinline__ void store_row_values(const BwdArgs &a, int64_t rows, int64_t row,
+                                                 float nd, float lse) {
+  const bool finite = isfinite(lse);
+  if (a.p.drop.on) {
+    a.delta[row] = nd / a.p.drop.scale;
+    a.delta[rows + row] = finite ? (logf(a.p.drop.scale) - lse) / a.scale : 0.f;
+  } else {
+    a.delta[row] = nd;
+    a.delta[rows + row] = finite ? -lse / a.scale : 0.f;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -462,8 +481,12 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     u32x4 pp[2], pd[2];
     // Dropout: the staged keep bits; lane (c, h) reads rows 8 g + 4 h + r
     // (four words per g) and takes bit c.  dV takes P * mask, dS = P (dP *
-    // mask - delta).
+    // mask - delta), m = 1 / (1 - p) folded into the row values.
     const char *btile = qt + BOFF + w * 128;
+    // (an offset the compiler cannot see through: otherwise it keeps the nd
+    // values it read to start dpacc live across the MFMA steps)
+    int nd_off = QT;
+    if constexpr (DR) asm volatile("" : "+v"(nd_off));
     // Staged mask: this lane's column (key 32 w + c) at row 4 h of the tile.
     const char *mrow_base = nullptr;
     if constexpr (MSTAGE) {
@@ -512,10 +535,11 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
             pv[r] = fast_exp2(mask_kind(MK) >= 2 ? xs[e] : xs[e] * sl);
           }
           if constexpr (DR) {
+            // pv = P m and dpacc = dP + nd / m (the row values absorb m)
             const bool keep = (bw[r] >> c) & 1u;
-            const float nd = rv[QT + 8 * g + 4 * h + r];
-            dsv[r] = pv[r] * (keep ? fmaf(dpacc[e], p.drop.scale, nd) : nd);
-            pv[r] = keep ? pv[r] * p.drop.scale : 0.f;
+            const float nd = rv[nd_off + 8 * g + 4 * h + r];
+            dsv[r] = pv[r] * (keep ? dpacc[e] + nd : nd);
+            pv[r] = keep ? pv[r] : 0.f;
           } else {
             dsv[r] = pv[r] * dpacc[e];
           }
@@ -793,13 +817,8 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
       for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
     }
     delta = -xor32_sum(dsum);
-    const bool finite = isfinite(l);
-    lse2 = finite ? -l * kLog2e : 0.f;
-    if (h == 0 && qrow < p.Sq) {
-      const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
-      a.delta[row] = delta;
-      a.delta[rows + row] = finite ? -l / a.scale : 0.f;
-    }
+    lse2 = isfinite(l) ? -l * kLog2e : 0.f;
+    if (h == 0 && qrow < p.Sq) store_row_values(a, static_cast<int64_t>(p.B) * p.Hq * p.Sq, row, delta, l);
   }
   // Resolve these loads before the DMA loads start (the compiler's vmcnt
   // waits do not count those).
@@ -1132,9 +1151,7 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a, int nqb) {
     for (int o = 1; o < G; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
     if (g == 0 && qr[u] < p.Sq) {
       const int64_t row = static_cast<int64_t>(bh) * p.Sq + qr[u];
-      const float l = a.lse[row];
-      a.delta[row] = -dsum;
-      a.delta[rows + row] = isfinite(l) ? -l / a.scale : 0.f;
+      store_row_values(a, rows, row, -dsum, a.lse[row]);
     }
   }
   if (p.rope.R > 0 && !p.rope.qrot) {  // (qrot: the forward stored them)
