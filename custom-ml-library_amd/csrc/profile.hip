@@ -6,6 +6,7 @@
 // folds the elapsed times into per-name totals and recycles the events.
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -26,7 +27,8 @@ struct Total {
 };
 
 std::mutex g_mu;
-bool g_on = false;
+// Read without the mutex on every launch; the pools and totals stay under it.
+std::atomic<bool> g_on{false};
 std::vector<hipEvent_t> g_pool;
 std::vector<Pending> g_pending;
 std::vector<Total> g_totals;
@@ -65,10 +67,7 @@ void fold_locked() {
 
 }  // namespace
 
-bool probes_on() {
-  std::lock_guard<std::mutex> lk(g_mu);
-  return g_on;
-}
+bool probes_on() { return g_on.load(std::memory_order_relaxed); }
 
 void probe_begin(const char *name, hipStream_t st) {
   std::lock_guard<std::mutex> lk(g_mu);
@@ -90,7 +89,7 @@ extern "C" {
 
 int tsattn_profile_enable(int on) {
   std::lock_guard<std::mutex> lk(tsattn::g_mu);
-  tsattn::g_on = on != 0;
+  tsattn::g_on.store(on != 0, std::memory_order_relaxed);
   return TSATTN_OK;
 }
 
