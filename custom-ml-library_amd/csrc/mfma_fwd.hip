@@ -359,15 +359,21 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     }
     // Dropout: the denominator sums the undropped probabilities (the
     // reference normalises first, attention.py:139-144); PV takes P * mask.
-    uint64_t dw[4];
+    // Pair masks km[k]: 0xFFFF in the half of each kept word of elements 2k,
+    // 2k + 1 (the order pack2 gives P), so P * mask is one AND per pair.  A
+    // threshold of 65536 keeps nothing: zero multiplier and bits instead.
+    uint32_t km[8];
+    const bool none_kept = p.drop.thr > 65535u;
     if constexpr (DR) {
+      uint64_t dw[4];
       dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
+      const uint32_t thr2 = (p.drop.thr & 0xFFFFu) * 0x00010001u;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        km[k] = keep_mask_pair(static_cast<uint32_t>(dw[k >> 1] >> (32 * (k & 1))), thr2);
       // keep bits for the backward: lane half h holds keys 8 g + 4 h + r
       if (p.drop.bits) {
-        uint32_t bits = 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-          bits |= (dropout_keeps(p.drop, dw, i) ? 1u : 0u) << (8 * (i >> 2) + 4 * h + (i & 3));
+        uint32_t bits = none_kept ? 0u : keep_bits16(km) << (4 * h);
         bits |= __shfl_xor(bits, 32, 64);
         if (h == 0 && qrow < p.Sq)
           p.drop.bits[((static_cast<int64_t>(b) * p.Hq + hq) * p.drop.nkt + kv0 / BN) * p.drop.sqp +
@@ -380,10 +386,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       float p1 = fast_exp2(fmaf(x[i + 1], slx, nbase));
       l += p0 + p1;  // fp32 sum of the unrounded probabilities, as the reference
       if constexpr (DR) {
-        p0 = dropout_keeps(p.drop, dw, i) ? p0 * p.drop.scale : 0.f;
-        p1 = dropout_keeps(p.drop, dw, i + 1) ? p1 * p.drop.scale : 0.f;
+        const float dsc = none_kept ? 0.f : p.drop.scale;
+        pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0 * dsc, p1 * dsc) & km[i >> 1];
+      } else {
+        pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
       }
-      pb[i >> 3][(i & 7) >> 1] = pack2<T>(p0, p1);
     }
   };
 

@@ -14,6 +14,15 @@
 
 namespace tsattn {
 
+// a ^ b ^ k in one instruction (gfx950's three-input bitwise op, truth table
+// 0x96); the compiler emits two two-input XORs for the plain expression.  k is
+// the round key, uniform over the wave.
+__device__ __forceinline__ uint32_t xor3_key(uint32_t a, uint32_t b, uint32_t k) {
+  uint32_t r;
+  asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+  return r;
+}
+
 __device__ __forceinline__ void philox4x32(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
   constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
   constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
@@ -24,8 +33,8 @@ __device__ __forceinline__ void philox4x32(uint32_t (&c)[4], uint32_t k0, uint32
       k1 += W1;
     }
     const uint64_t p0 = static_cast<uint64_t>(M0) * c[0], p1 = static_cast<uint64_t>(M1) * c[2];
-    const uint32_t n0 = static_cast<uint32_t>(p1 >> 32) ^ c[1] ^ k0;
-    const uint32_t n2 = static_cast<uint32_t>(p0 >> 32) ^ c[3] ^ k1;
+    const uint32_t n0 = xor3_key(static_cast<uint32_t>(p1 >> 32), c[1], k0);
+    const uint32_t n2 = xor3_key(static_cast<uint32_t>(p0 >> 32), c[3], k1);
     c[0] = n0;
     c[1] = static_cast<uint32_t>(p1);
     c[2] = n2;
@@ -80,6 +89,38 @@ __device__ __forceinline__ bool dropout_keeps_one(const Problem &p, int64_t row,
   uint64_t blk[4];
   dropout_block(p.drop, dropout_block_index(p, row, j & ~15), blk);
   return (static_cast<uint32_t>(blk[(j & 15) >> 2] >> (16 * (j & 3))) & 0xFFFFu) >= p.drop.thr;
+}
+
+// Keep masks of two dropout words packed in u (one per 16-bit half): 0xFFFF in
+// each half whose word is >= thr, else 0, in three packed 16-bit operations.
+// thr2 = thr in both halves (thr <= 65535; a threshold of 65536 keeps nothing
+// and is the caller's to handle).
+__device__ __forceinline__ uint32_t keep_mask_pair(uint32_t u, uint32_t thr2) {
+  uint32_t t, d, k;
+  // thr - w, saturated at 0: 0 iff kept
+  asm("v_pk_sub_u16 %0, %1, %2 clamp" : "=v"(t) : "s"(thr2), "v"(u));
+  // 0 kept, 1 dropped
+  asm("v_pk_min_u16 %0, %1, %2" : "=v"(d) : "v"(t), "s"(0x00010001u));
+  // kept: 0 - 1 = 0xFFFF; dropped: 1 - 1 = 0
+  asm("v_pk_sub_u16 %0, %1, %2" : "=v"(k) : "v"(d), "s"(0x00010001u));
+  return k;
+}
+
+// Keep bits of the 16 words of an MFMA accumulator lane from its pair masks
+// km[k] (keep_mask_pair of words 2k, 2k + 1): word i's bit at 8 (i / 4) +
+// i % 4 (lane half 0's key positions; the other half shifts them by 4).
+__device__ __forceinline__ uint32_t keep_bits16(const uint32_t (&km)[8]) {
+  uint32_t bits = 0;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int pos = 8 * (k >> 1) + 2 * (k & 1);  // bit of word 2k
+    const uint32_t sw = __builtin_amdgcn_alignbit(km[k], km[k], 16);  // halves swapped
+    // Every bit of a half equals that half's decision: bit pos (< 16) of km is
+    // word 2k's and bit pos + 1 of sw word 2k + 1's; past 16 the halves trade.
+    const uint32_t m = pos < 16 ? (1u << pos) : (2u << pos);
+    bits |= ((km[k] & m) | (sw & ~m)) & (3u << pos);
+  }
+  return bits;
 }
 
 __device__ __forceinline__ bool dropout_keeps(const DropDesc &d, const uint64_t (&w)[4], int i) {
