@@ -477,11 +477,6 @@ __device__ __forceinline__ float half_swap_max3(float x) {
   return max3f(__builtin_bit_cast(float, a), __builtin_bit_cast(float, b), __builtin_bit_cast(float, b));
 }
 
-__device__ __forceinline__ uint64_t partner64(uint64_t x, int h) {
-  return static_cast<uint64_t>(partner32(static_cast<unsigned>(x), h)) |
-         (static_cast<uint64_t>(partner32(static_cast<unsigned>(x >> 32), h)) << 32);
-}
-
 __device__ __forceinline__ uint32_t lds_addr(const void *p) {
   return static_cast<uint32_t>(
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void *)(p)));

@@ -234,6 +234,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     mstep = static_cast<uint32_t>(p.mask.s3 * mes);
     if (qrow >= p.Sq) klim = 0;
   }
+  // Dropout block index of this lane half's first 16 keys of its row (tile j
+  // adds 2 j).
+  uint64_t drow = 0;
+  if constexpr (DR)
+    drow = dropout_block_index(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, 16 * h);
   MaskFetch mf;
   // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
   const float slx = mask_kind(MK) >= 2 ? 1.f : a.sl;
@@ -366,7 +371,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     const bool none_kept = p.drop.thr > 65535u;
     if constexpr (DR) {
       uint64_t dw[4];
-      dropout_words_rows(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, kv0, h, dw);
+      dropout_words_rows(p.drop, drow + static_cast<uint32_t>(kv0 / 16), dw);
       const uint32_t thr2 = (p.drop.thr & 0xFFFFu) * 0x00010001u;
 #pragma unroll
       for (int k = 0; k < 8; ++k)

@@ -65,22 +65,35 @@ __device__ __forceinline__ uint64_t dropout_block_index(const Problem &p, int64_
 
 // The 16 dropout words of a lane holding query row `row` against keys
 // kv0 + 8 g + 4 h + r (g, r = 0..3; the MFMA accumulator row pattern of the
-// forward and dQ kernels), kv0 a multiple of 32: word (g, r) is bits 16 r ..
-// of out[g].  Lane half h computes the block of keys kv0 + 16 h .. + 15 and
-// the two halves exchange the quarters the other needs.
-__device__ __forceinline__ void dropout_words_rows(const Problem &p, int64_t row, int kv0, int h,
+// forward kernel), kv0 a multiple of 32: word (g, r) is bits 16 r .. of
+// out[g].  Lane half h computes the block of keys kv0 + 16 h .. + 15, index
+// n = dropout_block_index(p, row, kv0 + 16 h) (the caller keeps the row's
+// part, loop-invariant), and the two halves exchange the quarters the other
+// needs (v_permlane32_swap exchanges the upper half of its first register
+// with the lower half of its second).
+__device__ __forceinline__ void dropout_words_rows(const DropDesc &d, uint64_t n,
                                                    uint64_t (&out)[4]) {
   uint64_t blk[4];
-  dropout_block(p.drop, dropout_block_index(p, row, kv0 + 16 * h), blk);
-  // block quarter m = keys 4 m .. 4 m + 3 of the block; this lane needs
-  // quarters h and 2 + h of both blocks
-  const uint64_t keep0 = h ? blk[1] : blk[0], keep1 = h ? blk[3] : blk[2];
-  const uint64_t recv0 = partner64(h ? blk[0] : blk[1], h);
-  const uint64_t recv1 = partner64(h ? blk[2] : blk[3], h);
-  out[0] = h ? recv0 : keep0;
-  out[1] = h ? recv1 : keep1;
-  out[2] = h ? keep0 : recv0;
-  out[3] = h ? keep1 : recv1;
+  dropout_block(d, n, blk);
+  // Block quarter m = keys 4 m .. 4 m + 3 of the block.  Half 0 needs its own
+  // quarters 0, 2 and half 1's 0, 2 (keys 16 ..); half 1 needs half 0's 1, 3
+  // and its own 1, 3.  One upper/lower swap per dword of the pairs (q0, q1) and
+  // (q2, q3) leaves exactly that in both halves, with no selects.
+  uint32_t w[8];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    w[2 * m] = static_cast<uint32_t>(blk[m]);
+    w[2 * m + 1] = static_cast<uint32_t>(blk[m] >> 32);
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(w[e]), "+v"(w[2 + e]));
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(w[4 + e]), "+v"(w[6 + e]));
+  }
+  out[0] = w[0] | (static_cast<uint64_t>(w[1]) << 32);
+  out[2] = w[2] | (static_cast<uint64_t>(w[3]) << 32);
+  out[1] = w[4] | (static_cast<uint64_t>(w[5]) << 32);
+  out[3] = w[6] | (static_cast<uint64_t>(w[7]) << 32);
 }
 
 // Keep bit of element (row, key j) on its own (the generic kernels: each
