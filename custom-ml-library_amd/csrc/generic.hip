@@ -1,6 +1,16 @@
 // Generic attention kernels: one wavefront per query (or key) row, VALU math
 // in the accumulator type (float for f32/f16/bf16, double for f64).
 //
+// The dK/dV kernel's four waves (four keys) share each 64-row chunk of Q and
+// dO, which every lane walks along its own row: with ST the chunk is staged
+// through LDS once per workgroup by whole-row loads and each lane reads its
+// row there (rows padded by one element, so the 64 lanes' walks hit 64
+// banks), instead of 64 rows per load instruction from memory.  Same
+// arithmetic in the same order either way; problems whose chunk does not fit
+// in LDS run without it.  (The same staging of K / V in the forward and dQ
+// kernels measured slower: four rows per workgroup do not repay it at the
+// lower occupancy the staged chunk leaves.)
+//
 // These carry every case the reference allows that the MFMA kernels do not
 // specialise: fp32 / fp64 inputs, any head dims (Dv != Dqk included,
 // reference tests/test_transformer.py:44-46), boolean or additive masks of any
@@ -84,6 +94,26 @@ __device__ __forceinline__ const T *row_ptr(View v, int b, int h, int s) {
 template <typename T>
 __device__ __forceinline__ T *row_ptr_mut(View v, int b, int h, int s) {
   return const_cast<T *>(row_ptr<T>(v, b, h, s));
+}
+
+// Rows r0 .. r0 + 63 of operand x (batch b, head h), D elements each, into dst
+// as A with row stride D + 1; rows from n_rows on are zero.  Wave w of the
+// NW loads rows w, w + NW, ..., one coalesced row per step.  Every thread of
+// the workgroup calls it; the caller synchronises.
+template <typename T, typename A, int NW>
+__device__ __forceinline__ void stage_chunk(A *dst, View x, int b, int h, int64_t r0, int n_rows,
+                                            int D) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int r = w; r < kChunk; r += NW) {
+    const int64_t row = r0 + r;
+    A *out = dst + r * (D + 1);
+    if (row < n_rows) {
+      const T *src = row_ptr<T>(x, b, h, static_cast<int>(row));
+      for (int d = lane; d < D; d += 64) out[d] = to_acc<A>(src[d]);
+    } else {
+      for (int d = lane; d < D; d += 64) out[d] = A(0);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -254,22 +284,31 @@ __global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View
 // ---------------------------------------------------------------------------
 // Backward pass 3: per key row j of KV head hk, summed over the query heads
 // of its group (:240-247): dv_j = sum_i p_ij dout_i, dk_j = sum_i ds_ij q_i.
-// grid (ceil(Sk/4), Hkv, B).
+// grid (ceil(Sk/NW), Hkv, B), NW waves = keys per workgroup: eight when the
+// Q / dO chunk is staged (it serves twice the keys), else four.
 // ---------------------------------------------------------------------------
-template <typename T, typename A>
-__global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, View k, View v,
-                                                           View dout, const A *lse, const A *delta,
-                                                           View dk, View dv) {
+template <bool ST>
+constexpr int dkdv_waves() {
+  return ST ? 8 : 4;
+}
+
+template <typename T, typename A, bool ST>
+__global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
+    Problem p, View q, View k, View v, View dout, const A *lse, const A *delta, View dk, View dv) {
+  constexpr int NW = dkdv_waves<ST>();
   extern __shared__ unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int b = blockIdx.z, hk = blockIdx.y;
-  const int j = blockIdx.x * kWaves + w;
+  const int j = blockIdx.x * NW + w;
   const int kv_end = kv_end_for(p, b);
   const bool key_ok = j < p.Sk;
   A *krow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + p.Dv + 2 * kChunk);
   A *vrow = krow + p.Dqk;
   A *pbuf = vrow + p.Dv;
   A *dsbuf = pbuf + kChunk;
+  // staged Q / dO chunk (ST)
+  A *qst = reinterpret_cast<A *>(smem_raw) + NW * (p.Dqk + p.Dv + 2 * kChunk);
+  A *gst = qst + kChunk * (p.Dqk + 1);
   if (key_ok) {
     const T *kp = row_ptr<T>(k, b, hk, j);
     const T *vp = row_ptr<T>(v, b, hk, j);
@@ -277,7 +316,7 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
     for (int d = lane; d < p.Dv; d += 64) vrow[d] = to_acc<A>(vp[d]);
   }
   // First query row that can see any key of this workgroup (causal).
-  int64_t first_key = static_cast<int64_t>(blockIdx.x) * kWaves;
+  int64_t first_key = static_cast<int64_t>(blockIdx.x) * NW;
   int64_t start = 0;
   if (p.causal) {
     start = first_key - p.offset;
@@ -294,12 +333,22 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
     const int hq = hk * p.rep + r;
     for (int64_t i0 = start; i0 < p.Sq; i0 += kChunk) {
       const int i = static_cast<int>(i0) + lane;
+      if constexpr (ST) {
+        stage_chunk<T, A, NW>(qst, q, b, hq, i0, p.Sq, p.Dqk);
+        stage_chunk<T, A, NW>(gst, dout, b, hq, i0, p.Sq, p.Dv);
+        __syncthreads();
+      }
       A pij = 0, ds = 0;
       if (key_ok && j < kv_end && i < p.Sq) {
-        // q row i is read straight from memory (lane-private row)
-        const T *qp = row_ptr<T>(q, b, hq, i);
         A acc = 0;
-        for (int d = 0; d < p.Dqk; ++d) acc += to_acc<A>(qp[d]) * krow[d];
+        if constexpr (ST) {
+          const A *qr = qst + lane * (p.Dqk + 1);
+          for (int d = 0; d < p.Dqk; ++d) acc += qr[d] * krow[d];
+        } else {
+          // q row i is read straight from memory (lane-private row)
+          const T *qp = row_ptr<T>(q, b, hq, i);
+          for (int d = 0; d < p.Dqk; ++d) acc += to_acc<A>(qp[d]) * krow[d];
+        }
         A s = acc * scale;
         bool ok = !(p.causal && static_cast<int64_t>(i) + p.offset < static_cast<int64_t>(j));
         if (ok && p.mask.kind != TSATTN_MASK_NONE) {
@@ -317,9 +366,14 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
           if (!isfinite(l)) l = 0;
           pij = exp_acc(s - l);
           if (pij != A(0)) {
-            const T *gp = row_ptr<T>(dout, b, hq, i);
             A dp = 0;
-            for (int d = 0; d < p.Dv; ++d) dp += to_acc<A>(gp[d]) * vrow[d];
+            if constexpr (ST) {
+              const A *gr = gst + lane * (p.Dv + 1);
+              for (int d = 0; d < p.Dv; ++d) dp += gr[d] * vrow[d];
+            } else {
+              const T *gp = row_ptr<T>(dout, b, hq, i);
+              for (int d = 0; d < p.Dv; ++d) dp += to_acc<A>(gp[d]) * vrow[d];
+            }
             const A f = drop_factor<A>(p, rr, j);  // rr = the query row's index
             ds = pij * (dp * f - delta[rr]) * scale;
             pij *= f;  // dV takes P * mask
@@ -333,13 +387,23 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
       for (int ii = 0; ii < n; ++ii) {
         const A pv = pbuf[ii], dsv = dsbuf[ii];
         if (pv == A(0) && dsv == A(0)) continue;
-        const T *gp = row_ptr<T>(dout, b, hq, static_cast<int>(i0) + ii);
-        const T *qp = row_ptr<T>(q, b, hq, static_cast<int>(i0) + ii);
+        if constexpr (ST) {
+          const A *gr = gst + ii * (p.Dv + 1), *qr = qst + ii * (p.Dqk + 1);
 #pragma unroll
-        for (int t = 0; t < kMaxDimSlots; ++t) {
-          const int d = lane + 64 * t;
-          if (d < p.Dv) acc_v[t] += pv * to_acc<A>(gp[d]);
-          if (d < p.Dqk) acc_k[t] += dsv * to_acc<A>(qp[d]);
+          for (int t = 0; t < kMaxDimSlots; ++t) {
+            const int d = lane + 64 * t;
+            if (d < p.Dv) acc_v[t] += pv * gr[d];
+            if (d < p.Dqk) acc_k[t] += dsv * qr[d];
+          }
+        } else {
+          const T *gp = row_ptr<T>(dout, b, hq, static_cast<int>(i0) + ii);
+          const T *qp = row_ptr<T>(q, b, hq, static_cast<int>(i0) + ii);
+#pragma unroll
+          for (int t = 0; t < kMaxDimSlots; ++t) {
+            const int d = lane + 64 * t;
+            if (d < p.Dv) acc_v[t] += pv * to_acc<A>(gp[d]);
+            if (d < p.Dqk) acc_k[t] += dsv * to_acc<A>(qp[d]);
+          }
         }
       }
       __syncthreads();
@@ -354,6 +418,22 @@ __global__ __launch_bounds__(256) void generic_dkdv_kernel(Problem p, View q, Vi
     if (d < p.Dqk) kout[d] = from_acc<T, A>(acc_k[t]);
     if (d < p.Dv) vout[d] = from_acc<T, A>(acc_v[t]);
   }
+}
+
+// LDS of one staged 64-row chunk of each of two operands (row stride D + 1).
+template <typename A>
+size_t staged_bytes(const Problem &p) {
+  return static_cast<size_t>(kChunk) * (p.Dqk + 1 + p.Dv + 1) * sizeof(A);
+}
+
+// Whether `kernel` may take `smem` bytes of dynamic LDS: at most the 160 KiB a
+// gfx950 workgroup can hold, and above 64 KiB only once the runtime accepts
+// the kernel's raised limit (asked on every call: cheap, and per device).
+inline bool lds_ok(const void *kernel, size_t smem) {
+  if (smem > 160 * 1024) return false;
+  if (smem <= 64 * 1024) return true;
+  return hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             static_cast<int>(smem)) == hipSuccess;
 }
 
 template <typename T, typename A>
@@ -375,9 +455,20 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
   { Probe pr_("generic_bwd_delta", st); generic_delta_kernel<T, A><<<grid_q, dim3(256), 0, st>>>(p, o, dout, dl); }
   size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
   { Probe pr_("generic_bwd_dq", st); generic_dq_kernel<T, A><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq); }
-  dim3 grid_k((p.Sk + kWaves - 1) / kWaves, p.Hkv, p.B);
-  size_t smem_k = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A);
-  { Probe pr_("generic_bwd_dkdv", st); generic_dkdv_kernel<T, A><<<grid_k, dim3(256), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv); }
+  constexpr int nws = dkdv_waves<true>(), nwd = dkdv_waves<false>();
+  const size_t smem_ks = static_cast<size_t>(nws) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A) +
+                         staged_bytes<A>(p);
+  {
+    Probe pr_("generic_bwd_dkdv", st);
+    if (lds_ok(reinterpret_cast<const void *>(&generic_dkdv_kernel<T, A, true>), smem_ks)) {
+      const dim3 grid_k((p.Sk + nws - 1) / nws, p.Hkv, p.B);
+      generic_dkdv_kernel<T, A, true><<<grid_k, dim3(64 * nws), smem_ks, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
+    } else {
+      const dim3 grid_k((p.Sk + nwd - 1) / nwd, p.Hkv, p.B);
+      const size_t smem_k = static_cast<size_t>(nwd) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A);
+      generic_dkdv_kernel<T, A, false><<<grid_k, dim3(64 * nwd), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
+    }
+  }
   return hipGetLastError();
 }
 
