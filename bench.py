@@ -30,6 +30,9 @@ time.  The JSON line also carries
   32 / 8 heads of 128, fp16, batch 64, 1024 cached positions) with the
   projections, RoPE and K/V append in one kernel, against the same module
   with that kernel switched off, and the fused kernel's HBM rate;
+* ``fp32`` -- causal fp32 forward + backward on the generic kernels at the
+  reference's CPU-runnable shape (B=8 H=4 S=256 D=64) and at B=2 H=16
+  S=2048 D=128: step time, TFLOP/s and the fraction of the fp32 peak;
 * ``cpu_baseline`` -- the NumPy oracle (a restatement of the reference's
   streaming algorithm) on a bounded sample of the same inputs, on this
   host's cores.
@@ -54,6 +57,7 @@ sys.path.insert(0, str(ROOT / "custom-ml-library_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0     # MI355X HBM3E
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 (MFMA)
 B, H, S, D = 16, 16, 2048, 128
 DEC_B, DEC_H, DEC_D, DEC_CAP, DEC_LO, DEC_HI = 64, 32, 128, 8192, 512, 8192
 PF_B, PF_H, PF_S, PF_D, PF_LO = 2, 32, 32768, 128, 16384
@@ -78,7 +82,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload",
                     choices=["all", "fwd_bwd", "variants", "decode", "decode_int8", "prefill", "lm",
-                             "cached_step", "copy"],
+                             "cached_step", "fp32", "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -482,6 +486,49 @@ def bench_cached_step(ts, torch, steps, warmup):
     return out
 
 
+def bench_fp32(ts, torch, steps, warmup):
+    """Report-only: causal fp32 forward + backward through the public API on
+    the generic kernels (the path of fp32 models, the reference's default
+    dtype): the reference's CPU-runnable case (B8 H4 S256 D64) and a long
+    sequence (B2 H16 S2048 D128).  Per-kernel probe means and TFLOP/s against
+    the fp32 peak."""
+    from tensorsmith_hip import _lib
+
+    out = {}
+    for name, (b, h, s, d) in {"causal_fwd_bwd_f32_b8h4s256d64": (8, 4, 256, 64),
+                               "causal_fwd_bwd_f32_b2h16s2048d128": (2, 16, 2048, 128)}.items():
+        gen = torch.Generator(device="cuda").manual_seed(7)
+        raw = [torch.randn((b, h, s, d), generator=gen, device="cuda", dtype=torch.float32)
+               for _ in range(4)]
+        q, k, v = (ts.Tensor(t, device="hip", requires_grad=True) for t in raw[:3])
+        upstream = ts.Tensor(raw[3], device="hip")
+
+        def step():
+            for t in (q, k, v):
+                t.zero_grad()
+            o = ts.nn.scaled_dot_product_attention(q, k, v, is_causal=True)
+            o.backward(upstream)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        if _lib.last_kernel_path() != _lib.PATH_GENERIC:
+            raise RuntimeError("the generic kernels did not run for the fp32 workload")
+        _lib.profile_reset()
+        _lib.profile_enable(True)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) / steps * 1e3
+        _lib.profile_enable(False)
+        kernels = {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}
+        tf = causal_fwd_flops(b, h, s, d) * 3.5 / (ms * 1e-3) / 1e12
+        out[name] = {"ms_per_step": round(ms, 4), "tflops": round(tf, 2),
+                     "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4), "kernel_ms": kernels}
+    return out
+
+
 def bench_lm(ts, torch, steps, warmup):
     """6-layer decoder LM, fp16 autocast, forward + backward, random init."""
     from tensorsmith_hip import _lib
@@ -695,6 +742,9 @@ def main():
     if args.workload == "cached_step":
         print(json.dumps({"cached_step": bench_cached_step(ts, torch, 50, 5)}), flush=True)
         return
+    if args.workload == "fp32":
+        print(json.dumps({"fp32": bench_fp32(ts, torch, 5, 2)}), flush=True)
+        return
     print(f"[bench] fwd+bwd B{B} H{H} S{S} D{D} bf16: {args.warmup} warmup + {args.steps} steps",
           file=sys.stderr, flush=True)
     main_res, host = bench_fwd_bwd(ts, torch, args.steps, args.warmup)
@@ -723,6 +773,9 @@ def main():
     cs_res = bench_cached_step(ts, torch, 50, 5)
     print(f"[bench] cached MHA step {cs_res['fused']['ms_per_step']:.3f} ms "
           f"(unfused {cs_res['unfused']['ms_per_step']:.3f} ms)", file=sys.stderr, flush=True)
+    f32_res = bench_fp32(ts, torch, 5, 2)
+    print("[bench] fp32 (generic kernels) " + ", ".join(
+        f"{n} {r['ms_per_step']:.3f} ms" for n, r in f32_res.items()), file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (NumPy oracle sample)", file=sys.stderr, flush=True)
@@ -757,6 +810,7 @@ def main():
         "prefill": pf_res,
         "lm_step": lm_res,
         "cached_step": cs_res,
+        "fp32": f32_res,
     }
     print(json.dumps(line), flush=True)
 
