@@ -21,6 +21,8 @@ generator's published known-answer vectors).  Checked here:
   for every tile it computes, the generic path for all) are that mask
   packed; a backward that gets no bits draws the same ones into its
   workspace, and both give the same gradients bit for bit;
+* p at the top of the 16-bit threshold range (threshold 65535, and 65536,
+  which keeps nothing) gives the oracle's bits, outputs and gradients;
 * the same key and counter reproduce every output bit; another key changes
   them; the mirror drops on backend "hip" / "dense" / "auto" and raises the
   reference's ValueError on "streaming" (tests/test_transformer.py:164-171).
@@ -159,6 +161,37 @@ def test_dropout_attention_matches_oracle(case):
     kw3 = dict(kw, dropout=(p, key + 1, counter))
     out3, _, _ = abi.forward(q, k, v, **kw3)
     assert not torch.equal(out, out3)
+
+
+@pytest.mark.parametrize("p", [0.99999, 0.999995])
+def test_dropout_probability_near_one(p):
+    """The top of the 16-bit threshold range on the MFMA forward: p = 0.99999
+    gives threshold 65535 (a word is kept only when it is 65535), p = 0.999995
+    rounds it to 65536, which no word reaches (the kernel then zeroes the
+    probabilities and the keep bits without comparing): the written bits equal
+    the oracle's mask packed, and O and the gradients match the oracle's."""
+    dtype, b, h, s, d = "bfloat16", 1, 2, 256, 128
+    say(f"dropout near one: p={p}")
+    assert DR.threshold(p) == (65535 if p < 0.999995 else 65536)
+    inp = attention_inputs(b, h, s, d, dtype, value_scale=0.5, seed=5)
+    key, counter = 99, 0
+    keep = DR.keep_mask(key, counter, (b, h, s, s), p)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    kw = dict(causal=False, dropout=(p, key, counter))
+    bits = abi.dropout_bits_buffer(q, k, v, **kw)
+    out, lse, path = abi.forward(q, k, v, dropout_bits=bits, **kw)
+    assert path == _lib.PATH_MFMA
+    np.testing.assert_array_equal(bits.cpu().numpy(), packed_bits(keep))
+    dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, dropout_bits=bits, **kw)
+    out_c, _, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, None, False, dtype=dtype, p=p,
+                                     rng_key=key, rng_counter=counter)
+    say(f"  kept elements: {int(keep.sum())}")
+    if not keep.any():
+        for t in (out, dq, dk, dv):
+            assert not t.float().abs().max().item()
+    check(abi.host(out), out_c, dtype, "o", "O")
+    for got, want, name in zip((dq, dk, dv), back(inp.do), ("dQ", "dK", "dV")):
+        check(abi.host(got), want, dtype, "g", name)
 
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
