@@ -56,28 +56,6 @@ __device__ __forceinline__ A wave_sum(A x) {
   return x;
 }
 
-// Score of (query row held in `qrow`, key j), with the reference's order:
-// scale, then mask (bool -> -inf, additive -> +), then causal (:102-113).
-template <typename T, typename A>
-__device__ __forceinline__ A score(const Problem &p, const A *qrow, const T *krow, int b, int hq,
-                                   int i, int j, int kv_end) {
-  if (j >= kv_end) return neg_inf<A>();
-  if (p.causal && static_cast<int64_t>(i) + p.offset < static_cast<int64_t>(j)) return neg_inf<A>();
-  A acc = 0;
-  for (int d = 0; d < p.Dqk; ++d) acc += qrow[d] * to_acc<A>(krow[d]);
-  A s = acc * static_cast<A>(p.scale);
-  if (p.mask.kind != TSATTN_MASK_NONE) {
-    int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
-                 static_cast<int64_t>(j) * p.mask.s3;
-    if (p.mask.kind == TSATTN_MASK_BOOL) {
-      if (!static_cast<const uint8_t *>(p.mask.data)[mi]) return neg_inf<A>();
-    } else {
-      s += load_additive<A>(p.mask.data, mi, p.mask.dtype);
-    }
-  }
-  return s;
-}
-
 // Dropout mask value of element (row, j): 0, or the keep scale in the
 // compute type (the reference's keep.astype(compute dtype) / (1 - p)).
 template <typename A>
@@ -116,76 +94,151 @@ __device__ __forceinline__ void stage_chunk(A *dst, View x, int b, int h, int64_
   }
 }
 
+// Scores of query rows i0 .. i0 + R - 1 (held in qrows, row stride Dqk)
+// against key j, each with the reference's order: scale, then mask (bool ->
+// -inf, additive -> +), then causal (:102-113); rows from Sq on get -inf.
+// Each element of the key row is loaded once for the R rows.
+template <typename T, typename A, int R>
+__device__ __forceinline__ void score_rows(const Problem &p, const A *qrows, const T *krow, int b,
+                                           int hq, int i0, int j, int kv_end, A (&s)[R]) {
+  if (j >= kv_end) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) s[r] = neg_inf<A>();
+    return;
+  }
+  A acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0;
+  for (int d = 0; d < p.Dqk; ++d) {
+    const A kd = to_acc<A>(krow[d]);
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += qrows[r * p.Dqk + d] * kd;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    if (i >= p.Sq || (p.causal && static_cast<int64_t>(i) + p.offset < static_cast<int64_t>(j))) {
+      s[r] = neg_inf<A>();
+      continue;
+    }
+    A x = acc[r] * static_cast<A>(p.scale);
+    if (p.mask.kind != TSATTN_MASK_NONE) {
+      const int64_t mi = b * p.mask.s0 + hq * p.mask.s1 + static_cast<int64_t>(i) * p.mask.s2 +
+                         static_cast<int64_t>(j) * p.mask.s3;
+      if (p.mask.kind == TSATTN_MASK_BOOL) {
+        if (!static_cast<const uint8_t *>(p.mask.data)[mi]) x = neg_inf<A>();
+      } else {
+        x += load_additive<A>(p.mask.data, mi, p.mask.dtype);
+      }
+    }
+    s[r] = x;
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Forward: grid (ceil(Sq/4), Hq, B); wave w owns query row blockIdx.x*4 + w.
+// Forward: grid (ceil(Sq / (4 R)), Hq, B); wave w owns the R query rows from
+// (blockIdx.x * 4 + w) R, lane l the key j0 + l of each 64-key chunk, so each
+// K and V element a lane loads serves R rows.
 // ---------------------------------------------------------------------------
-template <typename T, typename A>
+template <typename T, typename A, int R>
 __global__ __launch_bounds__(256) void generic_forward_kernel(Problem p, View q, View k, View v,
                                                               View o, A *lse) {
   extern __shared__ unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int b = blockIdx.z, hq = blockIdx.y, hk = hq / p.rep;
-  const int i = blockIdx.x * kWaves + w;
-  const bool row_ok = i < p.Sq;
-  A *qrow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + kChunk);
-  A *pbuf = qrow + p.Dqk;
+  const int i0 = (blockIdx.x * kWaves + w) * R;
+  A *qrows = reinterpret_cast<A *>(smem_raw) + w * R * (p.Dqk + kChunk);
+  A *pbuf = qrows + R * p.Dqk;  // [R][kChunk]
   const int kv_end = kv_end_for(p, b);
 
-  if (row_ok) {
-    const T *qp = row_ptr<T>(q, b, hq, i);
-    for (int d = lane; d < p.Dqk; d += 64) qrow[d] = to_acc<A>(qp[d]);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    if (i < p.Sq) {
+      const T *qp = row_ptr<T>(q, b, hq, i);
+      for (int d = lane; d < p.Dqk; d += 64) qrows[r * p.Dqk + d] = to_acc<A>(qp[d]);
+    } else {
+      for (int d = lane; d < p.Dqk; d += 64) qrows[r * p.Dqk + d] = A(0);
+    }
   }
   // Uniform chunk count for the workgroup: the furthest key any of its rows sees.
-  int64_t last_row = static_cast<int64_t>(blockIdx.x) * kWaves + kWaves - 1;
+  int64_t last_row = (static_cast<int64_t>(blockIdx.x) * kWaves + kWaves) * R - 1;
   if (last_row > p.Sq - 1) last_row = p.Sq - 1;
   int64_t stop = kv_end;
   if (p.causal && last_row + p.offset + 1 < stop) stop = last_row + p.offset + 1;
   if (stop < 0) stop = 0;
   __syncthreads();
 
-  A m = neg_inf<A>(), l = 0;
-  A acc[kMaxDimSlots];
+  A m[R], l[R], acc[R][kMaxDimSlots];
 #pragma unroll
-  for (int t = 0; t < kMaxDimSlots; ++t) acc[t] = 0;
+  for (int r = 0; r < R; ++r) {
+    m[r] = neg_inf<A>();
+    l[r] = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxDimSlots; ++t) acc[r][t] = 0;
+  }
 
   for (int j0 = 0; j0 < stop; j0 += kChunk) {
     const int j = j0 + lane;
-    A s = neg_inf<A>();
-    if (row_ok) s = score<T, A>(p, qrow, row_ptr<T>(k, b, hk, j < p.Sk ? j : 0), b, hq, i, j, kv_end);
-    const A cmax = wave_max(s);
-    const A m_new = m > cmax ? m : cmax;
-    const A base = isfinite(m_new) ? m_new : A(0);
-    const A corr = exp_acc(m - base);
-    const A pj = exp_acc(s - base);
-    l = l * corr + wave_sum(pj);  // the denominator sums the undropped P
-    m = m_new;
+    A s[R];
+    score_rows<T, A, R>(p, qrows, row_ptr<T>(k, b, hk, j < p.Sk ? j : 0), b, hq, i0, j, kv_end, s);
 #pragma unroll
-    for (int t = 0; t < kMaxDimSlots; ++t) acc[t] *= corr;
-    pbuf[lane] = p.drop.on ? pj * drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i, j) : pj;
+    for (int r = 0; r < R; ++r) {
+      const A cmax = wave_max(s[r]);
+      const A m_new = m[r] > cmax ? m[r] : cmax;
+      const A base = isfinite(m_new) ? m_new : A(0);
+      const A corr = exp_acc(m[r] - base);
+      const A pj = exp_acc(s[r] - base);
+      l[r] = l[r] * corr + wave_sum(pj);  // the denominator sums the undropped P
+      m[r] = m_new;
+#pragma unroll
+      for (int t = 0; t < kMaxDimSlots; ++t) acc[r][t] *= corr;
+      // (a zero P stays zero under any mask value)
+      pbuf[r * kChunk + lane] =
+          p.drop.on && pj != A(0)
+              ? pj * drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i0 + r, j)
+              : pj;
+    }
     __syncthreads();
     const int n = (stop - j0) < kChunk ? static_cast<int>(stop - j0) : kChunk;
     for (int jj = 0; jj < n; ++jj) {
-      const A pv = pbuf[jj];
-      if (pv == A(0)) continue;  // masked or underflowed key: contributes nothing
+      A pv[R];
+      bool any = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        pv[r] = pbuf[r * kChunk + jj];
+        any |= pv[r] != A(0);
+      }
+      if (!any) continue;  // masked or underflowed key for every row: contributes nothing
       const T *vrow = row_ptr<T>(v, b, hk, j0 + jj);
 #pragma unroll
       for (int t = 0; t < kMaxDimSlots; ++t) {
         const int d = lane + 64 * t;
-        if (d < p.Dv) acc[t] += pv * to_acc<A>(vrow[d]);
+        if (d < p.Dv) {
+          const A vd = to_acc<A>(vrow[d]);
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (pv[r] != A(0)) acc[r][t] += pv[r] * vd;
+        }
       }
     }
     __syncthreads();
   }
-  if (!row_ok) return;
-  const A inv = l > A(0) ? A(1) / l : A(1);
-  T *op = row_ptr_mut<T>(o, b, hq, i);
 #pragma unroll
-  for (int t = 0; t < kMaxDimSlots; ++t) {
-    const int d = lane + 64 * t;
-    if (d < p.Dv) op[d] = from_acc<T, A>(acc[t] * inv);
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    if (i >= p.Sq) continue;
+    const A inv = l[r] > A(0) ? A(1) / l[r] : A(1);
+    T *op = row_ptr_mut<T>(o, b, hq, i);
+#pragma unroll
+    for (int t = 0; t < kMaxDimSlots; ++t) {
+      const int d = lane + 64 * t;
+      if (d < p.Dv) op[d] = from_acc<T, A>(acc[r][t] * inv);
+    }
+    if (lse && lane == 0)
+      lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i] =
+          l[r] > A(0) ? m[r] + log_acc(l[r]) : neg_inf<A>();
   }
-  if (lse && lane == 0)
-    lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i] = l > A(0) ? m + log_acc(l) : neg_inf<A>();
 }
 
 // ---------------------------------------------------------------------------
@@ -206,78 +259,119 @@ __global__ __launch_bounds__(256) void generic_delta_kernel(Problem p, View o, V
 
 // ---------------------------------------------------------------------------
 // Backward pass 2: dq_i = scale * sum_j p_ij (dp_ij - delta_i) k_j (:237-239).
+// Wave w owns the R query rows from (blockIdx.x * 4 + w) R, lane l the key
+// j0 + l of each chunk (each K and V element a lane loads serves R rows).
 // ---------------------------------------------------------------------------
-template <typename T, typename A>
+template <typename T, typename A, int R>
 __global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View k, View v,
                                                          View dout, const A *lse, const A *delta,
                                                          View dq) {
   extern __shared__ unsigned char smem_raw[];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int b = blockIdx.z, hq = blockIdx.y, hk = hq / p.rep;
-  const int i = blockIdx.x * kWaves + w;
-  const bool row_ok = i < p.Sq;
-  A *qrow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + p.Dv + kChunk);
-  A *grow = qrow + p.Dqk;
-  A *dsbuf = grow + p.Dv;
+  const int i0 = (blockIdx.x * kWaves + w) * R;
+  A *qrows = reinterpret_cast<A *>(smem_raw) + w * R * (p.Dqk + p.Dv + kChunk);
+  A *grows = qrows + R * p.Dqk;  // [R][Dv]
+  A *dsbuf = grows + R * p.Dv;   // [R][kChunk]
   const int kv_end = kv_end_for(p, b);
-  A row_lse = 0, row_delta = 0;
-  if (row_ok) {
-    const T *qp = row_ptr<T>(q, b, hq, i);
-    const T *gp = row_ptr<T>(dout, b, hq, i);
-    for (int d = lane; d < p.Dqk; d += 64) qrow[d] = to_acc<A>(qp[d]);
-    for (int d = lane; d < p.Dv; d += 64) grow[d] = to_acc<A>(gp[d]);
-    const int64_t r = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i;
-    row_lse = lse[r];
-    if (!isfinite(row_lse)) row_lse = 0;  // safe_lse (:231)
-    row_delta = delta[r];
+  A row_lse[R], row_delta[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    row_lse[r] = 0;
+    row_delta[r] = 0;
+    if (i < p.Sq) {
+      const T *qp = row_ptr<T>(q, b, hq, i);
+      const T *gp = row_ptr<T>(dout, b, hq, i);
+      for (int d = lane; d < p.Dqk; d += 64) qrows[r * p.Dqk + d] = to_acc<A>(qp[d]);
+      for (int d = lane; d < p.Dv; d += 64) grows[r * p.Dv + d] = to_acc<A>(gp[d]);
+      const int64_t rr = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i;
+      row_lse[r] = lse[rr];
+      if (!isfinite(row_lse[r])) row_lse[r] = 0;  // safe_lse (:231)
+      row_delta[r] = delta[rr];
+    } else {
+      for (int d = lane; d < p.Dqk; d += 64) qrows[r * p.Dqk + d] = A(0);
+      for (int d = lane; d < p.Dv; d += 64) grows[r * p.Dv + d] = A(0);
+    }
   }
-  int64_t last_row = static_cast<int64_t>(blockIdx.x) * kWaves + kWaves - 1;
+  int64_t last_row = (static_cast<int64_t>(blockIdx.x) * kWaves + kWaves) * R - 1;
   if (last_row > p.Sq - 1) last_row = p.Sq - 1;
   int64_t stop = kv_end;
   if (p.causal && last_row + p.offset + 1 < stop) stop = last_row + p.offset + 1;
   if (stop < 0) stop = 0;
   __syncthreads();
 
-  A acc[kMaxDimSlots];
+  A acc[R][kMaxDimSlots];
 #pragma unroll
-  for (int t = 0; t < kMaxDimSlots; ++t) acc[t] = 0;
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int t = 0; t < kMaxDimSlots; ++t) acc[r][t] = 0;
   const A scale = static_cast<A>(p.scale);
   for (int j0 = 0; j0 < stop; j0 += kChunk) {
     const int j = j0 + lane;
-    A ds = 0;
-    if (row_ok && j < kv_end) {
-      const T *krow = row_ptr<T>(k, b, hk, j);
-      const A s = score<T, A>(p, qrow, krow, b, hq, i, j, kv_end);
-      const A pij = exp_acc(s - row_lse);
-      if (pij != A(0)) {
-        const T *vrow = row_ptr<T>(v, b, hk, j);
-        A dp = 0;
-        for (int d = 0; d < p.Dv; ++d) dp += grow[d] * to_acc<A>(vrow[d]);
-        if (p.drop.on) dp *= drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i, j);
-        ds = pij * (dp - row_delta) * scale;
+    A ds[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) ds[r] = 0;
+    if (j < kv_end) {
+      A s[R];
+      score_rows<T, A, R>(p, qrows, row_ptr<T>(k, b, hk, j), b, hq, i0, j, kv_end, s);
+      A dp[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) dp[r] = 0;
+      const T *vrow = row_ptr<T>(v, b, hk, j);
+      for (int d = 0; d < p.Dv; ++d) {
+        const A vd = to_acc<A>(vrow[d]);
+#pragma unroll
+        for (int r = 0; r < R; ++r) dp[r] += grows[r * p.Dv + d] * vd;
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const A pij = exp_acc(s[r] - row_lse[r]);  // 0 for rows from Sq on
+        if (pij != A(0)) {
+          A dpr = dp[r];
+          if (p.drop.on)
+            dpr *= drop_factor<A>(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + i0 + r, j);
+          ds[r] = pij * (dpr - row_delta[r]) * scale;
+        }
       }
     }
-    dsbuf[lane] = ds;
+#pragma unroll
+    for (int r = 0; r < R; ++r) dsbuf[r * kChunk + lane] = ds[r];
     __syncthreads();
     const int n = (stop - j0) < kChunk ? static_cast<int>(stop - j0) : kChunk;
     for (int jj = 0; jj < n; ++jj) {
-      const A c = dsbuf[jj];
-      if (c == A(0)) continue;
+      A c[R];
+      bool any = false;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        c[r] = dsbuf[r * kChunk + jj];
+        any |= c[r] != A(0);
+      }
+      if (!any) continue;
       const T *krow = row_ptr<T>(k, b, hk, j0 + jj);
 #pragma unroll
       for (int t = 0; t < kMaxDimSlots; ++t) {
         const int d = lane + 64 * t;
-        if (d < p.Dqk) acc[t] += c * to_acc<A>(krow[d]);
+        if (d < p.Dqk) {
+          const A kd = to_acc<A>(krow[d]);
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (c[r] != A(0)) acc[r][t] += c[r] * kd;
+        }
       }
     }
     __syncthreads();
   }
-  if (!row_ok) return;
-  T *out = row_ptr_mut<T>(dq, b, hq, i);
 #pragma unroll
-  for (int t = 0; t < kMaxDimSlots; ++t) {
-    const int d = lane + 64 * t;
-    if (d < p.Dqk) out[d] = from_acc<T, A>(acc[t]);
+  for (int r = 0; r < R; ++r) {
+    const int i = i0 + r;
+    if (i >= p.Sq) continue;
+    T *out = row_ptr_mut<T>(dq, b, hq, i);
+#pragma unroll
+    for (int t = 0; t < kMaxDimSlots; ++t) {
+      const int d = lane + 64 * t;
+      if (d < p.Dqk) out[d] = from_acc<T, A>(acc[r][t]);
+    }
   }
 }
 
@@ -436,12 +530,23 @@ inline bool lds_ok(const void *kernel, size_t smem) {
                              static_cast<int>(smem)) == hipSuccess;
 }
 
+// Query rows per wave of the forward and dQ kernels: four, or one where the
+// runtime refuses their LDS (up to 139 KiB for fp64 at head dims of 512).
+constexpr int kRows = 4;
+
 template <typename T, typename A>
 hipError_t forward_impl(const Problem &p, View q, View k, View v, View o, void *lse,
                         hipStream_t st) {
-  dim3 grid((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
-  size_t smem = static_cast<size_t>(kWaves) * (p.Dqk + kChunk) * sizeof(A);
-  { Probe pr_("generic_fwd", st); generic_forward_kernel<T, A><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse)); }
+  const size_t smem4 = static_cast<size_t>(kWaves) * kRows * (p.Dqk + kChunk) * sizeof(A);
+  Probe pr_("generic_fwd", st);
+  if (lds_ok(reinterpret_cast<const void *>(&generic_forward_kernel<T, A, kRows>), smem4)) {
+    const dim3 grid((p.Sq + kWaves * kRows - 1) / (kWaves * kRows), p.Hq, p.B);
+    generic_forward_kernel<T, A, kRows><<<grid, dim3(256), smem4, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+  } else {
+    const dim3 grid((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
+    const size_t smem = static_cast<size_t>(kWaves) * (p.Dqk + kChunk) * sizeof(A);
+    generic_forward_kernel<T, A, 1><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+  }
   return hipGetLastError();
 }
 
@@ -453,8 +558,17 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
   const A *ls = static_cast<const A *>(lse);
   dim3 grid_q((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
   { Probe pr_("generic_bwd_delta", st); generic_delta_kernel<T, A><<<grid_q, dim3(256), 0, st>>>(p, o, dout, dl); }
-  size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
-  { Probe pr_("generic_bwd_dq", st); generic_dq_kernel<T, A><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq); }
+  {
+    const size_t smem4 = static_cast<size_t>(kWaves) * kRows * (p.Dqk + p.Dv + kChunk) * sizeof(A);
+    Probe pr_("generic_bwd_dq", st);
+    if (lds_ok(reinterpret_cast<const void *>(&generic_dq_kernel<T, A, kRows>), smem4)) {
+      const dim3 grid((p.Sq + kWaves * kRows - 1) / (kWaves * kRows), p.Hq, p.B);
+      generic_dq_kernel<T, A, kRows><<<grid, dim3(256), smem4, st>>>(p, q, k, v, dout, ls, dl, dq);
+    } else {
+      const size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
+      generic_dq_kernel<T, A, 1><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq);
+    }
+  }
   constexpr int nws = dkdv_waves<true>(), nwd = dkdv_waves<false>();
   const size_t smem_ks = static_cast<size_t>(nws) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A) +
                          staged_bytes<A>(p);
