@@ -74,17 +74,48 @@ __device__ __forceinline__ T *row_ptr_mut(View v, int b, int h, int s) {
   return const_cast<T *>(row_ptr<T>(v, b, h, s));
 }
 
+// Row stride, in elements of `esz` bytes, of a staged chunk of D-element rows:
+// a whole number of 16-byte units, and an odd one, so the 16-byte reads of
+// the 16 lanes an LDS pass serves fall in 16 different bank groups.
+__host__ __device__ inline int staged_ld(int D, int esz) {
+  const int vw = 16 / esz;
+  return (((D + vw - 1) / vw) | 1) * vw;
+}
+
+// Elements D rounded up to whole 16-byte units (keeps the next region aligned).
+__host__ __device__ inline int round16(int D, int esz) {
+  const int vw = 16 / esz;
+  return (D + vw - 1) / vw * vw;
+}
+
+// sum_d x[d] y[d] in order d = 0, 1, ... over 16-byte aligned LDS rows, read
+// 16 bytes at a time.
+template <typename A>
+__device__ __forceinline__ A dot_lds(const A *x, const A *y, int D) {
+  constexpr int VW = 16 / sizeof(A);
+  typedef A V __attribute__((ext_vector_type(VW)));
+  A acc = 0;
+  int d = 0;
+  for (; d + VW <= D; d += VW) {
+    const V a = *reinterpret_cast<const V *>(x + d), c = *reinterpret_cast<const V *>(y + d);
+#pragma unroll
+    for (int e = 0; e < VW; ++e) acc += a[e] * c[e];
+  }
+  for (; d < D; ++d) acc += x[d] * y[d];
+  return acc;
+}
+
 // Rows r0 .. r0 + 63 of operand x (batch b, head h), D elements each, into dst
-// as A with row stride D + 1; rows from n_rows on are zero.  Wave w of the
-// NW loads rows w, w + NW, ..., one coalesced row per step.  Every thread of
-// the workgroup calls it; the caller synchronises.
+// as A with row stride ld; rows from n_rows on are zero.  Wave w of the NW
+// loads rows w, w + NW, ..., one coalesced row per step.  Every thread of the
+// workgroup calls it; the caller synchronises.
 template <typename T, typename A, int NW>
 __device__ __forceinline__ void stage_chunk(A *dst, View x, int b, int h, int64_t r0, int n_rows,
-                                            int D) {
+                                            int D, int ld) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int r = w; r < kChunk; r += NW) {
     const int64_t row = r0 + r;
-    A *out = dst + r * (D + 1);
+    A *out = dst + r * ld;
     if (row < n_rows) {
       const T *src = row_ptr<T>(x, b, h, static_cast<int>(row));
       for (int d = lane; d < D; d += 64) out[d] = to_acc<A>(src[d]);
@@ -396,13 +427,17 @@ __global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
   const int j = blockIdx.x * NW + w;
   const int kv_end = kv_end_for(p, b);
   const bool key_ok = j < p.Sk;
-  A *krow = reinterpret_cast<A *>(smem_raw) + w * (p.Dqk + p.Dv + 2 * kChunk);
-  A *vrow = krow + p.Dqk;
-  A *pbuf = vrow + p.Dv;
+  // per wave: K row, V row (each from a 16-byte boundary), P and dS chunks
+  constexpr int esz = sizeof(A);
+  const int dq16 = round16(p.Dqk, esz), kreg = dq16 + round16(p.Dv, esz) + 2 * kChunk;
+  A *krow = reinterpret_cast<A *>(smem_raw) + w * kreg;
+  A *vrow = krow + dq16;
+  A *pbuf = vrow + round16(p.Dv, esz);
   A *dsbuf = pbuf + kChunk;
   // staged Q / dO chunk (ST)
-  A *qst = reinterpret_cast<A *>(smem_raw) + NW * (p.Dqk + p.Dv + 2 * kChunk);
-  A *gst = qst + kChunk * (p.Dqk + 1);
+  const int ldq = staged_ld(p.Dqk, esz), ldg = staged_ld(p.Dv, esz);
+  A *qst = reinterpret_cast<A *>(smem_raw) + NW * kreg;
+  A *gst = qst + kChunk * ldq;
   if (key_ok) {
     const T *kp = row_ptr<T>(k, b, hk, j);
     const T *vp = row_ptr<T>(v, b, hk, j);
@@ -428,16 +463,15 @@ __global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
     for (int64_t i0 = start; i0 < p.Sq; i0 += kChunk) {
       const int i = static_cast<int>(i0) + lane;
       if constexpr (ST) {
-        stage_chunk<T, A, NW>(qst, q, b, hq, i0, p.Sq, p.Dqk);
-        stage_chunk<T, A, NW>(gst, dout, b, hq, i0, p.Sq, p.Dv);
+        stage_chunk<T, A, NW>(qst, q, b, hq, i0, p.Sq, p.Dqk, ldq);
+        stage_chunk<T, A, NW>(gst, dout, b, hq, i0, p.Sq, p.Dv, ldg);
         __syncthreads();
       }
       A pij = 0, ds = 0;
       if (key_ok && j < kv_end && i < p.Sq) {
         A acc = 0;
         if constexpr (ST) {
-          const A *qr = qst + lane * (p.Dqk + 1);
-          for (int d = 0; d < p.Dqk; ++d) acc += qr[d] * krow[d];
+          acc = dot_lds(qst + lane * ldq, krow, p.Dqk);
         } else {
           // q row i is read straight from memory (lane-private row)
           const T *qp = row_ptr<T>(q, b, hq, i);
@@ -462,8 +496,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
           if (pij != A(0)) {
             A dp = 0;
             if constexpr (ST) {
-              const A *gr = gst + lane * (p.Dv + 1);
-              for (int d = 0; d < p.Dv; ++d) dp += gr[d] * vrow[d];
+              dp = dot_lds(gst + lane * ldg, vrow, p.Dv);
             } else {
               const T *gp = row_ptr<T>(dout, b, hq, i);
               for (int d = 0; d < p.Dv; ++d) dp += to_acc<A>(gp[d]) * vrow[d];
@@ -482,7 +515,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
         const A pv = pbuf[ii], dsv = dsbuf[ii];
         if (pv == A(0) && dsv == A(0)) continue;
         if constexpr (ST) {
-          const A *gr = gst + ii * (p.Dv + 1), *qr = qst + ii * (p.Dqk + 1);
+          const A *gr = gst + ii * ldg, *qr = qst + ii * ldq;
 #pragma unroll
           for (int t = 0; t < kMaxDimSlots; ++t) {
             const int d = lane + 64 * t;
@@ -514,10 +547,12 @@ __global__ __launch_bounds__(64 * dkdv_waves<ST>()) void generic_dkdv_kernel(
   }
 }
 
-// LDS of one staged 64-row chunk of each of two operands (row stride D + 1).
+// LDS of one staged 64-row chunk of each of two operands (row strides
+// staged_ld).
 template <typename A>
 size_t staged_bytes(const Problem &p) {
-  return static_cast<size_t>(kChunk) * (p.Dqk + 1 + p.Dv + 1) * sizeof(A);
+  return static_cast<size_t>(kChunk) *
+         (staged_ld(p.Dqk, sizeof(A)) + staged_ld(p.Dv, sizeof(A))) * sizeof(A);
 }
 
 // Whether `kernel` may take `smem` bytes of dynamic LDS: at most the 160 KiB a
@@ -570,7 +605,9 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
     }
   }
   constexpr int nws = dkdv_waves<true>(), nwd = dkdv_waves<false>();
-  const size_t smem_ks = static_cast<size_t>(nws) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A) +
+  const size_t smem_ks = static_cast<size_t>(nws) *
+                             (round16(p.Dqk, sizeof(A)) + round16(p.Dv, sizeof(A)) + 2 * kChunk) *
+                             sizeof(A) +
                          staged_bytes<A>(p);
   {
     Probe pr_("generic_bwd_dkdv", st);
@@ -579,7 +616,9 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
       generic_dkdv_kernel<T, A, true><<<grid_k, dim3(64 * nws), smem_ks, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
     } else {
       const dim3 grid_k((p.Sk + nwd - 1) / nwd, p.Hkv, p.B);
-      const size_t smem_k = static_cast<size_t>(nwd) * (p.Dqk + p.Dv + 2 * kChunk) * sizeof(A);
+      const size_t smem_k = static_cast<size_t>(nwd) *
+                            (round16(p.Dqk, sizeof(A)) + round16(p.Dv, sizeof(A)) + 2 * kChunk) *
+                            sizeof(A);
       generic_dkdv_kernel<T, A, false><<<grid_k, dim3(64 * nwd), smem_k, st>>>(p, q, k, v, dout, ls, dl, dk, dv);
     }
   }
