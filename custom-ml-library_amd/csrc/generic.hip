@@ -128,8 +128,9 @@ __device__ __forceinline__ void stage_chunk(A *dst, View x, int b, int h, int64_
 // Scores of query rows i0 .. i0 + R - 1 (held in qrows, row stride Dqk)
 // against key j, each with the reference's order: scale, then mask (bool ->
 // -inf, additive -> +), then causal (:102-113); rows from Sq on get -inf.
-// Each element of the key row is loaded once for the R rows.
-template <typename T, typename A, int R>
+// Each element of the key row is loaded once for the R rows; with VK (rows
+// 16-byte aligned) 16 bytes at a time, the sums in the same order.
+template <typename T, typename A, int R, bool VK>
 __device__ __forceinline__ void score_rows(const Problem &p, const A *qrows, const T *krow, int b,
                                            int hq, int i0, int j, int kv_end, A (&s)[R]) {
   if (j >= kv_end) {
@@ -140,7 +141,21 @@ __device__ __forceinline__ void score_rows(const Problem &p, const A *qrows, con
   A acc[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) acc[r] = 0;
-  for (int d = 0; d < p.Dqk; ++d) {
+  int d = 0;
+  if constexpr (VK) {
+    constexpr int VW = 16 / sizeof(T);
+    typedef T V __attribute__((ext_vector_type(VW)));
+    for (; d + VW <= p.Dqk; d += VW) {
+      const V kk = *reinterpret_cast<const V *>(krow + d);
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        const A kd = to_acc<A>(static_cast<T>(kk[e]));
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += qrows[r * p.Dqk + d + e] * kd;
+      }
+    }
+  }
+  for (; d < p.Dqk; ++d) {
     const A kd = to_acc<A>(krow[d]);
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] += qrows[r * p.Dqk + d] * kd;
@@ -171,7 +186,7 @@ __device__ __forceinline__ void score_rows(const Problem &p, const A *qrows, con
 // (blockIdx.x * 4 + w) R, lane l the key j0 + l of each 64-key chunk, so each
 // K and V element a lane loads serves R rows.
 // ---------------------------------------------------------------------------
-template <typename T, typename A, int R>
+template <typename T, typename A, int R, bool VK>
 __global__ __launch_bounds__(256) void generic_forward_kernel(Problem p, View q, View k, View v,
                                                               View o, A *lse) {
   extern __shared__ unsigned char smem_raw[];
@@ -212,7 +227,7 @@ __global__ __launch_bounds__(256) void generic_forward_kernel(Problem p, View q,
   for (int j0 = 0; j0 < stop; j0 += kChunk) {
     const int j = j0 + lane;
     A s[R];
-    score_rows<T, A, R>(p, qrows, row_ptr<T>(k, b, hk, j < p.Sk ? j : 0), b, hq, i0, j, kv_end, s);
+    score_rows<T, A, R, VK>(p, qrows, row_ptr<T>(k, b, hk, j < p.Sk ? j : 0), b, hq, i0, j, kv_end, s);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const A cmax = wave_max(s[r]);
@@ -293,7 +308,7 @@ __global__ __launch_bounds__(256) void generic_delta_kernel(Problem p, View o, V
 // Wave w owns the R query rows from (blockIdx.x * 4 + w) R, lane l the key
 // j0 + l of each chunk (each K and V element a lane loads serves R rows).
 // ---------------------------------------------------------------------------
-template <typename T, typename A, int R>
+template <typename T, typename A, int R, bool VK>
 __global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View k, View v,
                                                          View dout, const A *lse, const A *delta,
                                                          View dq) {
@@ -345,12 +360,26 @@ __global__ __launch_bounds__(256) void generic_dq_kernel(Problem p, View q, View
     for (int r = 0; r < R; ++r) ds[r] = 0;
     if (j < kv_end) {
       A s[R];
-      score_rows<T, A, R>(p, qrows, row_ptr<T>(k, b, hk, j), b, hq, i0, j, kv_end, s);
+      score_rows<T, A, R, VK>(p, qrows, row_ptr<T>(k, b, hk, j), b, hq, i0, j, kv_end, s);
       A dp[R];
 #pragma unroll
       for (int r = 0; r < R; ++r) dp[r] = 0;
       const T *vrow = row_ptr<T>(v, b, hk, j);
-      for (int d = 0; d < p.Dv; ++d) {
+      int d = 0;
+      if constexpr (VK) {
+        constexpr int VW = 16 / sizeof(T);
+        typedef T V __attribute__((ext_vector_type(VW)));
+        for (; d + VW <= p.Dv; d += VW) {
+          const V vv = *reinterpret_cast<const V *>(vrow + d);
+#pragma unroll
+          for (int e = 0; e < VW; ++e) {
+            const A vd = to_acc<A>(static_cast<T>(vv[e]));
+#pragma unroll
+            for (int r = 0; r < R; ++r) dp[r] += grows[r * p.Dv + d + e] * vd;
+          }
+        }
+      }
+      for (; d < p.Dv; ++d) {
         const A vd = to_acc<A>(vrow[d]);
 #pragma unroll
         for (int r = 0; r < R; ++r) dp[r] += grows[r * p.Dv + d] * vd;
@@ -569,18 +598,29 @@ inline bool lds_ok(const void *kernel, size_t smem) {
 // runtime refuses their LDS (up to 139 KiB for fp64 at head dims of 512).
 constexpr int kRows = 4;
 
+// Every row of the view starts on a 16-byte boundary (base and strides).
+template <typename T>
+bool rows16(const View &x) {
+  const auto al = [](int64_t n) { return (n * static_cast<int64_t>(sizeof(T))) % 16 == 0; };
+  return reinterpret_cast<uintptr_t>(x.data) % 16 == 0 && al(x.s0) && al(x.s1) && al(x.s2);
+}
+
 template <typename T, typename A>
 hipError_t forward_impl(const Problem &p, View q, View k, View v, View o, void *lse,
                         hipStream_t st) {
   const size_t smem4 = static_cast<size_t>(kWaves) * kRows * (p.Dqk + kChunk) * sizeof(A);
   Probe pr_("generic_fwd", st);
-  if (lds_ok(reinterpret_cast<const void *>(&generic_forward_kernel<T, A, kRows>), smem4)) {
+  if (lds_ok(reinterpret_cast<const void *>(&generic_forward_kernel<T, A, kRows, false>), smem4) &&
+      lds_ok(reinterpret_cast<const void *>(&generic_forward_kernel<T, A, kRows, true>), smem4)) {
     const dim3 grid((p.Sq + kWaves * kRows - 1) / (kWaves * kRows), p.Hq, p.B);
-    generic_forward_kernel<T, A, kRows><<<grid, dim3(256), smem4, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+    if (rows16<T>(k))
+      generic_forward_kernel<T, A, kRows, true><<<grid, dim3(256), smem4, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+    else
+      generic_forward_kernel<T, A, kRows, false><<<grid, dim3(256), smem4, st>>>(p, q, k, v, o, static_cast<A *>(lse));
   } else {
     const dim3 grid((p.Sq + kWaves - 1) / kWaves, p.Hq, p.B);
     const size_t smem = static_cast<size_t>(kWaves) * (p.Dqk + kChunk) * sizeof(A);
-    generic_forward_kernel<T, A, 1><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse));
+    generic_forward_kernel<T, A, 1, false><<<grid, dim3(256), smem, st>>>(p, q, k, v, o, static_cast<A *>(lse));
   }
   return hipGetLastError();
 }
@@ -596,12 +636,16 @@ hipError_t backward_impl(const Problem &p, View q, View k, View v, View o, View 
   {
     const size_t smem4 = static_cast<size_t>(kWaves) * kRows * (p.Dqk + p.Dv + kChunk) * sizeof(A);
     Probe pr_("generic_bwd_dq", st);
-    if (lds_ok(reinterpret_cast<const void *>(&generic_dq_kernel<T, A, kRows>), smem4)) {
+    if (lds_ok(reinterpret_cast<const void *>(&generic_dq_kernel<T, A, kRows, false>), smem4) &&
+        lds_ok(reinterpret_cast<const void *>(&generic_dq_kernel<T, A, kRows, true>), smem4)) {
       const dim3 grid((p.Sq + kWaves * kRows - 1) / (kWaves * kRows), p.Hq, p.B);
-      generic_dq_kernel<T, A, kRows><<<grid, dim3(256), smem4, st>>>(p, q, k, v, dout, ls, dl, dq);
+      if (rows16<T>(k) && rows16<T>(v))
+        generic_dq_kernel<T, A, kRows, true><<<grid, dim3(256), smem4, st>>>(p, q, k, v, dout, ls, dl, dq);
+      else
+        generic_dq_kernel<T, A, kRows, false><<<grid, dim3(256), smem4, st>>>(p, q, k, v, dout, ls, dl, dq);
     } else {
       const size_t smem_q = static_cast<size_t>(kWaves) * (p.Dqk + p.Dv + kChunk) * sizeof(A);
-      generic_dq_kernel<T, A, 1><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq);
+      generic_dq_kernel<T, A, 1, false><<<grid_q, dim3(256), smem_q, st>>>(p, q, k, v, dout, ls, dl, dq);
     }
   }
   constexpr int nws = dkdv_waves<true>(), nwd = dkdv_waves<false>();
