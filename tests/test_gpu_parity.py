@@ -168,6 +168,66 @@ def test_mfma_backward_both_dq_paths(case):
             check_half(abi.host(got), want, dtype, "g", f"{n} ({dq_probe})")
 
 
+GENERIC_LAYOUT_CASES = [
+    # (name, dtype, B, Hq, Hkv, Sq, Sk, Dqk, Dv, causal, offset, mask, misaligned view)
+    # K / V rows on 16-byte boundaries (16-byte row loads), GQA, a last wave
+    # whose four query rows run past Sq
+    ("f32-gqa-d36x20-rows77", "float32", 2, 4, 2, 77, 130, 36, 20, True, 0, None, False),
+    # rows not 16-byte aligned (element loads), an additive mask
+    ("f32-d33x17-floatmask", "float32", 1, 2, 2, 70, 90, 33, 17, False, 0, "float", False),
+    # views whose base is one element past a 16-byte boundary
+    ("f32-d64-misaligned-view", "float32", 1, 2, 2, 100, 100, 64, 64, True, 0, None, True),
+    # a Q / dO chunk too large for LDS (the unstaged dK/dV kernel), causal offset
+    ("f64-d256-unstaged-boolmask", "float64", 1, 1, 1, 80, 96, 256, 256, True, 16, "bool", False),
+]
+
+
+def _misaligned(t):
+    """The same values in a view whose rows start one element past the
+    allocation's 16-byte boundaries."""
+    pad = torch.zeros(*t.shape[:-1], t.shape[-1] + 1, dtype=t.dtype, device=t.device)
+    pad[..., 1:] = t
+    return pad[..., 1:]
+
+
+@pytest.mark.parametrize("case", GENERIC_LAYOUT_CASES, ids=lambda c: c[0])
+def test_generic_kernel_layouts_match_oracle(case):
+    """The generic kernels' load and staging variants (16-byte or element row
+    loads, four query rows per wave with a ragged last wave, the LDS-staged or
+    unstaged dK/dV kernel) against the oracle's streaming attention, at the
+    fp32 / fp64 bounds above."""
+    name, dtype, b, hq, hkv, sq, sk, dqk, dv, causal, off, mkind, mis = case
+    say(f"generic layout {name}")
+    inp = attention_inputs(b, hq, sq, dqk, dtype, heads_kv=hkv, seq_k=sk, dim_v=dv, seed=13)
+    rng = np.random.default_rng(3)
+    mask = None
+    if mkind == "bool":
+        mask = rng.random((sq, sk)) > 0.25
+    elif mkind == "float":
+        mask = (rng.standard_normal((sq, sk)) * 1.5).astype(np.float32)
+    ref = A.sdpa(inp.q, inp.k, inp.v, mask, causal, dtype=dtype, causal_offset=off,
+                 backend="streaming", enable_gqa=hkv != hq)
+    rdq, rdk, rdv = ref.backward(inp.do)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    if mis:
+        q, k, v, g = (_misaligned(t) for t in (q, k, v, g))
+    m = None if mask is None else torch.from_numpy(mask).cuda()
+    args = dict(causal=causal, offset=off, mask=m)
+    out, lse, path = abi.forward(q, k, v, **args)
+    assert path == _lib.PATH_GENERIC
+    dq, dk, dv_, _ = abi.backward(q, k, v, out, g, lse, **args)
+    torch.cuda.synchronize()
+    tol = dict(rtol=1e-10, atol=1e-12) if dtype == "float64" else dict(rtol=1e-4, atol=3e-5)
+    np.testing.assert_allclose(abi.host(out), ref.out_cast, **tol, err_msg=f"{name} out")
+    want_lse = ref.lse[..., 0]
+    got_lse = abi.host(lse)
+    np.testing.assert_array_equal(np.isneginf(got_lse), np.isneginf(want_lse))
+    live = np.isfinite(want_lse)
+    np.testing.assert_allclose(got_lse[live], want_lse[live], **tol, err_msg=f"{name} lse")
+    for got, want, key in ((dq, rdq, "dq"), (dk, rdk, "dk"), (dv_, rdv, "dv")):
+        np.testing.assert_allclose(abi.host(got), want, **tol, err_msg=f"{name} {key}")
+
+
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 def test_mfma_agrees_with_generic_on_same_inputs(dtype):
     inp = attention_inputs(2, 2, 190, 128, dtype, value_scale=0.5, seed=5)
