@@ -124,14 +124,21 @@ def bench_fwd_bwd(ts, torch, steps, warmup):
         raise RuntimeError("the MFMA kernels did not run for the headline workload")
     _lib.profile_reset()
     _lib.profile_enable(True)
+    # per-step GPU times from events between the steps (the reference's
+    # timing contract reports the median and p95 of the repeats,
+    # benchmarks/common.py:24-64); `value` stays whole-run wall time / steps
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    marks[0].record()
+    for i in range(steps):
         step()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     _lib.profile_enable(False)
     kernels = _lib.profile_read()
+    step_ms = sorted(marks[i].elapsed_time(marks[i + 1]) for i in range(steps))
     fwd = causal_fwd_flops(B, H, S, D)
     flops = fwd * 3.5
     ms = elapsed / steps * 1e3
@@ -149,6 +156,10 @@ def bench_fwd_bwd(ts, torch, steps, warmup):
             per_kernel[n]["tflops"] = round(w / (per_kernel[n]["mean_ms"] * 1e-3) / 1e12, 1)
     result = {
         "ms_per_step": ms,
+        "step_ms": {"mean": round(statistics.fmean(step_ms), 4),
+                    "median": round(statistics.median(step_ms), 4),
+                    "p95": round(step_ms[min(steps - 1, math.ceil(0.95 * steps) - 1)], 4),
+                    "min": round(step_ms[0], 4), "max": round(step_ms[-1], 4)},
         "value": flops / (ms * 1e-3) / 1e12,
         "kernels": {n: {k_: (round(v_, 4) if isinstance(v_, float) else v_) for k_, v_ in d.items()}
                     for n, d in per_kernel.items()},
@@ -751,6 +762,7 @@ def main():
     print(f"[bench] fwd+bwd {main_res['ms_per_step']:.3f} ms/step", file=sys.stderr, flush=True)
     if args.workload == "fwd_bwd":
         print(json.dumps({"value": main_res["value"], "ms_per_step": main_res["ms_per_step"],
+                          "step_ms": main_res["step_ms"],
                           "roofline": main_res["roofline"], "kernels": main_res["kernels"]}),
               flush=True)
         return
@@ -789,6 +801,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(main_res["ms_per_step"], 4),
+        "step_ms": main_res["step_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

@@ -163,6 +163,45 @@ def test_dropout_attention_matches_oracle(case):
     assert not torch.equal(out, out3)
 
 
+@pytest.mark.parametrize("case", [CASES[0], CASES[2]], ids=lambda c: "-".join(map(str, c)))
+def test_dropout_recomputing_dq_matches_oracle(case):
+    """Workspaces without room for stored dS run the dropout dQ kernel that
+    recomputes S and dP (reading the keep bits with each key tile): the row
+    values alone when the forward's bits are passed, the row values plus the
+    drawn bits otherwise.  Both match the oracle and give the same gradients."""
+    dtype, b, hq, hkv, sq, sk, d, causal, off, p, masked = case
+    say(f"dropout, recomputing dQ {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=37)
+    key, counter = 0x0DD5_EED0_0000_0000_0000_0000_4242_4242, 5
+    mask = np.random.default_rng(2).random((sq, sk)) > 0.25 if masked else None
+    _, _, back = DR.sdpa_dropout(inp.q, inp.k, inp.v, mask, causal, dtype=dtype, p=p,
+                                 rng_key=key, rng_counter=counter, causal_offset=off,
+                                 enable_gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    kw = dict(causal=causal, offset=off, dropout=(p, key, counter),
+              mask=None if mask is None else torch.from_numpy(mask).cuda())
+    bits = abi.dropout_bits_buffer(q, k, v, **kw)
+    out, lse, _ = abi.forward(q, k, v, dropout_bits=bits, **kw)
+    rows_bytes = 2 * b * hq * sq * 4
+    with_bits = -(-rows_bytes // 256) * 256 + bits.numel() * 4
+    results = []
+    for ws, given in ((rows_bytes, bits), (with_bits, None)):
+        _lib.profile_enable(True)
+        _lib.profile_reset()
+        grads = abi.backward(q, k, v, out, g, lse, ws_bytes=ws, dropout_bits=given, **kw)[:3]
+        torch.cuda.synchronize()
+        probes = _lib.profile_read()
+        _lib.profile_enable(False)
+        assert {"bwd_dq_mfma_dropout", "bwd_dkdv_mfma_dropout"} <= set(probes), sorted(probes)
+        assert "bwd_dq_ds_dropout" not in probes, sorted(probes)
+        assert ("dropout_bits" in probes) == (given is None), sorted(probes)
+        results.append(grads)
+        for got, want, name in zip(grads, back(inp.do), ("dQ", "dK", "dV")):
+            check(abi.host(got), want, dtype, "g", name)
+    for a_, b_ in zip(*results):
+        assert torch.equal(a_, b_)
+
+
 @pytest.mark.parametrize("p", [0.99999, 0.999995])
 def test_dropout_probability_near_one(p):
     """The top of the 16-bit threshold range on the MFMA forward: p = 0.99999

@@ -343,6 +343,41 @@ def test_mfma_general_masks(case):
         assert (abi.host(dq)[:, :, row] == 0).all()
 
 
+@pytest.mark.parametrize("case", MASK_CASES, ids=lambda c: c[0])
+def test_mfma_general_masks_recomputing_dq(case):
+    """A workspace of the row values alone (no room for stored dS) runs the
+    masked dQ kernel that recomputes S and dP per key tile, then dK/dV: the
+    only backward for a caller that passes a rows-only workspace."""
+    _, dtype, b, hq, hkv, sq, sk, d, causal, off, mshape, mdtype = case
+    say(f"mfma general mask, recomputing dQ {case}")
+    inp = attention_inputs(b, hq, sq, d, dtype, heads_kv=hkv, seq_k=sk, value_scale=0.5, seed=23)
+    rng = np.random.default_rng(sq + 2 * sk)
+    mask = _mask(rng, mshape, mdtype, sq)
+    ref = _oracle(inp, dtype, causal, off, mask=mask, gqa=hkv != hq)
+    q, k, v, g = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v, inp.do))
+    tm = (torch.from_numpy(mask).cuda() if mdtype == "bool"
+          else abi.dev_tensor(mask, mdtype))
+    out, lse, _ = abi.forward(q, k, v, causal=causal, offset=off, mask=tm)
+    rows_bytes = 2 * b * hq * sq * 4
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    dq, dk, dv, bpath = abi.backward(q, k, v, out, g, lse, ws_bytes=rows_bytes, causal=causal,
+                                     offset=off, mask=tm)
+    torch.cuda.synchronize()
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert bpath == _lib.PATH_MFMA
+    assert {"bwd_dq_mfma_masked", "bwd_dkdv_mfma_masked"} <= set(probes), sorted(probes)
+    assert "bwd_dq_ds_masked" not in probes and "bwd_rows" not in probes, sorted(probes)
+    rdq, rdk, rdv = ref.backward_compute(inp.do)
+    check_half(abi.host(dq), rdq, dtype, "g", "dQ")
+    check_half(abi.host(dk), rdk, dtype, "g", "dK")
+    check_half(abi.host(dv), rdv, dtype, "g", "dV")
+    if mshape[-2] == sq:
+        row = 5 if mdtype == "bool" else 7
+        assert (abi.host(dq)[:, :, row] == 0).all()
+
+
 def test_mfma_key_mask_without_lengths_reads_the_mask():
     """A [B,1,1,K] boolean mask passed without kv_len runs the general-mask
     kernels and agrees with the length-reduced path."""

@@ -93,8 +93,9 @@ def test_struct_layout_matches_header(tmp_path):
 def test_reference_binding_matches_header_and_integration_doc(tmp_path):
     """The ctypes binding a tensorsmith maintainer adds
     (tensorsmith_binding/_tsattn.py) declares the same structs as the header,
-    loads the library at ABI 7, and INTEGRATION.md quotes its struct
-    declarations verbatim (no stale copy of the layout in the guide)."""
+    loads the library at the current ABI, and INTEGRATION.md quotes its struct
+    declarations verbatim and names no other ABI version (no stale copy of
+    the layout or version in the guide)."""
     from tensorsmith_binding import _tsattn as B
 
     _check_ctypes_layout(_header_layout(tmp_path), {"tsattn_view": B.View,
@@ -109,6 +110,10 @@ def test_reference_binding_matches_header_and_integration_doc(tmp_path):
     for b in quoted:
         assert b.strip() in src, "INTEGRATION.md quotes a struct the binding does not declare"
     assert "dropout_bits" in quoted[0]
+    # every ABI version the guide's prose names is the library's
+    named = {int(v) for v in re.findall(r"ABI (\d+)", doc)}
+    named |= {int(v) for v in re.findall(r"tsattn_abi_version\(\) == (\d+)", doc)}
+    assert named == {_lib.ABI_VERSION}, f"INTEGRATION.md names ABI versions {sorted(named)}"
 
 
 def _problem(**kw):
