@@ -61,6 +61,7 @@ PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 (MFMA)
 B, H, S, D = 16, 16, 2048, 128
 DEC_B, DEC_H, DEC_D, DEC_CAP, DEC_LO, DEC_HI = 64, 32, 128, 8192, 512, 8192
 PF_B, PF_H, PF_S, PF_D, PF_LO = 2, 32, 32768, 128, 16384
+LONG_B, LONG_H, LONG_S = 16, 16, 8192
 LM_LAYERS, LM_DIM, LM_HEADS, LM_FFN, LM_VOCAB, LM_B, LM_S = 6, 512, 8, 2048, 32000, 8, 1024
 ATTN_KERNELS = ("fwd_mfma", "bwd_dkdv_mfma", "bwd_dq_ds", "bwd_dq_mfma", "bwd_rows", "generic_fwd",
                 "generic_bwd_delta", "generic_bwd_dq", "generic_bwd_dkdv", "key_mask_lengths",
@@ -82,7 +83,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload",
                     choices=["all", "fwd_bwd", "variants", "decode", "decode_int8", "prefill", "lm",
-                             "cached_step", "fp32", "copy"],
+                             "cached_step", "fp32", "long", "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -432,6 +433,53 @@ def bench_prefill(ts, torch, steps, warmup):
     }
 
 
+def bench_long(ts, torch, steps, warmup):
+    """Causal fwd+bwd at B16 H16 S8192 D128 bf16 through the public API: the
+    stored dS of all heads (17.4 GB) exceeds the backward's 8 GiB region, so
+    dK/dV and dQ-from-dS run over chunks of heads reusing one region (the
+    launch counts of their probes give the chunks)."""
+    from tensorsmith_hip import _lib
+
+    b, h, s, d = LONG_B, LONG_H, LONG_S, D
+    gen = torch.Generator(device="cuda").manual_seed(42)
+
+    def draw(scale):
+        return (torch.randn((b, h, s, d), generator=gen, device="cuda") * scale).to(torch.bfloat16)
+
+    q, k, v = (ts.Tensor(draw(0.5), device="hip", requires_grad=True) for _ in range(3))
+    upstream = ts.Tensor(draw(1.0), device="hip")
+
+    def step():
+        for t in (q, k, v):
+            t.zero_grad()
+        ts.nn.scaled_dot_product_attention(q, k, v, is_causal=True).backward(upstream)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    _lib.profile_reset()
+    _lib.profile_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    _lib.profile_enable(False)
+    kernels = _lib.profile_read()
+    flops = causal_fwd_flops(b, h, s, d) * 3.5
+    ms = elapsed / steps * 1e3
+    return {
+        "ms_per_step": round(ms, 3),
+        "value": round(flops / (ms * 1e-3) / 1e12, 1),
+        "unit": "TFLOP/s",
+        "frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "ds_chunks": kernels.get("bwd_dq_ds", (0, 0.0))[0] // max(steps, 1),
+        "kernels": {n: {"launches": c, "mean_ms": round(t / max(c, 1), 4)} for n, (c, t) in kernels.items()},
+        "config": {"workload": "causal_fwd_bwd_bf16_b16h16s8192d128", "batch": b, "heads": h,
+                   "seq_len": s, "head_dim": d, "flop_per_step": flops},
+    }
+
+
 def bench_cached_step(ts, torch, steps, warmup):
     """One cached MultiHeadAttention decode step (E 4096, 32 query heads, 8 KV
     heads of 128, fp16, batch 64, 1024 cached positions): the q/k/v
@@ -753,6 +801,9 @@ def main():
     if args.workload == "cached_step":
         print(json.dumps({"cached_step": bench_cached_step(ts, torch, 50, 5)}), flush=True)
         return
+    if args.workload == "long":
+        print(json.dumps({"long_fwd_bwd": bench_long(ts, torch, 3, 1)}), flush=True)
+        return
     if args.workload == "fp32":
         print(json.dumps({"fp32": bench_fp32(ts, torch, 5, 2)}), flush=True)
         return
@@ -780,6 +831,9 @@ def main():
           flush=True)
     pf_res = bench_prefill(ts, torch, 3, 1)
     print(f"[bench] prefill {pf_res['ms_per_step']:.2f} ms/step", file=sys.stderr, flush=True)
+    long_res = bench_long(ts, torch, 3, 1)
+    print(f"[bench] fwd+bwd S8192 {long_res['ms_per_step']:.2f} ms/step ({long_res['ds_chunks']} dS chunks)",
+          file=sys.stderr, flush=True)
     lm_res = bench_lm(ts, torch, 5, 2)
     print(f"[bench] lm step {lm_res['ms_per_step']:.2f} ms", file=sys.stderr, flush=True)
     cs_res = bench_cached_step(ts, torch, 50, 5)
@@ -821,6 +875,7 @@ def main():
         "decode": dec_res,
         "decode_int8": q8_res,
         "prefill": pf_res,
+        "long_fwd_bwd": long_res,
         "lm_step": lm_res,
         "cached_step": cs_res,
         "fp32": f32_res,

@@ -69,6 +69,11 @@ struct BwdArgs {
   char *ds;
   int ds_nkt, ds_tri;
   int64_t ds_slice;
+  // The KV-head groups (b, kv head), g = b Hkv + hk, this launch covers:
+  // [g0, g0 + ng).  With stored dS the backward runs in chunks of groups
+  // when the dS of all of them exceeds the region's cap: the region holds
+  // the slices of one chunk's query heads (slice index (g - g0) rep + r).
+  int g0, ng;
 };
 
 // Start of query tile qt's dS row within its slice, in tiles.
@@ -178,10 +183,11 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_kb = (p.Sk + KB - 1) / KB;
-  const int total = n_kb * p.Hkv * p.B;
+  const int total = n_kb * a.ng;
   const int logical = xcd_remap(blockIdx.x, total);
-  int bh, kb;  // early key blocks see the most queries: run them first
-  heavy_first(logical, n_kb, p.Hkv * p.B, 32 * dkdv_wg_per_cu<DK, DV, MK, DR>(), bh, kb);  // slots per XCD
+  int bhc, kb;  // early key blocks see the most queries: run them first
+  heavy_first(logical, n_kb, a.ng, 32 * dkdv_wg_per_cu<DK, DV, MK, DR>(), bhc, kb);  // slots per XCD
+  const int bh = a.g0 + bhc;  // group (b, kv head); bhc: its index within the chunk
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
   const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
@@ -377,7 +383,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   const TileIdx first{0, 0, 0, reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep)),
                       reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep)),
                       reinterpret_cast<uint64_t>(rowv),
-                      (static_cast<uint64_t>(b) * p.Hq + hk * p.rep) * dwrap};
+                      static_cast<uint64_t>(bhc) * p.rep * dwrap};
   TileIdx nxt_idx = first;
   for (int t = 0; t < KV_PD; ++t) {
     issue(nxt_idx);
@@ -1215,11 +1221,13 @@ __global__ __launch_bounds__(DQ_NT, 1) void dq_ds_kernel(BwdArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n_qb = (p.Sq + QB2 - 1) / QB2;
-  const int total = n_qb * p.Hq * p.B;
+  const int n_bh = a.ng * p.rep;  // query heads of the chunk's groups
+  const int total = n_qb * n_bh;
   const int logical = xcd_remap(blockIdx.x, total);
-  int bh, rank;
-  heavy_first(logical, n_qb, p.Hq * p.B, 32, bh, rank);  // 1 WG per CU
+  int bhc, rank;
+  heavy_first(logical, n_qb, n_bh, 32, bhc, rank);  // 1 WG per CU
   const int qb = n_qb - 1 - rank;  // long causal rows first
+  const int bh = a.g0 * p.rep + bhc;  // (b, q head); bhc: its dS slice in the region
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
   // Wave w takes the block's 32-row subtiles w and 15 - w, so that the
   // causal work of the four waves is alike (the subtiles share every K^T
@@ -1241,8 +1249,7 @@ __global__ __launch_bounds__(DQ_NT, 1) void dq_ds_kernel(BwdArgs a) {
   const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
   // dS of this (b, q head); the wave's subtiles are query tiles qa / 32, qz / 32
   const int64_t slice = a.ds_slice * DS_TILE;
-  const u32x4 sdesc = make_desc(a.ds + (static_cast<int64_t>(b) * p.Hq + hq) * slice,
-                                static_cast<uint32_t>(slice));
+  const u32x4 sdesc = make_desc(a.ds + static_cast<int64_t>(bhc) * slice, static_cast<uint32_t>(slice));
   // (rows past Sq: past the slice, or masked off below)
   const uint32_t dsa = static_cast<uint32_t>(ds_row_start(a.ds_tri, a.ds_nkt, qa / 32) * DS_TILE);
   const uint32_t dsz = static_cast<uint32_t>(ds_row_start(a.ds_tri, a.ds_nkt, qz / 32) * DS_TILE);
@@ -1417,10 +1424,13 @@ __global__ __launch_bounds__(DQ_NT, 1) void dq_ds_kernel(BwdArgs a) {
 // (1..3), or boolean / 16-bit row-piece masks staged through its LDS ring
 // (4, 6); f32 row-piece masks (5) read element by element there.
 template <typename T, int DK, int DV, int MKQ, int MK, bool DR>
-void launch_mk(const BwdArgs &a, hipStream_t st) {
-  const Problem &p = a.p;
+void launch_mk(const BwdArgs &a0, hipStream_t st) {
+  const Problem &p = a0.p;
+  BwdArgs a = a0;
   if (a.ds) {
-    // Stored dS: row values, then dK/dV (storing dS), then dQ as one GEMM.
+    // Stored dS: row values, then per chunk of KV-head groups (one chunk
+    // unless the dS of every group exceeds the region's cap) dK/dV storing
+    // the chunk's dS, then its dQ as one GEMM.
     {
       Probe pr_("bwd_rows", st);
       const int per_block = (NT / 64) * (64 / (DV / 8)) * ROWS_U;
@@ -1428,15 +1438,18 @@ void launch_mk(const BwdArgs &a, hipStream_t st) {
       bwd_rows_kernel<T, DK, DV><<<dim3(static_cast<unsigned>(static_cast<int64_t>(nqb) * p.B * p.Hq)),
                                   dim3(NT), 0, st>>>(a, nqb);
     }
-    const int n_kb = (p.Sk + KB - 1) / KB;
-    {
-      Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
-      dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
-    }
-    const int n_qb = (p.Sq + QB2 - 1) / QB2;
-    {
-      Probe pr_(DR ? "bwd_dq_ds_dropout" : (MK ? "bwd_dq_ds_masked" : "bwd_dq_ds"), st);
-      dq_ds_kernel<T, DK><<<dim3(n_qb * p.Hq * p.B), dim3(DQ_NT), 0, st>>>(a);
+    const int groups = p.B * p.Hkv, per_chunk = mfma_ds_chunk_groups(p);
+    const int n_kb = (p.Sk + KB - 1) / KB, n_qb = (p.Sq + QB2 - 1) / QB2;
+    for (a.g0 = 0; a.g0 < groups; a.g0 += per_chunk) {
+      a.ng = min(per_chunk, groups - a.g0);
+      {
+        Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
+        dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * a.ng), dim3(NT), 0, st>>>(a);
+      }
+      {
+        Probe pr_(DR ? "bwd_dq_ds_dropout" : (MK ? "bwd_dq_ds_masked" : "bwd_dq_ds"), st);
+        dq_ds_kernel<T, DK><<<dim3(n_qb * a.ng * p.rep), dim3(DQ_NT), 0, st>>>(a);
+      }
     }
     return;
   }
@@ -1449,7 +1462,7 @@ void launch_mk(const BwdArgs &a, hipStream_t st) {
   const int n_kb = (p.Sk + KB - 1) / KB;
   {
     Probe pr_(DR ? "bwd_dkdv_mfma_dropout" : (MK ? "bwd_dkdv_mfma_masked" : "bwd_dkdv_mfma"), st);
-    dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+    dkdv_kernel<T, DK, DV, MK, DR><<<dim3(n_kb * a.ng), dim3(NT), 0, st>>>(a);
   }
 }
 
@@ -1500,13 +1513,37 @@ static int64_t ds_slice_tiles(const Problem &p) {
   return ds_row_start(ds_packed(p), ds_key_tiles(p), (p.Sq + 31) / 32);
 }
 
-size_t mfma_ds_bytes(const Problem &p) {
-  // Stored dS stays within 8 GiB, and each (b, q head) slice within 2^31
-  // bytes (32-bit buffer offsets, bit 31 marking a zero read).
+// The stored-dS region holds at most 8 GiB, and each (b, q head) slice stays
+// within 2^31 bytes (32-bit buffer offsets, bit 31 marking a zero read).
+// When the dS of every KV-head group (its rep query heads) does not fit, the
+// backward runs over chunks of groups that reuse one region: as few chunks
+// as fit the cap, of (nearly) equal size.  0: no stored dS (a slice alone is
+// too large).
+static int ds_chunk_groups(const Problem &p, int64_t *bytes) {
   constexpr int64_t kCap = int64_t(8) << 30;
   const int64_t slice = ds_slice_tiles(p) * DS_TILE;
-  const int64_t total = slice * p.B * p.Hq;
-  return slice <= (int64_t(1) << 31) && total <= kCap ? static_cast<size_t>(total) : 0;
+  const int64_t per_group = slice * p.rep;
+  const int groups = p.B * p.Hkv;
+  if (slice > (int64_t(1) << 31) || per_group > kCap || groups <= 0) {
+    *bytes = 0;
+    return 0;
+  }
+  const int64_t max_groups = kCap / per_group;
+  const int64_t chunks = (groups + max_groups - 1) / max_groups;
+  const int per_chunk = static_cast<int>((groups + chunks - 1) / chunks);
+  *bytes = per_chunk * per_group;
+  return per_chunk;
+}
+
+int mfma_ds_chunk_groups(const Problem &p) {
+  int64_t bytes;
+  return ds_chunk_groups(p, &bytes);
+}
+
+size_t mfma_ds_bytes(const Problem &p) {
+  int64_t bytes;
+  ds_chunk_groups(p, &bytes);
+  return static_cast<size_t>(bytes);
 }
 
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
@@ -1522,7 +1559,8 @@ hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, Vie
   }
   BwdArgs a{p, q, k, v, o, dout, dq, dk, dv, qk, lse, delta,
             static_cast<float>(p.scale) * kLog2e, static_cast<float>(p.scale),
-            static_cast<char *>(ds), ds_key_tiles(p), ds_packed(p), ds_slice_tiles(p)};
+            static_cast<char *>(ds), ds_key_tiles(p), ds_packed(p), ds_slice_tiles(p),
+            0, p.B * p.Hkv};
   return dtype == TSATTN_BF16 ? launch<bf16>(a, st) : launch<f16>(a, st);
 }
 

@@ -179,9 +179,12 @@ hipError_t launch_mfma_forward(const Problem &p, int dtype, View q, View k, View
 hipError_t launch_mfma_backward(const Problem &p, int dtype, View q, View k, View v, View o,
                                 View dout, const float *lse, View dq, View dk, View dv,
                                 float *delta, void *ds, hipStream_t st);
-// Bytes of stored dS (bf16 / f16 32 x 32 tiles of every (b, q head)), or 0
-// when they would exceed the cap the backward keeps on its workspace.
+// Bytes of the stored-dS region (bf16 / f16 32 x 32 tiles of the (b, q
+// head) slices of one chunk of KV-head groups; every group when they fit the
+// cap the backward keeps on its workspace), or 0 when one slice is too large.
 size_t mfma_ds_bytes(const Problem &p);
+// KV-head groups (b, kv head) per chunk of the stored-dS backward.
+int mfma_ds_chunk_groups(const Problem &p);
 // With RoPE folded in (p.rope.R > 0) the backward workspace also holds the
 // rotated query rows [B, Hq, Sq, Dqk] (16-bit) from this byte offset on.
 size_t mfma_rope_stage_offset(const Problem &p);

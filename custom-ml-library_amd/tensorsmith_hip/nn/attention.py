@@ -55,6 +55,26 @@ def _view(t) -> _lib.View:
     return v
 
 
+def _round256(n: int) -> int:
+    return (n + 255) // 256 * 256
+
+
+def _rows_workspace(prob, fused: bool, dtype) -> int:
+    """Smallest backward workspace the C ABI accepts (tsattn.h: the row
+    values, then the rotated query rows with RoPE folded in, then the keep
+    bits when dropping without the forward's): the kernels then recompute S
+    and dP for dQ instead of storing dS."""
+    import torch
+
+    rows = prob.batch * prob.heads_q * prob.len_q
+    nbytes = 2 * rows * (8 if dtype == torch.float64 else 4)
+    if fused:
+        nbytes = _round256(nbytes) + rows * prob.dim_qk * 2
+    if prob.dropout_p > 0 and not prob.dropout_bits:
+        nbytes = _round256(nbytes) + _lib.load().tsattn_dropout_bits_bytes(ctypes.byref(prob))
+    return nbytes
+
+
 def _aligned16(t) -> bool:
     return t.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in t.stride()[:3])
 
@@ -300,7 +320,14 @@ def scaled_dot_product_attention(
         dv = torch.empty(v.shape, dtype=v.dtype, device=tdev)
         nbytes = (lib.tsattn_sdpa_backward_rope_workspace if fused
                   else lib.tsattn_sdpa_backward_workspace)(ctypes.byref(prob))
-        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
+        try:
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
+        except torch.OutOfMemoryError:
+            # no room for the stored-dS region: the row values alone (plus
+            # the rotated queries / drawn dropout bits the backward needs),
+            # with which the kernels recompute S and dP for dQ instead
+            nbytes = _rows_workspace(prob, fused, q.dtype)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=tdev)
         args = (vq, vk, vv, vo, _view(g), ctypes.c_void_p(lse.data_ptr()), _view(dq), _view(dk),
                 _view(dv), ctypes.c_void_p(ws.data_ptr()), nbytes,
                 ctypes.c_void_p(current_stream(query.device)))

@@ -7,8 +7,10 @@ max-abs 2e-2 * max|ref|; fp16: 2e-3 / 5e-3, 5e-3 * max|ref|; LSE max-abs
 schedule slot, so a head-dependent indexing mistake cannot hide behind a
 sample.  The causal bf16 fwd+bwd at B16 H16 S2048 D128 checks O, LSE, dQ, dK
 and dV of all 256 heads; the fp16 decode at B64 H32 all 2048 heads; the 32k
-key-padded prefill all 64 heads at the first and last query tiles and the
-rows around each sequence's valid length (L - 1 and L among them).
+key-padded prefill all 64 heads at every 16th 64-row query block, the blocks
+around each sequence's valid length (L - 1 and L among them) and the last
+block; the causal fwd+bwd at S8192 (stored dS in chunks) sampled heads from
+every chunk.
 """
 
 from __future__ import annotations
@@ -130,12 +132,63 @@ def test_padded_prefill_bf16_b2h32s32768d128():
     assert torch.isfinite(out._data).all()
     lens = lengths.cpu().numpy()
     kmh = keymask.cpu().numpy()
+    # Every head at every 16th 64-row block across the whole sequence (each
+    # (head, query block) runs in a schedule slot of its own), plus the blocks
+    # around the valid length L and the last block.  Rows r0 .. r0 + 63 see
+    # keys below min(r0 + 64, L) only, so the oracle takes that prefix.
     for b in range(B):  # all 32 heads of each sequence at once
         L = int(lens[b])
         kh, vh = host(k[b:b + 1]), host(v[b:b + 1])
         r_mid = min(max(L - 32, 0), S - 64)
-        for r0 in (0, r_mid, S - 64):  # first tile, rows L-32 .. L+31, last tile
-            ref = A.sdpa(host(q[b:b + 1, :, r0:r0 + 64]), kh, vh, kmh[b][None, None, None],
-                         True, dtype="bfloat16", causal_offset=r0, backend="streaming")
+        starts = sorted(set(range(0, S, 16 * 64)) | {r_mid, (L // 64) * 64 if L < S else S - 64,
+                                                     S - 64})
+        for r0 in starts:
+            kend = min(r0 + 64, S)
+            ref = A.sdpa(host(q[b:b + 1, :, r0:r0 + 64]), kh[:, :, :kend], vh[:, :, :kend],
+                         kmh[b][None, None, None, :kend], True, dtype="bfloat16",
+                         causal_offset=r0, backend="dense")
             check_heads(host(out._data[b:b + 1, :, r0:r0 + 64]), ref.out, "bfloat16", "o",
                         f"prefill b{b} rows {r0}..{r0 + 63} (len {L})")
+
+
+def test_long_causal_fwd_bwd_bf16_b16h16s8192d128_chunked_stored_ds():
+    """B16 H16 S8192 D128 causal bf16: the stored dS of all 256 heads (17.4 GB)
+    exceeds the backward's 8 GiB region, so the stored-dS pipeline runs over
+    chunks of heads that reuse one region -- dK/dV (storing the chunk's dS),
+    then dQ = dS K, per chunk -- instead of the kernels that recompute S and
+    dP for dQ.  Heads from every chunk (the first and the last of the problem
+    among them) against the oracle at the bf16 bounds."""
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    shape = (16, 16, 8192, 128)
+    q, k, v = (draw(gen, shape, 0.5, torch.bfloat16) for _ in range(3))
+    g = draw(gen, shape, 1.0, torch.bfloat16)
+    say("full-size bf16 causal fwd+bwd at S8192 (chunked stored dS)")
+    out, lse, path = abi.forward(q, k, v, causal=True)
+    assert path == _lib.PATH_MFMA
+    _lib.profile_enable(True)
+    _lib.profile_reset()
+    dq, dk, dv, bpath = abi.backward(q, k, v, out, g, lse, causal=True)
+    torch.cuda.synchronize()
+    probes = _lib.profile_read()
+    _lib.profile_enable(False)
+    assert bpath == _lib.PATH_MFMA
+    assert "bwd_dq_mfma" not in probes, sorted(probes)
+    chunks = probes["bwd_dq_ds"][0]
+    assert chunks >= 3 and probes["bwd_dkdv_mfma"][0] == chunks, probes
+    say(f"  {chunks} chunks of stored dS")
+    for t in (out, lse, dq, dk, dv):
+        assert torch.isfinite(t).all()
+    # 256 heads in `chunks` chunks of consecutive (b, head) groups: sample the
+    # first and last head of each chunk and one in its middle
+    per = -(-256 // chunks)
+    heads = sorted({x for c0 in range(0, 256, per) for x in (c0, min(c0 + per, 256) - 1, c0 + per // 2)
+                    if x < 256})
+    for bh in heads:
+        b, h = divmod(bh, 16)
+        sl = (slice(b, b + 1), slice(h, h + 1))
+        ref = A.sdpa(host(q[sl]), host(k[sl]), host(v[sl]), None, True, dtype="bfloat16",
+                     backend="streaming", block_size=1024)
+        check_heads(host(out[sl]), ref.out, "bfloat16", "o", f"O b{b} h{h}")
+        check_lse_heads(host(lse[sl]), ref.lse[..., 0], f"LSE b{b} h{h}")
+        for got, want, n in zip((dq, dk, dv), ref.backward_compute(host(g[sl])), ("dQ", "dK", "dV")):
+            check_heads(host(got[sl]), want, "bfloat16", "g", f"{n} b{b} h{h}")
