@@ -83,7 +83,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--workload",
                     choices=["all", "fwd_bwd", "variants", "decode", "decode_int8", "prefill", "lm",
-                             "cached_step", "fp32", "long", "copy"],
+                             "cached_step", "fp32", "d32", "long", "copy"],
                     default="all",
                     help="run one workload only (for profiling); 'all' prints the contract line")
     return ap.parse_args()
@@ -545,19 +545,16 @@ def bench_cached_step(ts, torch, steps, warmup):
     return out
 
 
-def bench_fp32(ts, torch, steps, warmup):
-    """Report-only: causal fp32 forward + backward through the public API on
-    the generic kernels (the path of fp32 models, the reference's default
-    dtype): the reference's CPU-runnable case (B8 H4 S256 D64) and a long
-    sequence (B2 H16 S2048 D128).  Per-kernel probe means and TFLOP/s against
-    the fp32 peak."""
+def _bench_shapes(ts, torch, steps, warmup, shapes, dtype, path, peak):
+    """Causal forward + backward through the public API at each (b, h, s, d)
+    of `shapes` in `dtype` (N(0, 1) inputs); the kernel family `path` must
+    run.  Per-kernel probe means and TFLOP/s against `peak`."""
     from tensorsmith_hip import _lib
 
     out = {}
-    for name, (b, h, s, d) in {"causal_fwd_bwd_f32_b8h4s256d64": (8, 4, 256, 64),
-                               "causal_fwd_bwd_f32_b2h16s2048d128": (2, 16, 2048, 128)}.items():
+    for name, (b, h, s, d) in shapes.items():
         gen = torch.Generator(device="cuda").manual_seed(7)
-        raw = [torch.randn((b, h, s, d), generator=gen, device="cuda", dtype=torch.float32)
+        raw = [torch.randn((b, h, s, d), generator=gen, device="cuda", dtype=torch.float32).to(dtype)
                for _ in range(4)]
         q, k, v = (ts.Tensor(t, device="hip", requires_grad=True) for t in raw[:3])
         upstream = ts.Tensor(raw[3], device="hip")
@@ -571,8 +568,8 @@ def bench_fp32(ts, torch, steps, warmup):
         for _ in range(warmup):
             step()
         torch.cuda.synchronize()
-        if _lib.last_kernel_path() != _lib.PATH_GENERIC:
-            raise RuntimeError("the generic kernels did not run for the fp32 workload")
+        if _lib.last_kernel_path() != path:
+            raise RuntimeError(f"kernel family {_lib.last_kernel_path()} ran for {name}, expected {path}")
         _lib.profile_reset()
         _lib.profile_enable(True)
         t0 = time.perf_counter()
@@ -584,8 +581,34 @@ def bench_fp32(ts, torch, steps, warmup):
         kernels = {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}
         tf = causal_fwd_flops(b, h, s, d) * 3.5 / (ms * 1e-3) / 1e12
         out[name] = {"ms_per_step": round(ms, 4), "tflops": round(tf, 2),
-                     "frac_fp32_peak": round(tf / PEAK_FP32_TFLOPS, 4), "kernel_ms": kernels}
+                     "frac_peak": round(tf / peak, 4), "kernel_ms": kernels}
     return out
+
+
+def bench_fp32(ts, torch, steps, warmup):
+    """Report-only: causal fp32 forward + backward through the public API (the
+    path of fp32 models, the reference's default dtype): the reference's
+    CPU-runnable case (B8 H4 S256 D64) and a long sequence (B2 H16 S2048
+    D128).  Fractions of the fp32 peak."""
+    from tensorsmith_hip import _lib
+
+    return _bench_shapes(ts, torch, steps, warmup,
+                         {"causal_fwd_bwd_f32_b8h4s256d64": (8, 4, 256, 64),
+                          "causal_fwd_bwd_f32_b2h16s2048d128": (2, 16, 2048, 128)},
+                         torch.float32, _lib.PATH_GENERIC, PEAK_FP32_TFLOPS)
+
+
+def bench_head_dim32(ts, torch, steps, warmup):
+    """Report-only: causal bf16 forward + backward at head dim 32 (the
+    reference's default TransformerConfig, dim 128 over 4 heads) on the MFMA
+    kernels: a small batch of its shape (B8 H4 S256) and B16 H16 S2048.
+    Fractions of the bf16 peak."""
+    from tensorsmith_hip import _lib
+
+    return _bench_shapes(ts, torch, steps, warmup,
+                         {"causal_fwd_bwd_bf16_b8h4s256d32": (8, 4, 256, 32),
+                          "causal_fwd_bwd_bf16_b16h16s2048d32": (16, 16, 2048, 32)},
+                         torch.bfloat16, _lib.PATH_MFMA, PEAK_BF16_TFLOPS)
 
 
 def bench_lm(ts, torch, steps, warmup):
@@ -804,6 +827,9 @@ def main():
     if args.workload == "long":
         print(json.dumps({"long_fwd_bwd": bench_long(ts, torch, 3, 1)}), flush=True)
         return
+    if args.workload == "d32":
+        print(json.dumps({"head_dim32": bench_head_dim32(ts, torch, 5, 2)}), flush=True)
+        return
     if args.workload == "fp32":
         print(json.dumps({"fp32": bench_fp32(ts, torch, 5, 2)}), flush=True)
         return
@@ -842,6 +868,9 @@ def main():
     f32_res = bench_fp32(ts, torch, 5, 2)
     print("[bench] fp32 (generic kernels) " + ", ".join(
         f"{n} {r['ms_per_step']:.3f} ms" for n, r in f32_res.items()), file=sys.stderr, flush=True)
+    d32_res = bench_head_dim32(ts, torch, 5, 2)
+    print("[bench] bf16 head dim 32 " + ", ".join(
+        f"{n} {r['ms_per_step']:.3f} ms" for n, r in d32_res.items()), file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (NumPy oracle sample)", file=sys.stderr, flush=True)
@@ -879,6 +908,7 @@ def main():
         "lm_step": lm_res,
         "cached_step": cs_res,
         "fp32": f32_res,
+        "head_dim32": d32_res,
     }
     print(json.dumps(line), flush=True)
 

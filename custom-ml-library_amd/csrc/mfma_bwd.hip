@@ -164,15 +164,21 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   constexpr int BOFF = MOFF + MTILE, BSZ = DR ? NW * 128 : 0;
   // Q | dO | nl (QT floats) | nd (QT floats) | mask tile | keep bits
   constexpr int STAGE_B = TILE_Q + TILE_G + 256 + MTILE + BSZ;
-  constexpr int QPARTS = TILE_Q / 1024 / NW, GPARTS = TILE_G / 1024 / NW;
-  constexpr int LPT = QPARTS + GPARTS;            // Q + dO DMA loads per wave per tile
+  // 1 KiB DMA blocks of a Q / dO tile; wave w loads blocks w, w + NW, ...
+  // (Q blocks, then dO blocks): a compile-time split at head dims 64 / 128,
+  // and at head dim 32 (two blocks per tile) waves 0, 1 load Q, 2, 3 dO.
+  constexpr int QBLK = TILE_Q / 1024, GBLK = TILE_G / 1024;
+  constexpr bool EVEN = QBLK % NW == 0 && GBLK % NW == 0;
+  constexpr int QPARTS = QBLK / NW, GPARTS = GBLK / NW;
+  constexpr int LPT = (QBLK + GBLK + NW - 1) / NW;  // Q + dO DMA loads per wave per tile
   constexpr int SKQ = DK / 16, SKV = DV / 16;     // k-steps of S (over DK) and dP (over DV)
   constexpr int PDK = DK / 32, PDV = DV / 32;     // 32-row blocks of dK^T / dV^T
   constexpr int STEPS = SKQ > SKV ? SKQ : SKV;    // MFMA steps of each block
   constexpr int QGQ = DK / 32, QGG = DV / 32;     // 4-chunk groups per Q / dO row
   constexpr int DMAX = DK > DV ? DK : DV;
-  static_assert(QPARTS >= 1 && GPARTS >= 1 && QPARTS * NW * 1024 == TILE_Q &&
-                GPARTS * NW * 1024 == TILE_G, "tile loads must split evenly over the waves");
+  static_assert(EVEN ? (QPARTS >= 1 && GPARTS >= 1 && LPT == QPARTS + GPARTS)
+                     : (QBLK + GBLK == NW && LPT == 1 && DK == 32 && DV == 32),
+                "tile loads must split over the waves");
   static_assert(2 * LPT <= STEPS, "one tile DMA part per two MFMA steps");
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
   // Q / dO ring, then a 1 KiB block that DMA parts of tiles past the last
@@ -281,15 +287,23 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   const uint32_t gvoff = lrow * gs_b + (4 * (w % QGG) + swz_chunk) * 16;
   // nl (wave 0) / nd (wave 1) rows of the group's first query head
   const float *rowv = a.delta + (static_cast<int64_t>(b) * p.Hq + hk * p.rep) * p.Sq + (w == 0 ? rows : 0);
+  auto issue_q = [&](const TileDma &t, int n) {
+    dma16(t.qdesc, spare + t.st + ((n * 1024) & t.keep), qvoff,
+          (static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b) | t.far);
+  };
+  auto issue_g = [&](const TileDma &t, int n) {
+    dma16(t.gdesc, spare + t.st + ((TILE_Q + n * 1024) & t.keep), gvoff,
+          (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
+  };
   auto issue_part = [&](const TileDma &t, int u) {
-    if (u < QPARTS) {
-      const int n = w + NW * u;
-      dma16(t.qdesc, spare + t.st + ((n * 1024) & t.keep), qvoff,
-            (static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b) | t.far);
-    } else if (u < LPT) {
-      const int n = w + NW * (u - QPARTS);
-      dma16(t.gdesc, spare + t.st + ((TILE_Q + n * 1024) & t.keep), gvoff,
-            (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
+    if (u < LPT) {
+      if constexpr (EVEN) {
+        if (u < QPARTS) issue_q(t, w + NW * u);
+        else issue_g(t, w + NW * (u - QPARTS));
+      } else {
+        if (w < QBLK) issue_q(t, w);  // (w is wave-uniform: a scalar branch)
+        else issue_g(t, w - QBLK);
+      }
     } else {
       const u32x4 rdesc = make_desc(reinterpret_cast<const void *>(t.ra),
                                     static_cast<uint32_t>(p.Sq) * 4);
@@ -735,15 +749,19 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   constexpr int TILE_K = KT * DK * 2, TILE_V = KT * DV * 2;  // bytes per K / V tile
   // K | V | with dropout each wave's 32 keep-bit words (its rows, this key tile)
   constexpr int STAGE = TILE_K + TILE_V + (DR ? NW * 128 : 0);
-  constexpr int KPARTS = TILE_K / 1024 / NW, VPARTS = TILE_V / 1024 / NW;
-  constexpr int LPT = KPARTS + VPARTS;        // DMA loads per wave per K+V tile
+  // 1 KiB DMA blocks of a K / V tile, split over the waves as in dkdv_kernel
+  constexpr int KBLK = TILE_K / 1024, VBLK = TILE_V / 1024;
+  constexpr bool EVEN = KBLK % NW == 0 && VBLK % NW == 0;
+  constexpr int KPARTS = KBLK / NW, VPARTS = VBLK / NW;
+  constexpr int LPT = (KBLK + VBLK + NW - 1) / NW;  // DMA loads per wave per K+V tile
   constexpr int PPT = LPT + (DR ? 1 : 0);     // all DMA loads per wave per tile
   constexpr int SKQ = DK / 16, SKV = DV / 16;  // k-steps of S (over DK), dP (over DV)
   constexpr int PDQ = DK / 32;                 // 32-row blocks of dQ^T (2 key k-steps each)
   constexpr int STEPS = SKQ > SKV ? SKQ : SKV;
   constexpr int QGK = DK / 32, QGV = DV / 32;
-  static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
-                VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
+  static_assert(EVEN ? (KPARTS >= 1 && VPARTS >= 1 && LPT == KPARTS + VPARTS)
+                     : (KBLK + VBLK == NW && LPT == 1 && DK == 32 && DV == 32),
+                "tile loads must split over the waves");
   static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
   // [stage][K | V (| bits)], then a 1 KiB block that DMA parts past the last
   // tile land in (nothing reads it)
@@ -868,16 +886,23 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
     d.st = (lds0 + (tile % DQ_NS) * STAGE - spare) & d.keep;
     return d;
   };
-  // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split).
+  // Parts u < KPARTS are K blocks, the rest V blocks (a compile-time split;
+  // at head dim 32 waves 0, 1 load K and waves 2, 3 V).
+  auto issue_k = [&](const DmaTile &d, int n) {
+    dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
+          d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+  };
+  auto issue_v = [&](const DmaTile &d, int n) {
+    dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
+          d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
+  };
   auto issue_part = [&](const DmaTile &d, int u) {
-    if (u < KPARTS) {
-      const int n = w + NW * u;
-      dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
-            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+    if constexpr (EVEN) {
+      if (u < KPARTS) issue_k(d, w + NW * u);
+      else issue_v(d, w + NW * (u - KPARTS));
     } else {
-      const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
-            d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
+      if (w < KBLK) issue_k(d, w);  // (w is wave-uniform: a scalar branch)
+      else issue_v(d, w - KBLK);
     }
   };
   // Dropout: the wave's 32 keep-bit words of the tile as one 8-lane part
@@ -1491,6 +1516,7 @@ hipError_t launch(const BwdArgs &a, hipStream_t st) {
   const Problem &p = a.p;
   if (p.Dqk == 128 && p.Dv == 128) launch_dims<T, 128, 128>(a, st);
   else if (p.Dqk == 64 && p.Dv == 64) launch_dims<T, 64, 64>(a, st);
+  else if (p.Dqk == 32) launch_dims<T, 32, 32>(a, st);
   else if (p.Dqk == 128) launch_dims<T, 128, 64>(a, st);
   else launch_dims<T, 64, 128>(a, st);
   return hipGetLastError();

@@ -1,7 +1,7 @@
 // Flash-style attention forward for gfx950: MFMA 32x32x16 (f16/bf16 in,
 // fp32 accumulate), online softmax in the exp2 domain, row LSE saved.  Head
 // dims 64 or 128, q / k and v / o independently (Dqk != Dv, the reference's
-// value_dim).
+// value_dim), or 32 for both.
 //
 // Algorithm: the reference's streaming forward (src/tensorsmith/nn/
 // attention.py:175-198) -- running max m, denominator l and accumulator per
@@ -80,16 +80,24 @@ template <typename T, int DK, int DV, int MK, bool DR>
 __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   constexpr int TILE_K = BN * DK * 2, TILE_V = BN * DV * 2;  // bytes per K / V tile
   constexpr int STAGE = TILE_K + TILE_V;
-  constexpr int KPARTS = TILE_K / 1024 / NW;  // 1 KiB DMA blocks per wave per K tile
-  constexpr int VPARTS = TILE_V / 1024 / NW;  // ... per V tile
-  constexpr int LPT = KPARTS + VPARTS;        // DMA loads per wave per K+V tile
+  // 1 KiB DMA blocks of a K / V tile; wave w loads blocks w, w + NW, ... of
+  // the stage (K blocks, then V blocks).  When both counts are multiples of
+  // NW (head dims 64 / 128) the split is the compile-time one below: parts
+  // u < KPARTS are K blocks.  At head dim 32 a tile is 2 blocks: waves 0, 1
+  // load K, waves 2, 3 load V.
+  constexpr int KBLK = TILE_K / 1024, VBLK = TILE_V / 1024;
+  constexpr bool EVEN = KBLK % NW == 0 && VBLK % NW == 0;
+  constexpr int KPARTS = KBLK / NW;           // K blocks per wave (EVEN split)
+  constexpr int VPARTS = VBLK / NW;           // ... V blocks
+  constexpr int LPT = (KBLK + VBLK + NW - 1) / NW;  // DMA loads per wave per K+V tile
   constexpr int SKS = DK / 16;                // k-steps of S^T = K Q^T
   constexpr int PDT = DV / 32;                // 32-row blocks of O^T
   constexpr int PVS = 2 * PDT;                // PV MFMAs per tile (two key k-steps each block)
   constexpr int STEPS = SKS > PVS ? SKS : PVS;
   constexpr int QGK = DK / 32, QGV = DV / 32;  // 4-chunk groups per K / V row
-  static_assert(KPARTS >= 1 && VPARTS >= 1 && KPARTS * NW * 1024 == TILE_K &&
-                VPARTS * NW * 1024 == TILE_V, "tile loads must split evenly over the waves");
+  static_assert(EVEN ? (KPARTS >= 1 && VPARTS >= 1 && LPT == KPARTS + VPARTS)
+                     : (KBLK + VBLK == NW && LPT == 1 && DK == 32 && DV == 32),
+                "tile loads must split over the waves");
   static_assert(2 * LPT <= STEPS, "one DMA part per two MFMA steps");
   // [stage][K | V], then one 1 KiB block that DMA parts past the last tile
   // land in (nothing reads it)
@@ -182,15 +190,21 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     d.st = (lds0 + (tile % NS) * STAGE - spare) & d.keep;
     return d;
   };
+  auto issue_k = [&](const DmaTile &d, int n) {
+    dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
+          d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+  };
+  auto issue_v = [&](const DmaTile &d, int n) {
+    dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
+          d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
+  };
   auto issue_part = [&](const DmaTile &d, int u) {
-    if (u < KPARTS) {
-      const int n = w + NW * u;
-      dma16(kdesc, spare + d.st + ((n * 1024) & d.keep), koff,
-            d.krow + static_cast<uint32_t>(16 * (n / QGK)) * ks_b);
+    if constexpr (EVEN) {
+      if (u < KPARTS) issue_k(d, w + NW * u);
+      else issue_v(d, w + NW * (u - KPARTS));
     } else {
-      const int n = w + NW * (u - KPARTS);
-      dma16(vdesc, spare + d.st + ((TILE_K + n * 1024) & d.keep), voff,
-            d.vrow + static_cast<uint32_t>(16 * (n / QGV)) * vs_b);
+      if (w < KBLK) issue_k(d, w);  // (w is wave-uniform: a scalar branch)
+      else issue_v(d, w - KBLK);
     }
   };
   auto issue = [&](int tile) {
@@ -497,6 +511,7 @@ hipError_t launch(const FwdArgs &a, hipStream_t st) {
   Probe pr_(p.drop.on ? "fwd_mfma_dropout" : (mk ? "fwd_mfma_masked" : "fwd_mfma"), st);
   if (p.Dqk == 128 && p.Dv == 128) launch_dims<T, 128, 128>(a, st);
   else if (p.Dqk == 64 && p.Dv == 64) launch_dims<T, 64, 64>(a, st);
+  else if (p.Dqk == 32) launch_dims<T, 32, 32>(a, st);
   else if (p.Dqk == 128) launch_dims<T, 128, 64>(a, st);
   else launch_dims<T, 64, 128>(a, st);
   return hipGetLastError();
@@ -506,7 +521,9 @@ hipError_t launch(const FwdArgs &a, hipStream_t st) {
 
 bool mfma_supported(const Problem &p, int dtype) {
   if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
-  if ((p.Dqk != 64 && p.Dqk != 128) || (p.Dv != 64 && p.Dv != 128)) return false;
+  // head dims 64 / 128 each, or 32 for both
+  const bool d32 = p.Dqk == 32 && p.Dv == 32;
+  if (!d32 && ((p.Dqk != 64 && p.Dqk != 128) || (p.Dv != 64 && p.Dv != 128))) return false;
   if (!(p.scale > 0.0)) return false;
   // the backward reads each (b, h) slice of the dropout keep bits with 32-bit offsets
   if (p.drop.on && static_cast<int64_t>((p.Sk + 31) / 32) * ((p.Sq + 3) / 4 * 4) * 4 >= (int64_t(1) << 31))

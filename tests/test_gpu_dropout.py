@@ -107,6 +107,7 @@ CASES = [
     ("bfloat16", 2, 2, 1, 77, 150, 128, False, 0, 0.1, True),
     ("float16", 1, 2, 2, 256, 256, 128, False, 0, 0.3, False),
     ("bfloat16", 1, 2, 2, 100, 140, (128, 64), True, 40, 0.25, False),
+    ("float16", 2, 2, 1, 130, 170, 32, True, 0, 0.2, True),
 ]
 
 

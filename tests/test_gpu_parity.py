@@ -111,6 +111,10 @@ MFMA_CASES = [
     (1, 4, 2, 160, 160, 64, True, 0),     # GQA
     (2, 2, 1, 65, 257, 128, True, 192),  # GQA + offset + ragged
     (1, 1, 1, 1, 300, 128, True, 299),    # one query row (decode shape through prefill)
+    # head dim 32 (the reference's default TransformerConfig: dim 128, 4 heads)
+    (2, 2, 2, 200, 333, 32, True, 133),
+    (1, 4, 2, 160, 160, 32, True, 0),     # GQA
+    (2, 3, 3, 77, 190, 32, False, 0),
 ]
 
 
@@ -293,6 +297,8 @@ MASK_CASES = [
     # rows 16-byte aligned, keys contiguous: the 16-byte row-piece reads
     ("bool-qk-rows", "bfloat16", 2, 2, 2, 160, 256, 128, True, 96, (160, 256), "bool"),
     ("add-bf16-rows", "float16", 1, 4, 2, 128, 192, 64, False, 0, (128, 192), "bfloat16"),
+    ("bool-qk-d32", "bfloat16", 2, 2, 2, 200, 333, 32, True, 133, (200, 333), "bool"),
+    ("add-f32-rows-d32", "float16", 1, 2, 1, 160, 256, 32, False, 0, (1, 2, 160, 256), "float32"),
 ]
 
 

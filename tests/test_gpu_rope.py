@@ -208,6 +208,7 @@ FUSED_CASES = [
     ("bfloat16", 2, 2, 1, 77, 150, 128, 64, False, 0, 9, 3),
     ("float16", 1, 2, 2, 256, 256, 128, 96, True, 0, 5, 5),
     ("bfloat16", 1, 2, 2, 90, 120, (128, 64), 128, True, 30, 30, 0),
+    ("float16", 2, 4, 2, 100, 140, 32, 32, True, 40, 40, 0),  # head dim 32
 ]
 
 
