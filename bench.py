@@ -587,15 +587,15 @@ def _bench_shapes(ts, torch, steps, warmup, shapes, dtype, path, peak):
 
 def bench_fp32(ts, torch, steps, warmup):
     """Report-only: causal fp32 forward + backward through the public API (the
-    path of fp32 models, the reference's default dtype): the reference's
-    CPU-runnable case (B8 H4 S256 D64) and a long sequence (B2 H16 S2048
-    D128).  Fractions of the fp32 peak."""
+    path of fp32 models, the reference's default dtype) on the fp32 MFMA
+    kernels: the reference's CPU-runnable case (B8 H4 S256 D64) and a long
+    sequence (B2 H16 S2048 D128).  Fractions of the fp32 peak."""
     from tensorsmith_hip import _lib
 
     return _bench_shapes(ts, torch, steps, warmup,
                          {"causal_fwd_bwd_f32_b8h4s256d64": (8, 4, 256, 64),
                           "causal_fwd_bwd_f32_b2h16s2048d128": (2, 16, 2048, 128)},
-                         torch.float32, _lib.PATH_GENERIC, PEAK_FP32_TFLOPS)
+                         torch.float32, _lib.PATH_MFMA, PEAK_FP32_TFLOPS)
 
 
 def bench_head_dim32(ts, torch, steps, warmup):

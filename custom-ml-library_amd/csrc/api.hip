@@ -121,6 +121,12 @@ bool mfma_view_ok(const tsattn::View &v, int64_t len) {
   return tsattn::aligned16(v) && v.s2 > 0 && (len + 256) * v.s2 * 2 < (int64_t(1) << 31);
 }
 
+// The same for the fp32 MFMA kernels (4-byte elements).
+bool mfma_f32_view_ok(const tsattn::View &v, int64_t len) {
+  return reinterpret_cast<uintptr_t>(v.data) % 16 == 0 && v.s0 % 4 == 0 && v.s1 % 4 == 0 &&
+         v.s2 % 4 == 0 && v.s2 > 0 && (len + 256) * v.s2 * 4 < (int64_t(1) << 31);
+}
+
 // The forward / backward behind the plain and the RoPE entry points.  With a
 // RoPE descriptor only the MFMA kernels apply (they fold the rotation in).
 int check_rope(const tsattn_rope_desc *r, const tsattn::Problem &pr, tsattn::RopeDesc *out) {
@@ -168,6 +174,12 @@ int sdpa_forward(const tsattn_problem *p, const tsattn_rope_desc *rope, const ts
                       "mfma forward launch");
   }
   if (rope) return rope_unsupported();
+  if (g_policy.load() == 0 && tsattn::mfma_f32_supported(pr, p->dtype) && mfma_f32_view_ok(vq, pr.Sq) &&
+      mfma_f32_view_ok(vk, pr.Sk) && mfma_f32_view_ok(vv, pr.Sk) && mfma_f32_view_ok(vo, pr.Sq)) {
+    g_last_path = 2;
+    return hip_status(tsattn::launch_mfma_f32_forward(pr, vq, vk, vv, vo, static_cast<float *>(lse), st),
+                      "fp32 mfma forward launch");
+  }
   g_last_path = 1;
   rc = hip_status(tsattn::launch_generic_forward(pr, p->dtype, vq, vk, vv, vo, lse, st),
                   "generic forward launch");
@@ -268,6 +280,15 @@ int sdpa_backward(const tsattn_problem *p, const tsattn_rope_desc *rope, const t
                       "mfma backward launch");
   }
   if (rope) return rope_unsupported();
+  if (g_policy.load() == 0 && tsattn::mfma_f32_supported(pr, p->dtype) && mfma_f32_view_ok(vq, pr.Sq) &&
+      mfma_f32_view_ok(vk, pr.Sk) && mfma_f32_view_ok(vv, pr.Sk) && mfma_f32_view_ok(vo, pr.Sq) &&
+      mfma_f32_view_ok(vg, pr.Sq) && mfma_f32_view_ok(vdq, pr.Sq) && mfma_f32_view_ok(vdk, pr.Sk) &&
+      mfma_f32_view_ok(vdv, pr.Sk)) {
+    g_last_path = 2;
+    return hip_status(tsattn::launch_mfma_f32_backward(pr, vq, vk, vv, vo, vg, static_cast<const float *>(lse),
+                                                       vdq, vdk, vdv, static_cast<float *>(workspace), st),
+                      "fp32 mfma backward launch");
+  }
   g_last_path = 1;
   return hip_status(tsattn::launch_generic_backward(pr, p->dtype, vq, vk, vv, vo, vg, lse, vdq,
                                                     vdk, vdv, workspace, st),

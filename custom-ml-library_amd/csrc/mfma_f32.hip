@@ -1,0 +1,766 @@
+// fp32 attention on the fp32 matrix cores (v_mfma_f32_32x32x2_f32): forward,
+// backward row values, dQ and dK/dV, for fp32 q / k / v with Dqk = Dv in
+// {32, 64, 128}, causal windows with offsets, key-padding lengths and GQA.
+// The reference keeps fp32 inputs in fp32 (src/tensorsmith/nn/attention.py:63)
+// and fp32 is its default dtype; these kernels follow the same streaming
+// algorithm as the 16-bit ones (attention.py:175-198 forward, :200-247 VJP),
+// with every product and accumulation in fp32 (P and dS stay fp32: nothing is
+// rounded to a narrower type).
+//
+// MFMA 32x32x2 f32, lane l = 32 h + c: A[m = c][k = h], B[k = h][n = c], C as
+// in mfma_common.h.  A contraction over K elements runs K / 2 MFMAs; lane half
+// h supplies element k = perm(s, h) of step s, any bijection shared by both
+// operands.  Over a head dimension the kernels take d = h D / 2 + s, so each
+// lane walks a contiguous half of every row (16-byte LDS reads serve four
+// steps); over a 32-row tile of an accumulator layout they take the row
+// crow(i, h) of register i, so a C tile feeds the next contraction as it is.
+//
+// LDS tiles hold 32 rows x D floats, row-major, 16-byte chunk q of row r at
+// q ^ fsw(r): 16 lanes reading one chunk each of 16 consecutive rows hit 16
+// different bank groups (the operands whose rows are lanes), and 64 lanes
+// reading a 32-float segment of rows r and r + 4 (the operands whose rows are
+// accumulator rows) hit the two halves of the banks (D >= 64; at D = 32 a row
+// is half the banks and the segment reads take two passes).  Tiles reach LDS
+// by direct buffer loads (DMA), each lane fetching the global chunk its
+// swizzled position holds; rows past the buffer range arrive as zeros.
+#include "mfma_common.h"
+
+namespace tsattn {
+namespace {
+
+constexpr int NT = 256;
+constexpr int NW = NT / 64;
+constexpr int BM = 128;  // query rows per forward / dQ workgroup
+constexpr int BN = 32;   // keys (forward, dQ) or query rows (dK/dV) per tile
+constexpr int KB = 128;  // keys per dK/dV workgroup
+constexpr float kTau = 8.f;
+
+__device__ __forceinline__ f32x16 mfma32f(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+template <int D>
+__host__ __device__ __forceinline__ constexpr int fsw(int r) {
+  return D >= 64 ? ((r & 3) | ((r & 4) << 1) | ((r & 8) >> 1)) : ((r >> 1) & 7);
+}
+
+template <typename X>
+__device__ __forceinline__ const X *f32_head(View v, int b, int h) {
+  return static_cast<const X *>(v.data) + b * v.s0 + h * v.s1;
+}
+
+// A [32 x D] fp32 tile in LDS (see the layout above).
+template <int D>
+struct FTile {
+  static constexpr int CPR = D / 4;                  // 16-byte chunks per row
+  static constexpr int BYTES = BN * D * 4;           // per tile
+  static constexpr int BLOCKS = BYTES / 1024;        // 1 KiB DMA blocks per tile
+  static constexpr int RPB = 1024 / (D * 4);         // rows per DMA block
+
+  // Byte offset (within the block's rows) of the global chunk lane l of a
+  // DMA of block n fetches: its LDS slot is 16 l of the block.
+  __device__ __forceinline__ static uint32_t dma_off(int n, int lane, uint32_t stride_b) {
+    const int rr = lane / CPR, p = lane % CPR, row = n * RPB + rr;
+    return static_cast<uint32_t>(rr) * stride_b + static_cast<uint32_t>((p ^ fsw<D>(row)) * 16);
+  }
+  // 16 bytes of row r, chunk q (d = 4 q .. 4 q + 3).
+  __device__ __forceinline__ static float4 chunk(const char *t, int r, int q) {
+    return *reinterpret_cast<const float4 *>(t + r * D * 4 + ((q ^ fsw<D>(r)) << 4));
+  }
+  // One float: row r, column d.
+  __device__ __forceinline__ static float elem(const char *t, int r, int d) {
+    return *reinterpret_cast<const float *>(t + r * D * 4 + (((d >> 2) ^ fsw<D>(r)) << 4) + ((d & 3) << 2));
+  }
+};
+
+struct F32Args {
+  Problem p;
+  View q, k, v, o, dout, dq, dk, dv;
+  float *lse;
+  float *rows;  // backward row values: [rows] -delta, then [rows] -safe(lse) / scale
+  float sl;     // scale * log2(e)
+  float scale;
+};
+
+// ---------------------------------------------------------------------------
+// Forward: one workgroup = 128 query rows of one (b, q head), 4 waves x 32
+// rows; key tiles of 32 keys double-buffered through LDS (the next tile's DMA
+// issued at the start of an iteration, between the S steps).  Per tile a wave
+// computes S^T = K Q^T (D / 2 MFMAs, Q in registers, K by 16-byte chunks),
+// the online softmax on its lane's query column (lazy rescale, exp2 domain),
+// and O^T += V^T P^T (D / 2 MFMAs, V by 32-float row segments, P^T the fp32
+// accumulator registers).  Two workgroups per CU.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
+  using TL = FTile<D>;
+  constexpr int HD = D / 2;             // MFMA steps over the head dimension
+  constexpr int PDT = D / 32;           // 32-row blocks of O^T
+  constexpr int STAGE = 2 * TL::BYTES;  // K | V
+  constexpr int PARTS = 2 * TL::BLOCKS / NW;  // DMA blocks per wave per tile
+  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
+  // two stages, then a 1 KiB block the parts of a tile past the last land in
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+
+  const Problem &p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_qb = (p.Sq + BM - 1) / BM;
+  const int total = n_qb * p.Hq * p.B;
+  const int logical = xcd_remap(blockIdx.x, total);
+  int bh, rank;
+  heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);
+  const int qb = n_qb - 1 - rank;
+  const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
+  const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
+  const int kv_end = kv_end_for(p, b);
+  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+
+  int64_t lim = kv_end, wlim = kv_end;
+  if (p.causal) {
+    lim = min(lim, static_cast<int64_t>(min(q0 + BM, p.Sq) - 1) + p.offset + 1);
+    wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
+  }
+  if (qw >= p.Sq) wlim = 0;
+  const int n_tiles = __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0);
+  const int w_tiles = __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0);
+
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4;
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4;
+  const uint32_t vs_b = static_cast<uint32_t>(a.v.s2) * 4;
+  const rsrc_t qrs = make_rsrc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+  const u32x4 kdesc = make_desc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const u32x4 vdesc = make_desc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+
+  // Q fragments: lane (c, h) holds Q[qrow][h D / 2 .. + D / 2), step s = d - h D / 2.
+  float qf[HD];
+#pragma unroll
+  for (int j = 0; j < HD / 4; ++j) {
+    const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b +
+                                                                    static_cast<uint32_t>((h * HD + 4 * j) * 4)));
+    qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+  }
+
+  const uint32_t lds0 = lds_addr(lds);
+  const uint32_t spare = lds0 + 2 * STAGE;
+  // Part u of wave w is block n = w + NW u of the stage: K blocks first.
+  // A tile past the last one reads past the buffer ranges (zeros, no memory
+  // access) into the spare block, so every wave issues the same parts.
+  auto issue_part = [&](int tile, int u) {
+    const int n = w + NW * u;
+    const bool real = tile < n_tiles;
+    const uint32_t st = real ? lds0 + (tile & 1) * STAGE : spare;
+    if (n < TL::BLOCKS) {
+      const uint32_t so = real ? static_cast<uint32_t>(tile * BN + n * TL::RPB) * ks_b : 0x80000000u;
+      dma16(kdesc, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, ks_b), so);
+    } else {
+      const int m = n - TL::BLOCKS;
+      const uint32_t so = real ? static_cast<uint32_t>(tile * BN + m * TL::RPB) * vs_b : 0x80000000u;
+      dma16(vdesc, st + (real ? TL::BYTES + m * 1024 : 0), TL::dma_off(m, lane, vs_b), so);
+    }
+  };
+
+  f32x16 oacc[PDT];
+#pragma unroll
+  for (int dt = 0; dt < PDT; ++dt) oacc[dt] = f32x16{};
+  float m = -INFINITY, l = 0.f, thr = -INFINITY, nbase = 0.f;
+  const float sl = a.sl, inv_sl = 1.f / sl;
+  int klim = kv_end;
+  if (p.causal) {
+    const int64_t cl = static_cast<int64_t>(qrow) + p.offset + 1;
+    if (cl < kv_end) klim = cl < 0 ? 0 : static_cast<int>(cl);
+  }
+  const uint8_t *kmask_b = keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
+  int j_edge = kv_end / BN;
+  if (keymask) j_edge = 0;
+  if (p.causal) {
+    const int64_t dd = static_cast<int64_t>(qw) + p.offset - (BN - 1);
+    const int jc = dd < 0 ? 0 : static_cast<int>(min(dd / BN + 1, static_cast<int64_t>(INT32_MAX)));
+    j_edge = min(j_edge, jc);
+  }
+
+#pragma unroll
+  for (int u = 0; u < PARTS; ++u) issue_part(0, u);
+  wait_vm_n<0>();  // the query fragments and the first tile
+#pragma unroll
+  for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]));
+  __syncthreads();
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const char *kt = lds + (j & 1) * STAGE;
+    const char *vt = kt + TL::BYTES;
+    if (j < w_tiles) {
+      // S^T = K Q^T, the next tile's parts spread over the steps; each
+      // 16-byte chunk of K serves four steps, read one chunk ahead
+      f32x16 s = f32x16{};
+      {
+        constexpr int NC = HD / 4;
+        float4 kc[2];
+        kc[0] = TL::chunk(kt, c, h * NC);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jj = 0; jj < NC; ++jj) {
+          if (jj + 1 < NC) kc[(jj + 1) & 1] = TL::chunk(kt, c, h * NC + jj + 1);
+          const float4 kv = kc[jj & 1];
+          s = mfma32f(kv.x, qf[4 * jj], s);
+          s = mfma32f(kv.y, qf[4 * jj + 1], s);
+          s = mfma32f(kv.z, qf[4 * jj + 2], s);
+          s = mfma32f(kv.w, qf[4 * jj + 3], s);
+          if (jj < PARTS) issue_part(j + 1, jj);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // softmax of this lane's query column: element i is key kv0 + crow(i, h)
+      const int kv0 = j * BN;
+      if (j >= j_edge) {
+        const int lm = klim - kv0 - 4 * h;
+        unsigned kbits = ~0u;
+        if (keymask) {
+          const int key = kv0 + lane;
+          const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+          kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kc_ = 8 * (i >> 2) + (i & 3);
+          s[i] = ((kc_ < lm) & (((kbits >> kc_) & 1u) != 0)) ? s[i] : -INFINITY;
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[i]);
+      const float mxr = half_swap_max3(mx);
+      if (__ballot(mxr > thr) != 0ull) {
+        const float m_new = fmaxf(m, mxr * sl);
+        const float corr = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+        m = m_new;
+        thr = (m + kTau) * inv_sl;
+        nbase = m == -INFINITY ? 0.f : -m;
+        l *= corr;
+#pragma unroll
+        for (int dt = 0; dt < PDT; ++dt) oacc[dt] *= corr;
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        s[i] = fast_exp2(fmaf(s[i], sl, nbase));
+        l += s[i];
+      }
+      // O^T += V^T P^T: step i takes keys crow(i, h) (register i of P^T); the
+      // V elements read two steps ahead
+      {
+        constexpr int NS_ = 16 * PDT, FD = 2;
+        float vf[FD + 1];
+        auto vload = [&](int t) {
+          const int i = t / PDT, dt = t % PDT;
+          vf[t % (FD + 1)] = TL::elem(vt, 8 * (i >> 2) + 4 * h + (i & 3), 32 * dt + c);
+        };
+#pragma unroll
+        for (int t = 0; t < FD; ++t) vload(t);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NS_; ++t) {
+          if (t + FD < NS_) vload(t + FD);
+          oacc[t % PDT] = mfma32f(vf[t % (FD + 1)], s[t / PDT], oacc[t % PDT]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < PARTS; ++u) issue_part(j + 1, u);
+    }
+    wait_vm_n<0>();  // tile j + 1 has landed
+    __syncthreads();
+  }
+
+  // O rows: lane holds O^T[d = 32 dt + 8 g + 4 h + r][row c], four consecutive
+  // channels per (dt, g): one 16-byte store each.
+  const float lt = xor32_sum(l);
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (qrow < p.Sq) {
+    float *orow = static_cast<float *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
+                  static_cast<int64_t>(qrow) * a.o.s2;
+#pragma unroll
+    for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
+            float4{oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv, oacc[dt][4 * g + 2] * inv,
+                   oacc[dt][4 * g + 3] * inv};
+    if (a.lse && h == 0)
+      a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
+          lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward row values: nd = -delta (delta = sum_d dO O, attention.py:232) and
+// nl = -safe(lse) / scale (safe: 0 for a row that sees no key, :231), the
+// layout the 16-bit kernels use: P = exp2((S + nl) sl), dS = P (dP + nd).  A
+// row is D / 4 lanes of 16 bytes.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(NT) void rows_f32_kernel(F32Args a) {
+  constexpr int G = D / 4, RPW = 64 / G;
+  const Problem &p = a.p;
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  const int lane = threadIdx.x & 63, g = lane % G;
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * NW + (threadIdx.x >> 6)) * RPW + lane / G;
+  const bool live = row < rows;
+  const int64_t rr = live ? row : rows - 1;
+  const int64_t bh = rr / p.Sq, i = rr - bh * p.Sq, b = bh / p.Hq, hq = bh - b * p.Hq;
+  const float *go = static_cast<const float *>(a.dout.data) + b * a.dout.s0 + hq * a.dout.s1 + i * a.dout.s2;
+  const float *oo = static_cast<const float *>(a.o.data) + b * a.o.s0 + hq * a.o.s1 + i * a.o.s2;
+  const float4 x = *reinterpret_cast<const float4 *>(go + 4 * g);
+  const float4 y = *reinterpret_cast<const float4 *>(oo + 4 * g);
+  float d = x.x * y.x + x.y * y.y + x.z * y.z + x.w * y.w;
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) d += __shfl_xor(d, o, 64);
+  if (live && g == 0) {
+    const float lse = a.lse[rr];
+    a.rows[rr] = -d;
+    a.rows[rows + rr] = isfinite(lse) ? -lse / a.scale : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ: one workgroup = 128 query rows of one (b, q head), 4 waves x 32 rows,
+// one workgroup per CU (a wave holds Q, dO and the dQ accumulators).  Key
+// tiles double-buffered through LDS as in the forward.  Per tile a wave
+// computes S^T = K Q^T and dP^T = V dO^T (K, V by 16-byte chunks; Q, dO in
+// registers), P = exp2((S + nl) sl) and dS = P (dP + nd) on its lane's query
+// column, then dQ^T += K^T dS^T (K by 32-float row segments, dS^T the
+// accumulator registers).  dQ = scale dQ^T^T.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
+  using TL = FTile<D>;
+  constexpr int HD = D / 2, PDT = D / 32;
+  constexpr int STAGE = 2 * TL::BYTES;  // K | V
+  constexpr int PARTS = 2 * TL::BLOCKS / NW;
+  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+
+  const Problem &p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_qb = (p.Sq + BM - 1) / BM;
+  const int total = n_qb * p.Hq * p.B;
+  const int logical = xcd_remap(blockIdx.x, total);
+  int bh, rank;
+  heavy_first(logical, n_qb, p.Hq * p.B, 32, bh, rank);
+  const int qb = n_qb - 1 - rank;
+  const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
+  const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
+  const int kv_end = kv_end_for(p, b);
+  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  int64_t lim = kv_end, wlim = kv_end;
+  if (p.causal) {
+    lim = min(lim, static_cast<int64_t>(min(q0 + BM, p.Sq) - 1) + p.offset + 1);
+    wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
+  }
+  if (qw >= p.Sq) wlim = 0;
+  const int n_tiles = __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0);
+  const int w_tiles = __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0);
+
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4, gs_b = static_cast<uint32_t>(a.dout.s2) * 4;
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4, vs_b = static_cast<uint32_t>(a.v.s2) * 4;
+  const rsrc_t qrs = make_rsrc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+  const rsrc_t grs = make_rsrc(f32_head<float>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+  const u32x4 kdesc = make_desc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const u32x4 vdesc = make_desc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  float qf[HD], gf[HD];
+#pragma unroll
+  for (int j = 0; j < HD / 4; ++j) {
+    const uint32_t off = static_cast<uint32_t>((h * HD + 4 * j) * 4);
+    const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + off));
+    const float4 y = __builtin_bit_cast(float4, buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + off));
+    qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+    gf[4 * j] = y.x, gf[4 * j + 1] = y.y, gf[4 * j + 2] = y.z, gf[4 * j + 3] = y.w;
+  }
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+  const int64_t rix = static_cast<int64_t>(bh) * p.Sq + (qrow < p.Sq ? qrow : p.Sq - 1);
+  const float nd = a.rows[rix], nl = a.rows[rows + rix];
+
+  const uint32_t lds0 = lds_addr(lds);
+  const uint32_t spare = lds0 + 2 * STAGE;
+  auto issue_part = [&](int tile, int u) {
+    const int n = w + NW * u;
+    const bool real = tile < n_tiles;
+    const uint32_t st = real ? lds0 + (tile & 1) * STAGE : spare;
+    if (n < TL::BLOCKS) {
+      const uint32_t so = real ? static_cast<uint32_t>(tile * BN + n * TL::RPB) * ks_b : 0x80000000u;
+      dma16(kdesc, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, ks_b), so);
+    } else {
+      const int m = n - TL::BLOCKS;
+      const uint32_t so = real ? static_cast<uint32_t>(tile * BN + m * TL::RPB) * vs_b : 0x80000000u;
+      dma16(vdesc, st + (real ? TL::BYTES + m * 1024 : 0), TL::dma_off(m, lane, vs_b), so);
+    }
+  };
+  int klim = kv_end;
+  if (p.causal) {
+    const int64_t cl = static_cast<int64_t>(qrow) + p.offset + 1;
+    if (cl < kv_end) klim = cl < 0 ? 0 : static_cast<int>(cl);
+  }
+  const uint8_t *kmask_b = keymask ? static_cast<const uint8_t *>(p.mask.data) + b * p.mask.s0 : nullptr;
+  int j_edge = kv_end / BN;
+  if (keymask) j_edge = 0;
+  if (p.causal) {
+    const int64_t dd = static_cast<int64_t>(qw) + p.offset - (BN - 1);
+    const int jc = dd < 0 ? 0 : static_cast<int>(min(dd / BN + 1, static_cast<int64_t>(INT32_MAX)));
+    j_edge = min(j_edge, jc);
+  }
+  const float sl = a.sl;
+  f32x16 acc[PDT];
+#pragma unroll
+  for (int dt = 0; dt < PDT; ++dt) acc[dt] = f32x16{};
+
+#pragma unroll
+  for (int u = 0; u < PARTS; ++u) issue_part(0, u);
+  wait_vm_n<0>();
+#pragma unroll
+  for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]), "+v"(gf[i]));
+  __syncthreads();
+
+  for (int j = 0; j < n_tiles; ++j) {
+    const char *kt = lds + (j & 1) * STAGE;
+    const char *vt = kt + TL::BYTES;
+    if (j < w_tiles) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+      {
+        constexpr int NC = HD / 4;
+        float4 kc[2], vc[2];
+        kc[0] = TL::chunk(kt, c, h * NC);
+        vc[0] = TL::chunk(vt, c, h * NC);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int jj = 0; jj < NC; ++jj) {
+          if (jj + 1 < NC) {
+            kc[(jj + 1) & 1] = TL::chunk(kt, c, h * NC + jj + 1);
+            vc[(jj + 1) & 1] = TL::chunk(vt, c, h * NC + jj + 1);
+          }
+          const float4 kv = kc[jj & 1], vv = vc[jj & 1];
+          s = mfma32f(kv.x, qf[4 * jj], s);
+          dp = mfma32f(vv.x, gf[4 * jj], dp);
+          s = mfma32f(kv.y, qf[4 * jj + 1], s);
+          dp = mfma32f(vv.y, gf[4 * jj + 1], dp);
+          s = mfma32f(kv.z, qf[4 * jj + 2], s);
+          dp = mfma32f(vv.z, gf[4 * jj + 2], dp);
+          s = mfma32f(kv.w, qf[4 * jj + 3], s);
+          dp = mfma32f(vv.w, gf[4 * jj + 3], dp);
+          if (jj < PARTS) issue_part(j + 1, jj);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      // P = exp2((S + nl) sl), dS = P (dP + nd): element i is key kv0 + crow(i, h)
+      const int kv0 = j * BN;
+      unsigned kbits = ~0u;
+      int lm = 64;
+      if (j >= j_edge) {
+        lm = klim - kv0 - 4 * h;
+        if (keymask) {
+          const int key = kv0 + lane;
+          const bool ok = key < p.Sk && kmask_b[static_cast<int64_t>(key) * p.mask.s3];
+          kbits = static_cast<unsigned>(__ballot(ok) >> (4 * h));
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kc_ = 8 * (i >> 2) + (i & 3);
+        const float pv = ((kc_ < lm) & (((kbits >> kc_) & 1u) != 0)) ? fast_exp2((s[i] + nl) * sl) : 0.f;
+        s[i] = pv * (dp[i] + nd);
+      }
+      // dQ^T += K^T dS^T: step i takes keys crow(i, h) (register i of dS^T)
+      {
+        constexpr int NS_ = 16 * PDT, FD = 2;
+        float kf[FD + 1];
+        auto kload = [&](int t) {
+          const int i = t / PDT, dt = t % PDT;
+          kf[t % (FD + 1)] = TL::elem(kt, 8 * (i >> 2) + 4 * h + (i & 3), 32 * dt + c);
+        };
+#pragma unroll
+        for (int t = 0; t < FD; ++t) kload(t);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NS_; ++t) {
+          if (t + FD < NS_) kload(t + FD);
+          acc[t % PDT] = mfma32f(kf[t % (FD + 1)], s[t / PDT], acc[t % PDT]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < PARTS; ++u) issue_part(j + 1, u);
+    }
+    wait_vm_n<0>();
+    __syncthreads();
+  }
+  if (qrow < p.Sq) {
+    float *orow = static_cast<float *>(const_cast<void *>(a.dq.data)) + b * a.dq.s0 + hq * a.dq.s1 +
+                  static_cast<int64_t>(qrow) * a.dq.s2;
+    const float sc = a.scale;
+#pragma unroll
+    for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
+            float4{acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc, acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc};
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV: one workgroup = 128 keys of one (b, kv head), 4 waves x 32 keys,
+// one workgroup per CU (a wave holds its K and V rows and the dK / dV
+// accumulators).  Query tiles of 32 rows -- Q, dO and their row values, for
+// every query head of the GQA group (attention.py:245-247) -- double-buffered
+// through LDS.  Per tile a wave computes S = Q K^T and dP = dO V^T (Q, dO by
+// 16-byte chunks; K, V in registers), P = exp2((S + nl) sl) and dS = P (dP +
+// nd) per (row, key), then dV^T += dO^T P and dK^T += Q^T dS (Q, dO by
+// 32-float row segments, P and dS the accumulator registers).  dK = scale
+// dK^T^T, dV = dV^T^T.
+// ---------------------------------------------------------------------------
+template <int D>
+__global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
+  using TL = FTile<D>;
+  constexpr int HD = D / 2, PDT = D / 32;
+  constexpr int RV = 2 * BN * 4;                 // nl | nd of the tile's rows
+  constexpr int STAGE = 2 * TL::BYTES + RV;      // Q | dO | row values
+  constexpr int PARTS = 2 * TL::BLOCKS / NW;
+  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
+  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+
+  const Problem &p = a.p;
+  const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n_kb = (p.Sk + KB - 1) / KB;
+  const int total = n_kb * p.Hkv * p.B;
+  const int logical = xcd_remap(blockIdx.x, total);
+  int bh, kb;
+  heavy_first(logical, n_kb, p.Hkv * p.B, 32, bh, kb);
+  const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
+  const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
+  const int kv_end = kv_end_for(p, b);
+  const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
+  const bool key_live = key < kv_end &&
+                        (!keymask || static_cast<const uint8_t *>(p.mask.data)[b * p.mask.s0 + static_cast<int64_t>(key) * p.mask.s3]);
+  int q_start = 0;
+  if (p.causal) {
+    const int64_t s0 = static_cast<int64_t>(k0) - p.offset;
+    q_start = s0 <= 0 ? 0 : static_cast<int>(s0 < p.Sq ? s0 : p.Sq);
+    q_start = (q_start / BN) * BN;
+  }
+  const int n_qt = __builtin_amdgcn_readfirstlane(k0 < kv_end ? (p.Sq - q_start + BN - 1) / BN : 0);
+  const int n_iter = __builtin_amdgcn_readfirstlane(n_qt * p.rep);
+  const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+
+  const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4, gs_b = static_cast<uint32_t>(a.dout.s2) * 4;
+  const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4, vs_b = static_cast<uint32_t>(a.v.s2) * 4;
+  const rsrc_t krs = make_rsrc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+  const rsrc_t vrs = make_rsrc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  float kf[HD], vf[HD];
+#pragma unroll
+  for (int j = 0; j < HD / 4; ++j) {
+    const uint32_t off = static_cast<uint32_t>((h * HD + 4 * j) * 4);
+    const float4 x = __builtin_bit_cast(float4, buf_load16(krs, static_cast<uint32_t>(key) * ks_b + off));
+    const float4 y = __builtin_bit_cast(float4, buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + off));
+    kf[4 * j] = x.x, kf[4 * j + 1] = x.y, kf[4 * j + 2] = x.z, kf[4 * j + 3] = x.w;
+    vf[4 * j] = y.x, vf[4 * j + 1] = y.y, vf[4 * j + 2] = y.z, vf[4 * j + 3] = y.w;
+  }
+
+  // tile it = query tile it % n_qt of query head hk rep + it / n_qt
+  const uint32_t lds0 = lds_addr(lds);
+  const uint32_t spare = lds0 + 2 * STAGE;
+  auto issue = [&](int it) {
+    const bool real = it < n_iter;
+    const int r = real ? it / n_qt : 0, qi = real ? it - r * n_qt : 0;
+    const int hq = hk * p.rep + r, q0 = q_start + qi * BN;
+    const uint32_t st = real ? lds0 + (it & 1) * STAGE : spare;
+    const u32x4 qd = make_desc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const u32x4 gd = make_desc(f32_head<float>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+#pragma unroll
+    for (int u = 0; u < PARTS; ++u) {
+      const int n = w + NW * u;
+      if (n < TL::BLOCKS) {
+        const uint32_t so = real ? static_cast<uint32_t>(q0 + n * TL::RPB) * qs_b : 0x80000000u;
+        dma16(qd, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, qs_b), so);
+      } else {
+        const int m = n - TL::BLOCKS;
+        const uint32_t so = real ? static_cast<uint32_t>(q0 + m * TL::RPB) * gs_b : 0x80000000u;
+        dma16(gd, st + (real ? TL::BYTES + m * 1024 : 0), TL::dma_off(m, lane, gs_b), so);
+      }
+    }
+    // the rows' nl (wave 0) and nd (wave 1): 8 lanes of 16 bytes each
+    const float *rv = a.rows + (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
+    const u32x4 rd = make_desc(rv, static_cast<uint32_t>(p.Sq) * 4);
+    const bool mine = real && w < 2;
+    if (lane < BN / 4)
+      dma16(rd, mine ? st + 2 * TL::BYTES + w * BN * 4 : spare, static_cast<uint32_t>(lane) * 16,
+            mine ? static_cast<uint32_t>(q0) * 4 : 0x80000000u);
+  };
+
+  f32x16 dka[PDT], dva[PDT];
+#pragma unroll
+  for (int dt = 0; dt < PDT; ++dt) dka[dt] = dva[dt] = f32x16{};
+  const float sl = a.sl;
+  const int64_t kd64 = static_cast<int64_t>(key) - p.offset;
+  const int kdiff = kd64 < -(1 << 30) ? -(1 << 30) : static_cast<int>(kd64);
+
+  issue(0);
+  wait_vm_n<0>();
+#pragma unroll
+  for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
+  __syncthreads();
+
+  for (int it = 0; it < n_iter; ++it) {
+    const char *qt = lds + (it & 1) * STAGE;
+    const char *gt = qt + TL::BYTES;
+    const float *rvl = reinterpret_cast<const float *>(qt + 2 * TL::BYTES);  // nl [32] | nd [32]
+    const int r = it / n_qt, qi = it - r * n_qt;
+    const int q0 = q_start + qi * BN;
+    issue(it + 1);
+    // S = Q K^T, dP = dO V^T over the tile's 32 rows x this wave's 32 keys
+    f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      constexpr int NC = HD / 4;
+      float4 qc[2], gc[2];
+      qc[0] = TL::chunk(qt, c, h * NC);
+      gc[0] = TL::chunk(gt, c, h * NC);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int jj = 0; jj < NC; ++jj) {
+        if (jj + 1 < NC) {
+          qc[(jj + 1) & 1] = TL::chunk(qt, c, h * NC + jj + 1);
+          gc[(jj + 1) & 1] = TL::chunk(gt, c, h * NC + jj + 1);
+        }
+        const float4 qv = qc[jj & 1], gv = gc[jj & 1];
+        s = mfma32f(qv.x, kf[4 * jj], s);
+        dp = mfma32f(gv.x, vf[4 * jj], dp);
+        s = mfma32f(qv.y, kf[4 * jj + 1], s);
+        dp = mfma32f(gv.y, vf[4 * jj + 1], dp);
+        s = mfma32f(qv.z, kf[4 * jj + 2], s);
+        dp = mfma32f(gv.z, vf[4 * jj + 2], dp);
+        s = mfma32f(qv.w, kf[4 * jj + 3], s);
+        dp = mfma32f(gv.w, vf[4 * jj + 3], dp);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // element i: row q0 + crow(i, h), key `key`; allowed iff the key is live,
+    // the row exists and (causal) key - offset <= row
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = 8 * (i >> 2) + 4 * h + (i & 3);
+      const bool ok = key_live && (q0 + rr < p.Sq) && (!p.causal || kdiff <= q0 + rr);
+      const float pv = ok ? fast_exp2((s[i] + rvl[rr]) * sl) : 0.f;
+      s[i] = pv;
+      dp[i] = pv * (dp[i] + rvl[BN + rr]);
+    }
+    // dV^T += dO^T P, dK^T += Q^T dS: step i takes rows crow(i, h)
+    {
+      constexpr int NS_ = 16 * PDT, FD = 2;
+      float gfr[FD + 1], qfr[FD + 1];
+      auto load = [&](int t) {
+        const int i = t / PDT, dt = t % PDT, rr = 8 * (i >> 2) + 4 * h + (i & 3);
+        gfr[t % (FD + 1)] = TL::elem(gt, rr, 32 * dt + c);
+        qfr[t % (FD + 1)] = TL::elem(qt, rr, 32 * dt + c);
+      };
+#pragma unroll
+      for (int t = 0; t < FD; ++t) load(t);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < NS_; ++t) {
+        if (t + FD < NS_) load(t + FD);
+        dva[t % PDT] = mfma32f(gfr[t % (FD + 1)], s[t / PDT], dva[t % PDT]);
+        dka[t % PDT] = mfma32f(qfr[t % (FD + 1)], dp[t / PDT], dka[t % PDT]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    wait_vm_n<0>();
+    __syncthreads();
+  }
+  if (key < p.Sk) {
+    float *krow = static_cast<float *>(const_cast<void *>(a.dk.data)) + b * a.dk.s0 + hk * a.dk.s1 +
+                  static_cast<int64_t>(key) * a.dk.s2;
+    float *vrow = static_cast<float *>(const_cast<void *>(a.dv.data)) + b * a.dv.s0 + hk * a.dv.s1 +
+                  static_cast<int64_t>(key) * a.dv.s2;
+    const float sc = a.scale;
+#pragma unroll
+    for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        *reinterpret_cast<float4 *>(krow + 32 * dt + 8 * g + 4 * h) =
+            float4{dka[dt][4 * g] * sc, dka[dt][4 * g + 1] * sc, dka[dt][4 * g + 2] * sc, dka[dt][4 * g + 3] * sc};
+        *reinterpret_cast<float4 *>(vrow + 32 * dt + 8 * g + 4 * h) =
+            float4{dva[dt][4 * g], dva[dt][4 * g + 1], dva[dt][4 * g + 2], dva[dt][4 * g + 3]};
+      }
+  }
+}
+
+template <int D>
+void launch_bwd_dims(const F32Args &a, hipStream_t st) {
+  const Problem &p = a.p;
+  {
+    Probe pr_("bwd_rows_f32", st);
+    const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
+    const int64_t per_block = NW * (64 / (D / 4));
+    rows_f32_kernel<D><<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)), dim3(NT), 0, st>>>(a);
+  }
+  {
+    Probe pr_("bwd_dq_mfma_f32", st);
+    const int n_qb = (p.Sq + BM - 1) / BM;
+    dq_f32_kernel<D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+  }
+  {
+    Probe pr_("bwd_dkdv_mfma_f32", st);
+    const int n_kb = (p.Sk + KB - 1) / KB;
+    dkdv_f32_kernel<D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+  }
+}
+
+template <int D>
+void launch_fwd_dims(const F32Args &a, hipStream_t st) {
+  const int n_qb = (a.p.Sq + BM - 1) / BM;
+  fwd_f32_kernel<D><<<dim3(n_qb * a.p.Hq * a.p.B), dim3(NT), 0, st>>>(a);
+}
+
+}  // namespace
+
+hipError_t launch_mfma_f32_backward(const Problem &p, View q, View k, View v, View o, View dout,
+                                    const float *lse, View dq, View dk, View dv, float *rows,
+                                    hipStream_t st) {
+  F32Args a{};
+  a.p = p;
+  a.q = q, a.k = k, a.v = v, a.o = o, a.dout = dout, a.dq = dq, a.dk = dk, a.dv = dv;
+  a.lse = const_cast<float *>(lse);
+  a.rows = rows;
+  a.sl = static_cast<float>(p.scale) * kLog2e;
+  a.scale = static_cast<float>(p.scale);
+  if (p.Dqk == 128) launch_bwd_dims<128>(a, st);
+  else if (p.Dqk == 64) launch_bwd_dims<64>(a, st);
+  else launch_bwd_dims<32>(a, st);
+  return hipGetLastError();
+}
+
+bool mfma_f32_supported(const Problem &p, int dtype) {
+  if (dtype != TSATTN_F32 || p.Dqk != p.Dv) return false;
+  if (p.Dqk != 32 && p.Dqk != 64 && p.Dqk != 128) return false;
+  if (!(p.scale > 0.0) || p.drop.on || p.rope.R > 0) return false;
+  // masks: none, or a [B,1,1,K] boolean key mask reduced to lengths
+  return p.mask.kind == TSATTN_MASK_NONE ||
+         (p.mask.kind == TSATTN_MASK_BOOL && p.mask.s1 == 0 && p.mask.s2 == 0 && p.kv_len != nullptr);
+}
+
+hipError_t launch_mfma_f32_forward(const Problem &p, View q, View k, View v, View o, float *lse,
+                                   hipStream_t st) {
+  F32Args a{};
+  a.p = p;
+  a.q = q, a.k = k, a.v = v, a.o = o;
+  a.lse = lse;
+  a.sl = static_cast<float>(p.scale) * kLog2e;
+  a.scale = static_cast<float>(p.scale);
+  Probe pr_("fwd_mfma_f32", st);
+  if (p.Dqk == 128) launch_fwd_dims<128>(a, st);
+  else if (p.Dqk == 64) launch_fwd_dims<64>(a, st);
+  else launch_fwd_dims<32>(a, st);
+  return hipGetLastError();
+}
+
+}  // namespace tsattn

@@ -189,6 +189,16 @@ int mfma_ds_chunk_groups(const Problem &p);
 // rotated query rows [B, Hq, Sq, Dqk] (16-bit) from this byte offset on.
 size_t mfma_rope_stage_offset(const Problem &p);
 
+// fp32 MFMA kernels (mfma_f32.hip): fp32, Dqk = Dv in {32, 64, 128}, no
+// dropout / folded RoPE, masks none or a key mask reduced to lengths.
+bool mfma_f32_supported(const Problem &p, int dtype);
+hipError_t launch_mfma_f32_forward(const Problem &p, View q, View k, View v, View o, float *lse,
+                                   hipStream_t st);
+// rows: the backward workspace's row values (2 B Hq Sq floats).
+hipError_t launch_mfma_f32_backward(const Problem &p, View q, View k, View v, View o, View dout,
+                                    const float *lse, View dq, View dk, View dv, float *rows,
+                                    hipStream_t st);
+
 // Split-K decode.
 bool decode_supported(const Problem &p, int dtype);
 size_t decode_workspace_bytes(const Problem &p, int split_len);
