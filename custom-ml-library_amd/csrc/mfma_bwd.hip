@@ -84,6 +84,13 @@ __host__ __device__ __forceinline__ int64_t ds_row_start(int tri, int nkt, int q
 }
 
 constexpr int DS_TILE = 2048;  // bytes of one stored dS tile
+
+// a if B, else c (of another type).
+template <bool B, typename X, typename Y>
+__device__ __forceinline__ const auto &pick(const X &a, const Y &c) {
+  if constexpr (B) return a;
+  else return c;
+}
 constexpr int kStreamStore = 18;  // buffer store cache policy: sc1 (16) | nt (2)
 
 template <typename T>
@@ -230,15 +237,74 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // wave's blocks are w, w + 4, ..., all with n % QG = w % QG.
   const uint32_t swz_chunk = (lane & 3) ^ ((lane >> 4) & 3);
   const uint32_t lrow = lane >> 2;
-  // Tile itn is query tile qi = itn % n_qt of query head hk rep + itn / n_qt;
-  // TileIdx walks that order without a division per tile.
-  // It also carries the byte addresses of the tile's Q, dO and row-value
-  // slices, advanced by one head when the walk wraps (no 64-bit products per
-  // tile).
+  // Tile itn is query tile qi = itn % n_qt of query head hk rep + r, r =
+  // itn / n_qt.  Two cursors walk that order without a division or a 64-bit
+  // product per tile: the issue cursor (the tile whose DMA loads go out, KV_PD
+  // tiles ahead) and the read cursor (the tile being computed).  Per tile a
+  // cursor moves its ring stage and its row offsets on by one tile; the move
+  // to the next query head, once per n_qt tiles, is a scalar branch that
+  // rebuilds the head's buffer descriptors.  Past the last head the issue
+  // cursor's descriptors are empty, so the loads issued past the last tile
+  // read zeros without touching memory, into the ring stages of tiles already
+  // consumed: every iteration issues the same loads, the waits are constants
+  // and no branch guards an issue.
+  //
+  // The dropout kernels keep a per-tile form instead (TileIdx / TileDma
+  // below): at D = 128 their registers are full, and the cursors' branches
+  // and held descriptors move their spills into the loop (an accumulator
+  // block reloaded every tile, 1.9x the dK/dV time).
   const uint64_t qstep = static_cast<uint64_t>(a.qk.s1) * 2, gstep = static_cast<uint64_t>(a.dout.s1) * 2;
   const uint64_t rstep = static_cast<uint64_t>(p.Sq) * 4;
   // With stored dS, da is the byte offset of the tile's head slice.
   const uint64_t dwrap = static_cast<uint64_t>(a.ds_slice) * DS_TILE;
+  const uint32_t q_bytes = static_cast<uint32_t>(p.Sq) * qs_b, g_bytes = static_cast<uint32_t>(p.Sq) * gs_b;
+  const uint32_t last_stage = ring0 + (KV_NS - 1) * STAGE_B;
+  // A 1 KiB block past the ring that nothing reads (dropout kernels: the
+  // loads past the last tile; every kernel: the prologue's stand-ins for dS
+  // stores).
+  const uint32_t spare = ring0 + KV_NS * STAGE_B;
+  // nl (waves 0, 2) / nd (waves 1, 3) rows of the group's first query head;
+  // waves 2, 3 load the same rows as 0, 1 (the same bytes to the same place;
+  // dropout kernels: into the spare block)
+  const float *rowv =
+      a.delta + (static_cast<int64_t>(b) * p.Hq + hk * p.rep) * p.Sq + ((DR ? w : w & 1) == 0 ? rows : 0);
+  struct IssueCur {
+    int qi, r;
+    uint32_t st;          // LDS address of the tile's ring stage
+    uint32_t qo, go, ro;  // byte offsets of the tile's first row in the head's Q, dO, row values
+    uint32_t far;         // 0 for a real tile, 2^31 past the last head
+    uint64_t qa, ga, ra;  // the head's Q, dO and row-value slices
+    u32x4 qdesc, gdesc, rdesc;
+  };
+  auto set_head = [&](IssueCur &c) {
+    const bool real = c.r < p.rep;
+    c.far = real ? 0u : 0x80000000u;
+    c.qo = static_cast<uint32_t>(q_start) * qs_b;
+    c.go = static_cast<uint32_t>(q_start) * gs_b;
+    c.ro = static_cast<uint32_t>(q_start) * 4;
+    c.qdesc = make_desc(reinterpret_cast<const void *>(c.qa), real ? q_bytes : 0u);
+    c.gdesc = make_desc(reinterpret_cast<const void *>(c.ga), real ? g_bytes : 0u);
+    c.rdesc = make_desc(reinterpret_cast<const void *>(c.ra), real ? static_cast<uint32_t>(p.Sq) * 4 : 0u);
+  };
+  auto issue_next = [&](IssueCur &c) {
+    c.st = c.st == last_stage ? ring0 : c.st + STAGE_B;
+    c.qo += QT * qs_b;
+    c.go += QT * gs_b;
+    c.ro += QT * 4;
+    if (++c.qi == n_qt) {
+      asm volatile("");  // (a branch taken once per head, not selects on every tile)
+      c.qi = 0;
+      ++c.r;
+      c.qa += qstep;
+      c.ga += gstep;
+      c.ra += rstep;
+      set_head(c);
+    }
+  };
+  // Dropout kernels: TileIdx walks the order with selects, carrying the
+  // head's slice addresses; TileDma holds one tile's load arguments, its
+  // stage addressed from the spare block and masked by keep (all ones for a
+  // real tile, else 0: tiles past the last one land in the spare block).
   struct TileIdx {
     int itn, r, qi;
     uint64_t qa, ga, ra, da;
@@ -254,16 +320,6 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     t.da += wrap ? dwrap : 0;
     return t;
   };
-  // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
-  // this wave's u-th Q / dO block, part LPT the nl / nd rows (waves 0, 1;
-  // waves 2, 3 load past the range into the spare block, so every wave
-  // issues the same count).  Tiles past the last one (itn >= n_iter) read
-  // at offsets >= 2^31 -- past every range: zeros, no memory access -- into
-  // the spare block: every iteration issues the same loads, so the waits are
-  // constants and no branch guards an issue.  keep = all ones for a real
-  // tile, else 0 (masks, not selects, which the compiler turns into
-  // branches between the MFMA steps).
-  const uint32_t spare = ring0 + KV_NS * STAGE_B;
   struct TileDma {
     uint32_t st, keep, far;
     int q0, hq;
@@ -277,25 +333,43 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     t.keep = ~static_cast<uint32_t>((n_iter - 1 - x.itn) >> 31);  // sign fill
     t.far = ~t.keep & 0x80000000u;
     t.st = (ring0 + (x.itn % KV_NS) * STAGE_B - spare) & t.keep;
-    t.qdesc = make_desc(reinterpret_cast<const void *>(x.qa), static_cast<uint32_t>(p.Sq) * qs_b);
-    t.gdesc = make_desc(reinterpret_cast<const void *>(x.ga), static_cast<uint32_t>(p.Sq) * gs_b);
+    t.qdesc = make_desc(reinterpret_cast<const void *>(x.qa), q_bytes);
+    t.gdesc = make_desc(reinterpret_cast<const void *>(x.ga), g_bytes);
     t.ra = x.ra;
     return t;
   };
+  // A tile's query head, first row and the LDS address of byte `off` of its
+  // stage, from either form.
+  auto t_hq = [&](const auto &t) {
+    if constexpr (DR) return t.hq;
+    else return hk * p.rep + t.r;
+  };
+  auto t_q0 = [&](const auto &t) {
+    if constexpr (DR) return t.q0;
+    else return q_start + t.qi * QT;
+  };
+  auto t_lds = [&](const auto &t, uint32_t off) {
+    if constexpr (DR) return spare + t.st + (off & t.keep);
+    else return t.st + off;
+  };
+  // DMA of a tile into its ring stage, in LPT + 1 parts: part u < LPT is
+  // this wave's u-th Q / dO block, part LPT the nl / nd rows.
   // Parts u < QPARTS are Q blocks, the rest dO blocks (a compile-time split).
   const uint32_t qvoff = lrow * qs_b + (4 * (w % QGQ) + swz_chunk) * 16;
   const uint32_t gvoff = lrow * gs_b + (4 * (w % QGG) + swz_chunk) * 16;
-  // nl (wave 0) / nd (wave 1) rows of the group's first query head
-  const float *rowv = a.delta + (static_cast<int64_t>(b) * p.Hq + hk * p.rep) * p.Sq + (w == 0 ? rows : 0);
-  auto issue_q = [&](const TileDma &t, int n) {
-    dma16(t.qdesc, spare + t.st + ((n * 1024) & t.keep), qvoff,
-          (static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b) | t.far);
+  auto issue_q = [&](const auto &t, int n) {
+    if constexpr (DR)
+      dma16(t.qdesc, t_lds(t, n * 1024), qvoff, (static_cast<uint32_t>(t.q0 + 16 * (n / QGQ)) * qs_b) | t.far);
+    else
+      dma16(t.qdesc, t_lds(t, n * 1024), qvoff, t.qo + static_cast<uint32_t>(16 * (n / QGQ)) * qs_b);
   };
-  auto issue_g = [&](const TileDma &t, int n) {
-    dma16(t.gdesc, spare + t.st + ((TILE_Q + n * 1024) & t.keep), gvoff,
-          (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
+  auto issue_g = [&](const auto &t, int n) {
+    if constexpr (DR)
+      dma16(t.gdesc, t_lds(t, TILE_Q + n * 1024), gvoff, (static_cast<uint32_t>(t.q0 + 16 * (n / QGG)) * gs_b) | t.far);
+    else
+      dma16(t.gdesc, t_lds(t, TILE_Q + n * 1024), gvoff, t.go + static_cast<uint32_t>(16 * (n / QGG)) * gs_b);
   };
-  auto issue_part = [&](const TileDma &t, int u) {
+  auto issue_part = [&](const auto &t, int u) {
     if (u < LPT) {
       if constexpr (EVEN) {
         if (u < QPARTS) issue_q(t, w + NW * u);
@@ -304,9 +378,8 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
         if (w < QBLK) issue_q(t, w);  // (w is wave-uniform: a scalar branch)
         else issue_g(t, w - QBLK);
       }
-    } else {
-      const u32x4 rdesc = make_desc(reinterpret_cast<const void *>(t.ra),
-                                    static_cast<uint32_t>(p.Sq) * 4);
+    } else if constexpr (DR) {
+      const u32x4 rdesc = make_desc(reinterpret_cast<const void *>(t.ra), static_cast<uint32_t>(p.Sq) * 4);
       // lane * 16, recomputed here rather than held in a register all loop
       uint32_t loff;
       asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
@@ -316,13 +389,19 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       if (lane < QT / 4)
         dma16(rdesc, spare + (t.st & mine) + ((TILE_Q + TILE_G + w * QT * 4) & mine), loff,
               (static_cast<uint32_t>(t.q0) * 4) | (~mine & 0x80000000u));
+    } else {
+      uint32_t loff;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0\n\t"
+                   "v_lshlrev_b32 %0, 4, %0"
+                   : "=v"(loff));
+      if (lane < QT / 4) dma16(t.rdesc, t.st + TILE_Q + TILE_G + (w & 1) * QT * 4, loff, t.ro);
     }
   };
   // Staged mask: 1 KiB block n = w + NW u of the tile holds rows
   // n * 1024 / MROW ..; lane l fetches 16 bytes at byte 16 l of the block.
   // The lane's offset is recomputed at each issue (no register held all loop:
   // the two-workgroup budget is full).
-  auto issue_mask = [&](const TileDma &t) {
+  auto issue_mask = [&](const auto &t) {
     if constexpr (MSTAGE) {
       const uint32_t ms2 = static_cast<uint32_t>(p.mask.s2 * MES);  // bytes between mask rows
       uint32_t l16;
@@ -332,20 +411,20 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       const uint32_t mvoff = (l16 / MROW) * ms2 + l16 % MROW;
       const int64_t extent = ((p.Sq - 1) * p.mask.s2 + (p.Sk - 1) * p.mask.s3 + 1) * MES;
       const u32x4 mdesc = make_desc(
-          static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + t.hq * p.mask.s1) * MES,
+          static_cast<const char *>(p.mask.data) + (b * p.mask.s0 + t_hq(t) * p.mask.s1) * MES,
           static_cast<uint32_t>(extent));
 #pragma unroll
       for (int u = 0; u < MPARTS; ++u) {
         const int n = w + NW * u;
-        dma16(mdesc, spare + t.st + ((MOFF + n * 1024) & t.keep), mvoff,
-              (static_cast<uint32_t>(t.q0 + n * (1024 / MROW)) * ms2 +
+        dma16(mdesc, t_lds(t, MOFF + n * 1024), mvoff,
+              (static_cast<uint32_t>(t_q0(t) + n * (1024 / MROW)) * ms2 +
                static_cast<uint32_t>(k0 * MES)) | t.far);
       }
     }
   };
   // Dropout: this wave's 32 keep-bit words (key tile kb * 4 + w, rows q0 ..
   // q0 + 31) as one 8-lane DMA part; past the slice they read as zero.
-  auto issue_bits = [&](const TileDma &t) {
+  auto issue_bits = [&](const auto &t) {
     if constexpr (DR) {
       const DropDesc &d = p.drop;
       const u32x4 bdesc = make_desc(d.bits + (static_cast<int64_t>(b) * p.Hq + t.hq) * d.nkt * d.sqp,
@@ -359,8 +438,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
               ((static_cast<uint32_t>(kb * (KB / 32) + w) * d.sqp + t.q0) * 4) | t.far);
     }
   };
-  auto issue = [&](TileIdx x) {
-    const TileDma t = tile_dma(x);
+  auto issue = [&](const auto &t) {
 #pragma unroll
     for (int u = 0; u <= LPT; ++u) issue_part(t, u);
     issue_mask(t);
@@ -394,14 +472,26 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 
   // No zeroing: every LDS byte the loop reads is written by a DMA load first
   // (lanes past a buffer's range write zeros).
-  const TileIdx first{0, 0, 0, reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep)),
-                      reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep)),
-                      reinterpret_cast<uint64_t>(rowv),
-                      static_cast<uint64_t>(bhc) * p.rep * dwrap};
+  IssueCur icur;
+  icur.qi = 0;
+  icur.r = n_qt > 0 ? 0 : p.rep;  // no tile at all: empty descriptors from the start
+  icur.st = ring0;
+  icur.qa = reinterpret_cast<uint64_t>(head_ptr<T>(a.qk, b, hk * p.rep));
+  icur.ga = reinterpret_cast<uint64_t>(head_ptr<T>(a.dout, b, hk * p.rep));
+  icur.ra = reinterpret_cast<uint64_t>(rowv);
+  const TileIdx first{0, 0, 0, icur.qa, icur.ga, icur.ra, static_cast<uint64_t>(bhc) * p.rep * dwrap};
   TileIdx nxt_idx = first;
-  for (int t = 0; t < KV_PD; ++t) {
-    issue(nxt_idx);
-    nxt_idx = tile_next(nxt_idx);
+  if constexpr (DR) {
+    for (int t = 0; t < KV_PD; ++t) {
+      issue(tile_dma(nxt_idx));
+      nxt_idx = tile_next(nxt_idx);
+    }
+  } else {
+    set_head(icur);
+    for (int t = 0; t < KV_PD; ++t) {
+      issue(icur);
+      issue_next(icur);
+    }
   }
   // The K / V loads were issued first, so this also waits for them; resolve
   // them here, where the compiler's own vmcnt waits (which do not count the
@@ -422,19 +512,55 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   }
   __syncthreads();
 
+  // Read cursor: the tile's ring stage, query head, first row and (stored
+  // dS) its dS row within the head's slice, advanced like the issue cursor.
+  const int ds_row0 = static_cast<int>(ds_row_start(a.ds_tri, a.ds_nkt, q_start / QT));
+  int cur_st = 0, cur_r = 0, cur_qi = 0, cur_q0 = q_start, cur_row = ds_row0;
+  uint64_t cur_da = first.da;
   TileIdx cur_idx = first;
   for (int itn = 0; itn < n_iter; ++itn) {
     // Tile itn + 2 is issued between the S / dP MFMA steps below, so a wave
     // never stalls on the address unit before its first MFMA.
-    const TileDma nxt = tile_dma(nxt_idx);
-    nxt_idx = tile_next(nxt_idx);
-    const char *qt = ring + (itn % KV_NS) * STAGE_B;
+    // (not an immediately-invoked lambda: one taking nxt_idx by reference
+    // moves the dropout kernels' spills into this loop)
+    TileDma tdma;
+    if constexpr (DR) {
+      tdma = tile_dma(nxt_idx);
+      nxt_idx = tile_next(nxt_idx);
+    }
+    const auto &nxt = pick<DR>(tdma, icur);
+    int st_off, hq, q0;
+    uint64_t cur_idx_da;
+    uint32_t ds_tile;
+    if constexpr (DR) {
+      st_off = (itn % KV_NS) * STAGE_B;
+      hq = hk * p.rep + cur_idx.r;
+      q0 = q_start + cur_idx.qi * QT;
+      cur_idx_da = cur_idx.da;
+      ds_tile = static_cast<uint32_t>((ds_row_start(a.ds_tri, a.ds_nkt, q0 / QT) + kw / 32) * DS_TILE);
+      cur_idx = tile_next(cur_idx);
+    } else {
+      st_off = cur_st;
+      hq = hk * p.rep + cur_r;
+      q0 = cur_q0;
+      cur_idx_da = cur_da;
+      ds_tile = static_cast<uint32_t>(cur_row + kw / 32) * DS_TILE;
+      cur_st = cur_st == (KV_NS - 1) * STAGE_B ? 0 : cur_st + STAGE_B;
+      cur_q0 += QT;
+      // dS rows: row qt holds 4 (qt / 4 + 1) tiles (packed causal) or ds_nkt
+      cur_row += a.ds_tri ? 4 * static_cast<int>(static_cast<uint32_t>(q0) / (4 * QT) + 1) : a.ds_nkt;
+      if (++cur_qi == n_qt) {
+        asm volatile("");  // (a branch taken once per head)
+        cur_qi = 0;
+        ++cur_r;
+        cur_q0 = q_start;
+        cur_row = ds_row0;
+        cur_da += dwrap;
+      }
+    }
+    const char *qt = ring + st_off;
     const char *gt = qt + TILE_Q;
     const float *rv = reinterpret_cast<const float *>(qt + TILE_Q + TILE_G);
-    const int hq = hk * p.rep + cur_idx.r, q0 = q_start + cur_idx.qi * QT;
-    const uint64_t cur_idx_da = cur_idx.da;
-    const int64_t ds_tile = (ds_row_start(a.ds_tri, a.ds_nkt, q0 / QT) + kw / 32) * DS_TILE;
-    cur_idx = tile_next(cur_idx);
 
     constexpr int FD = DKDV_FD;
     // A general mask: this tile's elements (b, hq, q0 + 4h + kc, key), kc
@@ -489,6 +615,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       }
       __builtin_amdgcn_s_setprio(0);
     }
+    if constexpr (!DR) issue_next(icur);
 
     // P = exp2(sacc sl), dS = P dpacc; rows crow(e, h) = 8 g + 4 h + e % 4.
     const bool edge = MK != 0 || keymask || kw + 32 > kv_end || q0 + QT > p.Sq ||
@@ -629,10 +756,13 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
     wait_lgkm0();
     phase_barrier();
   }
-  wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
+  // The loads issued past the last tile land in the ring (dropout kernels:
+  // the spare block): every wave's have landed before any wave's epilogue
+  // writes there.
+  wait_vm_n<0>();
+  if constexpr (!DR) __syncthreads();
 
-  // Epilogue.  The loop ended on a barrier after every wave's last LDS read,
-  // so the ring is free.  Each wave rounds its rows and stages them in its own
+  // Epilogue.  The ring is free.  Each wave rounds its rows and stages them in its own
   // slice of the ring -- key row r (0..31) at r * 2DX bytes, 16-byte chunk q
   // at q ^ (r % CPR), the XOR keeping the row writes off one bank -- then
   // reads them back as whole 16-byte chunks of rows, so the global stores are
