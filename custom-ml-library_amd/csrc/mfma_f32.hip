@@ -73,6 +73,18 @@ struct FTile {
   }
 };
 
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cus[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cus[dev]) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
 struct F32Args {
   Problem p;
   View q, k, v, o, dout, dq, dk, dv;
@@ -90,40 +102,55 @@ struct F32Args {
 // the online softmax on its lane's query column (lazy rescale, exp2 domain),
 // and O^T += V^T P^T (D / 2 MFMAs, V by 32-float row segments, P^T the fp32
 // accumulator registers).  Two workgroups per CU.
+//
+// SPLIT (problems with fewer 128-row workgroups than CUs, D <= 64): one
+// workgroup = 32 query rows, all 4 waves on them; wave w takes key tiles w,
+// w + 4, ... through its own double-buffered LDS ring (no barrier in the
+// loop), and the waves' (max, sum, O) merge through LDS at the end as the
+// online softmax merges tiles: the key loop of a row block runs 4 ways
+// parallel.  One workgroup per CU.
 // ---------------------------------------------------------------------------
-template <int D>
-__global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
+template <int D, bool SPLIT>
+__global__ __launch_bounds__(NT, SPLIT ? 1 : 2) void fwd_f32_kernel(F32Args a) {
   using TL = FTile<D>;
   constexpr int HD = D / 2;             // MFMA steps over the head dimension
   constexpr int PDT = D / 32;           // 32-row blocks of O^T
   constexpr int STAGE = 2 * TL::BYTES;  // K | V
-  constexpr int PARTS = 2 * TL::BLOCKS / NW;  // DMA blocks per wave per tile
-  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
-  // two stages, then a 1 KiB block the parts of a tile past the last land in
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+  constexpr int ROWS = SPLIT ? 32 : BM;  // query rows per workgroup
+  constexpr int RINGS = SPLIT ? NW : 1;  // double-buffered rings (one per wave when split)
+  constexpr int STRIDE = SPLIT ? NW : 1;  // tiles between a wave's consecutive tiles
+  // DMA blocks per wave per tile: a wave loads its whole tile when split
+  constexpr int PARTS = SPLIT ? 2 * TL::BLOCKS : 2 * TL::BLOCKS / NW;
+  static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
+  static_assert(PARTS <= 2 * (HD / 4), "at most two DMA parts per S step");
+  // the rings, then a 1 KiB block the parts of a tile past the last land in
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n_qb = (p.Sq + BM - 1) / BM;
+  const int n_qb = (p.Sq + ROWS - 1) / ROWS;
   const int total = n_qb * p.Hq * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, rank;
-  heavy_first(logical, n_qb, p.Hq * p.B, 64, bh, rank);
+  heavy_first(logical, n_qb, p.Hq * p.B, SPLIT ? 32 : 64, bh, rank);
   const int qb = n_qb - 1 - rank;
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
-  const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
+  const int q0 = qb * ROWS, qw = SPLIT ? q0 : q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
 
   int64_t lim = kv_end, wlim = kv_end;
   if (p.causal) {
-    lim = min(lim, static_cast<int64_t>(min(q0 + BM, p.Sq) - 1) + p.offset + 1);
+    lim = min(lim, static_cast<int64_t>(min(q0 + ROWS, p.Sq) - 1) + p.offset + 1);
     wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
   }
   if (qw >= p.Sq) wlim = 0;
   const int n_tiles = __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0);
   const int w_tiles = __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0);
+  // this wave's tiles: j = first + STRIDE jj, jj < my_tiles
+  const int first = SPLIT ? w : 0;
+  const int my_tiles = SPLIT ? (n_tiles > w ? (n_tiles - 1 - w) / NW + 1 : 0) : n_tiles;
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4;
@@ -142,14 +169,18 @@ __global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
   }
 
   const uint32_t lds0 = lds_addr(lds);
-  const uint32_t spare = lds0 + 2 * STAGE;
-  // Part u of wave w is block n = w + NW u of the stage: K blocks first.
-  // A tile past the last one reads past the buffer ranges (zeros, no memory
-  // access) into the spare block, so every wave issues the same parts.
-  auto issue_part = [&](int tile, int u) {
-    const int n = w + NW * u;
+  const uint32_t ring = lds0 + (SPLIT ? w * 2 * STAGE : 0);
+  const char *ring_p = lds + (SPLIT ? w * 2 * STAGE : 0);
+  const uint32_t spare = lds0 + RINGS * 2 * STAGE;
+  // Part u of this wave's share of local tile jj (tile first + STRIDE jj):
+  // block n = w + NW u of the stage (split: n = u), K blocks first.  A tile
+  // past the last one reads past the buffer ranges (zeros, no memory access)
+  // into the spare block, so every wave issues the same parts.
+  auto issue_part = [&](int jj, int u) {
+    const int n = SPLIT ? u : w + NW * u;
+    const int tile = first + STRIDE * jj;
     const bool real = tile < n_tiles;
-    const uint32_t st = real ? lds0 + (tile & 1) * STAGE : spare;
+    const uint32_t st = real ? ring + (jj & 1) * STAGE : spare;
     if (n < TL::BLOCKS) {
       const uint32_t so = real ? static_cast<uint32_t>(tile * BN + n * TL::RPB) * ks_b : 0x80000000u;
       dma16(kdesc, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, ks_b), so);
@@ -184,12 +215,13 @@ __global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
   wait_vm_n<0>();  // the query fragments and the first tile
 #pragma unroll
   for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]));
-  __syncthreads();
+  if constexpr (!SPLIT) __syncthreads();
 
-  for (int j = 0; j < n_tiles; ++j) {
-    const char *kt = lds + (j & 1) * STAGE;
+  for (int jj = 0; jj < my_tiles; ++jj) {
+    const int j = first + STRIDE * jj;
+    const char *kt = ring_p + (jj & 1) * STAGE;
     const char *vt = kt + TL::BYTES;
-    if (j < w_tiles) {
+    if (SPLIT || j < w_tiles) {
       // S^T = K Q^T, the next tile's parts spread over the steps; each
       // 16-byte chunk of K serves four steps, read one chunk ahead
       f32x16 s = f32x16{};
@@ -199,14 +231,16 @@ __global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
         kc[0] = TL::chunk(kt, c, h * NC);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jj = 0; jj < NC; ++jj) {
-          if (jj + 1 < NC) kc[(jj + 1) & 1] = TL::chunk(kt, c, h * NC + jj + 1);
-          const float4 kv = kc[jj & 1];
-          s = mfma32f(kv.x, qf[4 * jj], s);
-          s = mfma32f(kv.y, qf[4 * jj + 1], s);
-          s = mfma32f(kv.z, qf[4 * jj + 2], s);
-          s = mfma32f(kv.w, qf[4 * jj + 3], s);
-          if (jj < PARTS) issue_part(j + 1, jj);
+        for (int q = 0; q < NC; ++q) {
+          if (q + 1 < NC) kc[(q + 1) & 1] = TL::chunk(kt, c, h * NC + q + 1);
+          const float4 kv = kc[q & 1];
+          s = mfma32f(kv.x, qf[4 * q], s);
+          s = mfma32f(kv.y, qf[4 * q + 1], s);
+          s = mfma32f(kv.z, qf[4 * q + 2], s);
+          s = mfma32f(kv.w, qf[4 * q + 3], s);
+          if (2 * q < PARTS && PARTS > NC) issue_part(jj + 1, 2 * q);
+          if (2 * q + 1 < PARTS && PARTS > NC) issue_part(jj + 1, 2 * q + 1);
+          if (q < PARTS && PARTS <= NC) issue_part(jj + 1, q);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -266,29 +300,81 @@ __global__ __launch_bounds__(NT, 2) void fwd_f32_kernel(F32Args a) {
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < PARTS; ++u) issue_part(j + 1, u);
+      for (int u = 0; u < PARTS; ++u) issue_part(jj + 1, u);
     }
-    wait_vm_n<0>();  // tile j + 1 has landed
-    __syncthreads();
+    wait_vm_n<0>();  // tile jj + 1 has landed
+    if constexpr (SPLIT) {
+      // this wave's ring only: its LDS reads of the stage the next DMA
+      // overwrites are done once they have returned
+      wait_lgkm0();
+    } else {
+      __syncthreads();
+    }
   }
 
   // O rows: lane holds O^T[d = 32 dt + 8 g + 4 h + r][row c], four consecutive
   // channels per (dt, g): one 16-byte store each.
+  float *orow = static_cast<float *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
+                static_cast<int64_t>(qrow < p.Sq ? qrow : 0) * a.o.s2;
   const float lt = xor32_sum(l);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qrow < p.Sq) {
-    float *orow = static_cast<float *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1 +
-                  static_cast<int64_t>(qrow) * a.o.s2;
+  if constexpr (!SPLIT) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    if (qrow < p.Sq) {
+#pragma unroll
+      for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
+              float4{oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv, oacc[dt][4 * g + 2] * inv,
+                     oacc[dt][4 * g + 3] * inv};
+      if (a.lse && h == 0)
+        a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
+            lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+    }
+  } else {
+    // Merge the waves' partial rows: max mf = max_w m_w, sum L = sum_w l_w
+    // 2^(m_w - mf), O = sum_w O_w 2^(m_w - mf) / L, in wave order.  Wave w
+    // stores the (dt, g) groups w, w + 4, ...
+    wait_vm_n<0>();
+    __syncthreads();  // every wave's loop is done (and its past-the-end loads landed)
+    float *cm = reinterpret_cast<float *>(lds);  // [NW][32] maxima
+    float *cl = cm + NW * 32;                     // [NW][32] sums
+    float *co = cl + NW * 32;                     // [NW][PDT][16][64] O^T registers
+    if (h == 0) {
+      cm[w * 32 + c] = m;
+      cl[w * 32 + c] = lt;
+    }
 #pragma unroll
     for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+      for (int i = 0; i < 16; ++i) co[((w * PDT + dt) * 16 + i) * 64 + lane] = oacc[dt][i];
+    __syncthreads();
+    float mf = -INFINITY;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) mf = fmaxf(mf, cm[v * 32 + c]);
+    float sc[NW], lsum = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) {
+      const float mv = cm[v * 32 + c];
+      sc[v] = mv == -INFINITY ? 0.f : fast_exp2(mv - mf);
+      lsum += cl[v * 32 + c] * sc[v];
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    if (qrow < p.Sq) {
+      for (int grp = w; grp < PDT * 4; grp += NW) {
+        const int dt = grp >> 2, g = grp & 3;
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < NW; ++v)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4[r] = fmaf(co[((v * PDT + dt) * 16 + 4 * g + r) * 64 + lane], sc[v], o4[r]);
         *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
-            float4{oacc[dt][4 * g] * inv, oacc[dt][4 * g + 1] * inv, oacc[dt][4 * g + 2] * inv,
-                   oacc[dt][4 * g + 3] * inv};
-    if (a.lse && h == 0)
-      a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
-          lt > 0.f ? (m + log2f(lt)) * kLn2 : -INFINITY;
+            float4{o4[0] * inv, o4[1] * inv, o4[2] * inv, o4[3] * inv};
+      }
+      if (a.lse && w == 0 && h == 0)
+        a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
+            lsum > 0.f ? (mf + log2f(lsum)) * kLn2 : -INFINITY;
+    }
   }
 }
 
@@ -330,37 +416,46 @@ __global__ __launch_bounds__(NT) void rows_f32_kernel(F32Args a) {
 // registers), P = exp2((S + nl) sl) and dS = P (dP + nd) on its lane's query
 // column, then dQ^T += K^T dS^T (K by 32-float row segments, dS^T the
 // accumulator registers).  dQ = scale dQ^T^T.
+//
+// SPLIT (as the forward's): one workgroup = 32 query rows, wave w takes key
+// tiles w, w + 4, ... through its own ring, and the waves' dQ^T partial sums
+// add up through LDS in wave order at the end.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool SPLIT>
 __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
   using TL = FTile<D>;
   constexpr int HD = D / 2, PDT = D / 32;
   constexpr int STAGE = 2 * TL::BYTES;  // K | V
-  constexpr int PARTS = 2 * TL::BLOCKS / NW;
-  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+  constexpr int ROWS = SPLIT ? 32 : BM;
+  constexpr int RINGS = SPLIT ? NW : 1, STRIDE = SPLIT ? NW : 1;
+  constexpr int PARTS = SPLIT ? 2 * TL::BLOCKS : 2 * TL::BLOCKS / NW;
+  static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
+  static_assert(PARTS <= 2 * (HD / 4), "at most two DMA parts per S step");
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n_qb = (p.Sq + BM - 1) / BM;
+  const int n_qb = (p.Sq + ROWS - 1) / ROWS;
   const int total = n_qb * p.Hq * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, rank;
   heavy_first(logical, n_qb, p.Hq * p.B, 32, bh, rank);
   const int qb = n_qb - 1 - rank;
   const int b = bh / p.Hq, hq = bh - b * p.Hq, hk = hq / p.rep;
-  const int q0 = qb * BM, qw = q0 + 32 * w, qrow = qw + c;
+  const int q0 = qb * ROWS, qw = SPLIT ? q0 : q0 + 32 * w, qrow = qw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   int64_t lim = kv_end, wlim = kv_end;
   if (p.causal) {
-    lim = min(lim, static_cast<int64_t>(min(q0 + BM, p.Sq) - 1) + p.offset + 1);
+    lim = min(lim, static_cast<int64_t>(min(q0 + ROWS, p.Sq) - 1) + p.offset + 1);
     wlim = min(wlim, static_cast<int64_t>(min(qw + 32, p.Sq) - 1) + p.offset + 1);
   }
   if (qw >= p.Sq) wlim = 0;
   const int n_tiles = __builtin_amdgcn_readfirstlane(lim > 0 ? static_cast<int>((lim + BN - 1) / BN) : 0);
   const int w_tiles = __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + BN - 1) / BN) : 0);
+  const int first = SPLIT ? w : 0;
+  const int my_tiles = SPLIT ? (n_tiles > w ? (n_tiles - 1 - w) / NW + 1 : 0) : n_tiles;
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4, gs_b = static_cast<uint32_t>(a.dout.s2) * 4;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4, vs_b = static_cast<uint32_t>(a.v.s2) * 4;
@@ -382,11 +477,15 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
   const float nd = a.rows[rix], nl = a.rows[rows + rix];
 
   const uint32_t lds0 = lds_addr(lds);
-  const uint32_t spare = lds0 + 2 * STAGE;
-  auto issue_part = [&](int tile, int u) {
-    const int n = w + NW * u;
+  const uint32_t ring = lds0 + (SPLIT ? w * 2 * STAGE : 0);
+  const char *ring_p = lds + (SPLIT ? w * 2 * STAGE : 0);
+  const uint32_t spare = lds0 + RINGS * 2 * STAGE;
+  // part u of local tile jj (tile first + STRIDE jj), as in the forward
+  auto issue_part = [&](int jj, int u) {
+    const int n = SPLIT ? u : w + NW * u;
+    const int tile = first + STRIDE * jj;
     const bool real = tile < n_tiles;
-    const uint32_t st = real ? lds0 + (tile & 1) * STAGE : spare;
+    const uint32_t st = real ? ring + (jj & 1) * STAGE : spare;
     if (n < TL::BLOCKS) {
       const uint32_t so = real ? static_cast<uint32_t>(tile * BN + n * TL::RPB) * ks_b : 0x80000000u;
       dma16(kdesc, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, ks_b), so);
@@ -419,12 +518,13 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
   wait_vm_n<0>();
 #pragma unroll
   for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]), "+v"(gf[i]));
-  __syncthreads();
+  if constexpr (!SPLIT) __syncthreads();
 
-  for (int j = 0; j < n_tiles; ++j) {
-    const char *kt = lds + (j & 1) * STAGE;
+  for (int jj = 0; jj < my_tiles; ++jj) {
+    const int j = first + STRIDE * jj;
+    const char *kt = ring_p + (jj & 1) * STAGE;
     const char *vt = kt + TL::BYTES;
-    if (j < w_tiles) {
+    if (SPLIT || j < w_tiles) {
       f32x16 s = f32x16{}, dp = f32x16{};
       {
         constexpr int NC = HD / 4;
@@ -433,21 +533,26 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
         vc[0] = TL::chunk(vt, c, h * NC);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jj = 0; jj < NC; ++jj) {
-          if (jj + 1 < NC) {
-            kc[(jj + 1) & 1] = TL::chunk(kt, c, h * NC + jj + 1);
-            vc[(jj + 1) & 1] = TL::chunk(vt, c, h * NC + jj + 1);
+        for (int q = 0; q < NC; ++q) {
+          if (q + 1 < NC) {
+            kc[(q + 1) & 1] = TL::chunk(kt, c, h * NC + q + 1);
+            vc[(q + 1) & 1] = TL::chunk(vt, c, h * NC + q + 1);
           }
-          const float4 kv = kc[jj & 1], vv = vc[jj & 1];
-          s = mfma32f(kv.x, qf[4 * jj], s);
-          dp = mfma32f(vv.x, gf[4 * jj], dp);
-          s = mfma32f(kv.y, qf[4 * jj + 1], s);
-          dp = mfma32f(vv.y, gf[4 * jj + 1], dp);
-          s = mfma32f(kv.z, qf[4 * jj + 2], s);
-          dp = mfma32f(vv.z, gf[4 * jj + 2], dp);
-          s = mfma32f(kv.w, qf[4 * jj + 3], s);
-          dp = mfma32f(vv.w, gf[4 * jj + 3], dp);
-          if (jj < PARTS) issue_part(j + 1, jj);
+          const float4 kv = kc[q & 1], vv = vc[q & 1];
+          s = mfma32f(kv.x, qf[4 * q], s);
+          dp = mfma32f(vv.x, gf[4 * q], dp);
+          s = mfma32f(kv.y, qf[4 * q + 1], s);
+          dp = mfma32f(vv.y, gf[4 * q + 1], dp);
+          s = mfma32f(kv.z, qf[4 * q + 2], s);
+          dp = mfma32f(vv.z, gf[4 * q + 2], dp);
+          s = mfma32f(kv.w, qf[4 * q + 3], s);
+          dp = mfma32f(vv.w, gf[4 * q + 3], dp);
+          if (PARTS > NC) {
+            if (2 * q < PARTS) issue_part(jj + 1, 2 * q);
+            if (2 * q + 1 < PARTS) issue_part(jj + 1, 2 * q + 1);
+          } else if (q < PARTS) {
+            issue_part(jj + 1, q);
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
@@ -489,21 +594,46 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < PARTS; ++u) issue_part(j + 1, u);
+      for (int u = 0; u < PARTS; ++u) issue_part(jj + 1, u);
     }
     wait_vm_n<0>();
-    __syncthreads();
+    if constexpr (SPLIT) wait_lgkm0();  // (this wave's ring only)
+    else __syncthreads();
   }
-  if (qrow < p.Sq) {
-    float *orow = static_cast<float *>(const_cast<void *>(a.dq.data)) + b * a.dq.s0 + hq * a.dq.s1 +
-                  static_cast<int64_t>(qrow) * a.dq.s2;
-    const float sc = a.scale;
+  float *orow = static_cast<float *>(const_cast<void *>(a.dq.data)) + b * a.dq.s0 + hq * a.dq.s1 +
+                static_cast<int64_t>(qrow < p.Sq ? qrow : 0) * a.dq.s2;
+  const float sc = a.scale;
+  if constexpr (!SPLIT) {
+    if (qrow < p.Sq) {
+#pragma unroll
+      for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
+              float4{acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc, acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc};
+    }
+  } else {
+    // the waves' partial dQ^T, summed in wave order; wave w stores the
+    // (dt, g) groups w, w + 4, ...
+    __syncthreads();  // every wave's loop (and its last loads) done: the rings are free
+    float *co = reinterpret_cast<float *>(lds);  // [NW][PDT][16][64]
 #pragma unroll
     for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+      for (int i = 0; i < 16; ++i) co[((w * PDT + dt) * 16 + i) * 64 + lane] = acc[dt][i];
+    __syncthreads();
+    if (qrow < p.Sq) {
+      for (int grp = w; grp < PDT * 4; grp += NW) {
+        const int dt = grp >> 2, g = grp & 3;
+        float o4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < NW; ++v)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o4[r] += co[((v * PDT + dt) * 16 + 4 * g + r) * 64 + lane];
         *reinterpret_cast<float4 *>(orow + 32 * dt + 8 * g + 4 * h) =
-            float4{acc[dt][4 * g] * sc, acc[dt][4 * g + 1] * sc, acc[dt][4 * g + 2] * sc, acc[dt][4 * g + 3] * sc};
+            float4{o4[0] * sc, o4[1] * sc, o4[2] * sc, o4[3] * sc};
+      }
+    }
   }
 }
 
@@ -517,27 +647,34 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
 // nd) per (row, key), then dV^T += dO^T P and dK^T += Q^T dS (Q, dO by
 // 32-float row segments, P and dS the accumulator registers).  dK = scale
 // dK^T^T, dV = dV^T^T.
+//
+// SPLIT (problems with fewer 128-key workgroups than CUs, D <= 64): one
+// workgroup = 32 keys, all 4 waves on them; wave w takes tiles w, w + 4, ...
+// of the (query head, query tile) walk through its own ring, and the waves'
+// dK^T / dV^T partial sums add up through LDS in wave order at the end.
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, bool SPLIT>
 __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
   using TL = FTile<D>;
   constexpr int HD = D / 2, PDT = D / 32;
   constexpr int RV = 2 * BN * 4;                 // nl | nd of the tile's rows
   constexpr int STAGE = 2 * TL::BYTES + RV;      // Q | dO | row values
-  constexpr int PARTS = 2 * TL::BLOCKS / NW;
-  static_assert(PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1, "tile loads split over the waves");
-  __shared__ __attribute__((aligned(1024))) char lds[2 * STAGE + 1024];
+  constexpr int KEYS = SPLIT ? 32 : KB;          // keys per workgroup
+  constexpr int RINGS = SPLIT ? NW : 1, STRIDE = SPLIT ? NW : 1;
+  constexpr int PARTS = SPLIT ? 2 * TL::BLOCKS : 2 * TL::BLOCKS / NW;
+  static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n_kb = (p.Sk + KB - 1) / KB;
+  const int n_kb = (p.Sk + KEYS - 1) / KEYS;
   const int total = n_kb * p.Hkv * p.B;
   const int logical = xcd_remap(blockIdx.x, total);
   int bh, kb;
   heavy_first(logical, n_kb, p.Hkv * p.B, 32, bh, kb);
   const int b = bh / p.Hkv, hk = bh - b * p.Hkv;
-  const int k0 = kb * KB, kw = k0 + 32 * w, key = kw + c;
+  const int k0 = kb * KEYS, kw = SPLIT ? k0 : k0 + 32 * w, key = kw + c;
   const int kv_end = kv_end_for(p, b);
   const bool keymask = p.mask.kind == TSATTN_MASK_BOOL && !(p.kv_prefix && p.kv_prefix[b]);
   const bool key_live = key < kv_end &&
@@ -550,6 +687,9 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
   }
   const int n_qt = __builtin_amdgcn_readfirstlane(k0 < kv_end ? (p.Sq - q_start + BN - 1) / BN : 0);
   const int n_iter = __builtin_amdgcn_readfirstlane(n_qt * p.rep);
+  // this wave's tiles: it = first + STRIDE jj, jj < my_iter
+  const int first = SPLIT ? w : 0;
+  const int my_iter = SPLIT ? (n_iter > w ? (n_iter - 1 - w) / NW + 1 : 0) : n_iter;
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4, gs_b = static_cast<uint32_t>(a.dout.s2) * 4;
@@ -568,17 +708,22 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
 
   // tile it = query tile it % n_qt of query head hk rep + it / n_qt
   const uint32_t lds0 = lds_addr(lds);
-  const uint32_t spare = lds0 + 2 * STAGE;
-  auto issue = [&](int it) {
+  const uint32_t ring = lds0 + (SPLIT ? w * 2 * STAGE : 0);
+  const char *ring_p = lds + (SPLIT ? w * 2 * STAGE : 0);
+  const uint32_t spare = lds0 + RINGS * 2 * STAGE;
+  // the loads of local tile jj (tile first + STRIDE jj): this wave's share of
+  // its Q / dO blocks (split: all of them) and row values
+  auto issue = [&](int jj) {
+    const int it = first + STRIDE * jj;
     const bool real = it < n_iter;
     const int r = real ? it / n_qt : 0, qi = real ? it - r * n_qt : 0;
     const int hq = hk * p.rep + r, q0 = q_start + qi * BN;
-    const uint32_t st = real ? lds0 + (it & 1) * STAGE : spare;
+    const uint32_t st = real ? ring + (jj & 1) * STAGE : spare;
     const u32x4 qd = make_desc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const u32x4 gd = make_desc(f32_head<float>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
 #pragma unroll
     for (int u = 0; u < PARTS; ++u) {
-      const int n = w + NW * u;
+      const int n = SPLIT ? u : w + NW * u;
       if (n < TL::BLOCKS) {
         const uint32_t so = real ? static_cast<uint32_t>(q0 + n * TL::RPB) * qs_b : 0x80000000u;
         dma16(qd, st + (real ? n * 1024 : 0), TL::dma_off(n, lane, qs_b), so);
@@ -588,13 +733,18 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
         dma16(gd, st + (real ? TL::BYTES + m * 1024 : 0), TL::dma_off(m, lane, gs_b), so);
       }
     }
-    // the rows' nl (wave 0) and nd (wave 1): 8 lanes of 16 bytes each
-    const float *rv = a.rows + (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (w == 0 ? rows : 0);
-    const u32x4 rd = make_desc(rv, static_cast<uint32_t>(p.Sq) * 4);
-    const bool mine = real && w < 2;
-    if (lane < BN / 4)
-      dma16(rd, mine ? st + 2 * TL::BYTES + w * BN * 4 : spare, static_cast<uint32_t>(lane) * 16,
-            mine ? static_cast<uint32_t>(q0) * 4 : 0x80000000u);
+    // the rows' nl (wave 0; split: every wave) and nd (wave 1; split: every
+    // wave): 8 lanes of 16 bytes each
+#pragma unroll
+    for (int part = 0; part < (SPLIT ? 2 : 1); ++part) {
+      const int which = SPLIT ? part : w;  // 0: nl, 1: nd
+      const float *rv = a.rows + (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + (which == 0 ? rows : 0);
+      const u32x4 rd = make_desc(rv, static_cast<uint32_t>(p.Sq) * 4);
+      const bool mine = real && which < 2;
+      if (lane < BN / 4)
+        dma16(rd, mine ? st + 2 * TL::BYTES + which * BN * 4 : spare, static_cast<uint32_t>(lane) * 16,
+              mine ? static_cast<uint32_t>(q0) * 4 : 0x80000000u);
+    }
   };
 
   f32x16 dka[PDT], dva[PDT];
@@ -608,15 +758,16 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
   wait_vm_n<0>();
 #pragma unroll
   for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(kf[i]), "+v"(vf[i]));
-  __syncthreads();
+  if constexpr (!SPLIT) __syncthreads();
 
-  for (int it = 0; it < n_iter; ++it) {
-    const char *qt = lds + (it & 1) * STAGE;
+  for (int jj = 0; jj < my_iter; ++jj) {
+    const int it = first + STRIDE * jj;
+    const char *qt = ring_p + (jj & 1) * STAGE;
     const char *gt = qt + TL::BYTES;
     const float *rvl = reinterpret_cast<const float *>(qt + 2 * TL::BYTES);  // nl [32] | nd [32]
     const int r = it / n_qt, qi = it - r * n_qt;
     const int q0 = q_start + qi * BN;
-    issue(it + 1);
+    issue(jj + 1);
     // S = Q K^T, dP = dO V^T over the tile's 32 rows x this wave's 32 keys
     f32x16 s = f32x16{}, dp = f32x16{};
     {
@@ -674,23 +825,56 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
       }
     }
     wait_vm_n<0>();
-    __syncthreads();
+    if constexpr (SPLIT) wait_lgkm0();  // (this wave's ring only)
+    else __syncthreads();
   }
-  if (key < p.Sk) {
-    float *krow = static_cast<float *>(const_cast<void *>(a.dk.data)) + b * a.dk.s0 + hk * a.dk.s1 +
-                  static_cast<int64_t>(key) * a.dk.s2;
-    float *vrow = static_cast<float *>(const_cast<void *>(a.dv.data)) + b * a.dv.s0 + hk * a.dv.s1 +
-                  static_cast<int64_t>(key) * a.dv.s2;
-    const float sc = a.scale;
+  const int krow_i = key < p.Sk ? key : 0;
+  float *krow = static_cast<float *>(const_cast<void *>(a.dk.data)) + b * a.dk.s0 + hk * a.dk.s1 +
+                static_cast<int64_t>(krow_i) * a.dk.s2;
+  float *vrow = static_cast<float *>(const_cast<void *>(a.dv.data)) + b * a.dv.s0 + hk * a.dv.s1 +
+                static_cast<int64_t>(krow_i) * a.dv.s2;
+  const float sc = a.scale;
+  if constexpr (!SPLIT) {
+    if (key < p.Sk) {
+#pragma unroll
+      for (int dt = 0; dt < PDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          *reinterpret_cast<float4 *>(krow + 32 * dt + 8 * g + 4 * h) =
+              float4{dka[dt][4 * g] * sc, dka[dt][4 * g + 1] * sc, dka[dt][4 * g + 2] * sc, dka[dt][4 * g + 3] * sc};
+          *reinterpret_cast<float4 *>(vrow + 32 * dt + 8 * g + 4 * h) =
+              float4{dva[dt][4 * g], dva[dt][4 * g + 1], dva[dt][4 * g + 2], dva[dt][4 * g + 3]};
+        }
+    }
+  } else {
+    // the waves' partial dK^T / dV^T, summed in wave order; wave w stores the
+    // (dt, g) groups w, w + 4, ... of both
+    __syncthreads();  // every wave's loop (and its last loads) done: the rings are free
+    float *co = reinterpret_cast<float *>(lds);  // [NW][2 (dK, dV)][PDT][16][64]
 #pragma unroll
     for (int dt = 0; dt < PDT; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        *reinterpret_cast<float4 *>(krow + 32 * dt + 8 * g + 4 * h) =
-            float4{dka[dt][4 * g] * sc, dka[dt][4 * g + 1] * sc, dka[dt][4 * g + 2] * sc, dka[dt][4 * g + 3] * sc};
-        *reinterpret_cast<float4 *>(vrow + 32 * dt + 8 * g + 4 * h) =
-            float4{dva[dt][4 * g], dva[dt][4 * g + 1], dva[dt][4 * g + 2], dva[dt][4 * g + 3]};
+      for (int i = 0; i < 16; ++i) {
+        co[(((w * 2 + 0) * PDT + dt) * 16 + i) * 64 + lane] = dka[dt][i];
+        co[(((w * 2 + 1) * PDT + dt) * 16 + i) * 64 + lane] = dva[dt][i];
       }
+    __syncthreads();
+    if (key < p.Sk) {
+      for (int grp = w; grp < PDT * 4; grp += NW) {
+        const int dt = grp >> 2, g = grp & 3;
+        float k4[4] = {0.f, 0.f, 0.f, 0.f}, v4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int v = 0; v < NW; ++v)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            k4[r] += co[(((v * 2 + 0) * PDT + dt) * 16 + 4 * g + r) * 64 + lane];
+            v4[r] += co[(((v * 2 + 1) * PDT + dt) * 16 + 4 * g + r) * 64 + lane];
+          }
+        *reinterpret_cast<float4 *>(krow + 32 * dt + 8 * g + 4 * h) =
+            float4{k4[0] * sc, k4[1] * sc, k4[2] * sc, k4[3] * sc};
+        *reinterpret_cast<float4 *>(vrow + 32 * dt + 8 * g + 4 * h) = float4{v4[0], v4[1], v4[2], v4[3]};
+      }
+    }
   }
 }
 
@@ -703,22 +887,46 @@ void launch_bwd_dims(const F32Args &a, hipStream_t st) {
     const int64_t per_block = NW * (64 / (D / 4));
     rows_f32_kernel<D><<<dim3(static_cast<unsigned>((rows + per_block - 1) / per_block)), dim3(NT), 0, st>>>(a);
   }
-  {
-    Probe pr_("bwd_dq_mfma_f32", st);
-    const int n_qb = (p.Sq + BM - 1) / BM;
-    dq_f32_kernel<D><<<dim3(n_qb * p.Hq * p.B), dim3(NT), 0, st>>>(a);
+  const int64_t qheads = static_cast<int64_t>(p.Hq) * p.B, kheads = static_cast<int64_t>(p.Hkv) * p.B;
+  const int64_t n_qb = (p.Sq + BM - 1) / BM, n_kb = (p.Sk + KB - 1) / KB;
+  bool split_q = false, split_k = false;
+  if constexpr (D <= 64) {  // (the split rings of D = 128 would not fit in LDS)
+    split_q = n_qb * qheads < device_cus();
+    split_k = n_kb * kheads < device_cus();
   }
-  {
+  if (split_q) {
+    if constexpr (D <= 64) {
+      Probe pr_("bwd_dq_mfma_f32_split", st);
+      dq_f32_kernel<D, true><<<dim3(static_cast<unsigned>((p.Sq + 31) / 32 * qheads)), dim3(NT), 0, st>>>(a);
+    }
+  } else {
+    Probe pr_("bwd_dq_mfma_f32", st);
+    dq_f32_kernel<D, false><<<dim3(static_cast<unsigned>(n_qb * qheads)), dim3(NT), 0, st>>>(a);
+  }
+  if (split_k) {
+    if constexpr (D <= 64) {
+      Probe pr_("bwd_dkdv_mfma_f32_split", st);
+      dkdv_f32_kernel<D, true><<<dim3(static_cast<unsigned>((p.Sk + 31) / 32 * kheads)), dim3(NT), 0, st>>>(a);
+    }
+  } else {
     Probe pr_("bwd_dkdv_mfma_f32", st);
-    const int n_kb = (p.Sk + KB - 1) / KB;
-    dkdv_f32_kernel<D><<<dim3(n_kb * p.Hkv * p.B), dim3(NT), 0, st>>>(a);
+    dkdv_f32_kernel<D, false><<<dim3(static_cast<unsigned>(n_kb * kheads)), dim3(NT), 0, st>>>(a);
   }
 }
 
 template <int D>
 void launch_fwd_dims(const F32Args &a, hipStream_t st) {
-  const int n_qb = (a.p.Sq + BM - 1) / BM;
-  fwd_f32_kernel<D><<<dim3(n_qb * a.p.Hq * a.p.B), dim3(NT), 0, st>>>(a);
+  const int64_t heads = static_cast<int64_t>(a.p.Hq) * a.p.B;
+  const int64_t n_qb = (a.p.Sq + BM - 1) / BM;
+  if constexpr (D <= 64) {  // (the split rings of D = 128 would not fit in LDS)
+    if (n_qb * heads < device_cus()) {
+      Probe pr_("fwd_mfma_f32_split", st);
+      fwd_f32_kernel<D, true><<<dim3(static_cast<unsigned>((a.p.Sq + 31) / 32 * heads)), dim3(NT), 0, st>>>(a);
+      return;
+    }
+  }
+  Probe pr_("fwd_mfma_f32", st);
+  fwd_f32_kernel<D, false><<<dim3(static_cast<unsigned>(n_qb * heads)), dim3(NT), 0, st>>>(a);
 }
 
 }  // namespace
@@ -756,7 +964,6 @@ hipError_t launch_mfma_f32_forward(const Problem &p, View q, View k, View v, Vie
   a.lse = lse;
   a.sl = static_cast<float>(p.scale) * kLog2e;
   a.scale = static_cast<float>(p.scale);
-  Probe pr_("fwd_mfma_f32", st);
   if (p.Dqk == 128) launch_fwd_dims<128>(a, st);
   else if (p.Dqk == 64) launch_fwd_dims<64>(a, st);
   else launch_fwd_dims<32>(a, st);

@@ -27,7 +27,18 @@ from tensorsmith_hip import _lib  # noqa: E402
 
 TOL = dict(rtol=1e-4, atol=3e-5)
 DT = "float32"
-PROBES = ("fwd_mfma_f32", "bwd_rows_f32", "bwd_dq_mfma_f32", "bwd_dkdv_mfma_f32")
+
+
+def expected_probes(b, hq, hkv, sq, sk, d):
+    """The kernels a problem runs: at head dims <= 64 a problem with fewer
+    128-row (128-key) blocks than the device has CUs runs the split form of
+    the forward / dQ (dK/dV) kernel, 32 rows (keys) per workgroup."""
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    sq_split = d <= 64 and -(-sq // 128) * hq * b < cus
+    sk_split = d <= 64 and -(-sk // 128) * hkv * b < cus
+    sfx = lambda on: "_split" if on else ""
+    return ("fwd_mfma_f32" + sfx(sq_split), "bwd_rows_f32", "bwd_dq_mfma_f32" + sfx(sq_split),
+            "bwd_dkdv_mfma_f32" + sfx(sk_split))
 
 
 def say(msg):
@@ -47,6 +58,11 @@ F32_CASES = [
     (1, 4, 2, 160, 160, 32, True, 0),     # GQA
     (2, 3, 3, 77, 190, 32, False, 0),
     (1, 2, 2, 513, 513, 128, True, 0),    # several key blocks per query block and back
+    # enough 128-row blocks for the one-block-per-wave kernels at D = 64 / 32
+    (4, 16, 16, 512, 512, 64, True, 0),
+    (4, 16, 8, 520, 520, 32, True, 0),    # GQA, ragged: split dK/dV, whole dQ
+    (2, 32, 32, 600, 600, 64, False, 0),
+    (2, 16, 16, 64, 1100, 64, True, 1036),  # split dQ, whole dK/dV
 ]
 
 
@@ -83,13 +99,15 @@ def test_f32_mfma_forward_backward(case):
     finally:
         _lib.profile_enable(False)
     assert path == _lib.PATH_MFMA and bpath == _lib.PATH_MFMA
-    assert all(p in probes for p in PROBES), sorted(probes)
+    want = expected_probes(b, hq, hkv, sq, sk, d)
+    assert all(p in probes for p in want), (want, sorted(probes))
     _check(name, out, lse, (dq, dk, dv), ref, inp.do)
 
 
+@pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("prefix", [True, False, "empty"])
-def test_f32_mfma_key_padding_mask(prefix):
-    b, h, s, d = 3, 2, 200, 128
+def test_f32_mfma_key_padding_mask(prefix, d):
+    b, h, s = 3, 2, 200
     inp = attention_inputs(b, h, s, d, DT, seed=9)
     lengths = np.array([200, 131, 0 if prefix == "empty" else 64])
     keymask = np.arange(s)[None, :] < lengths[:, None]
@@ -97,7 +115,7 @@ def test_f32_mfma_key_padding_mask(prefix):
         keymask[1, 17] = False  # a hole inside the valid prefix
         keymask[2, 150] = True  # an allowed key past the padding
     # "empty": batch 2 sees no key at all (O = 0, LSE = -inf, zero gradients)
-    say(f"f32 key mask prefix={prefix}")
+    say(f"f32 key mask prefix={prefix} d={d}")
     ref = A.sdpa(inp.q, inp.k, inp.v, keymask[:, None, None, :], True, dtype=DT,
                  backend="streaming")
     q, k, v, g = (abi.dev_tensor(x, DT) for x in (inp.q, inp.k, inp.v, inp.do))
