@@ -534,13 +534,14 @@ def bench_cached_step(ts, torch, steps, warmup):
             out[name] = {"ms_per_step": round(ms, 4),
                          "kernel_ms": {n: round(t / max(c, 1), 4) for n, (c, t) in _lib.profile_read().items()}}
     qkv_ms = out["fused"]["kernel_ms"]["qkv_rope_append"]
-    # weights once per 32-row block (two blocks at batch 64), x, q, K/V rows
-    qkv_bytes = float((hq + 2 * hkv) * 128 * embed * 2 * 2 + bsz * embed * 2 + bsz * (hq + 2 * hkv) * 128 * 2)
+    # the algorithmic minimum: the weights once, x, the q and K/V rows
+    qkv_bytes = float((hq + 2 * hkv) * 128 * embed * 2 + bsz * embed * 2 + bsz * (hq + 2 * hkv) * 128 * 2)
     out["qkv_rope_append"] = {
         "bytes_per_launch": qkv_bytes,
         "roofline": {"bound": "hbm", "achieved": round(qkv_bytes / (qkv_ms * 1e-3) / 1e9, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(qkv_bytes / (qkv_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)}}
+                     "frac": round(qkv_bytes / (qkv_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                     "traffic": traffic_for("qkv_rope_append")}}
     out["config"] = {"workload": "mha_cached_step_f16_b64_e4096_h32kv8d128_len1024"}
     return out
 

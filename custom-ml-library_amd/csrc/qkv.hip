@@ -8,12 +8,18 @@
 //
 // One workgroup = one 32-channel tile of a head of q, k or v (16-bit
 // caches; the whole head for int8 caches, whose quantiser needs the row
-// maximum) for 32 rows (b, t) of x.  Its eight waves split the embedding in
-// 64-column chunks and run out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16
-// with W rows and x rows as row fragments -- staged through per-wave LDS
-// rings by DMA (whole cache lines per load instruction) for one-tile
-// workgroups, loaded directly for whole heads -- then sum their partial
-// tiles through LDS.  (For decode the weights dominate: (Hq + 2 Hkv) D E 2
+// maximum) for 32 rows (b, t) of x.  The embedding splits into 64-column
+// chunks over eight accumulators (chunks v, v + 8, ... into accumulator v)
+// that run out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16 with W rows and
+// x rows as row fragments, then sum in order 0..7 through LDS.  One-tile
+// workgroups stage the fragments through per-wave LDS rings by DMA (whole
+// cache lines per load instruction) and run four waves of two accumulators
+// each, two workgroups per CU; whole-head workgroups load them directly and
+// run eight waves of one accumulator.  Either way every accumulator sees the
+// same chunks in the same order, so the projections are bit-identical
+// across cache types.  The row blocks of one weight tile are consecutive in
+// the XCD-local dispatch order, so they read the tile from HBM about once
+// (the second read meets the first in that XCD's L2).  (For decode the weights dominate: (Hq + 2 Hkv) D E 2
 // bytes.)  Wave 0 finishes: bias, rounding to the dtype (as the
 // reference's Linear output), the rotation (lane (c, h) holds channels
 // 8 g + 4 h .. + 3 of row c, so every channel pair is lane-local), then the
@@ -25,8 +31,7 @@
 namespace tsattn {
 namespace {
 
-constexpr int NT = 512;
-constexpr int NW = NT / 64;
+constexpr int NACC = 8;  // chunk accumulators (summed in order)
 
 struct QkvArgs {
   int rows, len, E, Hq, Hkv, rope;
@@ -51,22 +56,32 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
 // CT: 32-channel tiles of the head per workgroup -- D / 32 (the whole head,
 // which the int8 quantiser's row maximum needs), or fewer for 16-bit caches,
 // so that more workgroups share the weight stream.
+// Threads per workgroup: four waves (two accumulators each) for staged
+// one-tile workgroups, eight (one each) for whole heads.
+template <int CT>
+constexpr int qkv_threads() { return CT == 1 ? 256 : 512; }
+
 template <typename T, int D, int CT>
-__global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
+__global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_append_kernel(QkvArgs a) {
   constexpr int TILES = CT, NCB = D / 32 / CT;
+  constexpr int NW = qkv_threads<CT>() / 64, APW = NACC / NW;  // waves, accumulators per wave
   static_assert(NCB * CT * 32 == D, "column blocks split the head");
+  static_assert(APW * NW == NACC && (CT == 1 || APW == 1), "accumulators split over the waves");
   // CT == 1: per-wave staging rings (two 8 KiB stages: 32 W rows and 32 x
   // rows of 64 columns) during the loop, the partial tiles after it
   constexpr int RING = 2 * 8192;
-  constexpr int PART = NW * TILES * 16 * 64 * 4;
+  constexpr int PART = NACC * TILES * 16 * 64 * 4;
   __shared__ __attribute__((aligned(1024))) char smem[(CT == 1 ? (NW * RING > PART ? NW * RING : PART) : PART) + 1024];
   auto part = reinterpret_cast<float (*)[TILES][16][64]>(smem);
 
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nslot = a.Hq + 2 * a.Hkv;
-  const int slot = blockIdx.x % nslot, rest = blockIdx.x / nslot;
-  const int cb = rest % NCB, rb = rest / NCB;
+  // logical id = ((cb nslot) + slot) rblocks + rb: the row blocks of a
+  // weight tile are consecutive, and consecutive logical ids share an XCD
+  const int nslot = a.Hq + 2 * a.Hkv, rblocks = (a.rows + 31) / 32;
+  const int logical = xcd_remap(blockIdx.x, static_cast<int>(gridDim.x));
+  const int rb = logical % rblocks, rest = logical / rblocks;
+  const int slot = rest % nslot, cb = rest / nslot;
   const int c0 = 32 * CT * cb;  // first channel of this workgroup's columns
   const int kind = slot < a.Hq ? 0 : (slot < a.Hq + a.Hkv ? 1 : 2);
   const int head = kind == 0 ? slot : (kind == 1 ? slot - a.Hq : slot - a.Hq - a.Hkv);
@@ -89,18 +104,22 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
                       (live ? 0u : 0x80000000u);
   const uint32_t wo = (static_cast<uint32_t>(c) * a.E + 8 * h) * 2;
   const uint32_t wt = 32u * a.E * 2;  // bytes between 32-row tiles of W
-  f32x16 acc[TILES];
+  f32x16 acc[APW][TILES];
 #pragma unroll
-  for (int t = 0; t < TILES; ++t) acc[t] = f32x16{};
+  for (int v = 0; v < APW; ++v)
+#pragma unroll
+    for (int t = 0; t < TILES; ++t) acc[v][t] = f32x16{};
   if constexpr (CT == 1) {
     // Staged through LDS: a wave takes the 64-column chunks w, w + NW, ...
-    // of the embedding and DMAs each chunk's 32 W rows and 32 x rows into
-    // its own two-stage ring, eight rows of 128 bytes (whole cache lines)
-    // per load instruction -- direct fragment loads touch 32 lines each, and
-    // the address unit, not HBM, bounded them.  In the ring, 16-byte unit u
-    // of row r holds unit u ^ (r % 8) of the chunk (conflict-free fragment
-    // reads); columns past the embedding, and rows past the last, read zeros.
-    // The loop needs no barrier: no wave reads another's ring.
+    // of the embedding (chunk ch into accumulator ch % 8: its accumulator
+    // k % APW for its k-th chunk) and DMAs each chunk's 32 W rows and 32 x
+    // rows into its own two-stage ring, eight rows of 128 bytes (whole cache
+    // lines) per load instruction -- direct fragment loads touch 32 lines
+    // each, and the address unit, not HBM, bounded them.  In the ring,
+    // 16-byte unit u of row r holds unit u ^ (r % 8) of the chunk
+    // (conflict-free fragment reads); columns past the embedding, and rows
+    // past the last, read zeros.  The loop needs no barrier: no wave reads
+    // another's ring.
     const uint32_t sbase = lds_addr(smem) + w * RING, spare = lds_addr(smem) + NW * RING;
     const int nch = (a.E + 63) / 64;
     const int mine = nch > w ? (nch - 1 - w) / NW + 1 : 0;  // this wave's chunks
@@ -133,8 +152,8 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     };
     // fragment of k-step s (0..3) of a staged 32 x 64 tile: row c, unit 2 s + h
     const uint32_t fo = static_cast<uint32_t>(c) * 128;
-    issue(0);
-    for (int k = 0; k < mine; ++k) {
+    // chunk k: into ring stage k % 2 and accumulator k % APW
+    auto step = [&](int k, f32x16 &ac) {
       issue(k + 1);
       wait_vm_n<8>();  // chunk k has landed; chunk k + 1's eight loads stay in flight
       const char *stg = smem + w * RING + (k & 1) * 8192;
@@ -143,9 +162,15 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
         const uint32_t u = static_cast<uint32_t>((2 * s + h) ^ (c & 7)) * 16;
         const u32x4 wf = *reinterpret_cast<const u32x4 *>(stg + fo + u);
         const u32x4 xf = *reinterpret_cast<const u32x4 *>(stg + 4096 + fo + u);
-        acc[0] = mfma32<T>(wf, xf, acc[0]);
+        ac = mfma32<T>(wf, xf, ac);
       }
       wait_lgkm0();  // reads of this stage done before chunk k + 2 overwrites it
+    };
+    static_assert(APW == 2, "staged workgroups: two accumulators per wave");
+    issue(0);
+    for (int k = 0; k < mine; k += 2) {
+      step(k, acc[0][0]);
+      if (k + 1 < mine) step(k + 1, acc[1][0]);
     }
     wait_vm_n<0>();
     __syncthreads();  // every ring read before the partial tiles reuse the LDS
@@ -173,7 +198,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-        for (int t = 0; t < TILES; ++t) acc[t] = mfma32<T>(wb[buf][s4][t], xb[buf][s4], acc[t]);
+        for (int t = 0; t < TILES; ++t) acc[0][t] = mfma32<T>(wb[buf][s4][t], xb[buf][s4], acc[0][t]);
     };
     load(0, 0);
     for (int k = 0; k < mine; k += 2) {
@@ -186,9 +211,11 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     }
   }
 #pragma unroll
-  for (int t = 0; t < TILES; ++t)
+  for (int v = 0; v < APW; ++v)
 #pragma unroll
-    for (int e = 0; e < 16; ++e) part[w][t][e][lane] = acc[t][e];
+    for (int t = 0; t < TILES; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) part[w + NW * v][t][e][lane] = acc[v][t][e];
   __syncthreads();
   if (w != 0) return;
 
@@ -202,7 +229,7 @@ __global__ __launch_bounds__(NT, 1) void qkv_rope_append_kernel(QkvArgs a) {
     for (int e = 0; e < 16; ++e) {
       float s = 0.f;
 #pragma unroll
-      for (int v = 0; v < NW; ++v) s += part[v][t][e][lane];
+      for (int v = 0; v < NACC; ++v) s += part[v][t][e][lane];
       if (bias) s += static_cast<float>(bias[head * D + c0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]);
       y[t][e] = static_cast<T>(s);
     }
@@ -288,7 +315,8 @@ hipError_t launch_qkv_rope_append(int dtype, int batch, int len, int embed, int 
   // 16-bit caches: one 32-channel tile of a head per workgroup; int8 caches:
   // the whole head (its row maximum)
   const int ncb = ks ? 1 : dim / 32;
-  const dim3 grid(static_cast<unsigned>((heads_q + 2 * heads_kv) * ncb * rblocks)), block(NT);
+  const dim3 grid(static_cast<unsigned>((heads_q + 2 * heads_kv) * ncb * rblocks));
+  const dim3 block(ks ? qkv_threads<4>() : qkv_threads<1>());
   Probe pr_(ks ? "qkv_rope_append_int8" : "qkv_rope_append", st);
   if (dtype == TSATTN_BF16) {
     if (dim == 128) {

@@ -114,7 +114,8 @@ def test_fused_projection_rope_append(dtype, d, e, t, bias):
         want_q, want_s = A.quantize_int8(abi.host(rows)[:, :, pos:pos + t])
         np.testing.assert_array_equal(abi.host(codes)[:, :, pos:pos + t], want_q)
         np.testing.assert_array_equal(abi.host(scales)[:, :, pos:pos + t], want_s)
-        assert (codes[:, :, :pos] == 0).all() and (scales[:, :, pos + t:] == 1).all()
+        assert (codes[:, :, :pos] == 0).all() and (codes[:, :, pos + t:] == 0).all()
+        assert (scales[:, :, :pos] == 1).all() and (scales[:, :, pos + t:] == 1).all()
 
 
 def test_fused_projection_rejects_bad_arguments():
