@@ -230,8 +230,12 @@ __global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_a
       float s = 0.f;
 #pragma unroll
       for (int v = 0; v < NACC; ++v) s += part[v][t][e][lane];
-      if (bias) s += static_cast<float>(bias[head * D + c0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]);
-      y[t][e] = static_cast<T>(s);
+      // the product in the dtype, then + bias in the dtype (functional.py:75-77)
+      T yv = static_cast<T>(s);
+      if (bias)
+        yv = static_cast<T>(static_cast<float>(yv) +
+                            static_cast<float>(bias[head * D + c0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3)]));
+      y[t][e] = yv;
     }
   if (kind < 2 && a.rope) {
     const T *cs = static_cast<const T *>(a.cos) + prow * (D / 2);

@@ -281,9 +281,24 @@ def project_rope_append(x, weights, biases, q_out, k_cache, v_cache, scales, cos
     sin: the device tables of ``rotary_embedding``, or None) and the append
     of k and v at ``pos`` (``scales``: (key, value) fp32 scale arrays of an
     int8 cache, or None).  q_out [B, Hq, T, D] receives the rotated queries.
-    Raises NotImplementedError outside the kernel's shapes (f16 / bf16, head
-    dim 64 / 128, E % 16 == 0): project and append in steps then."""
+    Raises NotImplementedError outside the kernel's shapes and layouts (f16 /
+    bf16, head dim 64 / 128, E % 16 == 0; contiguous weights [heads * D, E]
+    and biases [heads * D] of x's dtype; x rows and the weights 16-byte
+    aligned): project and append in steps then."""
     b, t, e = x.shape
+    d = q_out.shape[-1]
+    rows = (heads_q * d, heads_kv * d, heads_kv * d)
+    for name, w, n in zip("qkv", weights, rows):
+        if w.dtype != x.dtype or not w.is_contiguous() or tuple(w.shape) != (n, e) or w.data_ptr() % 16:
+            raise NotImplementedError(f"the fused projection needs w{name} as a contiguous, 16-byte aligned "
+                                      f"[{n}, {e}] {x.dtype} array (got {tuple(w.shape)} {w.dtype})")
+    if biases is not None:
+        for name, bz, n in zip("qkv", biases, rows):
+            if bz is not None and (bz.dtype != x.dtype or not bz.is_contiguous() or tuple(bz.shape) != (n,)):
+                raise NotImplementedError(f"the fused projection needs b{name} as a contiguous [{n}] "
+                                          f"{x.dtype} array (got {tuple(bz.shape)} {bz.dtype})")
+    if x.data_ptr() % 16 or x.stride(0) % 8 or x.stride(1) % 8 or x.stride(2) != 1:
+        raise NotImplementedError("the fused projection needs x rows 16-byte aligned with unit column stride")
     xv = View(x.data_ptr())
     xv.stride[0], xv.stride[1], xv.stride[2], xv.stride[3] = x.stride(0), 0, x.stride(1), 1
     ptr = lambda a: None if a is None else a.data_ptr()

@@ -371,9 +371,10 @@ int tsattn_rope_append(int32_t dtype, int32_t batch, int32_t heads, int32_t len,
  * heads_q, len, dim] (the rotated queries); caches [batch, heads_kv,
  * capacity >= pos + len, dim]; cos / sin as tsattn_rope's tables.  dtype f16
  * or bf16, dim 64 or 128, embed a multiple of 16.  The projections
- * accumulate in fp32 and round once to the dtype, as the reference's Linear
- * output; the rotation and the int8 rounding are then bit-identical to the
- * reference's on those rows.
+ * accumulate in fp32 and round to the dtype, then add the bias (when given)
+ * in the dtype with one more rounding, as the reference's Linear (matmul,
+ * then + bias); the rotation and the int8 rounding are then bit-identical to
+ * the reference's on those rows.
  */
 int tsattn_qkv_rope_append(int32_t dtype, int32_t batch, int32_t len, int32_t embed, int32_t heads_q,
                            int32_t heads_kv, int32_t dim, const tsattn_view *x, const void *wq,

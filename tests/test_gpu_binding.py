@@ -147,3 +147,23 @@ def test_binding_project_rope_append(quantized):
     for got, want in zip(outs[1], outs[0]):
         assert torch.equal(got, want)
     assert outs[0][1][:, :, pos:pos + t].abs().sum() > 0
+
+
+def test_binding_project_rope_append_refuses_other_layouts():
+    """Weights and biases reach the C entry point as bare pointers, so the
+    binding refuses, before any launch, what the kernel cannot read as
+    [heads * D, E] rows of x's dtype: a transposed weight view, a bias of
+    another dtype, a weight of the wrong shape."""
+    b, t, e, hq, hkv, d = 1, 1, 64, 2, 1, 64
+    x = torch.zeros((b, t, e), dtype=torch.float16, device="cuda")
+    ws = [torch.zeros((h * d, e), dtype=torch.float16, device="cuda") for h in (hq, hkv, hkv)]
+    q = torch.zeros((b, hq, t, d), dtype=torch.float16, device="cuda")
+    kc, vc = (torch.zeros((b, hkv, 4, d), dtype=torch.float16, device="cuda") for _ in range(2))
+    transposed = torch.zeros((e, hkv * d), dtype=torch.float16, device="cuda").t()
+    assert transposed.shape == ws[1].shape and not transposed.is_contiguous()
+    fp32_bias = [None, torch.zeros(hkv * d, device="cuda"), None]
+    for weights, biases in (([ws[0], transposed, ws[2]], None),
+                            (ws, fp32_bias),
+                            ([ws[0], ws[1], ws[1][:, :32]], None)):
+        with pytest.raises(NotImplementedError):
+            B.project_rope_append(x, weights, biases, q, kc, vc, None, None, None, 0, hq, hkv)

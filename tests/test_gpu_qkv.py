@@ -86,14 +86,16 @@ def test_fused_projection_rope_append(dtype, d, e, t, bias):
         torch.cuda.synchronize()
         return q, kc, vc, sc
 
-    # oracle projections: fp32 sums of the rounded operands, rounded once
+    # oracle projections as the reference's Linear (functional.py:75-77): the
+    # product of the rounded operands rounded to the dtype, then + bias
+    # rounded again
     heads = lambda y, h: y.reshape(b, t, h, d).transpose(0, 2, 1, 3)
     proj = []
     for i, (w, h) in enumerate(zip(ws, (hq, hkv, hkv))):
-        y = x.astype(np.float64) @ w.astype(np.float64).T
+        y = round_to((x.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32), dtype)
         if bias:
-            y = y + bs[i].astype(np.float64)
-        proj.append(heads(round_to(y.astype(np.float32), dtype), h))
+            y = round_to(y.astype(np.float32) + bs[i].astype(np.float32), dtype)
+        proj.append(heads(y, h))
 
     q0, k0, v0, _ = run(rope=False)
     q1, k1, v1, _ = run(rope=True)
