@@ -867,7 +867,7 @@ def main():
     print(f"[bench] cached MHA step {cs_res['fused']['ms_per_step']:.3f} ms "
           f"(unfused {cs_res['unfused']['ms_per_step']:.3f} ms)", file=sys.stderr, flush=True)
     f32_res = bench_fp32(ts, torch, 5, 2)
-    print("[bench] fp32 (generic kernels) " + ", ".join(
+    print("[bench] fp32 (fp32 MFMA kernels) " + ", ".join(
         f"{n} {r['ms_per_step']:.3f} ms" for n, r in f32_res.items()), file=sys.stderr, flush=True)
     d32_res = bench_head_dim32(ts, torch, 5, 2)
     print("[bench] bf16 head dim 32 " + ", ".join(
