@@ -323,15 +323,16 @@ int decode_forward(const tsattn_problem *p, const tsattn_rope_desc *rope, const 
       return reinterpret_cast<uintptr_t>(x.data) % 8 == 0 && x.s0 % 8 == 0 && x.s1 % 8 == 0 &&
              x.s2 % 8 == 0;
     };
-    if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(vq) || !aligned8(vk) ||
-        !aligned8(vv))
+    if (p->dtype == TSATTN_F32 || !tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(vq) ||
+        !aligned8(vk) || !aligned8(vv))
       return fail(TSATTN_ERR_UNSUPPORTED,
                   "int8 decode needs <= 8 query rows per KV head, f16/bf16 queries, equal head "
                   "dims in {64,128,256} and 8-byte aligned cache rows");
   } else if (!tsattn::decode_supported(pr, p->dtype) || !tsattn::aligned16(vq) ||
              !tsattn::aligned16(vk) || !tsattn::aligned16(vv)) {
     return fail(TSATTN_ERR_UNSUPPORTED,
-                "decode kernel needs <= 8 query rows per KV head, f16/bf16, equal head dims in "
+                "decode kernel needs <= 8 query rows per KV head, f16/bf16/f32 (f32: no folded "
+                "rotation), equal head dims in "
                 "{64,128,256} and 16-byte aligned rows");
   }
   const size_t need = tsattn::decode_workspace_bytes(pr, split_len);

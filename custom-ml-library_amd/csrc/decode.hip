@@ -9,10 +9,11 @@
 // traffic happens per key -- and decode_merge_kernel combines the splits with
 // the same rescale-by-exp(m - M) rule.  Fully masked rows give 0.
 //
-// Memory layout: each key row is read by D/8 neighbouring lanes as 16-byte
-// loads (one wave instruction covers 64*16 B of consecutive keys), kU such
-// instructions for K and kU for V are issued before any is consumed, so every
-// wave keeps 2*kU KiB in flight.
+// Memory layout: each key row is read by D/8 neighbouring lanes, 8 elements
+// each -- 16-byte loads for 16-bit caches (one wave instruction covers 64*16 B
+// of consecutive keys), two for fp32 caches -- and kU such row pieces for K
+// and kU for V are issued before any is consumed, so every wave keeps 2*kU
+// KiB (fp32: 4*kU KiB) in flight.
 //
 // int8 caches (the reference's quantised KVCache, src/tensorsmith/nn/
 // cache.py:73-77 and :91-98): K and V rows are int8 with one fp32 scale per
@@ -78,9 +79,54 @@ __device__ __forceinline__ void unpack8_i8(u32x2 x, float *out) {
   for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
 }
 
-// Cache rows as loaded: 8 half-precision values (16 B) or 8 int8 values (8 B).
-template <bool Q8>
-using KvChunk = std::conditional_t<Q8, u32x2, u32x4>;
+
+// Cache rows as loaded: 8 values of the cache type -- int8 (8 B), 16-bit
+// (16 B) or fp32 (32 B, two 16-byte loads).
+struct F32x8 {
+  u32x4 lo, hi;
+};
+template <typename KT>
+using KvChunk = std::conditional_t<std::is_same_v<KT, int8_t>, u32x2,
+                                   std::conditional_t<std::is_same_v<KT, float>, F32x8, u32x4>>;
+
+template <typename KT>
+__device__ __forceinline__ KvChunk<KT> load_chunk(const KT *p) {
+  if constexpr (std::is_same_v<KT, float>) {
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(p);
+    return F32x8{__builtin_nontemporal_load(q), __builtin_nontemporal_load(q + 1)};
+  } else {
+    return __builtin_nontemporal_load(reinterpret_cast<const KvChunk<KT> *>(p));
+  }
+}
+
+// 8 query (T) values of a row: 16 bytes, or 32 for fp32.
+template <typename T>
+__device__ __forceinline__ void load_q8(const T *p, float *out) {
+  if constexpr (std::is_same_v<T, float>) {
+    const float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+  } else {
+    const u32x4 raw = ld16(p);
+    const T *e = reinterpret_cast<const T *>(&raw);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) out[i] = static_cast<float>(e[i]);
+  }
+}
+
+// A loaded row piece as 8 floats.
+template <typename KT>
+__device__ __forceinline__ void unpack_kv(const KvChunk<KT> &x, float *out) {
+  if constexpr (std::is_same_v<KT, int8_t>) {
+    unpack8_i8(x, out);
+  } else if constexpr (std::is_same_v<KT, float>) {
+    const float4 a = __builtin_bit_cast(float4, x.lo), b = __builtin_bit_cast(float4, x.hi);
+    out[0] = a.x, out[1] = a.y, out[2] = a.z, out[3] = a.w;
+    out[4] = b.x, out[5] = b.y, out[6] = b.z, out[7] = b.w;
+  } else {
+    unpack8<KT>(x, out);
+  }
+}
 
 // Sum over each aligned group of LPK lanes (the lanes holding one key row).
 // For LPK = 16 (D = 128) a DPP butterfly inside each 16-lane row: quad_perm
@@ -143,9 +189,13 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
       const int hq = hk * p.rep + r / p.Sq, i = r % p.Sq;
       const T *qp = static_cast<const T *>(a.q.data) + b * a.q.s0 + hq * a.q.s1 +
                     static_cast<int64_t>(i) * a.q.s2 + dc * 8;
-      u32x4 raw = ld16(qp);
-      if (p.rope.R > 0) rotate_chunk<T>(raw, p.rope, p.rope.qpos0 + i, 4 * dc, false);
-      unpack8<T>(raw, qv[r]);
+      if constexpr (std::is_same_v<T, float>) {
+        load_q8<T>(qp, qv[r]);  // (fp32: no folded rotation; the host refuses it)
+      } else {
+        u32x4 raw = ld16(qp);
+        if (p.rope.R > 0) rotate_chunk<T>(raw, p.rope, p.rope.qpos0 + i, 4 * dc, false);
+        unpack8<T>(raw, qv[r]);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) qv[r][e] *= a.sl;
     } else {
@@ -173,7 +223,7 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
   auto body = [&](auto masked_tag) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     for (int kb = k_begin + w * BATCH; kb < k_stop; kb += 4 * BATCH) {
-      KvChunk<Q8> kr[U], vr[U];
+      KvChunk<KT> kr[U], vr[U];
       float ksc[U], vsc[U];
       float kslot = 0.f, vslot = 0.f;
       if constexpr (Q8) {
@@ -186,10 +236,8 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int key = min(kb + u * KPI + kg, k_stop - 1);
-        kr[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const KvChunk<Q8> *>(kbase + static_cast<int64_t>(key) * a.k.s2));
-        vr[u] = __builtin_nontemporal_load(
-            reinterpret_cast<const KvChunk<Q8> *>(vbase + static_cast<int64_t>(key) * a.v.s2));
+        kr[u] = load_chunk<KT>(kbase + static_cast<int64_t>(key) * a.k.s2);
+        vr[u] = load_chunk<KT>(vbase + static_cast<int64_t>(key) * a.v.s2);
       }
       if constexpr (Q8) {
 #pragma unroll
@@ -202,8 +250,7 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         float kf[8];
-        if constexpr (Q8) unpack8_i8(kr[u], kf);
-        else unpack8<T>(kr[u], kf);
+        unpack_kv<KT>(kr[u], kf);
 #pragma unroll
         for (int r = 0; r < R; ++r) {
           float d = 0.f;
@@ -251,8 +298,7 @@ __global__ __launch_bounds__(NT) void decode_split_kernel(DecArgs a) {
           const float pv = fast_exp2(s[u][r] - base);
           l[r] += pv;
           float vf[8];
-          if constexpr (Q8) unpack8_i8(vr[u], vf);
-          else unpack8<T>(vr[u], vf);
+          unpack_kv<KT>(vr[u], vf);
           const float pw = Q8 ? pv * vsc[u] : pv;  // int8: V's row scale folded into P
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[r][e] = fmaf(pw, vf[e], acc[r][e]);
@@ -398,6 +444,13 @@ hipError_t launch_dim(const DecArgs &a, hipStream_t st) {
 template <bool Q8>
 hipError_t launch_any(const DecArgs &a, int dtype, hipStream_t st) {
   const int d = a.p.Dqk;
+  if constexpr (!Q8) {
+    if (dtype == TSATTN_F32) {
+      if (d == 64) return launch_dim<float, 64, false>(a, st);
+      if (d == 128) return launch_dim<float, 128, false>(a, st);
+      return launch_dim<float, 256, false>(a, st);
+    }
+  }
   if (dtype == TSATTN_BF16) {
     if (d == 64) return launch_dim<bf16, 64, Q8>(a, st);
     if (d == 128) return launch_dim<bf16, 128, Q8>(a, st);
@@ -424,7 +477,8 @@ int choose_split(const Problem &p, int split_len) {
 }  // namespace
 
 bool decode_supported(const Problem &p, int dtype) {
-  if (dtype != TSATTN_F16 && dtype != TSATTN_BF16) return false;
+  if (dtype != TSATTN_F16 && dtype != TSATTN_BF16 && dtype != TSATTN_F32) return false;
+  if (dtype == TSATTN_F32 && p.rope.R > 0) return false;  // (the folded rotation is 16-bit)
   if (p.Dqk != p.Dv || (p.Dqk != 64 && p.Dqk != 128 && p.Dqk != 256)) return false;
   return p.rep * p.Sq <= kMaxRows;
 }

@@ -1294,12 +1294,14 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a, int nqb) {
   const T *oh = head_ptr<T>(a.o, b, hq) + 8 * g;
   int qr[ROWS_U];
   u32x4 gv[ROWS_U], ov[ROWS_U];
+  float lv[ROWS_U];  // the rows' LSE, loaded with the rows (its latency under theirs)
 #pragma unroll
   for (int u = 0; u < ROWS_U; ++u) {
     qr[u] = qb * RPB + (u * (NT / 64) + w) * RPW + lane / G;
     const int r = qr[u] < p.Sq ? qr[u] : p.Sq - 1;  // past the head: reload its last row, store nothing
     gv[u] = ld16(gh + static_cast<int64_t>(r) * a.dout.s2);
     ov[u] = ld16(oh + static_cast<int64_t>(r) * a.o.s2);
+    lv[u] = a.lse[static_cast<int64_t>(bh) * p.Sq + r];
   }
 #pragma unroll
   for (int u = 0; u < ROWS_U; ++u) {
@@ -1312,7 +1314,7 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a, int nqb) {
     for (int o = 1; o < G; o <<= 1) dsum += __shfl_xor(dsum, o, 64);
     if (g == 0 && qr[u] < p.Sq) {
       const int64_t row = static_cast<int64_t>(bh) * p.Sq + qr[u];
-      store_row_values(a, rows, row, -dsum, a.lse[row]);
+      store_row_values(a, rows, row, -dsum, lv[u]);
     }
   }
   if (p.rope.R > 0 && !p.rope.qrot) {  // (qrot: the forward stored them)

@@ -243,7 +243,7 @@ def scaled_dot_product_attention(
     use_decode = (
         not recording
         and not dropout_p
-        and code in (_lib.F16, _lib.BF16)
+        and code in (_lib.F16, _lib.BF16, _lib.F32)
         and dim == dim_v
         and dim in (64, 128, 256)
         and repetitions * qlen <= 8

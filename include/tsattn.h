@@ -250,7 +250,9 @@ size_t tsattn_decode_workspace(const tsattn_problem *p, int32_t split_len);
  * reference's online softmax (attention.py:185-193).  Replaces the dense
  * path the reference takes for cached decode (MultiHeadAttention.forward,
  * src/tensorsmith/nn/transformer.py:142-154 -> attention.py:132-145).
- * k/v are the cache views [B, Hkv, capacity, D] with len_kv active keys.
+ * k/v are the cache views [B, Hkv, capacity, D] with len_kv active keys;
+ * dtype f16, bf16 or f32 (f32 caches: 32-byte row pieces, every product and
+ * sum in fp32), head dims 64 / 128 / 256, 16-byte aligned rows.
  */
 int tsattn_decode_forward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                           const tsattn_view *v, const tsattn_view *out, int32_t split_len,

@@ -242,8 +242,7 @@ def test_mha_cached_decode_matches_full_prefix(dtype, kv_heads):
         path = _lib.last_kernel_path()
         parts += [mha(x[:, 258:259], cache=cache), mha(x[:, 259:], cache=cache)]
         got = ts.cat(parts, dim=1).numpy()
-    if dtype != "float32":
-        assert path == _lib.PATH_DECODE  # one-token step ran the split-K decode kernel
+    assert path == _lib.PATH_DECODE  # one-token step ran the split-K decode kernel
     tol = dict(rtol=3e-4, atol=3e-5) if dtype == "float32" else dict(rtol=0.02, atol=0.02)
     np.testing.assert_allclose(got, full, **tol)
     assert cache.length == 300

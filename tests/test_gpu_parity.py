@@ -475,7 +475,15 @@ DECODE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dtype", ["float16", "bfloat16"])
+def check_decode(got, ref, dtype, name):
+    """fp32: the fp32 bound (every product and sum in fp32); 16-bit: check_half."""
+    if dtype == "float32":
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=3e-5, err_msg=name)
+    else:
+        check_half(got, ref, dtype, "o", name)
+
+
+@pytest.mark.parametrize("dtype", ["float16", "bfloat16", "float32"])
 @pytest.mark.parametrize("case", DECODE_CASES, ids=lambda c: f"b{c[0]}h{c[1]}kv{c[2]}q{c[3]}d{c[5]}")
 def test_decode_matches_oracle(dtype, case):
     b, hq, hkv, sq, cap, d, lengths = case
@@ -489,16 +497,17 @@ def test_decode_matches_oracle(dtype, case):
     for split in (0, 64, 256):
         out = abi.decode(q, k, v, split_len=split, causal=True, offset=offset, kv_len=kv_len)
         torch.cuda.synchronize()
+        assert _lib.last_kernel_path() == _lib.PATH_DECODE
         got = abi.host(out)
         for bi in range(b):
             ref = A.sdpa(inp.q[bi:bi + 1], inp.k[bi:bi + 1, :, :lengths[bi]],
                          inp.v[bi:bi + 1, :, :lengths[bi]], None, True, dtype=dtype,
                          causal_offset=offset, backend="dense", enable_gqa=hkv != hq)
-            check_half(got[bi:bi + 1], ref.out, dtype, "o", f"b{bi} split{split}")
+            check_decode(got[bi:bi + 1], ref.out, dtype, f"b{bi} split{split}")
 
 
-def test_decode_with_bool_mask_and_float_mask():
-    dtype = "float16"
+@pytest.mark.parametrize("dtype", ["float16", "float32"])
+def test_decode_with_bool_mask_and_float_mask(dtype):
     inp = attention_inputs(2, 2, 1, 128, dtype, seq_k=300, with_grad=False, seed=4)
     q, k, v = (abi.dev_tensor(x, dtype) for x in (inp.q, inp.k, inp.v))
     rng = np.random.default_rng(0)
@@ -509,7 +518,7 @@ def test_decode_with_bool_mask_and_float_mask():
         out = abi.decode(q, k, v, mask=torch.from_numpy(mask).cuda())
         torch.cuda.synchronize()
         ref = A.sdpa(inp.q, inp.k, inp.v, mask, False, dtype=dtype, backend="dense")
-        check_half(abi.host(out), ref.out, dtype, "o", f"mask {mask.dtype}")
+        check_decode(abi.host(out), ref.out, dtype, f"mask {mask.dtype}")
 
 
 # ---------------------------------------------------------------------------
