@@ -806,7 +806,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-      if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr[u];
+      if (kw + r < p.Sk) __builtin_nontemporal_store(vr[u], reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8));
     }
   };
   if constexpr (DK == DV) {
@@ -849,7 +849,7 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
 #pragma unroll
       for (int u = 0; u < 32 * CPR / 64; ++u) {
         const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-        if (kw + r < p.Sk) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8) = vr[u];
+        if (kw + r < p.Sk) __builtin_nontemporal_store(vr[u], reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(kw + r) * ov.s2 + q * 8));
       }
     }
   } else {
@@ -1266,7 +1266,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
     const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.dq.s2 + q * 8) = vr[u];
+    if (qw + r < p.Sq) __builtin_nontemporal_store(vr[u], reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.dq.s2 + q * 8));
   }
 }
 
@@ -1299,8 +1299,9 @@ __global__ __launch_bounds__(NT) void bwd_rows_kernel(BwdArgs a, int nqb) {
   for (int u = 0; u < ROWS_U; ++u) {
     qr[u] = qb * RPB + (u * (NT / 64) + w) * RPW + lane / G;
     const int r = qr[u] < p.Sq ? qr[u] : p.Sq - 1;  // past the head: reload its last row, store nothing
-    gv[u] = ld16(gh + static_cast<int64_t>(r) * a.dout.s2);
-    ov[u] = ld16(oh + static_cast<int64_t>(r) * a.o.s2);
+    // (read once here: non-temporal, 49 -> 44 us at B16 H16 S2048 D128)
+    gv[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(gh + static_cast<int64_t>(r) * a.dout.s2));
+    ov[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(oh + static_cast<int64_t>(r) * a.o.s2));
     lv[u] = a.lse[static_cast<int64_t>(bh) * p.Sq + r];
   }
 #pragma unroll
@@ -1569,10 +1570,13 @@ __global__ __launch_bounds__(DQ_NT, 1) void dq_ds_kernel(BwdArgs a) {
       }
       rotate_chunks<T, 32 * CPR / 64>(vr, p.rope, rows, p0, true);
     }
+    // dQ is written once and not read back here: non-temporal stores keep
+    // it from evicting the dS / K stream (255 -> 225 us at B16 H16 S2048
+    // D128; the dK/dV and recomputing dQ epilogues store the same way)
 #pragma unroll
     for (int u = 0; u < 32 * CPR / 64; ++u) {
       const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-      if (qs + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qs + r) * a.dq.s2 + q * 8) = vr[u];
+      if (qs + r < p.Sq) __builtin_nontemporal_store(vr[u], reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qs + r) * a.dq.s2 + q * 8));
     }
   }
 }
