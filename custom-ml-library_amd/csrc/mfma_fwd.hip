@@ -472,11 +472,18 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     }
   }
   T *ob = static_cast<T *>(const_cast<void *>(a.o.data)) + b * a.o.s0 + hq * a.o.s1;
+  // every chunk read back before the first store (a read inside each store's
+  // row guard waits out one LDS latency per store)
+  u32x4 vr[32 * CPR / 64];
 #pragma unroll
   for (int u = 0; u < 32 * CPR / 64; ++u) {
     const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
-    const u32x4 vr = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DV + ((q ^ (r % CPR)) * 16));
-    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.o.s2 + q * 8) = vr;
+    vr[u] = *reinterpret_cast<const u32x4 *>(slice + r * 2 * DV + ((q ^ (r % CPR)) * 16));
+  }
+#pragma unroll
+  for (int u = 0; u < 32 * CPR / 64; ++u) {
+    const int idx = u * 64 + lane, r = idx / CPR, q = idx % CPR;
+    if (qw + r < p.Sq) *reinterpret_cast<u32x4 *>(ob + static_cast<int64_t>(qw + r) * a.o.s2 + q * 8) = vr[u];
   }
   if (a.lse && h == 0 && qrow < p.Sq)
     a.lse[(static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow] =
