@@ -1588,6 +1588,8 @@ template <typename T, int DK, int DV, int MKQ, int MK, bool DR>
 void launch_mk(const BwdArgs &a0, hipStream_t st) {
   const Problem &p = a0.p;
   BwdArgs a = a0;
+  // (stored dS only with a 128-wide head: the sizing gives the others none)
+  if constexpr (DK == 128 || DV == 128) {
   if (a.ds) {
     // Stored dS: row values, then per chunk of KV-head groups (one chunk
     // unless the dS of every group exceeds the region's cap) dK/dV storing
@@ -1614,6 +1616,8 @@ void launch_mk(const BwdArgs &a0, hipStream_t st) {
     }
     return;
   }
+  }
+  a.ds = nullptr;  // (the recomputing pipeline stores no dS)
   // dQ first: its prologue writes the nd / nl row values the dK/dV kernel reads.
   const int n_qb = (p.Sq + QB - 1) / QB;
   {
@@ -1681,12 +1685,19 @@ static int64_t ds_slice_tiles(const Problem &p) {
 // backward runs over chunks of groups that reuse one region: as few chunks
 // as fit the cap, of (nearly) equal size.  0: no stored dS (a slice alone is
 // too large).
+//
+// Stored dS pays only with a 128-wide head: its HBM round trip (written by
+// dK/dV, read by dQ) does not shrink with the head dim, while the recomputing
+// dQ kernel's S and dP products do.  With both dims 64 or below the
+// recomputing kernel is the faster backward (B16 H16 S2048 causal bf16: D32
+// 0.37 against 0.49 ms, D64 0.54 against 0.63 ms; D128 0.96 against 0.89 ms
+// the other way; 128 / 64 mixed within 1%), so those problems store none.
 static int ds_chunk_groups(const Problem &p, int64_t *bytes) {
   constexpr int64_t kCap = int64_t(8) << 30;
   const int64_t slice = ds_slice_tiles(p) * DS_TILE;
   const int64_t per_group = slice * p.rep;
   const int groups = p.B * p.Hkv;
-  if (slice > (int64_t(1) << 31) || per_group > kCap || groups <= 0) {
+  if ((p.Dqk < 128 && p.Dv < 128) || slice > (int64_t(1) << 31) || per_group > kCap || groups <= 0) {
     *bytes = 0;
     return 0;
   }

@@ -151,8 +151,10 @@ int tsattn_sdpa_forward(const tsattn_problem *p, const tsattn_view *q, const tsa
 
 /* Bytes of scratch tsattn_sdpa_backward needs: row deltas and row LSEs (fp32,
  * 2 per query row), the keep bits when dropping without
- * p->dropout_bits, and on the MFMA kernels room for dS stored once (2 KiB per
- * 32 x 32 tile the causal structure visits). */
+ * p->dropout_bits, and on the MFMA kernels with a head dim of 128 (q/k or v)
+ * room for dS stored once (2 KiB per 32 x 32 tile the causal structure
+ * visits); at head dims 64 and 32 the recomputing backward is the faster one
+ * and the query sizes no dS. */
 size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
 
 /*
@@ -161,8 +163,9 @@ size_t tsattn_sdpa_backward_workspace(const tsattn_problem *p);
  * src/tensorsmith/nn/attention.py:200-248 (incl. the GQA group sums at
  * :245-247).  Deterministic: no atomics, every element is written once.
  * With the queried workspace the MFMA path stores dS from the dK/dV kernel
- * and forms dQ as one GEMM over it; a smaller workspace that still holds the
- * row values (and keep bits) makes the dQ kernel recompute S and dP instead.
+ * and forms dQ as one GEMM over it (head dim 128); a smaller workspace that
+ * still holds the row values (and keep bits), or head dims 64 and 32, make
+ * the dQ kernel recompute S and dP instead.
  */
 int tsattn_sdpa_backward(const tsattn_problem *p, const tsattn_view *q, const tsattn_view *k,
                          const tsattn_view *v, const tsattn_view *out, const tsattn_view *dout,
