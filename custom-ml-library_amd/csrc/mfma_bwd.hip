@@ -190,7 +190,11 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   static_assert(STAGE_B % 256 == 0, "stages keep the bank mapping of the blocked layout");
   // Q / dO ring, then a 1 KiB block that DMA parts of tiles past the last
   // one land in (nothing reads it)
-  __shared__ __attribute__((aligned(1024))) char ring[KV_NS * STAGE_B + 1024];
+  // The prologue first stages the workgroup's K and V rows (128 keys each)
+  // in the same bytes.
+  constexpr int KV_STAGE = KB * (DK + DV) * 2;
+  constexpr int RING_B = KV_NS * STAGE_B + 1024 > KV_STAGE ? KV_NS * STAGE_B + 1024 : KV_STAGE;
+  __shared__ __attribute__((aligned(1024))) char ring[RING_B];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -448,20 +452,46 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
   // tiles already issued in flight once a tile has landed.
   constexpr int PARTS = LPT + 1 + MPARTS + (DR ? 1 : 0);
 
-  // This wave's K / V row fragments (B operands of S = Q K^T, dP = dO V^T):
-  // lane (c, h) holds row key, columns 16 i + 8 h .. +7.  Keys past the cache
-  // end read as zeros.
-  const rsrc_t krs = make_rsrc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-  const rsrc_t vrs = make_rsrc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
-  u32x4 kf[SKQ], vf[SKV];
-#pragma unroll
-  for (int i = 0; i < STEPS; ++i) {
-    if (i < SKQ) kf[i] = buf_load16(krs, static_cast<uint32_t>(key) * ks_b + (16 * i + 8 * h) * 2);
-    if (i < SKV) vf[i] = buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + (16 * i + 8 * h) * 2);
-  }
-
   const TileReader<T, DK> rdq(lane);
   const TileReader<T, DV> rdg(lane);
+  // This wave's K / V row fragments (B operands of S = Q K^T, dP = dO V^T):
+  // lane (c, h) holds row key, columns 16 i + 8 h .. +7.  Keys past the cache
+  // end read as zeros.  They come through LDS: the workgroup's 128 K rows
+  // and 128 V rows land there by DMA in the Q / dO tiles' blocked layout
+  // (as one 128-row tile each; wave w loads its blocks w, w + 4, ..., whole
+  // 128-byte lines, eight rows per instruction), then each wave reads its
+  // 32 rows' fragments.  Loaded straight into registers instead, every
+  // fragment instruction touches 32 rows, and the address unit takes 5 us
+  // per workgroup to issue them.
+  u32x4 kf[SKQ], vf[SKV];
+  {
+    const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+    const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+    const uint32_t kvoff = lrow * ks_b + (4 * (w % QGQ) + swz_chunk) * 16;
+    const uint32_t vvoff = lrow * vs_b + (4 * (w % QGG) + swz_chunk) * 16;
+    const uint32_t vst = ring0 + KB * DK * 2;
+#pragma unroll
+    for (int u = 0; u < KB / 16 * QGQ / NW; ++u) {
+      const int n = w + NW * u;  // block (16 rows (n / QGQ), chunk group n % QGQ = w % QGQ)
+      dma16(kdesc, ring0 + n * 1024, kvoff, static_cast<uint32_t>(k0 + 16 * (n / QGQ)) * ks_b);
+    }
+#pragma unroll
+    for (int u = 0; u < KB / 16 * QGG / NW; ++u) {
+      const int n = w + NW * u;
+      dma16(vdesc, vst + n * 1024, vvoff, static_cast<uint32_t>(k0 + 16 * (n / QGG)) * vs_b);
+    }
+    wait_vm_n<0>();
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < STEPS; ++i) {
+      if (i < SKQ) kf[i] = rdq.rows(ring, w, i);
+      if (i < SKV) vf[i] = rdg.rows(ring + KB * DK * 2, w, i);
+    }
+    // every wave's reads done before the ring takes the first Q / dO tiles
+    wait_lgkm0();
+    __syncthreads();
+  }
+
   f32x16 dk_acc[PDK], dv_acc[PDV];
 #pragma unroll
   for (int dt = 0; dt < (PDK > PDV ? PDK : PDV); ++dt) {
@@ -493,9 +523,6 @@ __global__ __launch_bounds__(NT, (dkdv_wg_per_cu<DK, DV, MK, DR>())) void dkdv_k
       issue_next(icur);
     }
   }
-  // The K / V loads were issued first, so this also waits for them; resolve
-  // them here, where the compiler's own vmcnt waits (which do not count the
-  // DMA loads) cannot land inside the loop.
   wait_vm_n<(KV_PD - 1) * PARTS>();
 #pragma unroll
   for (int i = 0; i < STEPS; ++i) {
