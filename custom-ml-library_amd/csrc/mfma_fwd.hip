@@ -140,10 +140,18 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   const u32x4 vdesc = make_desc(head_ptr<T>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
 
   // Q fragments (B operand of S^T = K Q^T): lane holds Q[qrow][16ks + 8h .. +7].
+  // When the workgroup's 128 Q rows fit in ring stages 2 and 3 (DK <= DV)
+  // they come through there: by DMA beside the first two tiles (whole
+  // lines, eight rows per instruction), then each wave's fragment reads.
+  // Otherwise straight into registers (each instruction then touches 32
+  // rows, slow to issue).
+  constexpr bool QSTAGE = BM * DK * 2 <= 2 * STAGE;
   u32x4 qf[SKS];  // (DK channels)
+  if constexpr (!QSTAGE) {
 #pragma unroll
-  for (int ks = 0; ks < SKS; ++ks)
-    qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+    for (int ks = 0; ks < SKS; ++ks)
+      qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
+  }
   // RoPE folded in: the lane's channels 16 ks + 8 h .. + 7 (pairs 8 ks +
   // 4 h ..) rotate by position qpos0 + qrow, exactly as tsattn_rope would.
   // The table loads and the rotation run after the first tiles' DMA issue,
@@ -152,8 +160,10 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // Resolve the Q loads here: the compiler's own vmcnt waits do not count the
   // DMA loads below, so a first use of qf inside the main loop would make it
   // wait there for tiles still in flight.
+  if constexpr (!QSTAGE) {
 #pragma unroll
-  for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]));
+    for (int ks = 0; ks < SKS; ++ks) asm volatile("" : "+v"(qf[ks]));
+  }
 
   const uint32_t lds0 = lds_addr(lds);
   // DMA of key tile `tile` into its ring stage.  The 1 KiB blocks of the K
@@ -262,9 +272,31 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // NS - 1, which no DMA has written yet: zero it (0 x stale NaN is NaN).
   // Every other LDS byte is written by a DMA load before it is read (lanes
   // past the buffer range write zeros).
-  zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
-  __syncthreads();
-  for (int t = 0; t < PD; ++t) issue(t);
+  if constexpr (QSTAGE) {
+    // Q rows into stages 2 and 3 (blocked layout, as a 128-row K tile: wave
+    // w loads blocks w, w + 4, ...), the first two tiles into stages 0 and
+    // 1; every wave's fragment reads done before the zeroing below, which
+    // falls in the staging area.
+    const u32x4 qdesc = make_desc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const uint32_t qoff = (lane >> 2) * qs_b + (4 * (w % QGK) + swz_chunk) * 16;
+#pragma unroll
+    for (int u = 0; u < BM / 16 * QGK / NW; ++u) {
+      const int n = w + NW * u;  // block (16 rows (n / QGK), chunk group n % QGK = w % QGK)
+      dma16(qdesc, lds0 + 2 * STAGE + n * 1024, qoff, static_cast<uint32_t>(q0 + 16 * (n / QGK)) * qs_b);
+    }
+    for (int t = 0; t < PD; ++t) issue(t);
+    wait_vm_n<0>();
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < SKS; ++ks) qf[ks] = rdk.rows(lds + 2 * STAGE, w, ks);
+    wait_lgkm0();
+    __syncthreads();
+    zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
+  } else {
+    zero_lds<NT>(lds + (NS - 1) * STAGE + TILE_K, TILE_V, tid);
+    __syncthreads();
+    for (int t = 0; t < PD; ++t) issue(t);
+  }
   if (rope) {
     // (the compiler's wait for the tables also covers the DMA parts issued
     // before them, which the wait below needs anyway)
