@@ -952,15 +952,19 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   const int w_tiles =
       __builtin_amdgcn_readfirstlane(wlim > 0 ? static_cast<int>((wlim + KT - 1) / KT) : 0);
 
-  u32x4 qf[SKQ], gf[SKV];
+  // The rows' Q, dO and O fragments (lane holds row qrow, channels 16 ks +
+  // 8 h .. +7) and LSE, issued here; consumed after the first tiles' DMA
+  // issue below, so the two latencies overlap.
+  u32x4 qf[SKQ], gf[SKV], of[SKV];
   float lse2, delta;  // -safe(lse) in exp2 units, -delta
+  const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
+  const float lrow_lse = qrow < p.Sq ? a.lse[row] : 0.f;
   {
     const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 2, gs_b = static_cast<uint32_t>(a.dout.s2) * 2;
     const uint32_t os_b = static_cast<uint32_t>(a.o.s2) * 2;
     const rsrc_t qrs = make_rsrc(head_ptr<T>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
     const rsrc_t grs = make_rsrc(head_ptr<T>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
     const rsrc_t ors = make_rsrc(head_ptr<T>(a.o, b, hq), static_cast<uint32_t>(p.Sq) * os_b);
-    u32x4 of[SKV];
 #pragma unroll
     for (int ks = 0; ks < STEPS; ++ks) {
       if (ks < SKQ) qf[ks] = buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + (ks * 16 + h * 8) * 2);
@@ -969,47 +973,7 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
         of[ks] = buf_load16(ors, static_cast<uint32_t>(qrow) * os_b + (ks * 16 + h * 8) * 2);
       }
     }
-    // RoPE folded in: rotate the query fragments as the forward did, and
-    // stage the rotated rows for the dK/dV kernel.
-    if (p.rope.R > 0) {
-      int64_t rows[SKQ];
-      int p0[SKQ];
-#pragma unroll
-      for (int ks = 0; ks < SKQ; ++ks) {
-        rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
-        p0[ks] = 8 * ks + 4 * h;
-      }
-      rotate_chunks<T, SKQ>(qf, p.rope, rows, p0, false);
-      if (qrow < p.Sq && !p.rope.qrot) {  // (qrot: the forward stored them)
-        T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
-#pragma unroll
-        for (int ks = 0; ks < SKQ; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
-      }
-    }
-    const int64_t row = (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow;
-    const float l = qrow < p.Sq ? a.lse[row] : 0.f;
-    // delta = sum_d dO O in fp32; lanes c and c + 32 hold the row's two halves
-    float dsum = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < SKV; ++ks) {
-      const T *ge = reinterpret_cast<const T *>(&gf[ks]);
-      const T *oe = reinterpret_cast<const T *>(&of[ks]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
-    }
-    delta = -xor32_sum(dsum);
-    lse2 = isfinite(l) ? -l * kLog2e : 0.f;
-    if (h == 0 && qrow < p.Sq) store_row_values(a, static_cast<int64_t>(p.B) * p.Hq * p.Sq, row, delta, l);
   }
-  // Resolve these loads before the DMA loads start (the compiler's vmcnt
-  // waits do not count those).
-#pragma unroll
-  for (int ks = 0; ks < STEPS; ++ks) {
-    if (ks < SKQ && ks < SKV) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
-    else if (ks < SKQ) asm volatile("" : "+v"(qf[ks]));
-    else asm volatile("" : "+v"(gf[ks]));
-  }
-  asm volatile("" : "+v"(delta), "+v"(lse2));
 
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 2, vs_b = static_cast<uint32_t>(a.v.s2) * 2;
   const u32x4 kdesc = make_desc(head_ptr<T>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
@@ -1120,9 +1084,53 @@ __global__ __launch_bounds__(NT, 2) void dq_kernel(BwdArgs a) {
   // written it yet) by dS = 0: zero it (0 x stale NaN is NaN).  Every other
   // LDS byte is written by a DMA load before it is read (lanes past the
   // buffer range write zeros).
+  // (no barrier between the zeroing and the DMA loads: they write other
+  // stages; the barrier below orders both before the loop)
   zero_lds<NT>(lds + (DQ_NS - 1) * STAGE, TILE_K, tid);
-  __syncthreads();
   for (int t = 0; t < DQ_PD; ++t) issue(t);
+  {
+    // RoPE folded in: rotate the query fragments as the forward did, and
+    // stage the rotated rows for the dK/dV kernel.
+    if (p.rope.R > 0) {
+      int64_t rows[SKQ];
+      int p0[SKQ];
+#pragma unroll
+      for (int ks = 0; ks < SKQ; ++ks) {
+        rows[ks] = p.rope.qpos0 + (qrow < p.Sq ? qrow : p.Sq - 1);  // rows past Sq: unused
+        p0[ks] = 8 * ks + 4 * h;
+      }
+      rotate_chunks<T, SKQ>(qf, p.rope, rows, p0, false);
+      if (qrow < p.Sq && !p.rope.qrot) {  // (qrot: the forward stored them)
+        T *qk = mut<T>(a.qk) + b * a.qk.s0 + hq * a.qk.s1 + static_cast<int64_t>(qrow) * a.qk.s2;
+#pragma unroll
+        for (int ks = 0; ks < SKQ; ++ks) *reinterpret_cast<u32x4 *>(qk + ks * 16 + h * 8) = qf[ks];
+      }
+    }
+    const float l = lrow_lse;
+    // delta = sum_d dO O in fp32; lanes c and c + 32 hold the row's two halves
+    float dsum = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < SKV; ++ks) {
+      const T *ge = reinterpret_cast<const T *>(&gf[ks]);
+      const T *oe = reinterpret_cast<const T *>(&of[ks]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dsum += static_cast<float>(ge[e]) * static_cast<float>(oe[e]);
+    }
+    delta = -xor32_sum(dsum);
+    lse2 = isfinite(l) ? -l * kLog2e : 0.f;
+    if (h == 0 && qrow < p.Sq) store_row_values(a, static_cast<int64_t>(p.B) * p.Hq * p.Sq, row, delta, l);
+  }
+  // (the compiler's wait for these loads -- it does not count the DMA
+  // loads, so it waits for everything in flight -- also covers the first
+  // tiles; resolved here, no use inside the main loop can make it wait for
+  // tiles in flight)
+#pragma unroll
+  for (int ks = 0; ks < STEPS; ++ks) {
+    if (ks < SKQ && ks < SKV) asm volatile("" : "+v"(qf[ks]), "+v"(gf[ks]));
+    else if (ks < SKQ) asm volatile("" : "+v"(qf[ks]));
+    else asm volatile("" : "+v"(gf[ks]));
+  }
+  asm volatile("" : "+v"(delta), "+v"(lse2));
   wait_vm_n<(DQ_PD - 1) * PPT>();
   __syncthreads();
 
