@@ -369,3 +369,24 @@ def test_random_tape_replays_attention_keys_and_counts_draws():
     y = ts.tensor(np.ones(2), dtype="float64", requires_grad=True)
     with pytest.raises(RuntimeError):
         ts.nn.checkpoint(g, y).sum().backward()
+
+
+@pytest.mark.parametrize("dims,stored", [((128, 128), True), ((128, 64), True), ((64, 128), True),
+                                         ((64, 64), False), ((32, 32), False)])
+def test_backward_workspace_stores_ds_only_with_a_128_wide_head(dims, stored):
+    """The backward workspace query (host logic, no launch): row deltas and
+    LSEs, plus -- on the 16-bit MFMA kernels with a 128-wide head -- the
+    stored dS, 2 KiB per visited 32 x 32 tile.  At head dims 64 and 32 the
+    recomputing dQ pipeline is the faster backward and no dS is sized."""
+    lib = _lib.load()
+    b, h, s = 2, 4, 256
+    p = _problem(dtype=_lib.BF16, batch=b, heads_q=h, heads_kv=h, len_q=s, len_kv=s,
+                 dim_qk=dims[0], dim_v=dims[1], is_causal=1, scale=0.125)
+    rows = -(-2 * b * h * s * 4 // 256) * 256
+    # causal, Sq == Sk: query tile qt keeps the 32-key tiles of the 128-key
+    # blocks up to its own: 4 (qt // 4 + 1) of them
+    tiles = sum(4 * (qt // 4 + 1) for qt in range(s // 32))
+    want = rows + (b * h * tiles * 2048 if stored else 0)
+    assert lib.tsattn_sdpa_backward_workspace(ctypes.byref(p)) == want
+    p.dtype = _lib.F32  # the fp32 kernels recompute: row values only
+    assert lib.tsattn_sdpa_backward_workspace(ctypes.byref(p)) == 2 * b * h * s * 4
