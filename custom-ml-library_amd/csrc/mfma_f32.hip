@@ -124,7 +124,9 @@ __global__ __launch_bounds__(NT, SPLIT ? 1 : 2) void fwd_f32_kernel(F32Args a) {
   static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
   static_assert(PARTS <= 2 * (HD / 4), "at most two DMA parts per S step");
   // the rings, then a 1 KiB block the parts of a tile past the last land in
-  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
+  // (split: then the workgroup's 32 Q rows, staged once for the four waves)
+  constexpr int QSTG = SPLIT ? TL::BYTES : 0;
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024 + QSTG];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -160,12 +162,26 @@ __global__ __launch_bounds__(NT, SPLIT ? 1 : 2) void fwd_f32_kernel(F32Args a) {
   const u32x4 vdesc = make_desc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
 
   // Q fragments: lane (c, h) holds Q[qrow][h D / 2 .. + D / 2), step s = d - h D / 2.
+  // Split: the four waves share the 32 rows, which land in LDS once by DMA
+  // (whole lines per instruction) beside the first tile and are read from
+  // there; fragment loads straight into registers touch 64 lines each.
   float qf[HD];
+  if constexpr (!SPLIT) {
 #pragma unroll
-  for (int j = 0; j < HD / 4; ++j) {
-    const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b +
-                                                                    static_cast<uint32_t>((h * HD + 4 * j) * 4)));
-    qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+    for (int j = 0; j < HD / 4; ++j) {
+      const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b +
+                                                                      static_cast<uint32_t>((h * HD + 4 * j) * 4)));
+      qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+    }
+  } else {
+    static_assert(TL::BLOCKS % NW == 0, "Q blocks split evenly over the waves");
+    const u32x4 qd = make_desc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const uint32_t qst = lds_addr(lds) + RINGS * 2 * STAGE + 1024;
+#pragma unroll
+    for (int u = 0; u < TL::BLOCKS / NW; ++u) {
+      const int n = w + NW * u;
+      dma16(qd, qst + n * 1024, TL::dma_off(n, lane, qs_b), static_cast<uint32_t>(q0 + n * TL::RPB) * qs_b);
+    }
   }
 
   const uint32_t lds0 = lds_addr(lds);
@@ -213,6 +229,15 @@ __global__ __launch_bounds__(NT, SPLIT ? 1 : 2) void fwd_f32_kernel(F32Args a) {
 #pragma unroll
   for (int u = 0; u < PARTS; ++u) issue_part(0, u);
   wait_vm_n<0>();  // the query fragments and the first tile
+  if constexpr (SPLIT) {
+    __syncthreads();  // every wave's Q blocks landed
+    const char *qt = lds + RINGS * 2 * STAGE + 1024;
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) {
+      const float4 x = TL::chunk(qt, c, h * (HD / 4) + j);
+      qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]));
   if constexpr (!SPLIT) __syncthreads();
@@ -431,7 +456,10 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
   constexpr int PARTS = SPLIT ? 2 * TL::BLOCKS : 2 * TL::BLOCKS / NW;
   static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
   static_assert(PARTS <= 2 * (HD / 4), "at most two DMA parts per S step");
-  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
+  // (split: after the rings and the spare block, the workgroup's 32 Q and 32
+  // dO rows, staged once for the four waves)
+  constexpr int QSTG = SPLIT ? 2 * TL::BYTES : 0;
+  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024 + QSTG];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -463,14 +491,29 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
   const rsrc_t grs = make_rsrc(f32_head<float>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
   const u32x4 kdesc = make_desc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
   const u32x4 vdesc = make_desc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  // Split: the four waves share the rows, which land in LDS once by DMA
+  // beside the first tile (as in the forward) and are read from there.
   float qf[HD], gf[HD];
+  if constexpr (!SPLIT) {
 #pragma unroll
-  for (int j = 0; j < HD / 4; ++j) {
-    const uint32_t off = static_cast<uint32_t>((h * HD + 4 * j) * 4);
-    const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + off));
-    const float4 y = __builtin_bit_cast(float4, buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + off));
-    qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
-    gf[4 * j] = y.x, gf[4 * j + 1] = y.y, gf[4 * j + 2] = y.z, gf[4 * j + 3] = y.w;
+    for (int j = 0; j < HD / 4; ++j) {
+      const uint32_t off = static_cast<uint32_t>((h * HD + 4 * j) * 4);
+      const float4 x = __builtin_bit_cast(float4, buf_load16(qrs, static_cast<uint32_t>(qrow) * qs_b + off));
+      const float4 y = __builtin_bit_cast(float4, buf_load16(grs, static_cast<uint32_t>(qrow) * gs_b + off));
+      qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+      gf[4 * j] = y.x, gf[4 * j + 1] = y.y, gf[4 * j + 2] = y.z, gf[4 * j + 3] = y.w;
+    }
+  } else {
+    static_assert(TL::BLOCKS % NW == 0, "Q / dO blocks split evenly over the waves");
+    const u32x4 qd = make_desc(f32_head<float>(a.q, b, hq), static_cast<uint32_t>(p.Sq) * qs_b);
+    const u32x4 gd = make_desc(f32_head<float>(a.dout, b, hq), static_cast<uint32_t>(p.Sq) * gs_b);
+    const uint32_t qst = lds_addr(lds) + RINGS * 2 * STAGE + 1024;
+#pragma unroll
+    for (int u = 0; u < TL::BLOCKS / NW; ++u) {
+      const int n = w + NW * u;
+      dma16(qd, qst + n * 1024, TL::dma_off(n, lane, qs_b), static_cast<uint32_t>(q0 + n * TL::RPB) * qs_b);
+      dma16(gd, qst + TL::BYTES + n * 1024, TL::dma_off(n, lane, gs_b), static_cast<uint32_t>(q0 + n * TL::RPB) * gs_b);
+    }
   }
   const int64_t rows = static_cast<int64_t>(p.B) * p.Hq * p.Sq;
   const int64_t rix = static_cast<int64_t>(bh) * p.Sq + (qrow < p.Sq ? qrow : p.Sq - 1);
@@ -516,6 +559,16 @@ __global__ __launch_bounds__(NT, 1) void dq_f32_kernel(F32Args a) {
 #pragma unroll
   for (int u = 0; u < PARTS; ++u) issue_part(0, u);
   wait_vm_n<0>();
+  if constexpr (SPLIT) {
+    __syncthreads();  // every wave's Q / dO blocks landed
+    const char *qt = lds + RINGS * 2 * STAGE + 1024, *gt = qt + TL::BYTES;
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) {
+      const float4 x = TL::chunk(qt, c, h * (HD / 4) + j), y = TL::chunk(gt, c, h * (HD / 4) + j);
+      qf[4 * j] = x.x, qf[4 * j + 1] = x.y, qf[4 * j + 2] = x.z, qf[4 * j + 3] = x.w;
+      gf[4 * j] = y.x, gf[4 * j + 1] = y.y, gf[4 * j + 2] = y.z, gf[4 * j + 3] = y.w;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < HD; ++i) asm volatile("" : "+v"(qf[i]), "+v"(gf[i]));
   if constexpr (!SPLIT) __syncthreads();
@@ -663,7 +716,10 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
   constexpr int RINGS = SPLIT ? NW : 1, STRIDE = SPLIT ? NW : 1;
   constexpr int PARTS = SPLIT ? 2 * TL::BLOCKS : 2 * TL::BLOCKS / NW;
   static_assert(SPLIT || (PARTS * NW == 2 * TL::BLOCKS && PARTS >= 1), "tile loads split over the waves");
-  __shared__ __attribute__((aligned(1024))) char lds[RINGS * 2 * STAGE + 1024];
+  // (the prologue first stages the workgroup's K and V rows in the same bytes)
+  constexpr int KVB = KEYS * D * 4;  // bytes of the workgroup's K (and of its V) rows
+  constexpr int LDS_B = RINGS * 2 * STAGE + 1024 > 2 * KVB ? RINGS * 2 * STAGE + 1024 : 2 * KVB;
+  __shared__ __attribute__((aligned(1024))) char lds[LDS_B];
 
   const Problem &p = a.p;
   const int tid = threadIdx.x, lane = tid & 63, c = lane & 31, h = lane >> 5;
@@ -694,16 +750,37 @@ __global__ __launch_bounds__(NT, 1) void dkdv_f32_kernel(F32Args a) {
 
   const uint32_t qs_b = static_cast<uint32_t>(a.q.s2) * 4, gs_b = static_cast<uint32_t>(a.dout.s2) * 4;
   const uint32_t ks_b = static_cast<uint32_t>(a.k.s2) * 4, vs_b = static_cast<uint32_t>(a.v.s2) * 4;
-  const rsrc_t krs = make_rsrc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
-  const rsrc_t vrs = make_rsrc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+  // This wave's K and V rows (key = kw + c, half h of the row): staged
+  // through LDS -- the workgroup's rows land there by DMA, whole lines per
+  // instruction, as 32-row FTiles, and each wave reads its 32 rows' halves.
+  // (Straight into registers each instruction touches 64 cache lines: the
+  // address unit, not memory, then bounds the prologue; split workgroups
+  // would also load the same rows four times.)  Keys past the cache end
+  // read as zeros.
   float kf[HD], vf[HD];
+  {
+    const uint32_t lds_kv = lds_addr(lds);
+    const u32x4 kd = make_desc(f32_head<float>(a.k, b, hk), static_cast<uint32_t>(kv_end) * ks_b);
+    const u32x4 vd = make_desc(f32_head<float>(a.v, b, hk), static_cast<uint32_t>(kv_end) * vs_b);
+    static_assert(KEYS / 32 * TL::BLOCKS % NW == 0, "K / V blocks split evenly over the waves");
 #pragma unroll
-  for (int j = 0; j < HD / 4; ++j) {
-    const uint32_t off = static_cast<uint32_t>((h * HD + 4 * j) * 4);
-    const float4 x = __builtin_bit_cast(float4, buf_load16(krs, static_cast<uint32_t>(key) * ks_b + off));
-    const float4 y = __builtin_bit_cast(float4, buf_load16(vrs, static_cast<uint32_t>(key) * vs_b + off));
-    kf[4 * j] = x.x, kf[4 * j + 1] = x.y, kf[4 * j + 2] = x.z, kf[4 * j + 3] = x.w;
-    vf[4 * j] = y.x, vf[4 * j + 1] = y.y, vf[4 * j + 2] = y.z, vf[4 * j + 3] = y.w;
+    for (int u = 0; u < KEYS / 32 * TL::BLOCKS / NW; ++u) {
+      const int m = w + NW * u, t = m / TL::BLOCKS, n = m % TL::BLOCKS;  // tile t (keys k0 + 32 t ..), block n
+      const int row = k0 + 32 * t + n * TL::RPB;
+      dma16(kd, lds_kv + t * TL::BYTES + n * 1024, TL::dma_off(n, lane, ks_b), static_cast<uint32_t>(row) * ks_b);
+      dma16(vd, lds_kv + KVB + t * TL::BYTES + n * 1024, TL::dma_off(n, lane, vs_b), static_cast<uint32_t>(row) * vs_b);
+    }
+    wait_vm_n<0>();
+    __syncthreads();
+    const char *kt = lds + (SPLIT ? 0 : w * TL::BYTES), *vt = lds + KVB + (SPLIT ? 0 : w * TL::BYTES);
+#pragma unroll
+    for (int j = 0; j < HD / 4; ++j) {
+      const float4 x = TL::chunk(kt, c, h * (HD / 4) + j), y = TL::chunk(vt, c, h * (HD / 4) + j);
+      kf[4 * j] = x.x, kf[4 * j + 1] = x.y, kf[4 * j + 2] = x.z, kf[4 * j + 3] = x.w;
+      vf[4 * j] = y.x, vf[4 * j + 1] = y.y, vf[4 * j + 2] = y.z, vf[4 * j + 3] = y.w;
+    }
+    wait_lgkm0();
+    __syncthreads();  // every wave's reads done before the ring takes the first tiles
   }
 
   // tile it = query tile it % n_qt of query head hk rep + it / n_qt
