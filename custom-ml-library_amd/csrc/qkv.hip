@@ -13,9 +13,9 @@
 // that run out^T[n][r] += W[n][e] x[r][e] on MFMA 32x32x16 with W rows and
 // x rows as row fragments, then sum in order 0..7 through LDS.  One-tile
 // workgroups stage the fragments through per-wave LDS rings by DMA (whole
-// cache lines per load instruction) and run four waves of two accumulators
-// each, two workgroups per CU; whole-head workgroups load them directly and
-// run eight waves of one accumulator.  Either way every accumulator sees the
+// cache lines per load instruction, three chunks ahead) and run two waves of
+// four accumulators each, two workgroups per CU; whole-head workgroups load
+// them directly and run eight waves of one accumulator.  Either way every accumulator sees the
 // same chunks in the same order, so the projections are bit-identical
 // across cache types.  The row blocks of one weight tile are consecutive in
 // the XCD-local dispatch order, so they read the tile from HBM about once
@@ -32,6 +32,10 @@ namespace tsattn {
 namespace {
 
 constexpr int NACC = 8;  // chunk accumulators (summed in order)
+#ifndef QKV_STAGES
+#define QKV_STAGES 4
+#endif
+constexpr int QKV_NS = QKV_STAGES;  // ring stages per wave of the staged workgroups
 
 struct QkvArgs {
   int rows, len, E, Hq, Hkv, rope;
@@ -56,22 +60,23 @@ __device__ __forceinline__ const void *uniform_ptr(const void *p) {
 // CT: 32-channel tiles of the head per workgroup -- D / 32 (the whole head,
 // which the int8 quantiser's row maximum needs), or fewer for 16-bit caches,
 // so that more workgroups share the weight stream.
-// Threads per workgroup: four waves (two accumulators each) for staged
+// Threads per workgroup: two waves (four accumulators each) for staged
 // one-tile workgroups, eight (one each) for whole heads.
 template <int CT>
-constexpr int qkv_threads() { return CT == 1 ? 256 : 512; }
+constexpr int qkv_threads() { return CT == 1 ? 128 : 512; }
 
+// (Staged workgroups run two per CU, bounded by their LDS: one wave per SIMD.)
 template <typename T, int D, int CT>
-__global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_append_kernel(QkvArgs a) {
+__global__ __launch_bounds__(qkv_threads<CT>(), 1) void qkv_rope_append_kernel(QkvArgs a) {
   constexpr int TILES = CT, NCB = D / 32 / CT;
   constexpr int NW = qkv_threads<CT>() / 64, APW = NACC / NW;  // waves, accumulators per wave
   static_assert(NCB * CT * 32 == D, "column blocks split the head");
   static_assert(APW * NW == NACC && (CT == 1 || APW == 1), "accumulators split over the waves");
-  // CT == 1: per-wave staging rings (two 8 KiB stages: 32 W rows and 32 x
-  // rows of 64 columns) during the loop, the partial tiles after it
-  constexpr int RING = 2 * 8192;
+  // CT == 1: per-wave staging rings (QKV_NS 8 KiB stages: 32 W rows and 32
+  // x rows of 64 columns) during the loop, the partial tiles after it
+  constexpr int RING = QKV_NS * 8192;
   constexpr int PART = NACC * TILES * 16 * 64 * 4;
-  __shared__ __attribute__((aligned(1024))) char smem[(CT == 1 ? (NW * RING > PART ? NW * RING : PART) : PART) + 1024];
+  __shared__ __attribute__((aligned(1024))) char smem[CT == 1 ? (NW * RING > PART ? NW * RING : PART) : PART];
   auto part = reinterpret_cast<float (*)[TILES][16][64]>(smem);
 
   const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
@@ -113,14 +118,18 @@ __global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_a
     // Staged through LDS: a wave takes the 64-column chunks w, w + NW, ...
     // of the embedding (chunk ch into accumulator ch % 8: its accumulator
     // k % APW for its k-th chunk) and DMAs each chunk's 32 W rows and 32 x
-    // rows into its own two-stage ring, eight rows of 128 bytes (whole cache
-    // lines) per load instruction -- direct fragment loads touch 32 lines
-    // each, and the address unit, not HBM, bounded them.  In the ring,
+    // rows into its own QKV_NS-stage ring, QKV_NS - 1 chunks ahead of the
+    // one it multiplies, eight rows of 128 bytes (whole cache lines) per load
+    // instruction -- direct fragment loads touch 32 lines each, and the
+    // address unit, not HBM, bounded them.  (At E 4096, 48 heads of 128 and
+    // 64 rows: four waves one chunk ahead 17.0 us; two waves three ahead, 1.5x
+    // the bytes in flight per CU, 16.2 us; four ahead 16.5 us.)  In the ring,
     // 16-byte unit u of row r holds unit u ^ (r % 8) of the chunk
     // (conflict-free fragment reads); columns past the embedding, and rows
-    // past the last, read zeros.  The loop needs no barrier: no wave reads
-    // another's ring.
-    const uint32_t sbase = lds_addr(smem) + w * RING, spare = lds_addr(smem) + NW * RING;
+    // past the last, read zeros; the loads past the wave's last chunk land in
+    // the stage of a chunk already multiplied, which nothing reads again.  The
+    // loop needs no barrier: no wave reads another's ring.
+    const uint32_t sbase = lds_addr(smem) + w * RING;
     const int nch = (a.E + 63) / 64;
     const int mine = nch > w ? (nch - 1 - w) / NW + 1 : 0;  // this wave's chunks
     const int lr = lane >> 3, gu = (lane & 7) ^ lr;  // row within 8, global unit
@@ -137,26 +146,28 @@ __global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_a
       xv[i] = (static_cast<uint32_t>(xb_ * a.xs_b + xt_ * a.xs_t + 8 * gu) * 2) |
               (xr_ < a.rows ? 0u : 0x80000000u);
     }
-    // chunk k of this wave (k-th of `mine`; past them: zeros into the spare)
-    auto issue = [&](int k) {
+    // chunk k of this wave (k-th of `mine`; past them: zeros) into the stage at st
+    auto issue = [&](int k, uint32_t st) {
       const int ch = w + NW * k;
       const bool real = k < mine;
-      const uint32_t st = real ? sbase + (k & 1) * 8192 : spare;
       const uint32_t col = static_cast<uint32_t>(ch) * 64 + 8 * gu;  // first column of the lane's unit
       const uint32_t far = (real && col < static_cast<uint32_t>(a.E)) ? 0u : 0x80000000u;
       const uint32_t soff = real ? static_cast<uint32_t>(ch) * 128 : 0u;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(wdesc, real ? st + i * 1024 : spare, wv[i] | far, soff);
+      for (int i = 0; i < 4; ++i) dma16(wdesc, st + i * 1024, wv[i] | far, soff);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dma16(xdesc, real ? st + 4096 + i * 1024 : spare, xv[i] | far, soff);
+      for (int i = 0; i < 4; ++i) dma16(xdesc, st + 4096 + i * 1024, xv[i] | far, soff);
     };
     // fragment of k-step s (0..3) of a staged 32 x 64 tile: row c, unit 2 s + h
     const uint32_t fo = static_cast<uint32_t>(c) * 128;
-    // chunk k: into ring stage k % 2 and accumulator k % APW
+    const uint32_t last = sbase + (QKV_NS - 1) * 8192;
+    uint32_t ist = sbase;  // stage of the next chunk issued
+    int rd = 0;            // ring offset of the stage of the chunk multiplied
     auto step = [&](int k, f32x16 &ac) {
-      issue(k + 1);
-      wait_vm_n<8>();  // chunk k has landed; chunk k + 1's eight loads stay in flight
-      const char *stg = smem + w * RING + (k & 1) * 8192;
+      issue(k + QKV_NS - 1, ist);
+      ist = ist == last ? sbase : ist + 8192;
+      wait_vm_n<8 * (QKV_NS - 1)>();  // chunk k has landed; the next chunks' loads stay in flight
+      const char *stg = smem + w * RING + rd;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const uint32_t u = static_cast<uint32_t>((2 * s + h) ^ (c & 7)) * 16;
@@ -164,13 +175,19 @@ __global__ __launch_bounds__(qkv_threads<CT>(), CT == 1 ? 2 : 1) void qkv_rope_a
         const u32x4 xf = *reinterpret_cast<const u32x4 *>(stg + 4096 + fo + u);
         ac = mfma32<T>(wf, xf, ac);
       }
-      wait_lgkm0();  // reads of this stage done before chunk k + 2 overwrites it
+      wait_lgkm0();  // reads of this stage done before chunk k + QKV_NS overwrites it
+      rd = rd == (QKV_NS - 1) * 8192 ? 0 : rd + 8192;
     };
-    static_assert(APW == 2, "staged workgroups: two accumulators per wave");
-    issue(0);
-    for (int k = 0; k < mine; k += 2) {
-      step(k, acc[0][0]);
-      if (k + 1 < mine) step(k + 1, acc[1][0]);
+    static_assert(8 * (QKV_NS - 1) <= 63 && QKV_NS >= 2, "the ring's loads fit the vector memory counter");
+#pragma unroll
+    for (int k = 0; k < QKV_NS - 1; ++k) {
+      issue(k, ist);
+      ist = ist == last ? sbase : ist + 8192;
+    }
+    for (int k = 0; k < mine; k += APW) {
+#pragma unroll
+      for (int v = 0; v < APW; ++v)
+        if (k + v < mine) step(k + v, acc[v][0]);
     }
     wait_vm_n<0>();
     __syncthreads();  // every ring read before the partial tiles reuse the LDS
