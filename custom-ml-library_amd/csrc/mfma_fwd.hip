@@ -263,6 +263,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   uint64_t drow = 0;
   if constexpr (DR)
     drow = dropout_block_index(p, (static_cast<int64_t>(b) * p.Hq + hq) * p.Sq + qrow, 16 * h);
+  PhiloxPair ph{};  // dropout: the keep words of the tile in flight
   MaskFetch mf;
   // Scores an additive mask has already scaled (x sl + mask log2 e) take 1.
   const float slx = mask_kind(MK) >= 2 ? 1.f : a.sl;
@@ -346,6 +347,11 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       if (i < PVS) vf[i % (FD + 1)] = rdv.cols(vt, i / PDT, i % PDT);
     };
     s = f32x16{};
+    // Dropout: the Philox rounds of tile j's keep words (the softmax after
+    // this block takes them) depend on no product, so they run among the
+    // MFMA steps, a step's share after its MFMAs, where they execute while
+    // the matrix pipe works; after the last tile's block they are not used.
+    if constexpr (DR) ph = philox_pair_start(p.drop, drow + static_cast<uint32_t>(j * BN / 16));
 #pragma unroll
     for (int i = 0; i < FD; ++i) load(i);
     // sched_barrier fences keep each step's reads FD steps ahead of its use.
@@ -356,6 +362,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
       if (i < PVS) oacc[i % PDT] = mfma32<T>(vf[i % (FD + 1)], pb[i / PDT], oacc[i % PDT]);
       if (i + FD < STEPS) load(i + FD);
       if ((i & 1) && (i >> 1) < LPT) issue_part(dt_next, i >> 1);
+      if constexpr (DR) philox_pair_rounds(ph, p.drop, 10 * i / STEPS, 10 * (i + 1) / STEPS);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -417,7 +424,7 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     const bool none_kept = p.drop.thr > 65535u;
     if constexpr (DR) {
       uint64_t dw[4];
-      dropout_words_rows(p.drop, drow + static_cast<uint32_t>(kv0 / 16), dw);
+      philox_pair_rows(ph, dw);  // (rounds run in the MFMA block of tile j)
       const uint32_t thr2 = (p.drop.thr & 0xFFFFu) * 0x00010001u;
 #pragma unroll
       for (int k = 0; k < 8; ++k)

@@ -63,28 +63,68 @@ __device__ __forceinline__ uint64_t dropout_block_index(const Problem &p, int64_
          static_cast<uint64_t>(j16 / 16);
 }
 
+// The two blocks of a word group (dropout_block), advanced a few rounds at a
+// time, so that a kernel can spread the rounds between instructions they do
+// not depend on (the MFMA steps of a tile); the arithmetic of philox4x32,
+// round r keyed (K0 lo + r W0, K0 hi + r W1) mod 2^32.
+struct PhiloxPair {
+  uint32_t c[2][4];
+};
+
+__device__ __forceinline__ PhiloxPair philox_pair_start(const DropDesc &d, uint64_t n) {
+  const uint64_t t = 2 * (d.c0 + n);
+  PhiloxPair s;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    s.c[half][0] = static_cast<uint32_t>(t) | static_cast<uint32_t>(half);
+    s.c[half][1] = static_cast<uint32_t>(t >> 32);
+    s.c[half][2] = static_cast<uint32_t>(d.k1);
+    s.c[half][3] = static_cast<uint32_t>(d.k1 >> 32);
+  }
+  return s;
+}
+
+// Rounds r0 .. r1 - 1 (of 10) of both blocks.
+__device__ __forceinline__ void philox_pair_rounds(PhiloxPair &s, const DropDesc &d, int r0, int r1) {
+  constexpr uint32_t M0 = 0xD2511F53u, M1 = 0xCD9E8D57u;
+  constexpr uint32_t W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+  for (int r = r0; r < r1; ++r) {
+    const uint32_t k0 = static_cast<uint32_t>(d.k0) + static_cast<uint32_t>(r) * W0;
+    const uint32_t k1 = static_cast<uint32_t>(d.k0 >> 32) + static_cast<uint32_t>(r) * W1;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      uint32_t(&c)[4] = s.c[half];
+      const uint64_t p0 = static_cast<uint64_t>(M0) * c[0], p1 = static_cast<uint64_t>(M1) * c[2];
+      const uint32_t n0 = xor3_key(static_cast<uint32_t>(p1 >> 32), c[1], k0);
+      const uint32_t n2 = xor3_key(static_cast<uint32_t>(p0 >> 32), c[3], k1);
+      c[0] = n0;
+      c[1] = static_cast<uint32_t>(p1);
+      c[2] = n2;
+      c[3] = static_cast<uint32_t>(p0);
+    }
+  }
+}
+
 // The 16 dropout words of a lane holding query row `row` against keys
 // kv0 + 8 g + 4 h + r (g, r = 0..3; the MFMA accumulator row pattern of the
-// forward kernel), kv0 a multiple of 32: word (g, r) is bits 16 r .. of
-// out[g].  Lane half h computes the block of keys kv0 + 16 h .. + 15, index
-// n = dropout_block_index(p, row, kv0 + 16 h) (the caller keeps the row's
-// part, loop-invariant), and the two halves exchange the quarters the other
-// needs (v_permlane32_swap exchanges the upper half of its first register
-// with the lower half of its second).
-__device__ __forceinline__ void dropout_words_rows(const DropDesc &d, uint64_t n,
-                                                   uint64_t (&out)[4]) {
-  uint64_t blk[4];
-  dropout_block(d, n, blk);
-  // Block quarter m = keys 4 m .. 4 m + 3 of the block.  Half 0 needs its own
-  // quarters 0, 2 and half 1's 0, 2 (keys 16 ..); half 1 needs half 0's 1, 3
-  // and its own 1, 3.  One upper/lower swap per dword of the pairs (q0, q1) and
-  // (q2, q3) leaves exactly that in both halves, with no selects.
+// forward kernel), kv0 a multiple of 32, from the finished pair of group
+// n = dropout_block_index(p, row, kv0 + 16 h) (lane half h computes the
+// block of keys kv0 + 16 h .. + 15): word (g, r) is bits 16 r .. of out[g].
+// The two halves exchange the quarters the other needs (v_permlane32_swap
+// exchanges the upper half of its first register with the lower half of its
+// second).
+__device__ __forceinline__ void philox_pair_rows(const PhiloxPair &s, uint64_t (&out)[4]) {
+  // Block quarter m = keys 4 m .. 4 m + 3 of the block (words 2m, 2m + 1 of
+  // w, the block's four outputs in order).  Half 0 needs its own quarters 0,
+  // 2 and half 1's 0, 2 (keys 16 ..); half 1 needs half 0's 1, 3 and its own
+  // 1, 3.  One upper/lower swap per dword of the pairs (q0, q1) and (q2, q3)
+  // leaves exactly that in both halves, with no selects.
   uint32_t w[8];
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    w[2 * m] = static_cast<uint32_t>(blk[m]);
-    w[2 * m + 1] = static_cast<uint32_t>(blk[m] >> 32);
-  }
+  for (int half = 0; half < 2; ++half)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[4 * half + i] = s.c[half][i];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(w[e]), "+v"(w[2 + e]));
@@ -94,6 +134,15 @@ __device__ __forceinline__ void dropout_words_rows(const DropDesc &d, uint64_t n
   out[2] = w[2] | (static_cast<uint64_t>(w[3]) << 32);
   out[1] = w[4] | (static_cast<uint64_t>(w[5]) << 32);
   out[3] = w[6] | (static_cast<uint64_t>(w[7]) << 32);
+}
+
+// All of it at once: the lane's 16 words of group n (the caller keeps the
+// row's part of n, loop-invariant).
+__device__ __forceinline__ void dropout_words_rows(const DropDesc &d, uint64_t n,
+                                                   uint64_t (&out)[4]) {
+  PhiloxPair s = philox_pair_start(d, n);
+  philox_pair_rounds(s, d, 0, 10);
+  philox_pair_rows(s, out);
 }
 
 // Keep bit of element (row, key j) on its own (the generic kernels: each
