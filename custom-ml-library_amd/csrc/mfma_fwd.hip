@@ -46,6 +46,8 @@
 // entering as scores * scale + mask (attention.py:105-107) in log2 units
 // (MK = 2 for an f32 mask, 3 for f16 / bf16; 4..6 the same read as 16-byte
 // row pieces when the keys are contiguous and the rows aligned).
+#include <type_traits>
+
 #include "mfma_common.h"
 #include "philox.h"
 #include "rope_math.h"
@@ -429,13 +431,29 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int k = 0; k < 8; ++k)
         km[k] = keep_mask_pair(static_cast<uint32_t>(dw[k >> 1] >> (32 * (k & 1))), thr2);
-      // keep bits for the backward: lane half h holds keys 8 g + 4 h + r
-      if (p.drop.bits) {
+      // keep bits for the backward: lane half h holds keys 8 g + 4 h + r.
+      // One buffer store per tile, always (past the range, so dropped, for
+      // half 1, rows past Sq and without a bits buffer): the end-of-tile wait
+      // counts it and leaves it in flight, where a store it did not count
+      // held each tile until the store, or a DMA part issued after the
+      // previous tile's, had completed.
+      {
         uint32_t bits = none_kept ? 0u : keep_bits16(km) << (4 * h);
-        bits |= __shfl_xor(bits, 32, 64);
-        if (h == 0 && qrow < p.Sq)
-          p.drop.bits[((static_cast<int64_t>(b) * p.Hq + hq) * p.drop.nkt + kv0 / BN) * p.drop.sqp +
-                      qrow] = bits;
+        // lanes 0..31 take their partner's half (v_permlane32_swap exchanges
+        // the upper half of its first register with the lower half of its
+        // second: no LDS round trip)
+        uint32_t mine = bits, other = bits;
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(mine), "+v"(other));
+        bits |= other;
+        // the tile's words: rows 0 .. sqp - 1 of key tile kv0 / BN
+        const uintptr_t tbase =
+            reinterpret_cast<uintptr_t>(p.drop.bits) +
+            ((static_cast<uint64_t>(b) * p.Hq + hq) * p.drop.nkt + static_cast<uint64_t>(kv0 / BN)) *
+                static_cast<uint64_t>(p.drop.sqp) * 4;
+        const rsrc_t br = make_rsrc(reinterpret_cast<const void *>(tbase),
+                                    p.drop.bits ? static_cast<uint32_t>(p.drop.sqp) * 4 : 0u);
+        const uint32_t boff = (static_cast<uint32_t>(qrow) * 4) | (h == 0 && qrow < p.Sq ? 0u : 0x80000000u);
+        __builtin_amdgcn_raw_buffer_store_b32(bits, br, static_cast<int>(boff), 0, 0);
       }
     }
 #pragma unroll
@@ -458,8 +476,10 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
   // wave's work is one straight loop, so the accumulators stay in place;
   // iterations past the wave's last tile only keep the barrier count.
   auto next_dma = [&](int j) { return j + PD; };
-  auto it_end = [&](int) {
-    wait_vm_n<(PD - 1) * LPT>();  // tile j + 1 has landed
+  // (stored: the iteration issued a dropout keep-bit store after its DMA
+  // parts, which may stay in flight)
+  auto it_end = [&](auto stored) {
+    wait_vm_n<(PD - 1) * LPT + (decltype(stored)::value ? 1 : 0)>();  // tile j + 1 has landed
     wait_lgkm0();
     phase_barrier();
   };
@@ -469,15 +489,15 @@ __global__ __launch_bounds__(NT, 2) void fwd_kernel(FwdArgs a) {
     for (; j < w_tiles; ++j) {
       mfma_block(j, next_dma(j), true);
       softmax(j, next_dma(j));
-      it_end(j);
+      it_end(std::bool_constant<DR>{});
     }
     mfma_block(j, next_dma(j), false);  // PV of the last tile
-    it_end(j);
+    it_end(std::false_type{});
     ++j;
   }
   for (; j <= n_tiles; ++j) {
     issue(next_dma(j));
-    it_end(j);
+    it_end(std::false_type{});
   }
   wait_vm_n<0>();  // the last (spare-block) loads, before the epilogue reuses the ring
 

@@ -171,18 +171,16 @@ __device__ __forceinline__ uint32_t keep_mask_pair(uint32_t u, uint32_t thr2) {
 // Keep bits of the 16 words of an MFMA accumulator lane from its pair masks
 // km[k] (keep_mask_pair of words 2k, 2k + 1): word i's bit at 8 (i / 4) +
 // i % 4 (lane half 0's key positions; the other half shifts them by 4).
+// Pair mask k's two halves land at bits 2k and 16 + 2k, the upper ones move
+// down by 15 (word i at bit i), then nibble g (words 4g ..) spreads to bits
+// 8g ..: two instructions per pair and five after.
 __device__ __forceinline__ uint32_t keep_bits16(const uint32_t (&km)[8]) {
-  uint32_t bits = 0;
+  uint32_t acc = 0;
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    const int pos = 8 * (k >> 1) + 2 * (k & 1);  // bit of word 2k
-    const uint32_t sw = __builtin_amdgcn_alignbit(km[k], km[k], 16);  // halves swapped
-    // Every bit of a half equals that half's decision: bit pos (< 16) of km is
-    // word 2k's and bit pos + 1 of sw word 2k + 1's; past 16 the halves trade.
-    const uint32_t m = pos < 16 ? (1u << pos) : (2u << pos);
-    bits |= ((km[k] & m) | (sw & ~m)) & (3u << pos);
-  }
-  return bits;
+  for (int k = 0; k < 8; ++k) acc |= (km[k] & 0x00010001u) << (2 * k);
+  uint32_t x = (acc | (acc >> 15)) & 0xFFFFu;
+  x = (x | (x << 8)) & 0x00FF00FFu;
+  return (x | (x << 4)) & 0x0F0F0F0Fu;
 }
 
 __device__ __forceinline__ bool dropout_keeps(const DropDesc &d, const uint64_t (&w)[4], int i) {
