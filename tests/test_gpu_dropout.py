@@ -129,6 +129,10 @@ def test_dropout_attention_matches_oracle(case):
     bits = abi.dropout_bits_buffer(q, k, v, **kw)
     out, lse, path = abi.forward(q, k, v, dropout_bits=bits, **kw)
     assert path == _lib.PATH_MFMA
+    # a forward given no bits buffer (its per-tile bit stores then fall
+    # outside an empty range) computes the same output and LSE
+    out_nb, lse_nb, _ = abi.forward(q, k, v, **kw)
+    assert torch.equal(out_nb, out) and torch.equal(lse_nb, lse)
     dq, dk, dv, _ = abi.backward(q, k, v, out, g, lse, dropout_bits=bits, **kw)
     # without the forward's bits the backward draws them itself: same gradients
     _lib.profile_enable(True)
