@@ -11,8 +11,9 @@ kernel (tsattn_qkv_rope_append; needs an MI355X).
 * int8 caches bit-exact: codes and scales equal the reference quantiser
   (cache.py:73-77) on the kernel's own 16-bit rows.
 * Cache rows outside [pos, pos + len) untouched; GQA, bias, embed widths
-  that split unevenly over the waves (E 64: one 64-column chunk, a wave with
-  none), one and several new rows.
+  that split unevenly over the waves (E 64: one 64-column chunk, so one
+  wave of the 16-bit kernel and seven of the int8 one have none), one and
+  several new rows.
 """
 
 from __future__ import annotations
@@ -51,7 +52,7 @@ def _check(got, ref, dtype, name):
 
 @pytest.mark.parametrize("dtype", ["bfloat16", "float16"])
 @pytest.mark.parametrize("d,e,t,bias", [(64, 208, 1, False), (128, 256, 5, True), (64, 512, 3, True),
-                                        (128, 96, 1, False), (128, 64, 2, True)])
+                                        (128, 96, 1, False), (128, 64, 2, True), (64, 64, 1, False)])
 def test_fused_projection_rope_append(dtype, d, e, t, bias):
     say(f"qkv rope append {dtype} D{d} E{e} T{t} bias={bias}")
     rng = np.random.default_rng(d + e + t)
